@@ -1,0 +1,225 @@
+/*
+ * logan-hip: MI355X (gfx950) backend for Logan's quantized decode hot path —
+ * the MLX-affine 4/5/6/8-bit dequant-GEMV and the routed-expert MoE block.
+ *
+ * C ABI. Two layers:
+ *
+ *  1. Host-pointer drop-in for the subset of logan-metal's C ABI that the
+ *     Qwen/Llama/Spark runtimes use on this path
+ *     (logan-metal/metal/backend_metal.h). Same argument meaning, same return
+ *     convention: 1 = success, 0 = declined before anything was submitted
+ *     (caller keeps its CPU path, no state changed), -1 = failure after
+ *     submission. Activations and outputs are host f32 arrays; packed weights
+ *     and their [scales][biases] sidecar are host byte arrays uploaded to HBM
+ *     once on first use and cached behind an opaque tensor handle that the
+ *     caller keeps and frees (backend_metal.h:59-66, :180).
+ *     Every `logan_hip_*` symbol of this layer is also exported under its
+ *     `coli_metal_*` name, so logan-metal's unmodified Rust FFI block links.
+ *
+ *  2. Device-native entry points (`logan_hip_affine_*`, `logan_hip_route_topk`,
+ *     `logan_hip_moe_block*`): every pointer is device memory already resident
+ *     in HBM, activations/outputs bf16, work enqueued on the caller's HIP
+ *     stream (`stream` is a hipStream_t; NULL = the null stream). These have no
+ *     direct logan-metal counterpart: they are the HBM-resident form of the
+ *     same operations (cited per function) and what the benchmarks time.
+ *
+ * Formats (fmt codes of backend_metal.mm:206-213, logan-metal/src/lib.rs:860-880):
+ *   15      affine-8, group 64, bf16 sidecar (Spark/MLX raw bytes)
+ *   16..19  affine 4/5/6/8-bit, bf16 sidecar;  20 = 4-bit (Q4 FMA variant, same math)
+ *   21..24  affine 4/5/6/8-bit, fp16 sidecar
+ * Packed weights: O rows of I*bits/8 bytes, one LSB-first little-endian u32
+ * bitstream per row (logan-qwen4/src/lib.rs:3688-3701). Sidecar: O*(I/gs) u16
+ * scales followed by O*(I/gs) u16 biases (backend_metal.mm:218-220).
+ * Dequantised weight: code*scale + bias (logan-qwen4/src/lib.rs:3703-3727).
+ *
+ * Threading: every entry point of layer 1 serialises on one process-wide
+ * mutex (as backend_metal.mm:1678); route begin/finish is single-in-flight per
+ * process (a second begin waits for the first one's work to retire).
+ */
+#ifndef LOGAN_HIP_H
+#define LOGAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Layer 1: host-pointer drop-in                                             */
+/* ------------------------------------------------------------------------ */
+
+typedef struct LoganHipTensor LoganHipTensor;
+
+/* Replaces coli_metal_init (backend_metal.h:22; backend_metal.mm:1934-2045).
+ * 1 when a gfx950 device is usable, else 0. Idempotent. */
+int logan_hip_init(void);
+/* Replaces coli_metal_available (backend_metal.h:35). */
+int logan_hip_available(void);
+/* Replaces coli_metal_shutdown (backend_metal.h:34). Frees staging buffers;
+ * tensor handles stay valid until freed. */
+void logan_hip_shutdown(void);
+/* Replaces coli_metal_stats (backend_metal.h:37): live tensor count/bytes. */
+void logan_hip_stats(size_t *tensor_count, size_t *tensor_bytes);
+/* Replaces coli_metal_mem_info (backend_metal.h:38). 1 ok, 0 unavailable. */
+int logan_hip_mem_info(size_t *used_bytes, size_t *total_bytes);
+
+/* Replace coli_metal_profile_set_on/reset/get (backend_metal.h:42-45).
+ * encode = host time building launches, submit = enqueue time, wait = host
+ * blocking time, kernel = device time between events around each call. */
+void logan_hip_profile_set_on(int on);
+void logan_hip_profile_reset(void);
+void logan_hip_profile_get(uint64_t *encode_ns, uint64_t *submit_ns, uint64_t *wait_ns,
+                           uint64_t *kernel_ns);
+
+/* Replaces coli_metal_matmul (backend_metal.h:63-66) for the affine formats.
+ * y[S,O] = x[S,I] . W^T with W the dequantised affine matrix. `scales` is the
+ * [scales][biases] sidecar. gs is ignored for fmt 15 (fixed 64). Other fmt
+ * codes decline with 0. The first call uploads W and the sidecar to HBM and
+ * stores the handle in *tensor; later calls with the same handle reuse it
+ * (weights assumed stable, backend_metal.h:59-60). A handle whose geometry
+ * differs from the call declines. */
+int logan_hip_matmul(LoganHipTensor **tensor, float *y, const float *x, const void *weights,
+                     const void *scales, int fmt, int S, int I, int O, int gs);
+
+/* Same layout as ColiMetalMatmulDesc (backend_metal.h:68-88). */
+typedef struct LoganHipMatmulDesc {
+  LoganHipTensor *tensor;
+  float *y;
+  const void *weights;
+  const float *scales; /* [scales][biases] u16 sidecar, typed as in the reference */
+  int fmt;
+  int I;
+  int O;
+  int gs;
+  const float *x; /* NULL: use the function-level x */
+  int S;
+} LoganHipMatmulDesc;
+
+/* Replaces coli_metal_matmul_multi (backend_metal.h:100-101): up to 16
+ * independent GEMVs in one submission, one wait. Descriptors with x == NULL
+ * use the shared x/S. Updates descs[n].tensor. */
+int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int count);
+
+/* Replace coli_metal_moe_route_begin/finish/discard/drop_model
+ * (backend_metal.h:163-168; backend_metal.mm:3749-3911). `descs` holds exactly
+ * count*3 descriptors, expert-major [e0.gate, e0.up, e0.down, e1.gate, ...],
+ * gate/up [M rows, D cols], down [D rows, M cols]; count = K <= 16 experts.
+ * One submission: K gate + K up GEMVs, SwiGLU h = silu(g)*u, K down GEMVs.
+ * begin returns an opaque pending handle (NULL = pre-submit decline);
+ * finish waits and writes the K expert outputs (count*D floats, expert-major);
+ * the caller does its own rank-ordered weighted reduction. Unlike the
+ * reference, fmt 16..19 (bf16 sidecars) are accepted as well as 21..24; fmt 7
+ * (MXFP4) declines. */
+void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                                const float *x, int D, int M);
+int logan_hip_moe_route_finish(void *pending, float *out, int count);
+void logan_hip_moe_route_discard(void *pending);
+void logan_hip_moe_route_drop_model(uint64_t model_id);
+
+/* Replaces coli_metal_shared_mxfp4 (backend_metal.h:146-149) for affine
+ * weights: descs = [gate, up, down] (count == 3), out[D] =
+ * down(silu(gate.x) * (up.x)). The scalar shared-expert gate stays with the
+ * caller (logan-qwen4/src/lib.rs:7602-7604). fmt 7 declines. */
+int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                            const float *x, float *out, int D, int Iinter);
+void logan_hip_shared_expert_drop_model(uint64_t model_id);
+
+/* Replace coli_metal_tensor_free / coli_metal_tensor_bytes (backend_metal.h:180-181). */
+void logan_hip_tensor_free(LoganHipTensor *tensor);
+size_t logan_hip_tensor_bytes(const LoganHipTensor *tensor);
+
+/* ------------------------------------------------------------------------ */
+/* Layer 2: device-native (HBM-resident, bf16)                              */
+/* ------------------------------------------------------------------------ */
+
+enum { LOGAN_HIP_F32 = 0, LOGAN_HIP_BF16 = 1 };
+
+/* One affine matrix in device memory (the MLX dense layout,
+ * logan-qwen4/src/lib.rs:11818-11937): weights [O][I*bits/8] (16-byte
+ * aligned), scales [O][I/gs] u16, biases [O][I/gs] u16. */
+typedef struct LoganHipAffine {
+  const void *weights;
+  const void *scales;
+  const void *biases;
+  int O;
+  int I;
+  int bits;       /* 4, 5, 6, 8 */
+  int group_size; /* multiple of 32 dividing I for the fast kernels */
+  int aux_fp16;   /* 0: bf16 sidecars, 1: fp16 */
+} LoganHipAffine;
+
+/* y[M][y_stride] = x[M][x_stride] . W^T  (matmul_mlx_affine_storage,
+ * logan-qwen4/src/lib.rs:3729-3764, per activation row). x bf16, y bf16 or
+ * f32 (y_dtype). f32 accumulation. 1 ok, 0 unsupported geometry, -1 launch
+ * failure. */
+int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
+                          int y_stride, int y_dtype, void *stream);
+
+/* Same product with f32 activations and f32 output, exact per-element
+ * dequantisation (any group size dividing I). */
+int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,
+                              float *y, int y_stride, void *stream);
+
+/* out[nrows][I] = code*scale + bias for rows [row0, row0+nrows), f32 — the
+ * dequantised-weight oracle form (logan-qwen4/src/colisource.rs:779-856),
+ * for bit-exact checks. */
+int logan_hip_affine_dequant(const LoganHipAffine *w, int row0, int nrows, float *out,
+                             void *stream);
+
+/* Router: per token, softmax over E logits then top-k with lower-index ties
+ * (logan-qwen4/src/lib.rs:7993-8043); idx[B][k] in rank order, w[B][k] =
+ * val_r / sum_{r<k} val (:8694). logits_dtype LOGAN_HIP_F32/BF16; E <= 1024,
+ * k <= 32. */
+int logan_hip_route_topk(const void *logits, int logits_dtype, int B, int E, int k, int32_t *idx,
+                         float *w, void *stream);
+
+/* A stack of E experts' matrices (MLX switch_mlp layout,
+ * logan-qwen4/src/lib.rs:11939-12078): expert e's weights start at
+ * weights + e*O*(I*bits/8), its params at e*O*(I/gs) elements. */
+typedef struct LoganHipAffineBank {
+  const void *weights;
+  const void *scales;
+  const void *biases;
+  int E;
+  int O;
+  int I;
+  int bits;
+  int group_size;
+  int aux_fp16;
+} LoganHipAffineBank;
+
+/* Routed-MoE block (logan-qwen/src/lib.rs:535-593; logan-qwen4/src/lib.rs
+ * :8692-8711, :8758-8815, :7597-7759). Routed banks gate/up [E][inter][D],
+ * down [E][D][inter]. Shared expert: shared_gate/up/down with E == 1
+ * (weights NULL = no shared expert); shared_gate_vec bf16 [D] is the scalar
+ * gate row (NULL = gate 1.0). Shared banks must use the routed bits and
+ * group sizes. */
+typedef struct LoganHipMoeBlock {
+  LoganHipAffineBank gate, up, down;
+  LoganHipAffineBank shared_gate, shared_up, shared_down;
+  const void *shared_gate_vec;
+  int top_k;
+} LoganHipMoeBlock;
+
+/* Device workspace bytes for B tokens. */
+size_t logan_hip_moe_workspace_bytes(const LoganHipMoeBlock *blk, int B);
+
+/* out[B][D] = MoE(x[B][D] bf16, logits[B][E]); out_dtype LOGAN_HIP_BF16
+ * (RNE of the f32 result) or LOGAN_HIP_F32. idx_out [B][k] and w_out [B][k]
+ * are optional (NULL) copies of the routing. workspace: device memory of at
+ * least logan_hip_moe_workspace_bytes(blk, B) bytes (256-byte aligned), or
+ * NULL to use a library-owned buffer (allocated on growth). B <= 64,
+ * E <= 1024, k <= 32. 1 ok, 0 unsupported geometry, -1 failure. */
+int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *logits,
+                        int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
+                        float *w_out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Library version string. */
+const char *logan_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LOGAN_HIP_H */

@@ -1,0 +1,129 @@
+"""ctypes binding of liblogan_hip.so (the C ABI in include/logan_hip.h).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "liblogan_hip.so"
+
+LOGAN_HIP_F32 = 0
+LOGAN_HIP_BF16 = 1
+
+
+class MatmulDesc(C.Structure):
+    """LoganHipMatmulDesc == ColiMetalMatmulDesc (backend_metal.h:68-88)."""
+
+    _fields_ = [
+        ("tensor", C.c_void_p),
+        ("y", C.c_void_p),
+        ("weights", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("fmt", C.c_int),
+        ("I", C.c_int),
+        ("O", C.c_int),
+        ("gs", C.c_int),
+        ("x", C.c_void_p),
+        ("S", C.c_int),
+    ]
+
+
+class Affine(C.Structure):
+    _fields_ = [
+        ("weights", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("O", C.c_int),
+        ("I", C.c_int),
+        ("bits", C.c_int),
+        ("group_size", C.c_int),
+        ("aux_fp16", C.c_int),
+    ]
+
+
+class AffineBank(C.Structure):
+    _fields_ = [
+        ("weights", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("E", C.c_int),
+        ("O", C.c_int),
+        ("I", C.c_int),
+        ("bits", C.c_int),
+        ("group_size", C.c_int),
+        ("aux_fp16", C.c_int),
+    ]
+
+
+class MoeBlock(C.Structure):
+    _fields_ = [
+        ("gate", AffineBank),
+        ("up", AffineBank),
+        ("down", AffineBank),
+        ("shared_gate", AffineBank),
+        ("shared_up", AffineBank),
+        ("shared_down", AffineBank),
+        ("shared_gate_vec", C.c_void_p),
+        ("top_k", C.c_int),
+    ]
+
+
+_P = C.c_void_p
+_I = C.c_int
+_SZ = C.c_size_t
+_U64 = C.c_uint64
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "logan_hip_init": (_I, []),
+    "logan_hip_available": (_I, []),
+    "logan_hip_shutdown": (None, []),
+    "logan_hip_stats": (None, [C.POINTER(_SZ), C.POINTER(_SZ)]),
+    "logan_hip_mem_info": (_I, [C.POINTER(_SZ), C.POINTER(_SZ)]),
+    "logan_hip_profile_set_on": (None, [_I]),
+    "logan_hip_profile_reset": (None, []),
+    "logan_hip_profile_get": (None, [C.POINTER(_U64)] * 4),
+    "logan_hip_matmul": (_I, [C.POINTER(_P), _P, _P, _P, _P, _I, _I, _I, _I, _I]),
+    "logan_hip_matmul_multi": (_I, [_P, _I, C.POINTER(MatmulDesc), _I]),
+    "logan_hip_moe_route_begin": (_P, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _I, _I]),
+    "logan_hip_moe_route_finish": (_I, [_P, _P, _I]),
+    "logan_hip_moe_route_discard": (None, [_P]),
+    "logan_hip_moe_route_drop_model": (None, [_U64]),
+    "logan_hip_shared_expert": (_I, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _P, _I, _I]),
+    "logan_hip_shared_expert_drop_model": (None, [_U64]),
+    "logan_hip_tensor_free": (None, [_P]),
+    "logan_hip_tensor_bytes": (_SZ, [_P]),
+    "logan_hip_affine_gemv": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
+    "logan_hip_affine_gemv_f32": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _P]),
+    "logan_hip_affine_dequant": (_I, [C.POINTER(Affine), _I, _I, _P, _P]),
+    "logan_hip_route_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "logan_hip_moe_workspace_bytes": (_SZ, [C.POINTER(MoeBlock), _I]),
+    "logan_hip_moe_block": (_I, [C.POINTER(MoeBlock), _P, _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _P]),
+    "logan_hip_version": (C.c_char_p, []),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("LOGAN_HIP_LIB", LIB_PATH))
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is missing: build it with `python logan_amd/build.py` "
+                "(logan-hip has no CPU fallback)"
+            )
+        handle = C.CDLL(str(path))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib

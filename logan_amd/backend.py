@@ -1,0 +1,288 @@
+"""Host-side mirror of logan-metal's backend-neutral Rust surface, over the C ABI.
+
+Same names and argument meaning as logan-metal/src/lib.rs, with `metal_`
+replaced by `hip_` where the reference name carries the backend:
+
+    metal_init / metal_available            :757-770   -> hip_init / hip_available
+    metal_matmul (fmt 15, Spark)            :795-854   -> hip_matmul
+    metal_matmul_mlx_affine                 :950-975   -> hip_matmul_mlx_affine
+    metal_matmul_mlx_affine_multi           :977-1062  -> hip_matmul_mlx_affine_multi
+    moe_route_begin / moe_route_finish      :3822-3883 -> moe_route_begin / moe_route_finish
+    MoeRoutePending (Drop => discard)       :3803-3815 -> MoeRoutePending (close/__del__)
+    shared_mxfp4 (affine form)              :2583-2678 -> shared_expert
+    dense_profile_start / _stop             :772-789   -> dense_profile_start / _stop
+
+Host arrays are numpy (f32 activations/outputs, u8 packed weights and the
+[scales][biases] u16 sidecar as bytes). Validation declines (returns False /
+None) exactly where the reference's wrappers do (:888-948, :977-1062,
+:3822-3849). Tensor handles are plain ints kept by the caller in `Tensor`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib as L
+
+
+def hip_init() -> bool:
+    return L.lib().logan_hip_init() == 1
+
+
+def hip_available() -> bool:
+    return L.lib().logan_hip_available() == 1
+
+
+def mlx_affine_fmt(bits: int, aux_fp16: bool) -> Optional[int]:
+    """logan-metal/src/lib.rs:860-880 (the Q4-FMA fmt 20 computes the same
+    product, so the plain code 16 is used)."""
+    table = {4: 0, 5: 1, 6: 2, 8: 3}
+    if bits not in table:
+        return None
+    return (21 if aux_fp16 else 16) + table[bits]
+
+
+@dataclass
+class Tensor:
+    """Caller-owned slot for the lazily created device handle
+    (`Mutex<usize>` in the reference, logan-qwen4/src/lib.rs:1576-1577)."""
+
+    handle: int = 0
+
+    def free(self) -> None:
+        if self.handle:
+            L.lib().logan_hip_tensor_free(C.c_void_p(self.handle))
+            self.handle = 0
+
+    def nbytes(self) -> int:
+        return int(L.lib().logan_hip_tensor_bytes(C.c_void_p(self.handle))) if self.handle else 0
+
+
+def _f32(a: np.ndarray) -> np.ndarray:
+    if a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError("expected a C-contiguous float32 array")
+    return a
+
+
+def _bytes(a) -> np.ndarray:
+    a = np.asarray(a)
+    if not a.flags.c_contiguous:
+        raise TypeError("expected a C-contiguous array")
+    return a.view(np.uint8).reshape(-1)
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def hip_matmul(tensor: Tensor, y: np.ndarray, x: np.ndarray, weights, scales, fmt: int,
+               i: int, o: int, gs: int = 0, s: int = 1) -> bool:
+    """logan-metal/src/lib.rs:795-854 (coli_metal_matmul, any fmt; this
+    backend serves 15..24 and declines the rest)."""
+    if not hip_available() or i <= 0 or o <= 0 or s <= 0:
+        return False
+    y, x = _f32(y), _f32(x)
+    if x.size < s * i or y.size < s * o:
+        return False
+    w, a = _bytes(weights), _bytes(scales)
+    h = C.c_void_p(tensor.handle or None)
+    rc = L.lib().logan_hip_matmul(C.byref(h), _ptr(y), _ptr(x), _ptr(w), _ptr(a), fmt, s, i, o, gs)
+    tensor.handle = h.value or 0
+    return rc == 1
+
+
+def _affine_geometry_ok(bits: int, group_size: int, aux_fp16: bool, i: int, o: int,
+                        weights: np.ndarray, aux: np.ndarray) -> Optional[int]:
+    """Rust-side validation of logan-metal/src/lib.rs:901-933; returns fmt."""
+    if i == 0 or o == 0 or group_size == 0 or i % group_size != 0:
+        return None
+    fmt = mlx_affine_fmt(bits, aux_fp16)
+    if fmt is None:
+        return None
+    row_bits = i * bits
+    if row_bits % 32 != 0:
+        return None
+    if weights.size < o * (row_bits // 8):
+        return None
+    if aux.size < 2 * o * (i // group_size) * 2:
+        return None
+    return fmt
+
+
+def hip_matmul_mlx_affine(tensor: Tensor, y: np.ndarray, x: np.ndarray, weights, aux, bits: int,
+                          group_size: int, aux_fp16: bool, i: int, o: int) -> bool:
+    """logan-metal/src/lib.rs:888-975."""
+    if not hip_available():
+        return False
+    y, x = _f32(y), _f32(x)
+    if x.size < i or y.size < o:
+        return False
+    w, a = _bytes(weights), _bytes(aux)
+    fmt = _affine_geometry_ok(bits, group_size, aux_fp16, i, o, w, a)
+    if fmt is None:
+        return False
+    h = C.c_void_p(tensor.handle or None)
+    rc = L.lib().logan_hip_matmul(C.byref(h), _ptr(y), _ptr(x), _ptr(w), _ptr(a), fmt, 1, i, o,
+                                  group_size)
+    tensor.handle = h.value or 0
+    return rc == 1
+
+
+@dataclass
+class MlxAffineMatmulDesc:
+    """logan-metal/src/lib.rs:170-186."""
+
+    tensor: Tensor
+    y: np.ndarray
+    weights: np.ndarray
+    aux: np.ndarray
+    bits: int
+    group_size: int
+    aux_fp16: bool
+    i: int
+    o: int
+    x: Optional[np.ndarray] = None
+
+
+def _raw_descs(descs: Sequence[MlxAffineMatmulDesc], with_y: bool):
+    raw = (L.MatmulDesc * len(descs))()
+    keep = []
+    for k, d in enumerate(descs):
+        w, a = _bytes(d.weights), _bytes(d.aux)
+        fmt = _affine_geometry_ok(d.bits, d.group_size, d.aux_fp16, d.i, d.o, w, a)
+        if fmt is None:
+            return None, None
+        if with_y:
+            y = _f32(d.y)
+            if y.size < d.o:
+                return None, None
+            raw[k].y = _ptr(y)
+        if d.x is not None:
+            x = _f32(d.x)
+            if x.size < d.i:
+                return None, None
+            raw[k].x = _ptr(x)
+            raw[k].S = 1
+            keep.append(x)
+        else:
+            raw[k].x = None
+            raw[k].S = 1
+        raw[k].tensor = d.tensor.handle or None
+        raw[k].weights = _ptr(w)
+        raw[k].scales = _ptr(a)
+        raw[k].fmt = fmt
+        raw[k].I = d.i
+        raw[k].O = d.o
+        raw[k].gs = d.group_size
+        keep += [w, a]
+    return raw, keep
+
+
+def _write_back(descs, raw) -> None:
+    for d, r in zip(descs, raw):
+        d.tensor.handle = r.tensor or 0
+
+
+def hip_matmul_mlx_affine_multi(x: np.ndarray, descs: Sequence[MlxAffineMatmulDesc]) -> bool:
+    """logan-metal/src/lib.rs:977-1062: up to 16 descriptors, one submission."""
+    if not hip_available() or not descs or len(descs) > 16:
+        return False
+    x = _f32(x) if x is not None and x.size else np.zeros(0, np.float32)
+    for d in descs:
+        if d.x is None and x.size < d.i:
+            return False
+    raw, keep = _raw_descs(descs, with_y=True)
+    if raw is None:
+        return False
+    rc = L.lib().logan_hip_matmul_multi(_ptr(x) if x.size else None, 1, raw, len(descs))
+    _write_back(descs, raw)
+    return rc == 1
+
+
+class MoeRoutePending:
+    """Owning handle of one submitted route island (logan-metal/src/lib.rs:3803-3815)."""
+
+    def __init__(self, raw: int, k: int, d: int):
+        self.raw, self.k, self.d = raw, k, d
+
+    def close(self) -> None:
+        if self.raw:
+            L.lib().logan_hip_moe_route_discard(C.c_void_p(self.raw))
+            self.raw = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def moe_route_begin(descs: Sequence[MlxAffineMatmulDesc], x: np.ndarray, d: int,
+                    m: int) -> Optional[MoeRoutePending]:
+    """logan-metal/src/lib.rs:3822-3871: descs are K*3, expert-major
+    [gate, up, down]; None is the pre-submit decline."""
+    if not hip_available() or not descs or len(descs) % 3 != 0:
+        return None
+    x = _f32(x)
+    if x.size < d:
+        return None
+    k = len(descs) // 3
+    if k == 0 or k > 16:
+        return None
+    raw, keep = _raw_descs(descs, with_y=False)
+    if raw is None:
+        return None
+    p = L.lib().logan_hip_moe_route_begin(0, 0, raw, k, _ptr(x), d, m)
+    _write_back(descs, raw)
+    if not p:
+        return None
+    return MoeRoutePending(p, k, d)
+
+
+def moe_route_finish(pending: MoeRoutePending, out: np.ndarray) -> int:
+    """logan-metal/src/lib.rs:3875-3883: 1 success, 0 decline, -1 failure."""
+    out = _f32(out)
+    if out.size < pending.k * pending.d:
+        return 0
+    raw, pending.raw = pending.raw, 0
+    if not raw:
+        return 0
+    return int(L.lib().logan_hip_moe_route_finish(C.c_void_p(raw), _ptr(out), pending.k))
+
+
+def shared_expert(descs: Sequence[MlxAffineMatmulDesc], x: np.ndarray, out: np.ndarray, d: int,
+                  iinter: int) -> Optional[bool]:
+    """Affine form of logan-metal/src/lib.rs:2583-2678 (shared_mxfp4):
+    Ok(Some(())) -> True, Ok(None) (decline) -> None, Err(()) -> False."""
+    if not hip_available() or len(descs) != 3:
+        return None
+    x, out = _f32(x), _f32(out)
+    if x.size < d or out.size < d:
+        return None
+    raw, keep = _raw_descs(descs, with_y=False)
+    if raw is None:
+        return None
+    rc = L.lib().logan_hip_shared_expert(0, 0, raw, 3, _ptr(x), _ptr(out), d, iinter)
+    _write_back(descs, raw)
+    if rc == 1:
+        return True
+    if rc == 0:
+        return None
+    return False
+
+
+def dense_profile_start() -> None:
+    """logan-metal/src/lib.rs:772-779."""
+    L.lib().logan_hip_profile_reset()
+    L.lib().logan_hip_profile_set_on(1)
+
+
+def dense_profile_stop():
+    """logan-metal/src/lib.rs:781-789: (encode, submit, wait, kernel) ns."""
+    vals = [C.c_uint64(0) for _ in range(4)]
+    L.lib().logan_hip_profile_get(*[C.byref(v) for v in vals])
+    L.lib().logan_hip_profile_set_on(0)
+    return tuple(int(v.value) for v in vals)

@@ -1,0 +1,700 @@
+// C ABI of logan-hip: host-pointer drop-in for logan-metal's affine/MoE entry
+// points plus the device-native (HBM-resident) entry points.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/logan_hip.h"
+#include "lh_internal.hpp"
+
+struct LoganHipTensor {
+  uint8_t *w = nullptr;
+  uint16_t *sc = nullptr;
+  uint16_t *bi = nullptr;
+  int fmt = 0, I = 0, O = 0, gs = 0, bits = 0, fp16 = 0;
+  size_t wbytes = 0, abytes = 0;
+};
+
+namespace {
+
+std::mutex g_mtx;
+bool g_tried = false;
+bool g_ok = false;
+int g_dev = -1;
+hipStream_t g_stream = nullptr;
+hipEvent_t g_prof_ev0 = nullptr, g_prof_ev1 = nullptr;
+size_t g_tensor_count = 0, g_tensor_bytes = 0;
+bool g_prof_on = false;
+uint64_t g_prof[4] = {0, 0, 0, 0};  // encode, submit, wait, kernel
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  // Grows the buffer; the caller guarantees no in-flight work uses it.
+  bool ensure(size_t bytes) {
+    if (bytes <= n) return true;
+    if (p) hipFree(p);
+    p = nullptr;
+    n = 0;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      p = nullptr;
+      return false;
+    }
+    n = bytes;
+    return true;
+  }
+  void release() {
+    if (p) hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+DevBuf g_xbuf, g_ybuf, g_gubuf, g_ws;
+
+struct RoutePending {
+  hipEvent_t ev = nullptr;
+  int K = 0, D = 0;
+};
+RoutePending *g_route_inflight = nullptr;  // at most one (single in-flight)
+
+using clk = std::chrono::steady_clock;
+inline uint64_t now_ns() {
+  return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+             clk::now().time_since_epoch())
+      .count();
+}
+
+bool init_locked() {
+  if (g_tried) return g_ok;
+  g_tried = true;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    std::fprintf(stderr, "[logan-hip] device %d is %s, library is built for gfx950\n", dev,
+                 prop.gcnArchName);
+    return false;
+  }
+  if (hipSetDevice(dev) != hipSuccess) return false;
+  // default-priority stream
+  if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) return false;
+  if (hipEventCreate(&g_prof_ev0) != hipSuccess || hipEventCreate(&g_prof_ev1) != hipSuccess)
+    return false;
+  g_dev = dev;
+  g_ok = true;
+  return true;
+}
+
+// fmt -> (bits, fp16, effective group size); false for non-affine codes.
+bool fmt_info(int fmt, int gs_in, int &bits, int &fp16, int &gs) {
+  static const int kBits[5] = {4, 5, 6, 8, 4};
+  if (fmt == 15) {
+    bits = 8;
+    fp16 = 0;
+    gs = 64;
+    return true;
+  }
+  if (fmt >= 16 && fmt <= 20) {
+    bits = kBits[fmt - 16];
+    fp16 = 0;
+  } else if (fmt >= 21 && fmt <= 24) {
+    bits = kBits[fmt - 21];
+    fp16 = 1;
+  } else {
+    return false;
+  }
+  gs = gs_in;
+  return gs > 0;
+}
+
+bool geom_ok(long long I, long long O, int bits, int gs) {
+  if (I <= 0 || O <= 0 || gs <= 0) return false;
+  if (I % gs != 0) return false;
+  if ((I * bits) % 32 != 0) return false;
+  return true;
+}
+
+// Create (first use) or validate the device copy of one affine tensor.
+// Returns nullptr on decline.
+LoganHipTensor *resolve_tensor_locked(LoganHipTensor **slot, const void *weights,
+                                      const void *aux, int fmt, int I, int O, int gs_in) {
+  int bits, fp16, gs;
+  if (!fmt_info(fmt, gs_in, bits, fp16, gs)) return nullptr;
+  if (!geom_ok(I, O, bits, gs)) return nullptr;
+  LoganHipTensor *t = slot ? *slot : nullptr;
+  if (t) {
+    if (t->I != I || t->O != O || t->bits != bits || t->fp16 != fp16 || t->gs != gs)
+      return nullptr;
+    return t;
+  }
+  if (!weights || !aux) return nullptr;
+  t = new LoganHipTensor();
+  t->fmt = fmt;
+  t->I = I;
+  t->O = O;
+  t->gs = gs;
+  t->bits = bits;
+  t->fp16 = fp16;
+  t->wbytes = (size_t)O * ((size_t)I * bits / 8);
+  const size_t pbytes = (size_t)O * (I / gs) * 2;
+  t->abytes = 2 * pbytes;
+  if (hipMalloc(&t->w, t->wbytes) != hipSuccess) {
+    delete t;
+    return nullptr;
+  }
+  if (hipMalloc(&t->sc, t->abytes) != hipSuccess) {
+    hipFree(t->w);
+    delete t;
+    return nullptr;
+  }
+  t->bi = t->sc + pbytes / 2;
+  if (hipMemcpy(t->w, weights, t->wbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(t->sc, aux, t->abytes, hipMemcpyHostToDevice) != hipSuccess) {
+    hipFree(t->w);
+    hipFree(t->sc);
+    delete t;
+    return nullptr;
+  }
+  g_tensor_count++;
+  g_tensor_bytes += t->wbytes + t->abytes;
+  if (slot) *slot = t;
+  return t;
+}
+
+lh::GenDesc gen_desc(const LoganHipTensor *t, const float *x, const float *up, float *y, int S,
+                     int x_stride, int y_stride, int xmode) {
+  lh::GenDesc d{};
+  d.w = t->w;
+  d.sc = t->sc;
+  d.bi = t->bi;
+  d.x = x;
+  d.up = up;
+  d.y = y;
+  d.row_bytes = (long long)t->I * t->bits / 8;
+  d.I = t->I;
+  d.O = t->O;
+  d.gs = t->gs;
+  d.bits = t->bits;
+  d.fp16 = t->fp16;
+  d.S = S;
+  d.x_stride = x_stride;
+  d.y_stride = y_stride;
+  d.xmode = xmode;
+  return d;
+}
+
+// Launch descriptors in batches of 16.
+hipError_t launch_descs(const std::vector<lh::GenDesc> &ds, hipStream_t st) {
+  for (size_t b0 = 0; b0 < ds.size(); b0 += lh::kMaxDescs) {
+    lh::GenBatch b{};
+    b.n = (int)std::min(ds.size() - b0, (size_t)lh::kMaxDescs);
+    b.block_start[0] = 0;
+    for (int i = 0; i < b.n; ++i) {
+      b.d[i] = ds[b0 + i];
+      b.block_start[i + 1] =
+          b.block_start[i] + (b.d[i].O + lh::kGenRowsPerBlock - 1) / lh::kGenRowsPerBlock;
+    }
+    hipError_t e = lh::launch_gemv_generic(b, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+void prof_add(int i, uint64_t v) {
+  if (g_prof_on) g_prof[i] += v;
+}
+
+// After a synchronising wait: fold the device time between the two events.
+void prof_kernel_time() {
+  if (!g_prof_on) return;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, g_prof_ev0, g_prof_ev1) == hipSuccess)
+    g_prof[3] += (uint64_t)(ms * 1e6);
+}
+
+void retire_route_locked() {
+  if (g_route_inflight) {
+    hipEventSynchronize(g_route_inflight->ev);
+    // the pending handle stays owned by the caller; only buffers are released
+    g_route_inflight = nullptr;
+  }
+}
+
+lh::DevMat devmat(const LoganHipAffine &a) {
+  lh::DevMat m{};
+  m.w = reinterpret_cast<const uint8_t *>(a.weights);
+  m.sc = reinterpret_cast<const uint16_t *>(a.scales);
+  m.bi = reinterpret_cast<const uint16_t *>(a.biases);
+  m.I = a.I;
+  m.O = a.O;
+  m.gs = a.group_size;
+  m.bits = a.bits;
+  m.fp16 = a.aux_fp16;
+  m.row_bytes = (long long)a.I * a.bits / 8;
+  m.ng = a.group_size > 0 ? a.I / a.group_size : 0;
+  return m;
+}
+
+bool affine_ok(const LoganHipAffine *a) {
+  if (!a || !a->weights || !a->scales || !a->biases) return false;
+  if (!(a->bits == 4 || a->bits == 5 || a->bits == 6 || a->bits == 8)) return false;
+  return geom_ok(a->I, a->O, a->bits, a->group_size);
+}
+
+lh::DevBank devbank(const LoganHipAffineBank &b) {
+  lh::DevBank d{};
+  LoganHipAffine a{b.weights, b.scales, b.biases, b.O, b.I, b.bits, b.group_size, b.aux_fp16};
+  d.m = devmat(a);
+  d.w_stride = (long long)b.O * d.m.row_bytes;
+  d.p_stride = (long long)b.O * d.m.ng;
+  d.E = b.E;
+  return d;
+}
+
+int rc_from(hipError_t e) { return e == hipSuccess ? 1 : -1; }
+
+}  // namespace
+
+extern "C" {
+
+int logan_hip_init(void) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  return init_locked() ? 1 : 0;
+}
+
+int logan_hip_available(void) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  return g_ok ? 1 : 0;
+}
+
+void logan_hip_shutdown(void) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return;
+  retire_route_locked();
+  hipStreamSynchronize(g_stream);
+  g_xbuf.release();
+  g_ybuf.release();
+  g_gubuf.release();
+  g_ws.release();
+}
+
+void logan_hip_stats(size_t *tensor_count, size_t *tensor_bytes) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (tensor_count) *tensor_count = g_tensor_count;
+  if (tensor_bytes) *tensor_bytes = g_tensor_bytes;
+}
+
+int logan_hip_mem_info(size_t *used_bytes, size_t *total_bytes) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return 0;
+  size_t fr = 0, tot = 0;
+  if (hipMemGetInfo(&fr, &tot) != hipSuccess) return 0;
+  if (used_bytes) *used_bytes = tot - fr;
+  if (total_bytes) *total_bytes = tot;
+  return 1;
+}
+
+void logan_hip_profile_set_on(int on) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  g_prof_on = on != 0;
+}
+
+void logan_hip_profile_reset(void) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  for (auto &v : g_prof) v = 0;
+}
+
+void logan_hip_profile_get(uint64_t *encode_ns, uint64_t *submit_ns, uint64_t *wait_ns,
+                           uint64_t *kernel_ns) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (encode_ns) *encode_ns = g_prof[0];
+  if (submit_ns) *submit_ns = g_prof[1];
+  if (wait_ns) *wait_ns = g_prof[2];
+  if (kernel_ns) *kernel_ns = g_prof[3];
+}
+
+int logan_hip_matmul(LoganHipTensor **tensor, float *y, const float *x, const void *weights,
+                     const void *scales, int fmt, int S, int I, int O, int gs) {
+  if (!tensor || !y || !x || S <= 0) return 0;
+  LoganHipMatmulDesc d{};
+  d.tensor = *tensor;
+  d.y = y;
+  d.weights = weights;
+  d.scales = reinterpret_cast<const float *>(scales);
+  d.fmt = fmt;
+  d.I = I;
+  d.O = O;
+  d.gs = gs;
+  d.x = nullptr;
+  d.S = S;
+  const int rc = logan_hip_matmul_multi(x, S, &d, 1);
+  *tensor = d.tensor;
+  return rc;
+}
+
+int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int count) {
+  if (!descs || count <= 0 || count > 16) return 0;
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return 0;
+  uint64_t t0 = now_ns();
+  // shared activation: every descriptor without its own x must agree on I
+  int shared_I = -1;
+  for (int i = 0; i < count; ++i) {
+    const LoganHipMatmulDesc &d = descs[i];
+    if (!d.y) return 0;
+    if (!d.x) {
+      if (!x || S <= 0) return 0;
+      if (shared_I >= 0 && shared_I != d.I) return 0;
+      shared_I = d.I;
+    } else if (d.S <= 0) {
+      return 0;
+    }
+  }
+  std::vector<LoganHipTensor *> ts(count);
+  for (int i = 0; i < count; ++i) {
+    ts[i] = resolve_tensor_locked(&descs[i].tensor, descs[i].weights, descs[i].scales,
+                                  descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
+    if (!ts[i]) return 0;
+  }
+  retire_route_locked();
+  // staging: shared x, then private x's; outputs concatenated
+  size_t xn = shared_I > 0 ? (size_t)S * shared_I : 0, yn = 0;
+  std::vector<size_t> xoff(count, 0), yoff(count, 0);
+  for (int i = 0; i < count; ++i) {
+    const int s = descs[i].x ? descs[i].S : S;
+    if (descs[i].x) {
+      xoff[i] = xn;
+      xn += (size_t)s * descs[i].I;
+    }
+    yoff[i] = yn;
+    yn += (size_t)s * descs[i].O;
+  }
+  if (!g_xbuf.ensure(xn * 4 + 16) || !g_ybuf.ensure(yn * 4 + 16)) return 0;
+  float *dx = reinterpret_cast<float *>(g_xbuf.p);
+  float *dy = reinterpret_cast<float *>(g_ybuf.p);
+  std::vector<lh::GenDesc> ds;
+  for (int i = 0; i < count; ++i) {
+    const int s = descs[i].x ? descs[i].S : S;
+    const float *xs = descs[i].x ? dx + xoff[i] : dx;
+    ds.push_back(gen_desc(ts[i], xs, nullptr, dy + yoff[i], s, ts[i]->I, ts[i]->O, 0));
+  }
+  uint64_t t1 = now_ns();
+  prof_add(0, t1 - t0);
+  hipError_t e = hipSuccess;
+  if (shared_I > 0)
+    e = hipMemcpyAsync(dx, x, (size_t)S * shared_I * 4, hipMemcpyHostToDevice, g_stream);
+  for (int i = 0; i < count && e == hipSuccess; ++i)
+    if (descs[i].x)
+      e = hipMemcpyAsync(dx + xoff[i], descs[i].x, (size_t)descs[i].S * descs[i].I * 4,
+                         hipMemcpyHostToDevice, g_stream);
+  if (e != hipSuccess) return -1;
+  if (g_prof_on) hipEventRecord(g_prof_ev0, g_stream);
+  e = launch_descs(ds, g_stream);
+  if (e != hipSuccess) return -1;
+  if (g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
+  uint64_t t2 = now_ns();
+  prof_add(1, t2 - t1);
+  for (int i = 0; i < count && e == hipSuccess; ++i) {
+    const int s = descs[i].x ? descs[i].S : S;
+    e = hipMemcpyAsync(descs[i].y, dy + yoff[i], (size_t)s * descs[i].O * 4,
+                       hipMemcpyDeviceToHost, g_stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  prof_add(2, now_ns() - t2);
+  if (e != hipSuccess) return -1;
+  prof_kernel_time();
+  return 1;
+}
+
+void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                                const float *x, int D, int M) {
+  (void)model_id;
+  (void)layer;
+  if (!descs || count <= 0 || count > 16 || !x || D <= 0 || M <= 0) return nullptr;
+  const int K = count;
+  const int expected_I[3] = {D, D, M};
+  const int expected_O[3] = {M, M, D};
+  for (int i = 0; i < K; ++i)
+    for (int r = 0; r < 3; ++r) {
+      const LoganHipMatmulDesc &d = descs[i * 3 + r];
+      int bits, fp16, gs;
+      if (!fmt_info(d.fmt, d.gs, bits, fp16, gs)) return nullptr;
+      if (d.I != expected_I[r] || d.O != expected_O[r]) return nullptr;
+    }
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return nullptr;
+  uint64_t t0 = now_ns();
+  std::vector<LoganHipTensor *> ts((size_t)K * 3);
+  for (int i = 0; i < K * 3; ++i) {
+    ts[i] = resolve_tensor_locked(&descs[i].tensor, descs[i].weights, descs[i].scales,
+                                  descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
+    if (!ts[i]) return nullptr;
+  }
+  retire_route_locked();
+  if (!g_xbuf.ensure((size_t)D * 4 + 16) || !g_gubuf.ensure((size_t)2 * K * M * 4 + 16) ||
+      !g_ybuf.ensure((size_t)K * D * 4 + 16))
+    return nullptr;
+  RoutePending *p = new (std::nothrow) RoutePending();
+  if (!p) return nullptr;
+  if (hipEventCreateWithFlags(&p->ev, hipEventDisableTiming) != hipSuccess) {
+    delete p;
+    return nullptr;
+  }
+  p->K = K;
+  p->D = D;
+  float *dx = reinterpret_cast<float *>(g_xbuf.p);
+  float *gu = reinterpret_cast<float *>(g_gubuf.p);
+  float *out = reinterpret_cast<float *>(g_ybuf.p);
+  // gate -> gu[i*M], up -> gu[K*M + i*M]; down(silu(gate)*up) -> out[i*D]
+  std::vector<lh::GenDesc> s1, s2;
+  for (int i = 0; i < K; ++i) {
+    s1.push_back(gen_desc(ts[i * 3 + 0], dx, nullptr, gu + (size_t)i * M, 1, D, M, 0));
+    s1.push_back(gen_desc(ts[i * 3 + 1], dx, nullptr, gu + (size_t)K * M + (size_t)i * M, 1, D, M, 0));
+    s2.push_back(gen_desc(ts[i * 3 + 2], gu + (size_t)i * M, gu + (size_t)K * M + (size_t)i * M,
+                          out + (size_t)i * D, 1, M, D, 1));
+  }
+  uint64_t t1 = now_ns();
+  prof_add(0, t1 - t0);
+  hipError_t e = hipMemcpyAsync(dx, x, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = launch_descs(s1, g_stream);
+  if (e == hipSuccess) e = launch_descs(s2, g_stream);
+  if (e == hipSuccess) e = hipEventRecord(p->ev, g_stream);
+  prof_add(1, now_ns() - t1);
+  if (e != hipSuccess) {
+    // submitted work may be partially queued: drain it, report as a decline
+    // would hide a real failure, so the handle is still returned and finish
+    // reports -1.
+    hipStreamSynchronize(g_stream);
+    p->K = -1;
+    return p;
+  }
+  g_route_inflight = p;
+  return p;
+}
+
+int logan_hip_moe_route_finish(void *pending, float *out, int count) {
+  if (!pending) return 0;
+  RoutePending *p = reinterpret_cast<RoutePending *>(pending);
+  std::lock_guard<std::mutex> lk(g_mtx);
+  int rc = 1;
+  const uint64_t t0 = now_ns();
+  if (p->K < 0) {
+    rc = -1;
+  } else if (!out || count <= 0) {
+    hipEventSynchronize(p->ev);
+    rc = 0;
+  } else if (hipEventSynchronize(p->ev) != hipSuccess) {
+    rc = -1;
+  } else {
+    const int K = std::min(count, p->K);
+    if (hipMemcpy(out, g_ybuf.p, (size_t)K * p->D * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      rc = -1;
+  }
+  prof_add(2, now_ns() - t0);
+  if (g_route_inflight == p) g_route_inflight = nullptr;
+  hipEventDestroy(p->ev);
+  delete p;
+  return rc;
+}
+
+void logan_hip_moe_route_discard(void *pending) {
+  if (!pending) return;
+  RoutePending *p = reinterpret_cast<RoutePending *>(pending);
+  std::lock_guard<std::mutex> lk(g_mtx);
+  hipEventSynchronize(p->ev);
+  if (g_route_inflight == p) g_route_inflight = nullptr;
+  hipEventDestroy(p->ev);
+  delete p;
+}
+
+void logan_hip_moe_route_drop_model(uint64_t model_id) {
+  (void)model_id;
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return;
+  retire_route_locked();
+  hipStreamSynchronize(g_stream);
+  g_gubuf.release();
+}
+
+int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                            const float *x, float *out, int D, int Iinter) {
+  (void)model_id;
+  (void)layer;
+  if (!descs || count != 3 || !x || !out || D <= 0 || Iinter <= 0) return 0;
+  void *p = logan_hip_moe_route_begin(0, 0, descs, 1, x, D, Iinter);
+  if (!p) return 0;
+  return logan_hip_moe_route_finish(p, out, 1);
+}
+
+void logan_hip_shared_expert_drop_model(uint64_t model_id) { logan_hip_moe_route_drop_model(model_id); }
+
+void logan_hip_tensor_free(LoganHipTensor *t) {
+  if (!t) return;
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (g_ok) {
+    retire_route_locked();
+    hipStreamSynchronize(g_stream);
+  }
+  if (t->w) hipFree(t->w);
+  if (t->sc) hipFree(t->sc);
+  if (g_tensor_count) g_tensor_count--;
+  g_tensor_bytes -= std::min(g_tensor_bytes, t->wbytes + t->abytes);
+  delete t;
+}
+
+size_t logan_hip_tensor_bytes(const LoganHipTensor *t) { return t ? t->wbytes + t->abytes : 0; }
+
+// ---------------------------------------------------------------------------
+
+int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
+                          int y_stride, int y_dtype, void *stream) {
+  if (!affine_ok(w) || !x || !y || M <= 0 || x_stride < w->I || y_stride < w->O) return 0;
+  if (y_dtype != LOGAN_HIP_F32 && y_dtype != LOGAN_HIP_BF16) return 0;
+  const lh::DevMat m = devmat(*w);
+  if (!lh::gemv_bf16_supported(m)) return 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return 0;
+  return rc_from(lh::launch_gemv_bf16(m, reinterpret_cast<const uint16_t *>(x), x_stride, M, y,
+                                      y_stride, y_dtype == LOGAN_HIP_BF16,
+                                      reinterpret_cast<hipStream_t>(stream)));
+}
+
+int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,
+                              float *y, int y_stride, void *stream) {
+  if (!affine_ok(w) || !x || !y || M <= 0 || x_stride < w->I || y_stride < w->O) return 0;
+  LoganHipTensor t;
+  t.w = const_cast<uint8_t *>(reinterpret_cast<const uint8_t *>(w->weights));
+  t.sc = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(w->scales));
+  t.bi = const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(w->biases));
+  t.I = w->I;
+  t.O = w->O;
+  t.gs = w->group_size;
+  t.bits = w->bits;
+  t.fp16 = w->aux_fp16;
+  std::vector<lh::GenDesc> ds{gen_desc(&t, x, nullptr, y, M, x_stride, y_stride, 0)};
+  return rc_from(launch_descs(ds, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int logan_hip_affine_dequant(const LoganHipAffine *w, int row0, int nrows, float *out,
+                             void *stream) {
+  if (!affine_ok(w) || !out || row0 < 0 || nrows < 0 || row0 + nrows > w->O) return 0;
+  return rc_from(lh::launch_dequant(devmat(*w), row0, nrows, out,
+                                    reinterpret_cast<hipStream_t>(stream)));
+}
+
+int logan_hip_route_topk(const void *logits, int logits_dtype, int B, int E, int k, int32_t *idx,
+                         float *w, void *stream) {
+  if (!logits || !idx || !w || B <= 0 || E <= 0 || E > 1024 || k <= 0 || k > 32 || k > E) return 0;
+  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
+  return rc_from(lh::launch_route_topk(logits, logits_dtype == LOGAN_HIP_F32, B, E, k, idx, w,
+                                       reinterpret_cast<hipStream_t>(stream)));
+}
+
+static bool fill_moe_args(const LoganHipMoeBlock *blk, lh::MoeArgs &a) {
+  if (!blk) return false;
+  a = lh::MoeArgs{};
+  a.gate = devbank(blk->gate);
+  a.up = devbank(blk->up);
+  a.down = devbank(blk->down);
+  if (blk->shared_gate.weights) {
+    a.sgate = devbank(blk->shared_gate);
+    a.sup = devbank(blk->shared_up);
+    a.sdown = devbank(blk->shared_down);
+    a.sinter = blk->shared_gate.O;
+  }
+  a.se_gate_vec = reinterpret_cast<const uint16_t *>(blk->shared_gate_vec);
+  a.D = blk->gate.I;
+  a.inter = blk->gate.O;
+  a.E = blk->gate.E;
+  a.k = blk->top_k;
+  return a.D > 0 && a.inter > 0 && a.E > 0 && a.k > 0;
+}
+
+size_t logan_hip_moe_workspace_bytes(const LoganHipMoeBlock *blk, int B) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || B <= 0) return 0;
+  return lh::moe_workspace_bytes(B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
+}
+
+int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *logits,
+                        int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
+                        float *w_out, void *workspace, size_t workspace_bytes, void *stream) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || !x || !logits || !out || B <= 0) return 0;
+  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
+  if (out_dtype != LOGAN_HIP_F32 && out_dtype != LOGAN_HIP_BF16) return 0;
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.logits = logits;
+  a.logits_f32 = logits_dtype == LOGAN_HIP_F32;
+  a.B = B;
+  a.out = out;
+  a.out_f32 = out_dtype == LOGAN_HIP_F32;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  const size_t need =
+      lh::moe_workspace_bytes(B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (workspace) {
+    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return 0;
+    a.ws = workspace;
+    a.ws_bytes = workspace_bytes;
+    return lh::launch_moe_block(a, st);
+  }
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (g_ws.n < need) {
+    // the old buffer may still be read by queued work on any stream
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    if (!g_ws.ensure(need)) return 0;
+  }
+  a.ws = g_ws.p;
+  a.ws_bytes = g_ws.n;
+  return lh::launch_moe_block(a, st);
+}
+
+const char *logan_hip_version(void) { return "logan-hip 0.1.0 (gfx950)"; }
+
+// ---------------------------------------------------------------------------
+// logan-metal symbol names (backend_metal.h) for the implemented subset, so
+// logan-metal's Rust FFI block links against this library unchanged.
+
+int coli_metal_init(void) { return logan_hip_init(); }
+int coli_metal_available(void) { return logan_hip_available(); }
+void coli_metal_shutdown(void) { logan_hip_shutdown(); }
+void coli_metal_stats(size_t *c, size_t *b) { logan_hip_stats(c, b); }
+int coli_metal_mem_info(size_t *u, size_t *t) { return logan_hip_mem_info(u, t); }
+void coli_metal_profile_set_on(int on) { logan_hip_profile_set_on(on); }
+void coli_metal_profile_reset(void) { logan_hip_profile_reset(); }
+void coli_metal_profile_get(uint64_t *a, uint64_t *b, uint64_t *c, uint64_t *d) {
+  logan_hip_profile_get(a, b, c, d);
+}
+int coli_metal_matmul(LoganHipTensor **t, float *y, const float *x, const void *w,
+                      const float *scales, int fmt, int S, int I, int O, int gs) {
+  return logan_hip_matmul(t, y, x, w, scales, fmt, S, I, O, gs);
+}
+int coli_metal_matmul_multi(const float *x, int S, LoganHipMatmulDesc *d, int count) {
+  return logan_hip_matmul_multi(x, S, d, count);
+}
+void *coli_metal_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc *d, int count,
+                                 const float *x, int D, int M) {
+  return logan_hip_moe_route_begin(model_id, layer, d, count, x, D, M);
+}
+int coli_metal_moe_route_finish(void *p, float *out, int count) {
+  return logan_hip_moe_route_finish(p, out, count);
+}
+void coli_metal_moe_route_discard(void *p) { logan_hip_moe_route_discard(p); }
+void coli_metal_moe_route_drop_model(uint64_t m) { logan_hip_moe_route_drop_model(m); }
+int coli_metal_shared_mxfp4(uint64_t model_id, int layer, LoganHipMatmulDesc *d, int count,
+                            const float *x, float *out, int D, int Iinter) {
+  return logan_hip_shared_expert(model_id, layer, d, count, x, out, D, Iinter);
+}
+void coli_metal_shared_mxfp4_drop_model(uint64_t m) { logan_hip_shared_expert_drop_model(m); }
+void coli_metal_tensor_free(LoganHipTensor *t) { logan_hip_tensor_free(t); }
+size_t coli_metal_tensor_bytes(const LoganHipTensor *t) { return logan_hip_tensor_bytes(t); }
+
+}  // extern "C"

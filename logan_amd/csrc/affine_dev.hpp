@@ -1,0 +1,307 @@
+// Device-side building blocks for MLX-affine packed rows on gfx950 (CDNA4).
+//
+// Packed format (logan-qwen4/src/lib.rs:3688-3701, colisource.rs:719-722): a
+// row of I codes is I*bits/32 little-endian u32 words holding one LSB-first
+// bitstream. A "chunk" here is 32 consecutive codes = exactly `bits` words
+// (16/20/24/32 bytes for 4/5/6/8-bit), which always lies inside one
+// quantisation group because group sizes are multiples of 32.
+//
+// Dequantised weight (lib.rs:3723-3724): w = code * scale + bias, f32.
+// The chunk dot product is evaluated in the factored form
+//     sum_k w_k x_k = scale * sum_k code_k x_k + bias * sum_k x_k
+// with the code*x products done by v_dot2c_f32_bf16 on bf16 pairs:
+//   * 4/5/6-bit: each half of a pair is the bf16 bit pattern 0x43nn, i.e.
+//     128 + (code << a) exactly (a <= 2 keeps it inside the 7 mantissa bits);
+//     the x operand carries x * 2^-a (exact), so
+//     sum (128 + code 2^a)(x 2^-a) = 128 * xs' + sum code x,
+//     where xs' = sum x * 2^-a is precomputed once per x.
+//   * 8-bit: v_cvt_f32_ubyteN gives code exactly in f32; its top 16 bits are
+//     the exact bf16 of the code (<= 8 significant bits).
+// All products code*x are exact in f32; sums are f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lh {
+
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a),
+                                         __builtin_bit_cast(bf16x2_v, b), c,
+                                         false);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+__device__ __forceinline__ float aux_to_f32(uint32_t b, bool fp16) {
+  return fp16 ? f16_to_f32(b) : bf16_to_f32(b);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (logan-core/src/math.rs:279-283).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Exact bf16 bits of a float that is known to be representable (power-of-two
+// scaled bf16 value).
+__device__ __forceinline__ uint32_t f32_hi16(float f) {
+  return __float_as_uint(f) >> 16;
+}
+
+// Which two codes of a 32-code chunk form bf16 pair p (0..15), and the
+// power-of-two exponent each code is shifted by inside its pair half.
+template <int BITS>
+struct PairMap;
+
+template <>
+struct PairMap<4> {
+  // word t = p/4 holds codes 8t..8t+7; pair (t,j) = nibbles j and j+4.
+  static __device__ __forceinline__ int lo(int p) { return 8 * (p >> 2) + (p & 3); }
+  static __device__ __forceinline__ int hi(int p) { return lo(p) + 4; }
+  static __device__ __forceinline__ int alo(int) { return 0; }
+  static __device__ __forceinline__ int ahi(int) { return 0; }
+};
+
+template <>
+struct PairMap<5> {
+  // groups q of 6 codes (30 bits); pair (q,i) = codes 6q+i and 6q+i+3, the
+  // low one shifted left by 1 inside its half; pair 15 = codes 30, 31.
+  static __device__ __forceinline__ int lo(int p) {
+    return p == 15 ? 30 : 6 * (p / 3) + (p % 3);
+  }
+  static __device__ __forceinline__ int hi(int p) { return p == 15 ? 31 : lo(p) + 3; }
+  static __device__ __forceinline__ int alo(int p) { return p == 15 ? 0 : 1; }
+  static __device__ __forceinline__ int ahi(int) { return 0; }
+};
+
+template <>
+struct PairMap<6> {
+  static __device__ __forceinline__ int lo(int p) { return 2 * p; }
+  static __device__ __forceinline__ int hi(int p) { return 2 * p + 1; }
+  static __device__ __forceinline__ int alo(int) { return 0; }
+  static __device__ __forceinline__ int ahi(int) { return 0; }
+};
+
+template <>
+struct PairMap<8> {
+  static __device__ __forceinline__ int lo(int p) { return 2 * p; }
+  static __device__ __forceinline__ int hi(int p) { return 2 * p + 1; }
+  static __device__ __forceinline__ int alo(int) { return 0; }
+  static __device__ __forceinline__ int ahi(int) { return 0; }
+};
+
+// 128.0 offset applies to every width except 8-bit.
+template <int BITS>
+struct Magic {
+  static constexpr float offset = BITS == 8 ? 0.0f : 128.0f;
+};
+
+// x operand of one chunk for one activation row: 16 bf16 pairs plus the two
+// chunk sums (xs = sum x, xsp = sum x*2^-a) used by the scale/bias fold.
+struct XChunk {
+  uint32_t p[16];
+  float xs;
+  float xsp;
+};
+
+// Build the x operand from 32 bf16 activations (raw bits, xb[k] = x[k]).
+template <int BITS>
+__device__ __forceinline__ void make_xchunk_bf16(XChunk &xc, const uint32_t (&xb)[32]) {
+  float s = 0.f, sp = 0.f;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
+    const float xl = bf16_to_f32(xb[kl]) * (PairMap<BITS>::alo(p) ? 0.5f : 1.0f);
+    const float xh = bf16_to_f32(xb[kh]) * (PairMap<BITS>::ahi(p) ? 0.5f : 1.0f);
+    xc.p[p] = f32_hi16(xl) | (f32_hi16(xh) << 16);
+    s += bf16_to_f32(xb[kl]) + bf16_to_f32(xb[kh]);
+    sp += xl + xh;
+  }
+  xc.xs = s;
+  xc.xsp = sp;
+}
+
+// f32 activations: split x = hi + lo (both bf16, RNE) so the pair dot keeps
+// ~16 significant bits of x; hi and lo chunks share xs/xsp of the full x.
+template <int BITS>
+__device__ __forceinline__ void make_xchunk_f32(XChunk &hi, XChunk &lo,
+                                                const float (&xf)[32]) {
+  float s = 0.f, sp = 0.f;
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+    const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
+    const float sl = PairMap<BITS>::alo(p) ? 0.5f : 1.0f;
+    const float sh = PairMap<BITS>::ahi(p) ? 0.5f : 1.0f;
+    const float xl = xf[kl] * sl, xh = xf[kh] * sh;
+    const uint32_t hl = f32_to_bf16_rne(xl), hh = f32_to_bf16_rne(xh);
+    const uint32_t ll = f32_to_bf16_rne(xl - bf16_to_f32(hl));
+    const uint32_t lh = f32_to_bf16_rne(xh - bf16_to_f32(hh));
+    hi.p[p] = hl | (hh << 16);
+    lo.p[p] = ll | (lh << 16);
+    s += xf[kl] + xf[kh];
+    sp += xl + xh;
+  }
+  hi.xs = lo.xs = s;
+  hi.xsp = lo.xsp = sp;
+}
+
+// Constants kept in registers so the unpack uses v_and_or_b32 (VOP3 on gfx9
+// takes no literal operands).
+struct UnpackConsts {
+  uint32_t m4;     // 0x000F000F (SGPR)
+  uint32_t m5;     // 0x001F003E (SGPR)
+  uint32_t magic;  // 0x43004300 (VGPR)
+  __device__ __forceinline__ void init() {
+    m4 = 0x000F000Fu;
+    m5 = 0x001F003Eu;
+    magic = 0x43004300u;
+    asm volatile("" : "+s"(m4));
+    asm volatile("" : "+s"(m5));
+    asm volatile("" : "+v"(magic));
+  }
+};
+
+// Unpack one chunk (BITS words) into 16 bf16 pairs in PairMap order.
+template <int BITS>
+__device__ __forceinline__ void unpack_chunk(uint32_t (&q)[16], const uint32_t (&w)[BITS],
+                                             const UnpackConsts &k);
+
+template <>
+__device__ __forceinline__ void unpack_chunk<4>(uint32_t (&q)[16], const uint32_t (&w)[4],
+                                                const UnpackConsts &k) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    q[4 * t + 0] = (w[t] & k.m4) | k.magic;
+    q[4 * t + 1] = ((w[t] >> 4) & k.m4) | k.magic;
+    q[4 * t + 2] = ((w[t] >> 8) & k.m4) | k.magic;
+    q[4 * t + 3] = ((w[t] >> 12) & k.m4) | k.magic;
+  }
+}
+
+template <>
+__device__ __forceinline__ void unpack_chunk<5>(uint32_t (&q)[16], const uint32_t (&w)[5],
+                                                const UnpackConsts &k) {
+  // window q holds stream bits [30q-1, 30q+31): code 6q+i at bit 1+5i.
+  uint32_t win[5];
+  win[0] = w[0] << 1;
+  win[1] = __builtin_amdgcn_alignbit(w[1], w[0], 29);
+  win[2] = __builtin_amdgcn_alignbit(w[2], w[1], 27);
+  win[3] = __builtin_amdgcn_alignbit(w[3], w[2], 25);
+  win[4] = __builtin_amdgcn_alignbit(w[4], w[3], 23);
+#pragma unroll
+  for (int g = 0; g < 5; ++g) {
+    q[3 * g + 0] = (win[g] & k.m5) | k.magic;
+    q[3 * g + 1] = ((win[g] >> 5) & k.m5) | k.magic;
+    q[3 * g + 2] = ((win[g] >> 10) & k.m5) | k.magic;
+  }
+  // codes 30, 31 live in w[4] bits 22..31
+  const uint32_t c30 = (w[4] >> 22) & 31u, c31 = w[4] >> 27;
+  q[15] = c30 | (c31 << 16) | k.magic;
+}
+
+template <int BITS, int K>
+__device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[BITS]) {
+  constexpr int bit = K * BITS, wi = bit / 32, sh = bit % 32;
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  if constexpr (sh + BITS <= 32) {
+    return (w[wi] >> sh) & mask;
+  } else {
+    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & mask;
+  }
+}
+
+template <int P>
+__device__ __forceinline__ void unpack6_pair(uint32_t (&q)[16], const uint32_t (&w)[6],
+                                             const UnpackConsts &k) {
+  q[P] = code_at<6, 2 * P>(w) | (code_at<6, 2 * P + 1>(w) << 16) | k.magic;
+  if constexpr (P + 1 < 16) unpack6_pair<P + 1>(q, w, k);
+}
+
+template <>
+__device__ __forceinline__ void unpack_chunk<6>(uint32_t (&q)[16], const uint32_t (&w)[6],
+                                                const UnpackConsts &k) {
+  unpack6_pair<0>(q, w, k);
+}
+
+template <>
+__device__ __forceinline__ void unpack_chunk<8>(uint32_t (&q)[16], const uint32_t (&w)[8],
+                                                const UnpackConsts &) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t f0 = __float_as_uint((float)(w[t] & 255u));
+    const uint32_t f1 = __float_as_uint((float)((w[t] >> 8) & 255u));
+    const uint32_t f2 = __float_as_uint((float)((w[t] >> 16) & 255u));
+    const uint32_t f3 = __float_as_uint((float)(w[t] >> 24));
+    q[2 * t + 0] = (f1 & 0xffff0000u) | (f0 >> 16);
+    q[2 * t + 1] = (f3 & 0xffff0000u) | (f2 >> 16);
+  }
+}
+
+// sum over the chunk of pair(q) . pair(x) with two independent accumulators.
+__device__ __forceinline__ float pairs_dot(const uint32_t (&q)[16], const uint32_t (&x)[16]) {
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int p = 0; p < 16; p += 2) {
+    a0 = dot2(q[p], x[p], a0);
+    a1 = dot2(q[p + 1], x[p + 1], a1);
+  }
+  return a0 + a1;
+}
+
+// Contribution of one chunk: scale * (acc - offset*xsp) + bias * xs.
+template <int BITS>
+__device__ __forceinline__ float chunk_fold(float acc, float sc, float bi, float xs,
+                                            float xsp) {
+  if constexpr (BITS == 8) {
+    return fmaf(bi, xs, sc * acc);
+  } else {
+    return fmaf(bi, xs, sc * fmaf(-Magic<BITS>::offset, xsp, acc));
+  }
+}
+
+// Load one chunk (BITS dwords) starting at a byte address aligned to 4*BITS
+// bytes modulo 16 (4-bit: 16 B, 5-bit: 4 B, 6-bit: 8 B, 8-bit: 32 B).
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+template <int BITS>
+__device__ __forceinline__ void load_chunk(uint32_t (&w)[BITS], const uint8_t *p) {
+  if constexpr (BITS == 4) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (BITS == 8) {
+    const uint4 v0 = reinterpret_cast<const uint4 *>(p)[0];
+    const uint4 v1 = reinterpret_cast<const uint4 *>(p)[1];
+    w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+    w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+  } else if constexpr (BITS == 6) {
+    const uint2 *q = reinterpret_cast<const uint2 *>(p);
+    const uint2 a = q[0], b = q[1], c = q[2];
+    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+  } else {
+    const u32x4_a4 a = *reinterpret_cast<const u32x4_a4 *>(p);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    w[4] = *reinterpret_cast<const uint32_t *>(p + 16);
+  }
+}
+
+// Sum over `WIDTH` consecutive lanes (WIDTH a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float team_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+}  // namespace lh

@@ -1,0 +1,324 @@
+// Dense MLX-affine GEMV kernels for gfx950.
+//
+//  * gemv_bf16_kernel: the decode hot path. A "team" of LANES lanes owns one
+//    weight row at a time; lane l owns chunks c = l + LANES*j (32 codes each),
+//    so a team's loads of one row are contiguous 16-32 B per lane. The x
+//    operand of the lane's chunks is built once (bf16 pairs in the unpack
+//    order) and kept in VGPRs for every row the team visits. U rows are
+//    loaded before any is consumed to keep several 128-bit loads in flight
+//    per lane. The team sum is a butterfly over LANES lanes.
+//  * gemv_generic_kernel: any bits/group size, f32 activations, f32 output,
+//    per-element exact dequantisation (code*scale+bias, as
+//    logan-qwen4/src/lib.rs:3752-3762); serves the f32 host ABI and shapes
+//    without a fast kernel. Up to 16 descriptors per launch.
+//  * dequant_kernel: writes code*scale+bias per element (bit-exact probe).
+#include "affine_dev.hpp"
+#include "lh_internal.hpp"
+
+namespace lh {
+
+struct GemvParams {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  const uint16_t *x;
+  void *y;
+  long long row_bytes;
+  int I, O, ng, gsc;  // gsc = chunks per group
+  int fp16, x_stride, M, y_stride, y_bf16;
+};
+
+// SPLIT > 1: SPLIT teams share one row, each over a contiguous K segment of
+// LANES*CPL chunks; their partial sums meet in LDS and are added in segment
+// order.
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
+  constexpr int TEAMS = 256 / LANES;
+  constexpr int ROWTEAMS = TEAMS / SPLIT;
+  const int lane = threadIdx.x & (LANES - 1);
+  const int team = threadIdx.x / LANES;
+  const int rteam = team / SPLIT, seg = team % SPLIT;
+  const int cbase = seg * LANES * CPL;
+  const int C = a.I >> 5;
+  UnpackConsts kc;
+  kc.init();
+  __shared__ float s_part[SPLIT > 1 ? TEAMS * U * MT : 1];
+
+  int gidx[CPL];
+  bool cval[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = cbase + lane + LANES * j;
+    cval[j] = c < C;
+    gidx[j] = c / a.gsc;
+  }
+
+  XChunk xc[MT][CPL];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = cbase + lane + LANES * j;
+      uint32_t xb[32];
+      if (cval[j] && m < a.M) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)m * a.x_stride + 32 * c);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const uint4 t = src[v];
+          xb[8 * v + 0] = t.x & 0xffffu; xb[8 * v + 1] = t.x >> 16;
+          xb[8 * v + 2] = t.y & 0xffffu; xb[8 * v + 3] = t.y >> 16;
+          xb[8 * v + 4] = t.z & 0xffffu; xb[8 * v + 5] = t.z >> 16;
+          xb[8 * v + 6] = t.w & 0xffffu; xb[8 * v + 7] = t.w >> 16;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 32; ++v) xb[v] = 0;
+      }
+      make_xchunk_bf16<BITS>(xc[m][j], xb);
+    }
+  }
+
+  const int rows_per_block = ROWTEAMS * U;
+  for (int base = blockIdx.x * rows_per_block; base < a.O; base += gridDim.x * rows_per_block) {
+    const int r0 = base + rteam * U;
+    uint32_t wv[U][CPL][BITS];
+    float scv[U][CPL], biv[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + u;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = cbase + lane + LANES * j;
+        if (row < a.O && cval[j]) {
+          load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)c * (4 * BITS));
+        } else {
+#pragma unroll
+          for (int t = 0; t < BITS; ++t) wv[u][j][t] = 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + u;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (row < a.O && cval[j]) {
+          const size_t pi = (size_t)row * a.ng + gidx[j];
+          scv[u][j] = aux_to_f32(a.sc[pi], a.fp16);
+          biv[u][j] = aux_to_f32(a.bi[pi], a.fp16);
+        } else {
+          scv[u][j] = 0.f;
+          biv[u][j] = 0.f;
+        }
+      }
+    }
+    float part[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) part[u][m] = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        uint32_t q[16];
+        unpack_chunk<BITS>(q, wv[u][j], kc);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const float acc = pairs_dot(q, xc[m][j].p);
+          part[u][m] += chunk_fold<BITS>(acc, scv[u][j], biv[u][j], xc[m][j].xs, xc[m][j].xsp);
+        }
+      }
+    }
+    float tot[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) tot[u][m] = team_sum<LANES>(part[u][m]);
+    if constexpr (SPLIT > 1) {
+      if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int m = 0; m < MT; ++m) s_part[(team * U + u) * MT + m] = tot[u][m];
+      }
+      __syncthreads();
+      if (seg == 0 && lane == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int m = 0; m < MT; ++m) {
+            float v = tot[u][m];
+#pragma unroll
+            for (int s = 1; s < SPLIT; ++s) v += s_part[((team + s) * U + u) * MT + m];
+            tot[u][m] = v;
+          }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = r0 + u;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = tot[u][m];
+        if (seg == 0 && lane == 0 && row < a.O && m < a.M) {
+          if (a.y_bf16)
+            reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
+                (uint16_t)f32_to_bf16_rne(v);
+          else
+            reinterpret_cast<float *>(a.y)[(size_t)m * a.y_stride + row] = v;
+        }
+      }
+    }
+  }
+}
+
+template <int BITS, int LANES, int CPL, int MT, int SPLIT = 1>
+static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st) {
+  constexpr int U = CPL == 1 ? 4 : (CPL == 2 ? 2 : 1);
+  constexpr int rows_per_block = (256 / LANES / SPLIT) * U;
+  const int blocks = (p.O + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((gemv_bf16_kernel<BITS, LANES, CPL, U, MT, SPLIT>), dim3(blocks), dim3(256), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+template <int BITS, int MT>
+static hipError_t gemv_dispatch_shape(const GemvParams &p, hipStream_t st) {
+  const int C = p.I >> 5;
+  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT>(p, st);
+  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT>(p, st);
+  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT>(p, st);
+  if (C <= 128) return gemv_launch_t<BITS, 64, 2, MT>(p, st);
+  if (C <= 256) return gemv_launch_t<BITS, 64, 4, MT>(p, st);
+  if (C <= 512) return gemv_launch_t<BITS, 64, 4, MT, 2>(p, st);
+  return hipErrorInvalidValue;
+}
+
+template <int MT>
+static hipError_t gemv_dispatch_bits(const GemvParams &p, int bits, hipStream_t st) {
+  switch (bits) {
+    case 4: return gemv_dispatch_shape<4, MT>(p, st);
+    case 5: return gemv_dispatch_shape<5, MT>(p, st);
+    case 6: return gemv_dispatch_shape<6, MT>(p, st);
+    case 8: return gemv_dispatch_shape<8, MT>(p, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+bool gemv_bf16_supported(const DevMat &m) {
+  if (!(m.bits == 4 || m.bits == 5 || m.bits == 6 || m.bits == 8)) return false;
+  if (m.gs <= 0 || m.gs % 32 != 0 || m.I % m.gs != 0) return false;
+  if ((m.I >> 5) > 512) return false;
+  if ((reinterpret_cast<uintptr_t>(m.w) & 15) != 0) return false;
+  // every chunk must start on the alignment load_chunk assumes
+  const long long cb = 4ll * m.bits;
+  if (m.row_bytes % cb != 0) return false;
+  return true;
+}
+
+hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                            int y_stride, int y_bf16, hipStream_t st) {
+  if (!gemv_bf16_supported(m) || M <= 0) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0)
+    return hipErrorInvalidValue;
+  GemvParams p;
+  p.w = m.w;
+  p.sc = m.sc;
+  p.bi = m.bi;
+  p.row_bytes = m.row_bytes;
+  p.I = m.I;
+  p.O = m.O;
+  p.ng = m.ng;
+  p.gsc = m.gs / 32;
+  p.fp16 = m.fp16;
+  p.x_stride = x_stride;
+  p.y_stride = y_stride;
+  p.y_bf16 = y_bf16;
+  // token blocks of at most 2 rows of x per launch
+  for (int m0 = 0; m0 < M; m0 += 2) {
+    const int mt = M - m0 >= 2 ? 2 : 1;
+    p.x = x + (size_t)m0 * x_stride;
+    p.M = mt;
+    p.y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
+                 : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
+    hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st) : gemv_dispatch_bits<1>(p, m.bits, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// ---------------------------------------------------------------------------
+// Generic exact-dequant GEMV (f32 activations), descriptor-batched.
+
+__device__ __forceinline__ uint32_t code_generic(const uint8_t *row, int col, int bits) {
+  const int bit = col * bits;
+  const int wi = bit >> 5, sh = bit & 31;
+  const uint32_t *wr = reinterpret_cast<const uint32_t *>(row);
+  uint64_t comb = wr[wi];
+  if (sh + bits > 32) comb |= (uint64_t)wr[wi + 1] << 32;
+  return (uint32_t)((comb >> sh) & ((1ull << bits) - 1ull));
+}
+
+__global__ __launch_bounds__(256) void gemv_generic_kernel(GenBatch b) {
+  int di = 0;
+#pragma unroll 1
+  while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
+  const GenDesc &d = b.d[di];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = (blockIdx.x - b.block_start[di]) * kGenRowsPerBlock + wave;
+  if (row >= d.O) return;
+  const uint8_t *wr = d.w + (size_t)row * d.row_bytes;
+  const int ng = d.I / d.gs;
+  for (int s = 0; s < d.S; ++s) {
+    const float *xs = d.x + (size_t)s * d.x_stride;
+    const float *us = d.xmode ? d.up + (size_t)s * d.x_stride : nullptr;
+    float acc = 0.f;
+    for (int c = lane; c < d.I; c += 64) {
+      const int g = row * ng + c / d.gs;
+      const float sc = aux_to_f32(d.sc[g], d.fp16);
+      const float bi = aux_to_f32(d.bi[g], d.fp16);
+      const float wv = fmaf((float)code_generic(wr, c, d.bits), sc, bi);
+      float xv = xs[c];
+      if (d.xmode) xv = (xv / (1.0f + expf(-xv))) * us[c];
+      acc = fmaf(wv, xv, acc);
+    }
+    acc = team_sum<64>(acc);
+    if (lane == 0) d.y[(size_t)s * d.y_stride + row] = acc;
+  }
+}
+
+hipError_t launch_gemv_generic(const GenBatch &b, hipStream_t st) {
+  if (b.n <= 0 || b.n > kMaxDescs) return hipErrorInvalidValue;
+  const int blocks = b.block_start[b.n];
+  if (blocks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gemv_generic_kernel, dim3(blocks), dim3(256), 0, st, b);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void dequant_kernel(DevMat m, int row0, int nrows, float *out) {
+  const long long n = (long long)nrows * m.I;
+  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < n; e += (long long)gridDim.x * 256) {
+    const int r = (int)(e / m.I), c = (int)(e % m.I);
+    const int row = row0 + r;
+    const int g = row * m.ng + c / m.gs;
+    const float code = (float)code_generic(m.w + (size_t)row * m.row_bytes, c, m.bits);
+    // separate multiply and add, as the reference (colisource.rs:852)
+    const float prod = __fmul_rn(code, aux_to_f32(m.sc[g], m.fp16));
+    out[e] = __fadd_rn(prod, aux_to_f32(m.bi[g], m.fp16));
+  }
+}
+
+hipError_t launch_dequant(const DevMat &m, int row0, int nrows, float *out, hipStream_t st) {
+  if (nrows <= 0) return hipSuccess;
+  const long long n = (long long)nrows * m.I;
+  long long blocks = (n + 255) / 256;
+  if (blocks > 65535) blocks = 65535;
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, m, row0, nrows, out);
+  return hipGetLastError();
+}
+
+}  // namespace lh

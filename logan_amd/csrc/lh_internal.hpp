@@ -1,0 +1,80 @@
+// Internal (C++) launch interface shared by the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace lh {
+
+// One MLX-affine matrix resident in device memory.
+struct DevMat {
+  const uint8_t *w;     // rows * row_bytes, 16-byte aligned
+  const uint16_t *sc;   // rows * ng
+  const uint16_t *bi;   // rows * ng
+  int I, O, gs, bits, fp16;
+  long long row_bytes;  // I*bits/8
+  int ng;               // I/gs
+};
+
+// ---- fast dense GEMV: bf16 activations [M, I], y [M, O] (bf16 or f32) ----
+// Returns hipSuccess, or hipErrorInvalidValue when the geometry has no fast
+// kernel (caller then uses the generic kernel).
+hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, int M,
+                            void *y, int y_stride, int y_bf16, hipStream_t st);
+bool gemv_bf16_supported(const DevMat &m);
+
+// ---- generic GEMV over up to 16 descriptors, f32 activations ----
+struct GenDesc {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  const float *x;       // [S, x_stride]; with xmode 1 this is the gate input
+  const float *up;      // xmode 1: x_eff = silu(x) * up
+  float *y;             // [S, y_stride]
+  long long row_bytes;
+  int I, O, gs, bits, fp16, S, x_stride, y_stride, xmode;
+};
+constexpr int kMaxDescs = 16;
+struct GenBatch {
+  GenDesc d[kMaxDescs];
+  int block_start[kMaxDescs + 1];
+  int n;
+};
+constexpr int kGenRowsPerBlock = 4;
+hipError_t launch_gemv_generic(const GenBatch &b, hipStream_t st);
+
+// ---- exact dequantisation of rows [row0, row0+nrows) to f32 ----
+hipError_t launch_dequant(const DevMat &m, int row0, int nrows, float *out, hipStream_t st);
+
+// ---- router: softmax top-k on logits [B, E] (bf16 or f32) ----
+hipError_t launch_route_topk(const void *logits, int logits_f32, int B, int E, int k,
+                             int32_t *idx, float *w, hipStream_t st);
+
+// ---- routed-MoE block, device-native ----
+struct DevBank {
+  DevMat m;               // one expert's geometry; w/sc/bi point at expert 0
+  long long w_stride;     // bytes between experts
+  long long p_stride;     // u16 elements between experts' params
+  int E;
+};
+struct MoeArgs {
+  DevBank gate, up, down;          // routed
+  DevBank sgate, sup, sdown;       // shared (E = 1); sgate.m.w == nullptr: none
+  const uint16_t *se_gate_vec;     // bf16 [D] or nullptr (gate = 1)
+  const uint16_t *x;               // bf16 [B, D]
+  const void *logits;              // [B, E]
+  int logits_f32;
+  int B, D, inter, sinter, E, k;
+  void *out;                       // [B, D], bf16 or f32 (out_f32)
+  int out_f32;
+  int32_t *idx_out;                // optional [B, k]
+  float *w_out;                    // optional [B, k]
+  void *ws;                        // workspace
+  size_t ws_bytes;
+};
+size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k);
+// 1 ok, 0 unsupported geometry (nothing launched), -1 launch failure
+int launch_moe_block(const MoeArgs &a, hipStream_t st);
+
+}  // namespace lh

@@ -1,0 +1,212 @@
+"""Device-native (HBM-resident) entry points with torch tensors as plumbing.
+
+torch provides device memory and streams only; every computation is a call
+into liblogan_hip.so (include/logan_hip.h layer 2). A failure of the library
+raises — nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+
+class LoganHipError(RuntimeError):
+    pass
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == 1:
+        return
+    if rc == 0:
+        raise LoganHipError(f"{what}: declined (unsupported geometry or arguments)")
+    raise LoganHipError(f"{what}: device failure ({rc})")
+
+
+def _stream(stream) -> Optional[int]:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream or None
+
+
+def _dev(t: torch.Tensor, name: str) -> int:
+    if not t.is_cuda:
+        raise LoganHipError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise LoganHipError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+@dataclass
+class AffineMatrix:
+    """One MLX-affine matrix in HBM: weights u8 [O, I*bits/8], scales/biases
+    u16 (bf16 or fp16 bits) [O, I/gs]."""
+
+    weights: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    O: int
+    I: int
+    bits: int
+    group_size: int
+    aux_fp16: bool = False
+
+    def c(self) -> L.Affine:
+        return L.Affine(_dev(self.weights, "weights"), _dev(self.scales, "scales"),
+                        _dev(self.biases, "biases"), self.O, self.I, self.bits,
+                        self.group_size, int(self.aux_fp16))
+
+
+@dataclass
+class AffineBank:
+    """E stacked experts (MLX switch_mlp): weights [E, O, I*bits/8],
+    scales/biases [E, O, I/gs]."""
+
+    weights: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    E: int
+    O: int
+    I: int
+    bits: int
+    group_size: int
+    aux_fp16: bool = False
+
+    def c(self) -> L.AffineBank:
+        return L.AffineBank(_dev(self.weights, "weights"), _dev(self.scales, "scales"),
+                            _dev(self.biases, "biases"), self.E, self.O, self.I, self.bits,
+                            self.group_size, int(self.aux_fp16))
+
+    def expert(self, e: int) -> AffineMatrix:
+        return AffineMatrix(self.weights[e], self.scales[e], self.biases[e], self.O, self.I,
+                            self.bits, self.group_size, self.aux_fp16)
+
+
+def affine_gemv(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                out_dtype: torch.dtype = torch.bfloat16, stream=None) -> torch.Tensor:
+    """y[M, O] = x[M, I] . W^T, x bf16 (logan-qwen4/src/lib.rs:3729-3764)."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    x2 = x.reshape(-1, w.I)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((M, w.O), dtype=out_dtype, device=x.device)
+    yd = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("out must be bf16 or f32")
+    a = w.c()
+    rc = L.lib().logan_hip_affine_gemv(C.byref(a), _dev(x2, "x"), M, w.I, _dev(out, "out"), w.O,
+                                       yd, _stream(stream))
+    _check(rc, "affine_gemv")
+    return out
+
+
+def affine_gemv_f32(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                    stream=None) -> torch.Tensor:
+    """f32 activations, exact per-element dequantisation, f32 output."""
+    if x.dtype != torch.float32:
+        raise LoganHipError("x must be f32")
+    x2 = x.reshape(-1, w.I)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((M, w.O), dtype=torch.float32, device=x.device)
+    a = w.c()
+    rc = L.lib().logan_hip_affine_gemv_f32(C.byref(a), _dev(x2, "x"), M, w.I, _dev(out, "out"),
+                                           w.O, _stream(stream))
+    _check(rc, "affine_gemv_f32")
+    return out
+
+
+def affine_dequant(w: AffineMatrix, row0: int = 0, nrows: Optional[int] = None,
+                   stream=None) -> torch.Tensor:
+    """code*scale+bias as f32 for rows [row0, row0+nrows)."""
+    n = w.O - row0 if nrows is None else nrows
+    out = torch.empty((n, w.I), dtype=torch.float32, device=w.weights.device)
+    a = w.c()
+    rc = L.lib().logan_hip_affine_dequant(C.byref(a), row0, n, _dev(out, "out"), _stream(stream))
+    _check(rc, "affine_dequant")
+    return out
+
+
+def route_topk(logits: torch.Tensor, k: int, stream=None):
+    """Per row: softmax top-k, lower-index ties; returns (idx int32 [B,k],
+    weights f32 [B,k])."""
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("logits must be bf16 or f32")
+    B, E = logits.shape
+    idx = torch.empty((B, k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((B, k), dtype=torch.float32, device=logits.device)
+    dt = L.LOGAN_HIP_BF16 if logits.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    rc = L.lib().logan_hip_route_topk(_dev(logits, "logits"), dt, B, E, k, _dev(idx, "idx"),
+                                      _dev(w, "w"), _stream(stream))
+    _check(rc, "route_topk")
+    return idx, w
+
+
+@dataclass
+class MoeLayer:
+    """Routed experts + optional shared expert of one MoE block."""
+
+    gate: AffineBank
+    up: AffineBank
+    down: AffineBank
+    top_k: int
+    shared_gate: Optional[AffineBank] = None
+    shared_up: Optional[AffineBank] = None
+    shared_down: Optional[AffineBank] = None
+    shared_gate_vec: Optional[torch.Tensor] = None  # bf16 [D]
+
+    def c(self) -> L.MoeBlock:
+        blk = L.MoeBlock()
+        blk.gate, blk.up, blk.down = self.gate.c(), self.up.c(), self.down.c()
+        if self.shared_gate is not None:
+            blk.shared_gate = self.shared_gate.c()
+            blk.shared_up = self.shared_up.c()
+            blk.shared_down = self.shared_down.c()
+        blk.shared_gate_vec = (_dev(self.shared_gate_vec, "shared_gate_vec")
+                               if self.shared_gate_vec is not None else None)
+        blk.top_k = self.top_k
+        return blk
+
+    def workspace_bytes(self, B: int) -> int:
+        blk = self.c()
+        return int(L.lib().logan_hip_moe_workspace_bytes(C.byref(blk), B))
+
+
+def moe_block(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
+              out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+              return_routing: bool = False, out_dtype: torch.dtype = torch.bfloat16,
+              stream=None):
+    """out[B, D] = routed MoE + shared expert (logan-qwen/src/lib.rs:535-593),
+    bf16 (RNE of the f32 result) or f32."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("logits must be bf16 or f32")
+    B, D = x.shape
+    if out is None:
+        out = torch.empty((B, D), dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("out must be bf16 or f32")
+    od = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    idx = w = None
+    if return_routing:
+        idx = torch.empty((B, layer.top_k), dtype=torch.int32, device=x.device)
+        w = torch.empty((B, layer.top_k), dtype=torch.float32, device=x.device)
+    blk = layer.c()
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = _dev(workspace, "workspace"), workspace.numel() * workspace.element_size()
+    dt = L.LOGAN_HIP_BF16 if logits.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    rc = L.lib().logan_hip_moe_block(C.byref(blk), _dev(x, "x"), _dev(logits, "logits"), dt, B,
+                                     _dev(out, "out"), od,
+                                     idx.data_ptr() if idx is not None else None,
+                                     w.data_ptr() if w is not None else None, ws_ptr, ws_bytes,
+                                     _stream(stream))
+    _check(rc, "moe_block")
+    if return_routing:
+        return out, idx, w
+    return out

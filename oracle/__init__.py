@@ -1,0 +1,185 @@
+"""CPU oracle for the logan-hip hot path — TEST INFRASTRUCTURE ONLY.
+
+ctypes wrapper over liblogan_oracle.so (oracle/oracle.c), a plain-C
+restatement of the reference's CPU arithmetic (each C function cites the
+reference file:line it follows). Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg may import this module, and only as the checker
+or the reported CPU baseline; the library (logan_amd) never uses it.
+
+Pinning (tests/test_oracle.py): every function is checked against the
+reference's own known-answer vectors (tests/golden/kat_vectors.json, taken
+from the reference tests cited there) and against independent arithmetic
+(numpy unpacking, float64 matmuls, exhaustive fp16 decoding, stable-argsort
+top-k, closed forms). No function is "parity unpinned".
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+SO = HERE / "liblogan_oracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return SO
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not SO.exists():
+            build()
+        h = C.CDLL(str(SO))
+        P, SZ, I = C.c_void_p, C.c_size_t, C.c_int
+        h.lo_f16_to_f32.restype = C.c_float
+        h.lo_f16_to_f32.argtypes = [C.c_uint16]
+        h.lo_f32_to_bf16.restype = C.c_uint16
+        h.lo_f32_to_bf16.argtypes = [C.c_float]
+        h.lo_bf16_to_f32.restype = C.c_float
+        h.lo_bf16_to_f32.argtypes = [C.c_uint16]
+        h.lo_affine_code.restype = C.c_uint32
+        h.lo_affine_code.argtypes = [P, SZ, I]
+        h.lo_affine_param.restype = C.c_float
+        h.lo_affine_param.argtypes = [P, SZ, I]
+        h.lo_affine_dequant.restype = I
+        h.lo_affine_dequant.argtypes = [P, P, P, P, SZ, SZ, I, SZ, I, SZ, SZ]
+        h.lo_affine_gemv.restype = None
+        h.lo_affine_gemv.argtypes = [P, P, P, P, P, SZ, SZ, I, SZ, I]
+        h.lo_affine_gemv_mt.restype = None
+        h.lo_affine_gemv_mt.argtypes = [P, P, P, P, P, SZ, SZ, I, SZ, I, I]
+        h.lo_spark_affine8_gemv.restype = None
+        h.lo_spark_affine8_gemv.argtypes = [P, P, P, P, SZ, SZ]
+        h.lo_silu.restype = C.c_float
+        h.lo_silu.argtypes = [C.c_float]
+        h.lo_softmax_row.restype = None
+        h.lo_softmax_row.argtypes = [P, SZ]
+        h.lo_topk.restype = C.c_float
+        h.lo_topk.argtypes = [P, SZ, SZ, P, P]
+        h.lo_moe_token.restype = None
+        h.lo_moe_token.argtypes = [P, P, P, SZ, SZ, SZ, P, P, P, P, P, P, P, P, P]
+        h.lo_moe_token_mt.restype = None
+        h.lo_moe_token_mt.argtypes = [P, P, P, SZ, SZ, SZ, P, P, P, P, P, P, P, P, P, I]
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags.c_contiguous
+    return a.ctypes.data
+
+
+def threads() -> int:
+    return int(os.environ.get("LOGAN_ORACLE_THREADS", min(8, os.cpu_count() or 1)))
+
+
+def affine_code(row: np.ndarray, column: int, bits: int) -> int:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    return int(lib().lo_affine_code(_p(row), column, bits))
+
+
+def affine_dequant(w, sc, bi, rows, cols, bits, gs, fp16=False, row0=0, nrows=None) -> np.ndarray:
+    n = rows - row0 if nrows is None else nrows
+    out = np.empty((n, cols), np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(sc).view(np.uint8)
+    bi = np.ascontiguousarray(bi).view(np.uint8)
+    rc = lib().lo_affine_dequant(_p(out), _p(w), _p(sc), _p(bi), rows, cols, bits, gs, int(fp16),
+                                 row0, n)
+    if rc != 0:
+        raise ValueError("invalid affine geometry")
+    return out
+
+
+def affine_gemv(x: np.ndarray, w, sc, bi, O, I, bits, gs, fp16=False, nthreads=None) -> np.ndarray:
+    """y = W x for one f32 activation row (logan-qwen4/src/lib.rs:3729-3764)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(O, np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(sc).view(np.uint8)
+    bi = np.ascontiguousarray(bi).view(np.uint8)
+    t = threads() if nthreads is None else nthreads
+    if t <= 1:
+        lib().lo_affine_gemv(_p(y), _p(x), _p(w), _p(sc), _p(bi), O, I, bits, gs, int(fp16))
+    else:
+        lib().lo_affine_gemv_mt(_p(y), _p(x), _p(w), _p(sc), _p(bi), O, I, bits, gs, int(fp16), t)
+    return y
+
+
+def spark_affine8_gemv(x, w, aux, O, I) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(O, np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    aux = np.ascontiguousarray(aux).view(np.uint8)
+    lib().lo_spark_affine8_gemv(_p(y), _p(x), _p(w), _p(aux), O, I)
+    return y
+
+
+def softmax_row(x: np.ndarray) -> np.ndarray:
+    y = np.array(x, np.float32, copy=True)
+    lib().lo_softmax_row(_p(y), y.size)
+    return y
+
+
+def topk(probs: np.ndarray, k: int):
+    probs = np.ascontiguousarray(probs, np.float32)
+    idx = np.empty(k, np.int32)
+    val = np.empty(k, np.float32)
+    wsum = lib().lo_topk(_p(probs), probs.size, k, _p(idx), _p(val))
+    return idx, val, float(wsum)
+
+
+class Bank(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("scales", C.c_void_p), ("biases", C.c_void_p),
+                ("o", C.c_size_t), ("i", C.c_size_t), ("bits", C.c_int),
+                ("group_size", C.c_size_t), ("fp16", C.c_int)]
+
+
+def _bank(w, sc, bi, O, I, bits, gs, fp16, keep):
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(sc).view(np.uint8)
+    bi = np.ascontiguousarray(bi).view(np.uint8)
+    b = Bank(_p(w), _p(sc), _p(bi), O, I, bits, gs, int(fp16))
+    keep += [w, sc, bi, b]
+    return C.addressof(b)
+
+
+def moe_token(x, logits, k, D, inter, bits, gs, gate, up, down, shared=None, se_g=None,
+              sinter=None, fp16=False, nthreads=None):
+    """One token of the routed-MoE block. gate/up/down are (w, sc, bi) of
+    stacked banks; shared is (gate, up, down) of single experts (or None).
+    Returns (out[D], idx[k], w[k])."""
+    keep = []
+    x = np.ascontiguousarray(x, np.float32)
+    logits = np.ascontiguousarray(logits, np.float32)
+    E = logits.size
+    g = _bank(*gate, inter, D, bits, gs, fp16, keep)
+    u = _bank(*up, inter, D, bits, gs, fp16, keep)
+    dn = _bank(*down, D, inter, bits, gs, fp16, keep)
+    out = np.empty(D, np.float32)
+    idx = np.empty(k, np.int32)
+    wt = np.empty(k, np.float32)
+    sp = [None, None, None]
+    seg = None
+    if shared is not None:
+        si = inter if sinter is None else sinter
+        sp = [_bank(*shared[0], si, D, bits, gs, fp16, keep),
+              _bank(*shared[1], si, D, bits, gs, fp16, keep),
+              _bank(*shared[2], D, si, bits, gs, fp16, keep)]
+        seg = np.ascontiguousarray(se_g, np.float32)
+        keep.append(seg)
+    t = threads() if nthreads is None else nthreads
+    args = [_p(out), _p(x), _p(logits), E, k, D, g, u, dn,
+            sp[0], sp[1], sp[2], _p(seg) if seg is not None else None, _p(idx), _p(wt)]
+    if t <= 1:
+        lib().lo_moe_token(*args)
+    else:
+        lib().lo_moe_token_mt(*args, t)
+    return out, idx, wt

@@ -1,0 +1,214 @@
+"""GPU parity of the router top-k and the routed-MoE block against the oracle.
+
+Bars: routing indices bit-exact (same experts, same rank order, ties to the
+lower index); routing weights within 1e-5 relative; MoE f32 output within
+max|y-ŷ|/max|ŷ| <= 2e-3 of the oracle (observed ~1e-6); bf16 output ==
+RNE(f32 output) bit for bit; B>1 rows identical to B=1 runs of the same
+token (grouping does not change any token's arithmetic).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from logan_amd.synth import bf16_bits, bf16_to_f32, make_affine, make_logits, make_x
+
+from _util import normwise_rel
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def to_dev(a, torch, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.cuda()
+
+
+def oracle_route(logits_f32, k):
+    probs = oracle.softmax_row(logits_f32)
+    idx, val, wsum = oracle.topk(probs, k)
+    return idx, (val / np.float32(wsum)).astype(np.float32)
+
+
+@pytest.mark.parametrize("E,k,B,kind", [(512, 10, 64, "normal"), (512, 10, 32, "zipf"),
+                                        (512, 10, 16, "ties"), (100, 7, 5, "normal"),
+                                        (64, 64, 3, "normal"), (1024, 32, 4, "normal"),
+                                        (512, 1, 8, "ties"), (8, 2, 9, "ties")])
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_route_topk_bit_exact(gpu, E, k, B, kind, dtype):
+    import torch
+    from logan_amd.device import route_topk
+
+    rng = np.random.default_rng(E + k + B)
+    lb = make_logits(rng, B, E, zipf_s=1.1 if kind == "zipf" else None)
+    lf = bf16_to_f32(lb)
+    if kind == "ties":
+        for b in range(B):
+            order = np.argsort(-lf[b], kind="stable")
+            lo, hi = max(0, k - 3), min(E, k + 3)
+            lf[b, order[lo:hi]] = lf[b, order[lo]]
+            lf[b, order[hi:hi + 4]] = lf[b, order[-1]]
+        lb = bf16_bits(lf)
+    if dtype == "bf16":
+        ld = to_dev(lb.view(np.int16), torch).view(torch.bfloat16)
+    else:
+        ld = to_dev(lf, torch)
+    idx, w = route_topk(ld, k)
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    for b in range(B):
+        ri, rw = oracle_route(lf[b], k)
+        np.testing.assert_array_equal(idx[b], ri)
+        np.testing.assert_allclose(w[b], rw, rtol=1e-5, atol=1e-7)
+
+
+def test_route_negative_zero_and_equal_logits(gpu):
+    import torch
+    from logan_amd.device import route_topk
+
+    lf = np.zeros((2, 16), np.float32)
+    lf[0, ::2] = -0.0
+    lf[1] = 1.0
+    idx, w = route_topk(to_dev(lf, torch), 4)
+    for b in range(2):
+        ri, rw = oracle_route(lf[b], 4)
+        np.testing.assert_array_equal(idx.cpu().numpy()[b], ri)
+        np.testing.assert_allclose(w.cpu().numpy()[b], rw, rtol=1e-6)
+
+
+class Layer:
+    """Seeded MoE layer in the benchmark scheme, host copies + device banks."""
+
+    def __init__(self, torch, E, k, D, inter, bits, gs, shared=True, seed=0, sinter=None):
+        from logan_amd.device import AffineBank, MoeLayer
+
+        rng = np.random.default_rng(seed)
+        self.E, self.k, self.D, self.inter, self.bits, self.gs = E, k, D, inter, bits, gs
+        self.sinter = inter if sinter is None else sinter
+        self.gate = make_affine(rng, inter, D, bits, gs, E=E)
+        self.up = make_affine(rng, inter, D, bits, gs, E=E)
+        self.down = make_affine(rng, D, inter, bits, gs, E=E)
+
+        def bank(t, O, I, n):
+            w, sc, bi = t
+            return AffineBank(to_dev(w, torch), to_dev(sc.view(np.int16), torch),
+                              to_dev(bi.view(np.int16), torch), n, O, I, bits, gs)
+
+        kw = {}
+        self.shared = None
+        self.se_g = None
+        if shared:
+            si = self.sinter
+            sg = make_affine(rng, si, D, bits, gs, E=1)
+            su = make_affine(rng, si, D, bits, gs, E=1)
+            sd = make_affine(rng, D, si, bits, gs, E=1)
+            self.shared = tuple(tuple(a[0] for a in t) for t in (sg, su, sd))
+            self.se_g_bits = bf16_bits(rng.standard_normal(D).astype(np.float32) * np.float32(0.05))
+            self.se_g = bf16_to_f32(self.se_g_bits)
+            kw = dict(shared_gate=bank(sg, si, D, 1), shared_up=bank(su, si, D, 1),
+                      shared_down=bank(sd, D, si, 1),
+                      shared_gate_vec=to_dev(self.se_g_bits.view(np.int16), torch).view(torch.bfloat16))
+        self.dev = MoeLayer(bank(self.gate, inter, D, E), bank(self.up, inter, D, E),
+                            bank(self.down, D, inter, E), k, **kw)
+
+    def ref(self, xf, lf):
+        return oracle.moe_token(xf, lf, self.k, self.D, self.inter, self.bits, self.gs, self.gate,
+                                self.up, self.down, self.shared, self.se_g, sinter=self.sinter)
+
+
+def run_layer(torch, layer, xb, lb, out_dtype):
+    from logan_amd.device import moe_block
+
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    lg = to_dev(lb.view(np.int16), torch).view(torch.bfloat16)
+    out, idx, w = moe_block(layer.dev, x, lg, return_routing=True, out_dtype=out_dtype)
+    return out, idx.cpu().numpy(), w.cpu().numpy()
+
+
+@pytest.mark.parametrize("bits,B,zipf", [(4, 1, False), (4, 16, False), (5, 1, True),
+                                         (6, 1, True), (5, 32, True), (6, 32, True),
+                                         (8, 4, False)])
+def test_moe_block_matches_oracle(gpu, bits, B, zipf):
+    """Configs 3 and 4: E=512, top-10, D=2048, inter=512, g64, shared expert."""
+    import torch
+
+    print(f"moe bits={bits} B={B} zipf={zipf}", flush=True)
+    layer = Layer(torch, 512, 10, 2048, 512, bits, 64, seed=bits * 10 + B)
+    rng = np.random.default_rng(1000 + B)
+    xb = make_x(rng, B, 2048)
+    lb = make_logits(rng, B, 512, zipf_s=1.1 if zipf else None)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    out16, idx2, _ = run_layer(torch, layer, xb, lb, torch.bfloat16)
+    out32 = out32.cpu().numpy()
+    out16 = out16.view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(idx, idx2)
+    np.testing.assert_array_equal(out16, bf16_bits(out32))
+    xf, lf = bf16_to_f32(xb), bf16_to_f32(lb)
+    for t in range(B):
+        ref, ridx, rw = layer.ref(xf[t], lf[t])
+        np.testing.assert_array_equal(idx[t], ridx)
+        np.testing.assert_allclose(w[t], rw, rtol=1e-5)
+        err = normwise_rel(out32[t], ref)
+        assert err <= TOL, f"token {t}: {err:.3e}"
+        assert err <= 1e-4, f"token {t}: {err:.3e}"
+
+
+def test_moe_batch_rows_equal_single_token_runs(gpu):
+    import torch
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=3)
+    rng = np.random.default_rng(4)
+    B = 12
+    xb = make_x(rng, B, 2048)
+    lb = make_logits(rng, B, 512, zipf_s=1.1)
+    full, _, _ = run_layer(torch, layer, xb, lb, torch.float32)
+    for t in range(B):
+        one, _, _ = run_layer(torch, layer, xb[t:t + 1], lb[t:t + 1], torch.float32)
+        assert torch.equal(full[t:t + 1], one)
+
+
+def test_moe_without_shared_expert_and_small_shapes(gpu):
+    import torch
+
+    layer = Layer(torch, 16, 4, 256, 128, 4, 32, shared=False, seed=9)
+    rng = np.random.default_rng(10)
+    B = 5
+    xb = make_x(rng, B, 256)
+    lb = make_logits(rng, B, 16)
+    out, idx, _ = run_layer(torch, layer, xb, lb, torch.float32)
+    out = out.cpu().numpy()
+    xf, lf = bf16_to_f32(xb), bf16_to_f32(lb)
+    for t in range(B):
+        ref, ridx, _ = layer.ref(xf[t], lf[t])
+        np.testing.assert_array_equal(idx[t], ridx)
+        assert normwise_rel(out[t], ref) <= 1e-4
+
+
+def test_moe_shared_inter_differs(gpu):
+    import torch
+
+    layer = Layer(torch, 32, 4, 512, 256, 4, 64, seed=11, sinter=384)
+    rng = np.random.default_rng(12)
+    xb = make_x(rng, 3, 512)
+    lb = make_logits(rng, 3, 32)
+    out, idx, _ = run_layer(torch, layer, xb, lb, torch.float32)
+    out = out.cpu().numpy()
+    for t in range(3):
+        ref, ridx, _ = layer.ref(bf16_to_f32(xb[t]), bf16_to_f32(lb[t]))
+        np.testing.assert_array_equal(idx[t], ridx)
+        assert normwise_rel(out[t], ref) <= 1e-4
+
+
+def test_moe_deterministic_and_workspace(gpu):
+    import torch
+    from logan_amd.device import moe_block
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=21)
+    rng = np.random.default_rng(22)
+    x = to_dev(make_x(rng, 2, 2048).view(np.int16), torch).view(torch.bfloat16)
+    lg = to_dev(make_logits(rng, 2, 512).view(np.int16), torch).view(torch.bfloat16)
+    ws = torch.empty(layer.dev.workspace_bytes(2), dtype=torch.uint8, device="cuda")
+    a = moe_block(layer.dev, x, lg, workspace=ws, out_dtype=torch.float32)
+    b = moe_block(layer.dev, x, lg, out_dtype=torch.float32)
+    c = moe_block(layer.dev, x, lg, workspace=ws, out_dtype=torch.float32)
+    assert torch.equal(a, b) and torch.equal(a, c)

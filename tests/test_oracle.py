@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against the reference's own known-answer
+vectors (tests/golden/kat_vectors.json) and against arithmetic that shares
+nothing with the oracle's code path: numpy bit unpacking, float64 matmuls of
+the dequantised matrix, exhaustive fp16 decoding, torch's bf16 rounding,
+numpy's stable argsort, closed forms. A planted mistake (wrong shift, dropped
+bias, transposed index, reversed tie rule) fails at least one of them.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from logan_amd.synth import bf16_bits, bf16_to_f32, make_affine, make_logits, make_x
+
+from _util import dequant_f64, pack_codes, unpack_codes
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "kat_vectors.json").read_text())
+
+
+@pytest.mark.parametrize("case", GOLDEN["decode"], ids=lambda c: f"{c['source'].split(':')[-1]}-b{c['bits']}")
+def test_dequant_matches_reference_kat(case):
+    words = np.array(case["words"], dtype=np.uint32)
+    sc = bf16_bits(np.array(case["scales"], np.float32))
+    bi = bf16_bits(np.array(case["biases"], np.float32))
+    got = oracle.affine_dequant(words.view(np.uint8), sc, bi, case["rows"], case["cols"],
+                                case["bits"], case["group_size"])
+    np.testing.assert_array_equal(got.reshape(-1), np.array(case["expected"], np.float32))
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6, 8])
+def test_code_extraction_bruteforce(bits):
+    """Every column of random rows, including every straddling position."""
+    rng = np.random.default_rng(bits)
+    I = 256
+    codes = rng.integers(0, 1 << bits, size=(3, I))
+    packed = pack_codes(codes, bits)
+    np.testing.assert_array_equal(unpack_codes(packed, I, bits), codes)
+    for r in range(3):
+        got = [oracle.affine_code(packed[r], c, bits) for c in range(I)]
+        np.testing.assert_array_equal(got, codes[r])
+
+
+def test_f16_decode_exhaustive():
+    lib = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.lo_f16_to_f32(int(b)) for b in bits], np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+    assert np.array_equal(got[np.isinf(want)], want[np.isinf(want)])
+
+
+def test_bf16_rne_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0,
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 65504.0, 3.0e38, -3.0e38, 1e-40],
+                 np.float32),
+        # exact ties: low 16 bits == 0x8000 with even and odd kept LSB
+        (np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000], np.uint32)).view(np.float32),
+    ])
+    lib = oracle.lib()
+    got = np.array([lib.lo_f32_to_bf16(float(v)) for v in vals], np.uint16)
+    want = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(bf16_bits(vals), want)
+
+
+@pytest.mark.parametrize("bits,gs,fp16", [(4, 64, False), (5, 128, False), (6, 64, False),
+                                          (8, 128, False), (4, 32, True), (8, 64, True)])
+def test_dequant_matches_independent_decode(bits, gs, fp16):
+    rng = np.random.default_rng(10 + bits)
+    O, I = 5, 256
+    w, sc, bi = make_affine(rng, O, I, bits, gs, fp16=fp16)
+    got = oracle.affine_dequant(w, sc, bi, O, I, bits, gs, fp16=fp16)
+    want = dequant_f64(w, sc, bi, O, I, bits, gs, fp16)
+    # code*scale is exact in f32 and adding the bias rounds once
+    np.testing.assert_array_equal(got, want.astype(np.float32))
+
+
+def test_dequant_rejects_bad_geometry():
+    w = np.zeros(64, np.uint8)
+    sc = np.zeros(4, np.uint16)
+    with pytest.raises(ValueError):
+        oracle.affine_dequant(w, sc, sc, 1, 60, 4, 32)  # 60 % 32 != 0
+    with pytest.raises(ValueError):
+        oracle.affine_dequant(w, sc, sc, 1, 64, 7, 32)  # unsupported width
+
+
+@pytest.mark.parametrize("case", GOLDEN["gemv"], ids=lambda c: f"b{c['bits']}")
+def test_gemv_reference_closed_forms(case):
+    O, I, bits, gs = case["O"], case["I"], case["bits"], case["group_size"]
+    w = np.full((O, I * bits // 8), case["byte"], np.uint8)
+    sc = bf16_bits(np.full(O * (I // gs), case["scale"], np.float32))
+    bi = bf16_bits(np.full(O * (I // gs), case["bias"], np.float32))
+    x = np.full(I, case["x"], np.float32)
+    y = oracle.affine_gemv(x, w, sc, bi, O, I, bits, gs, nthreads=1)
+    np.testing.assert_array_equal(y, np.full(O, case["expected"], np.float32))
+
+
+def test_spark_affine8_reference_closed_form():
+    c = GOLDEN["spark_affine8"]
+    O, I = c["O"], c["I"]
+    aux = np.concatenate([bf16_bits(np.full(O, c["scale"], np.float32)),
+                          bf16_bits(np.full(O, c["bias"], np.float32))])
+    y = oracle.spark_affine8_gemv(np.full(I, c["x"], np.float32), np.full(O * I, c["byte"], np.uint8),
+                                  aux, O, I)
+    np.testing.assert_array_equal(y, np.full(O, c["expected"], np.float32))
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (5, 128), (6, 64), (8, 128)])
+def test_gemv_reference_generator_against_float64(bits, gs):
+    """The generator of logan-metal/src/lib.rs:1310-1378 (codes
+    (17r+7c+3)&mask, scale 0.125(r+g+1), bias -0.25+0.0625(r+g),
+    x ((i%11)-5)*0.125), checked with that test's own tolerance
+    max(2e-3, 2e-4|ref|) against a float64 matmul of the decoded matrix."""
+    O, I = 3, 128
+    mask = (1 << bits) - 1
+    codes = np.array([[(r * 17 + c * 7 + 3) & mask for c in range(I)] for r in range(O)])
+    w = pack_codes(codes, bits)
+    g = I // gs
+    sc = bf16_bits(np.array([[0.125 * (r + q + 1) for q in range(g)] for r in range(O)], np.float32))
+    bi = bf16_bits(np.array([[-0.25 + 0.0625 * (r + q) for q in range(g)] for r in range(O)], np.float32))
+    x = np.array([((i % 11) - 5) * 0.125 for i in range(I)], np.float32)
+    y = oracle.affine_gemv(x, w, sc, bi, O, I, bits, gs, nthreads=1)
+    ref = dequant_f64(w, sc, bi, O, I, bits, gs) @ x.astype(np.float64)
+    tol = np.maximum(2e-3, 2e-4 * np.abs(ref))
+    assert np.all(np.abs(y - ref) <= tol)
+
+
+@pytest.mark.parametrize("bits,gs,fp16", [(4, 64, False), (5, 64, False), (6, 64, False),
+                                          (8, 64, False), (4, 128, True)])
+def test_gemv_random_against_float64(bits, gs, fp16):
+    rng = np.random.default_rng(bits * 7)
+    O, I = 64, 1024
+    w, sc, bi = make_affine(rng, O, I, bits, gs, fp16=fp16)
+    x = bf16_to_f32(make_x(rng, I))
+    y1 = oracle.affine_gemv(x, w, sc, bi, O, I, bits, gs, fp16, nthreads=1)
+    y8 = oracle.affine_gemv(x, w, sc, bi, O, I, bits, gs, fp16, nthreads=8)
+    np.testing.assert_array_equal(y1, y8)  # row split leaves each row's order intact
+    ref = dequant_f64(w, sc, bi, O, I, bits, gs, fp16) @ x.astype(np.float64)
+    assert np.abs(y1 - ref).max() / np.abs(ref).max() < 1e-5
+
+
+def test_softmax_matches_float64():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(512).astype(np.float32) * 3
+    p = oracle.softmax_row(x)
+    e = np.exp(x.astype(np.float64) - x.max())
+    np.testing.assert_allclose(p, e / e.sum(), rtol=1e-5, atol=1e-9)
+    assert abs(float(p.astype(np.float64).sum()) - 1.0) < 1e-5
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_matches_stable_argsort(seed):
+    rng = np.random.default_rng(seed)
+    E, k = 512, 10
+    logits = bf16_to_f32(make_logits(rng, 1, E, zipf_s=1.1 if seed % 2 else None)[0])
+    if seed >= 4:
+        # force ties straddling the k-th place
+        order = np.argsort(-logits, kind="stable")
+        logits[order[7:14]] = logits[order[8]]
+    probs = oracle.softmax_row(logits)
+    idx, val, wsum = oracle.topk(probs, k)
+    want = np.argsort(-probs, kind="stable")[:k]  # descending prob, lower index first
+    np.testing.assert_array_equal(idx, want)
+    np.testing.assert_array_equal(val, probs[want])
+    assert wsum == pytest.approx(float(probs[want].astype(np.float64).sum()), rel=1e-6)
+
+
+def test_topk_tie_rule_prefers_lower_index():
+    probs = np.array([0.1, 0.3, 0.3, 0.05, 0.3, 0.25], np.float32)
+    idx, _, _ = oracle.topk(probs, 4)
+    np.testing.assert_array_equal(idx, [1, 2, 4, 5])
+
+
+def _moe_f64(x, logits, k, D, inter, bits, gs, gate, up, down, shared, se_g):
+    """Float64 statement of the MoE block for the oracle check."""
+    x64 = x.astype(np.float64)
+    p = np.exp(logits.astype(np.float64) - logits.max())
+    p /= p.sum()
+    idx = np.argsort(-p, kind="stable")[:k]
+    w = p[idx] / p[idx].sum()
+    out = np.zeros(D)
+
+    def mlp(g_, u_, d_, e, hi):
+        G = dequant_f64(g_[0][e], g_[1][e], g_[2][e], hi, D, bits, gs)
+        U = dequant_f64(u_[0][e], u_[1][e], u_[2][e], hi, D, bits, gs)
+        Dn = dequant_f64(d_[0][e], d_[1][e], d_[2][e], D, hi, bits, gs)
+        gv, uv = G @ x64, U @ x64
+        h = gv / (1 + np.exp(-gv)) * uv
+        return Dn @ h
+
+    for r in range(k):
+        out += w[r] * mlp(gate, up, down, idx[r], inter)
+    if shared is not None:
+        gsig = 1 / (1 + np.exp(-(se_g.astype(np.float64) @ x64)))
+        sg, su, sd = shared
+        out += gsig * mlp((sg[0][None], sg[1][None], sg[2][None]),
+                          (su[0][None], su[1][None], su[2][None]),
+                          (sd[0][None], sd[1][None], sd[2][None]), 0, inter)
+    return out, idx, w
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_moe_token_against_float64(bits):
+    rng = np.random.default_rng(100 + bits)
+    E, k, D, inter, gs = 16, 4, 128, 64, 64
+    gate = make_affine(rng, inter, D, bits, gs, E=E)
+    up = make_affine(rng, inter, D, bits, gs, E=E)
+    down = make_affine(rng, D, inter, bits, gs, E=E)
+    shared = (make_affine(rng, inter, D, bits, gs), make_affine(rng, inter, D, bits, gs),
+              make_affine(rng, D, inter, bits, gs))
+    se_g = bf16_to_f32(make_x(rng, D)) * np.float32(0.05)
+    x = bf16_to_f32(make_x(rng, D))
+    logits = bf16_to_f32(make_logits(rng, 1, E)[0])
+    out, idx, w = oracle.moe_token(x, logits, k, D, inter, bits, gs, gate, up, down, shared, se_g)
+    ref, ridx, rw = _moe_f64(x, logits, k, D, inter, bits, gs, gate, up, down, shared, se_g)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=1e-5)
+    assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def test_moe_expert_source_closed_form():
+    """logan-qwen4/src/lib.rs:17277-17348: expert 0 (zero codes) gives 0,
+    expert 1 (code 1, scale 1, bias 0, x = 1, D = M = 64) gives
+    64 * silu(64) * 64 per element."""
+    c = GOLDEN["expert"]
+    D = M = c["D"]
+    words = D * 4 // 32
+    def bank(rows):
+        w = np.empty((2, rows, words), np.uint32)
+        w[0] = c["expert0_word"]
+        w[1] = c["expert1_word"]
+        sc = bf16_bits(np.full((2, rows, 1), c["scale"], np.float32))
+        bi = bf16_bits(np.full((2, rows, 1), c["bias"], np.float32))
+        return w.view(np.uint8).reshape(2, rows, -1), sc, bi
+    gate, up, down = bank(M), bank(M), bank(D)
+    x = np.full(D, c["x"], np.float32)
+    for expert, want in ((0, c["expected_expert0"]), (1, c["expected_expert1"])):
+        logits = np.array([0.0, 0.0], np.float32)
+        logits[expert] = 10.0
+        out, idx, w = oracle.moe_token(x, logits, 1, D, M, 4, 64, gate, up, down)
+        assert idx[0] == expert and w[0] == 1.0
+        if want == 0.0:
+            assert np.all(out == 0.0)
+        else:
+            assert np.all(np.abs(out - want) <= abs(want) * c["rel_tol"])
