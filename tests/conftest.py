@@ -4,6 +4,11 @@ from pathlib import Path
 
 import pytest
 
+try:  # first import on a fresh box is slow: keep it out of per-test timeouts
+    import torch  # noqa: F401
+except Exception:  # pragma: no cover
+    torch = None
+
 ROOT = Path(__file__).resolve().parent.parent
 sys.path.insert(0, str(ROOT))
 
