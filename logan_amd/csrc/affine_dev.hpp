@@ -10,14 +10,17 @@
 // The chunk dot product is evaluated in the factored form
 //     sum_k w_k x_k = scale * sum_k code_k x_k + bias * sum_k x_k
 // with the code*x products done by v_dot2c_f32_bf16 on bf16 pairs:
-//   * 4/5/6-bit: each half of a pair is the bf16 bit pattern 0x43nn, i.e.
-//     128 + (code << a) exactly (a <= 2 keeps it inside the 7 mantissa bits);
-//     the x operand carries x * 2^-a (exact), so
-//     sum (128 + code 2^a)(x 2^-a) = 128 * xs' + sum code x,
-//     where xs' = sum x * 2^-a is precomputed once per x.
+//   * 4/5/6-bit: each half of a pair is the bf16 pattern 0x3F80 | code << s,
+//     i.e. exactly 1 + code * 2^(s-7) (code << s stays inside the 7 mantissa
+//     bits: s = 3 for 4-bit, 2/1 for 5-bit, 1 for 6-bit). The x operand of
+//     that half carries x' = x * 2^(7-s) (exact), so
+//         sum (1 + code 2^(s-7)) x' = sum x' + sum code x,
+//     and the chunk sum xsp = sum x' (of the values the products actually
+//     used) is subtracted once per chunk. Placing the code high in the
+//     mantissa keeps that offset small (16x for 4-bit) relative to code*x.
 //   * 8-bit: v_cvt_f32_ubyteN gives code exactly in f32; its top 16 bits are
-//     the exact bf16 of the code (<= 8 significant bits).
-// All products code*x are exact in f32; sums are f32.
+//     the exact bf16 of the code (<= 8 significant bits); no offset.
+// All products are exact in f32; sums are f32.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -58,55 +61,56 @@ __device__ __forceinline__ uint32_t f32_hi16(float f) {
 }
 
 // Which two codes of a 32-code chunk form bf16 pair p (0..15), and the
-// power-of-two exponent each code is shifted by inside its pair half.
+// mantissa bit s at which each code sits inside its pair half.
 template <int BITS>
 struct PairMap;
 
 template <>
 struct PairMap<4> {
-  // word t = p/4 holds codes 8t..8t+7; pair (t,j) = nibbles j and j+4.
+  // word t = p/4 holds codes 8t..8t+7; pair (t,j) = nibbles j and j+4,
+  // both placed at mantissa bits 3..6.
   static __device__ __forceinline__ int lo(int p) { return 8 * (p >> 2) + (p & 3); }
   static __device__ __forceinline__ int hi(int p) { return lo(p) + 4; }
-  static __device__ __forceinline__ int alo(int) { return 0; }
-  static __device__ __forceinline__ int ahi(int) { return 0; }
+  static __device__ __forceinline__ int slo(int) { return 3; }
+  static __device__ __forceinline__ int shi(int) { return 3; }
 };
 
 template <>
 struct PairMap<5> {
-  // groups q of 6 codes (30 bits); pair (q,i) = codes 6q+i and 6q+i+3, the
-  // low one shifted left by 1 inside its half; pair 15 = codes 30, 31.
+  // groups q of 6 codes (30 bits); pair (q,i) = codes 6q+i (mantissa bits
+  // 2..6) and 6q+i+3 (bits 1..5, 15 bits later in the stream); pair 15 =
+  // codes 30, 31, both at bits 2..6.
   static __device__ __forceinline__ int lo(int p) {
     return p == 15 ? 30 : 6 * (p / 3) + (p % 3);
   }
   static __device__ __forceinline__ int hi(int p) { return p == 15 ? 31 : lo(p) + 3; }
-  static __device__ __forceinline__ int alo(int p) { return p == 15 ? 0 : 1; }
-  static __device__ __forceinline__ int ahi(int) { return 0; }
+  static __device__ __forceinline__ int slo(int) { return 2; }
+  static __device__ __forceinline__ int shi(int p) { return p == 15 ? 2 : 1; }
 };
 
 template <>
 struct PairMap<6> {
   static __device__ __forceinline__ int lo(int p) { return 2 * p; }
   static __device__ __forceinline__ int hi(int p) { return 2 * p + 1; }
-  static __device__ __forceinline__ int alo(int) { return 0; }
-  static __device__ __forceinline__ int ahi(int) { return 0; }
+  static __device__ __forceinline__ int slo(int) { return 1; }
+  static __device__ __forceinline__ int shi(int) { return 1; }
 };
 
 template <>
 struct PairMap<8> {
+  // exact codes, no offset: x' = x
   static __device__ __forceinline__ int lo(int p) { return 2 * p; }
   static __device__ __forceinline__ int hi(int p) { return 2 * p + 1; }
-  static __device__ __forceinline__ int alo(int) { return 0; }
-  static __device__ __forceinline__ int ahi(int) { return 0; }
+  static __device__ __forceinline__ int slo(int) { return 7; }
+  static __device__ __forceinline__ int shi(int) { return 7; }
 };
 
-// 128.0 offset applies to every width except 8-bit.
-template <int BITS>
-struct Magic {
-  static constexpr float offset = BITS == 8 ? 0.0f : 128.0f;
-};
+// x' = x * 2^(7-s): the x-operand scale that pairs with a code at mantissa
+// bit s.
+__device__ __forceinline__ float xscale(int s) { return (float)(1 << (7 - s)); }
 
 // x operand of one chunk for one activation row: 16 bf16 pairs plus the two
-// chunk sums (xs = sum x, xsp = sum x*2^-a) used by the scale/bias fold.
+// chunk sums (xs = sum x, xsp = sum x') used by the scale/bias fold.
 struct XChunk {
   uint32_t p[16];
   float xs;
@@ -120,18 +124,21 @@ __device__ __forceinline__ void make_xchunk_bf16(XChunk &xc, const uint32_t (&xb
 #pragma unroll
   for (int p = 0; p < 16; ++p) {
     const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
-    const float xl = bf16_to_f32(xb[kl]) * (PairMap<BITS>::alo(p) ? 0.5f : 1.0f);
-    const float xh = bf16_to_f32(xb[kh]) * (PairMap<BITS>::ahi(p) ? 0.5f : 1.0f);
+    const float vl = bf16_to_f32(xb[kl]), vh = bf16_to_f32(xb[kh]);
+    const float xl = vl * xscale(PairMap<BITS>::slo(p));
+    const float xh = vh * xscale(PairMap<BITS>::shi(p));
     xc.p[p] = f32_hi16(xl) | (f32_hi16(xh) << 16);
-    s += bf16_to_f32(xb[kl]) + bf16_to_f32(xb[kh]);
+    s += vl + vh;
     sp += xl + xh;
   }
   xc.xs = s;
   xc.xsp = sp;
 }
 
-// f32 activations: split x = hi + lo (both bf16, RNE) so the pair dot keeps
-// ~16 significant bits of x; hi and lo chunks share xs/xsp of the full x.
+// f32 activations: x' = hi + lo (both bf16, RNE) so the pair dot keeps ~16
+// significant bits of x. xs is the sum of the true x (bias term); xsp is the
+// sum of hi + lo, i.e. of exactly what the products saw, so the offset
+// cancels without amplifying the split residual.
 template <int BITS>
 __device__ __forceinline__ void make_xchunk_f32(XChunk &hi, XChunk &lo,
                                                 const float (&xf)[32]) {
@@ -139,16 +146,15 @@ __device__ __forceinline__ void make_xchunk_f32(XChunk &hi, XChunk &lo,
 #pragma unroll
   for (int p = 0; p < 16; ++p) {
     const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
-    const float sl = PairMap<BITS>::alo(p) ? 0.5f : 1.0f;
-    const float sh = PairMap<BITS>::ahi(p) ? 0.5f : 1.0f;
-    const float xl = xf[kl] * sl, xh = xf[kh] * sh;
+    const float xl = xf[kl] * xscale(PairMap<BITS>::slo(p));
+    const float xh = xf[kh] * xscale(PairMap<BITS>::shi(p));
     const uint32_t hl = f32_to_bf16_rne(xl), hh = f32_to_bf16_rne(xh);
     const uint32_t ll = f32_to_bf16_rne(xl - bf16_to_f32(hl));
     const uint32_t lh = f32_to_bf16_rne(xh - bf16_to_f32(hh));
     hi.p[p] = hl | (hh << 16);
     lo.p[p] = ll | (lh << 16);
     s += xf[kl] + xf[kh];
-    sp += xl + xh;
+    sp += (bf16_to_f32(hl) + bf16_to_f32(ll)) + (bf16_to_f32(hh) + bf16_to_f32(lh));
   }
   hi.xs = lo.xs = s;
   hi.xsp = lo.xsp = sp;
@@ -157,13 +163,13 @@ __device__ __forceinline__ void make_xchunk_f32(XChunk &hi, XChunk &lo,
 // Constants kept in registers so the unpack uses v_and_or_b32 (VOP3 on gfx9
 // takes no literal operands).
 struct UnpackConsts {
-  uint32_t m4;     // 0x000F000F (SGPR)
-  uint32_t m5;     // 0x001F003E (SGPR)
-  uint32_t magic;  // 0x43004300 (VGPR)
+  uint32_t m4;     // 0x00780078: nibble at mantissa bits 3..6 of both halves (SGPR)
+  uint32_t m5;     // 0x003E007C: 5-bit code at bits 2..6 (lo) and 1..5 (hi) (SGPR)
+  uint32_t magic;  // 0x3F803F80: 1.0 in both halves (VGPR)
   __device__ __forceinline__ void init() {
-    m4 = 0x000F000Fu;
-    m5 = 0x001F003Eu;
-    magic = 0x43004300u;
+    m4 = 0x00780078u;
+    m5 = 0x003E007Cu;
+    magic = 0x3F803F80u;
     asm volatile("" : "+s"(m4));
     asm volatile("" : "+s"(m5));
     asm volatile("" : "+v"(magic));
@@ -180,32 +186,32 @@ __device__ __forceinline__ void unpack_chunk<4>(uint32_t (&q)[16], const uint32_
                                                 const UnpackConsts &k) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    q[4 * t + 0] = (w[t] & k.m4) | k.magic;
-    q[4 * t + 1] = ((w[t] >> 4) & k.m4) | k.magic;
-    q[4 * t + 2] = ((w[t] >> 8) & k.m4) | k.magic;
-    q[4 * t + 3] = ((w[t] >> 12) & k.m4) | k.magic;
+    q[4 * t + 0] = ((w[t] << 3) & k.m4) | k.magic;
+    q[4 * t + 1] = ((w[t] >> 1) & k.m4) | k.magic;
+    q[4 * t + 2] = ((w[t] >> 5) & k.m4) | k.magic;
+    q[4 * t + 3] = ((w[t] >> 9) & k.m4) | k.magic;
   }
 }
 
 template <>
 __device__ __forceinline__ void unpack_chunk<5>(uint32_t (&q)[16], const uint32_t (&w)[5],
                                                 const UnpackConsts &k) {
-  // window q holds stream bits [30q-1, 30q+31): code 6q+i at bit 1+5i.
+  // window q holds stream bits [30q-2, 30q+30): code 6q+i at bit 2+5i, and
+  // code 6q+i+3 15 bits later at 17+5i (bit 1+5i of the high half).
   uint32_t win[5];
-  win[0] = w[0] << 1;
-  win[1] = __builtin_amdgcn_alignbit(w[1], w[0], 29);
-  win[2] = __builtin_amdgcn_alignbit(w[2], w[1], 27);
-  win[3] = __builtin_amdgcn_alignbit(w[3], w[2], 25);
-  win[4] = __builtin_amdgcn_alignbit(w[4], w[3], 23);
+  win[0] = w[0] << 2;
+  win[1] = __builtin_amdgcn_alignbit(w[1], w[0], 28);
+  win[2] = __builtin_amdgcn_alignbit(w[2], w[1], 26);
+  win[3] = __builtin_amdgcn_alignbit(w[3], w[2], 24);
+  win[4] = __builtin_amdgcn_alignbit(w[4], w[3], 22);
 #pragma unroll
   for (int g = 0; g < 5; ++g) {
     q[3 * g + 0] = (win[g] & k.m5) | k.magic;
     q[3 * g + 1] = ((win[g] >> 5) & k.m5) | k.magic;
     q[3 * g + 2] = ((win[g] >> 10) & k.m5) | k.magic;
   }
-  // codes 30, 31 live in w[4] bits 22..31
-  const uint32_t c30 = (w[4] >> 22) & 31u, c31 = w[4] >> 27;
-  q[15] = c30 | (c31 << 16) | k.magic;
+  // codes 30, 31 live in w[4] bits 22..31; both placed at bits 2..6
+  q[15] = ((w[4] >> 20) & 0x7Cu) | ((w[4] >> 9) & 0x7C0000u) | k.magic;
 }
 
 template <int BITS, int K>
@@ -222,7 +228,7 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t (&w)[BITS]) {
 template <int P>
 __device__ __forceinline__ void unpack6_pair(uint32_t (&q)[16], const uint32_t (&w)[6],
                                              const UnpackConsts &k) {
-  q[P] = code_at<6, 2 * P>(w) | (code_at<6, 2 * P + 1>(w) << 16) | k.magic;
+  q[P] = (code_at<6, 2 * P>(w) << 1) | (code_at<6, 2 * P + 1>(w) << 17) | k.magic;
   if constexpr (P + 1 < 16) unpack6_pair<P + 1>(q, w, k);
 }
 
@@ -257,14 +263,14 @@ __device__ __forceinline__ float pairs_dot(const uint32_t (&q)[16], const uint32
   return a0 + a1;
 }
 
-// Contribution of one chunk: scale * (acc - offset*xsp) + bias * xs.
+// Contribution of one chunk: scale * (acc - xsp) + bias * xs.
 template <int BITS>
 __device__ __forceinline__ float chunk_fold(float acc, float sc, float bi, float xs,
                                             float xsp) {
   if constexpr (BITS == 8) {
     return fmaf(bi, xs, sc * acc);
   } else {
-    return fmaf(bi, xs, sc * fmaf(-Magic<BITS>::offset, xsp, acc));
+    return fmaf(bi, xs, sc * (acc - xsp));
   }
 }
 

@@ -79,12 +79,16 @@ def test_gemv_bf16_matches_oracle(gpu, O, I, bits, gs, M):
     y32 = affine_gemv(m, xd, out_dtype=torch.float32).cpu().numpy()
     y16 = affine_gemv(m, xd, out_dtype=torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
     xf = bf16_to_f32(xb)
+    # the bf16 output is the RNE of the same f32 accumulator
+    np.testing.assert_array_equal(y16, bf16_bits(y32))
     for r in range(M):
         ref = oracle.affine_gemv(xf[r], w, sc, bi, O, I, bits, gs)
         err = normwise_rel(y32[r], ref)
         assert err <= TOL, f"row {r}: normwise {err:.3e}"
-        assert err <= 1e-4, f"row {r}: normwise {err:.3e} (expected f32-accumulation level)"
-        assert bf16_ulp_ok(y16[r], ref, 1)
+        assert err <= 2e-5, f"row {r}: normwise {err:.3e} (expected f32-accumulation level)"
+        # away from cancellation the bf16 output is within 1 ulp of RNE(oracle)
+        big = np.abs(ref) > 1e-2 * np.abs(ref).max()
+        assert bf16_ulp_ok(y16[r][big], ref[big], 1)
 
 
 def test_gemv_fp16_sidecar(gpu):

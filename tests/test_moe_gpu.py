@@ -33,7 +33,7 @@ def oracle_route(logits_f32, k):
 
 @pytest.mark.parametrize("E,k,B,kind", [(512, 10, 64, "normal"), (512, 10, 32, "zipf"),
                                         (512, 10, 16, "ties"), (100, 7, 5, "normal"),
-                                        (64, 64, 3, "normal"), (1024, 32, 4, "normal"),
+                                        (32, 32, 3, "normal"), (1024, 32, 4, "normal"),
                                         (512, 1, 8, "ties"), (8, 2, 9, "ties")])
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_route_topk_bit_exact(gpu, E, k, B, kind, dtype):
@@ -60,6 +60,18 @@ def test_route_topk_bit_exact(gpu, E, k, B, kind, dtype):
         ri, rw = oracle_route(lf[b], k)
         np.testing.assert_array_equal(idx[b], ri)
         np.testing.assert_allclose(w[b], rw, rtol=1e-5, atol=1e-7)
+
+
+def test_route_rejects_out_of_range_k(gpu):
+    import torch
+    from logan_amd.device import LoganHipError, route_topk
+
+    lg = torch.zeros((1, 64), device="cuda")
+    for k in (0, 33, 65):
+        with pytest.raises(LoganHipError):
+            route_topk(lg, k)
+    with pytest.raises(LoganHipError):
+        route_topk(torch.zeros((1, 1025), device="cuda"), 4)
 
 
 def test_route_negative_zero_and_equal_logits(gpu):
@@ -150,7 +162,7 @@ def test_moe_block_matches_oracle(gpu, bits, B, zipf):
         np.testing.assert_allclose(w[t], rw, rtol=1e-5)
         err = normwise_rel(out32[t], ref)
         assert err <= TOL, f"token {t}: {err:.3e}"
-        assert err <= 1e-4, f"token {t}: {err:.3e}"
+        assert err <= 5e-5, f"token {t}: {err:.3e} (expected f32-accumulation level)"
 
 
 def test_moe_batch_rows_equal_single_token_runs(gpu):
@@ -181,7 +193,7 @@ def test_moe_without_shared_expert_and_small_shapes(gpu):
     for t in range(B):
         ref, ridx, _ = layer.ref(xf[t], lf[t])
         np.testing.assert_array_equal(idx[t], ridx)
-        assert normwise_rel(out[t], ref) <= 1e-4
+        assert normwise_rel(out[t], ref) <= 5e-5
 
 
 def test_moe_shared_inter_differs(gpu):
@@ -196,7 +208,7 @@ def test_moe_shared_inter_differs(gpu):
     for t in range(3):
         ref, ridx, _ = layer.ref(bf16_to_f32(xb[t]), bf16_to_f32(lb[t]))
         np.testing.assert_array_equal(idx[t], ridx)
-        assert normwise_rel(out[t], ref) <= 1e-4
+        assert normwise_rel(out[t], ref) <= 5e-5
 
 
 def test_moe_deterministic_and_workspace(gpu):
