@@ -216,6 +216,18 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
                         int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
                         float *w_out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Controls of the routed-MoE block's single-launch B = 1 path (one kernel
+ * with an in-kernel hand-off between the gate/up and down phases). It is on
+ * by default (LOGAN_HIP_MOE_FUSED=0 in the environment turns it off);
+ * set_moe_fused(0/1) overrides, like the reference's LOGAN_MOE_ISLAND switch
+ * (logan-qwen4/src/lib.rs:14907-14922). Launches of that path on one device
+ * must not overlap. sync_errors returns its sticky error word for the
+ * current device: 0 = healthy; bit 0 = a phase hand-off wait timed out (the
+ * output of that call was not valid); bits 1-2 = arrival counters not at
+ * rest between launches. */
+void logan_hip_set_moe_fused(int on);
+uint32_t logan_hip_moe_sync_errors(void);
+
 /* Library version string. */
 const char *logan_hip_version(void);
 

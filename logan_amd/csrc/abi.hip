@@ -657,6 +657,10 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
   return lh::launch_moe_block(a, st);
 }
 
+void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }
+
+uint32_t logan_hip_moe_sync_errors(void) { return lh::moe_fused_sync_errors(); }
+
 const char *logan_hip_version(void) { return "logan-hip 0.1.0 (gfx950)"; }
 
 // ---------------------------------------------------------------------------

@@ -74,6 +74,14 @@ struct MoeArgs {
   size_t ws_bytes;
 };
 size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k);
+// single-launch B = 1 path (moe_fused.hip): 1 launched, 0 not applicable
+int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st);
+size_t moe_fused_workspace_bytes(int slots, int inter, int sinter);
+// sticky error bits of the fused path (bit 0: a wait timed out; bits 1-2:
+// arrival counters not at rest)
+uint32_t moe_fused_sync_errors();
+// 0 disables the fused B = 1 path (LOGAN_HIP_MOE_FUSED=0); default on
+void set_moe_fused_enabled(int on);
 // 1 ok, 0 unsupported geometry (nothing launched), -1 launch failure
 int launch_moe_block(const MoeArgs &a, hipStream_t st);
 

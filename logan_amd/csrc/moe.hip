@@ -23,6 +23,8 @@
 //                               -> y[slot][d] (f32)
 //   4. moe_combine_kernel       out[t][d] = sum_r w_r y[t,r][d] (rank order)
 //                               + gs_t * y[t,shared][d] -> bf16
+#include <cstdlib>
+
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 
@@ -179,7 +181,21 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
 }
 
 size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k) {
-  return moe_ws_layout(nullptr, B, D, inter, sinter, E, k).total;
+  const size_t general = moe_ws_layout(nullptr, B, D, inter, sinter, E, k).total;
+  const size_t fused = moe_fused_workspace_bytes(k + 1, inter, sinter);
+  return general > fused ? general : fused;
+}
+
+static int g_fused_enabled = -1;
+
+void set_moe_fused_enabled(int on) { g_fused_enabled = on; }
+
+static bool fused_enabled() {
+  if (g_fused_enabled < 0) {
+    const char *v = getenv("LOGAN_HIP_MOE_FUSED");
+    g_fused_enabled = (v && v[0] == '0') ? 0 : 1;
+  }
+  return g_fused_enabled != 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -626,6 +642,10 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
   if (a.ws_bytes < moe_workspace_bytes(a.B, a.D, a.inter, sinter, a.E, a.k)) return 0;
   MoeArgs aa = a;
   aa.sinter = sinter;
+  if (fused_enabled()) {
+    const int rc = launch_moe_fused_b1(aa, st);
+    if (rc != 0) return rc;
+  }
   MoeWs w = moe_ws_layout(a.ws, a.B, a.D, a.inter, sinter, a.E, a.k);
   hipLaunchKernelGGL(moe_route_group_kernel, dim3(1), dim3(kGroupThreads), 0, st, aa, w);
   if (hipGetLastError() != hipSuccess) return -1;

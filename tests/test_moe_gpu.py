@@ -137,14 +137,29 @@ def run_layer(torch, layer, xb, lb, out_dtype):
     return out, idx.cpu().numpy(), w.cpu().numpy()
 
 
+@pytest.fixture
+def fused_mode(request):
+    """Force the single-launch B=1 path on or off for one test, restore after."""
+    from logan_amd import _lib
+
+    on = getattr(request, "param", 1)
+    _lib.lib().logan_hip_set_moe_fused(on)
+    yield on
+    _lib.lib().logan_hip_set_moe_fused(1)
+    assert _lib.lib().logan_hip_moe_sync_errors() == 0
+
+
+@pytest.mark.parametrize("fused_mode", [1, 0], indirect=True, ids=["fused", "multi"])
 @pytest.mark.parametrize("bits,B,zipf", [(4, 1, False), (4, 16, False), (5, 1, True),
                                          (6, 1, True), (5, 32, True), (6, 32, True),
-                                         (8, 4, False)])
-def test_moe_block_matches_oracle(gpu, bits, B, zipf):
+                                         (8, 4, False), (8, 1, False)])
+def test_moe_block_matches_oracle(gpu, fused_mode, bits, B, zipf):
     """Configs 3 and 4: E=512, top-10, D=2048, inter=512, g64, shared expert."""
     import torch
 
-    print(f"moe bits={bits} B={B} zipf={zipf}", flush=True)
+    if fused_mode == 0 and B > 1:
+        pytest.skip("B > 1 always takes the multi-launch path")
+    print(f"moe bits={bits} B={B} zipf={zipf} fused={fused_mode}", flush=True)
     layer = Layer(torch, 512, 10, 2048, 512, bits, 64, seed=bits * 10 + B)
     rng = np.random.default_rng(1000 + B)
     xb = make_x(rng, B, 2048)
@@ -165,7 +180,11 @@ def test_moe_block_matches_oracle(gpu, bits, B, zipf):
         assert err <= 5e-5, f"token {t}: {err:.3e} (expected f32-accumulation level)"
 
 
-def test_moe_batch_rows_equal_single_token_runs(gpu):
+@pytest.mark.parametrize("fused_mode", [0], indirect=True)
+def test_moe_batch_rows_equal_single_token_runs(gpu, fused_mode):
+    """With the multi-launch path for every B, grouping tokens by expert does
+    not change any token's arithmetic: rows of a B=12 run are bit-identical to
+    B=1 runs."""
     import torch
 
     layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=3)
@@ -224,3 +243,47 @@ def test_moe_deterministic_and_workspace(gpu):
     b = moe_block(layer.dev, x, lg, out_dtype=torch.float32)
     c = moe_block(layer.dev, x, lg, workspace=ws, out_dtype=torch.float32)
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_moe_fused_repeated_launches_are_identical(gpu, fused_mode):
+    """200 back-to-back single-launch calls (different routes each time, the
+    last repeated): counters return to rest, outputs are deterministic."""
+    import torch
+    from logan_amd import _lib
+    from logan_amd.device import moe_block
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=31)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    xs = torch.randn((200, 1, 2048), device="cuda", generator=g).to(torch.bfloat16)
+    ls = torch.randn((200, 1, 512), device="cuda", generator=g).to(torch.bfloat16)
+    ws = torch.empty(layer.dev.workspace_bytes(1), dtype=torch.uint8, device="cuda")
+    out = torch.empty((200, 1, 2048), dtype=torch.float32, device="cuda")
+    for i in range(200):
+        moe_block(layer.dev, xs[i], ls[i], out=out[i], workspace=ws)
+    again = moe_block(layer.dev, xs[199], ls[199], workspace=ws, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert _lib.lib().logan_hip_moe_sync_errors() == 0
+    assert torch.equal(again, out[199])
+    assert torch.isfinite(out).all()
+
+
+def test_moe_fused_agrees_with_multi_launch(gpu):
+    import torch
+    from logan_amd import _lib
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=41)
+    rng = np.random.default_rng(42)
+    xb = make_x(rng, 1, 2048)
+    lb = make_logits(rng, 1, 512)
+    try:
+        _lib.lib().logan_hip_set_moe_fused(1)
+        a, ia, wa = run_layer(torch, layer, xb, lb, torch.float32)
+        _lib.lib().logan_hip_set_moe_fused(0)
+        b, ib, wb = run_layer(torch, layer, xb, lb, torch.float32)
+    finally:
+        _lib.lib().logan_hip_set_moe_fused(1)
+    np.testing.assert_array_equal(ia, ib)
+    np.testing.assert_allclose(wa, wb, rtol=1e-6)
+    assert normwise_rel(a.cpu().numpy(), b.cpu().numpy()) < 2e-5
+    assert _lib.lib().logan_hip_moe_sync_errors() == 0
