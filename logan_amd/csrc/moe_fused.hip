@@ -4,28 +4,37 @@
 //
 //   A blocks (first in the grid): each wave owns UA rows j of one expert slot
 //   (rank r < k of the route, or the shared expert) and computes
-//   h[slot][j] = silu(gate_j . x) * (up_j . x) for them, then publishes with an
-//   agent-scope release and one atomic arrival.
+//   h[slot][j] = silu(gate_j . x) * (up_j . x) for them; once the block's h
+//   stores have completed, the block makes one atomic arrival.
 //
-//   B blocks: each wave owns ROWS_B output rows d for all k+1 slots. It
-//   issues the loads of its down-projection weights for every slot right
-//   after routing (so they stream from HBM while A runs), computes the
-//   shared-expert scalar gate sigmoid(se_g . x), then waits for all A
-//   arrivals, stages every h (as bf16 hi/lo x-operands) in LDS, and forms
-//   out[d] = sum_{r<k} w_r * (down_r . h_r)[d]  (rank order)
-//            + gs * (down_shared . h_shared)[d]
+//   B blocks: a block owns ROWS_B output rows d; wave w covers a quarter of
+//   them for one half of the k+1 slots. Each wave issues the loads of its
+//   down-projection weights right after routing (so they stream from HBM
+//   while A runs); wave 0 computes the shared-expert scalar gate
+//   sigmoid(se_g . x). After every A arrival the block stages all h (as bf16
+//   hi/lo x-operands) in LDS, each wave forms its per-slot down products, and
+//   the block combines them per row in rank order:
+//   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
 //
 // Every wave computes the route itself from the bf16 logits (top-k with the
 // key (logit desc, index asc): per-lane sorted keys, k rounds of a DPP wave
 // max), so no block waits for another before streaming weights.
 //
-// Progress: A waves never wait. Workgroups are dispatched in ID order on each
-// XCD, and every A block precedes every B block, so a B block can only be
-// resident after all A blocks of its XCD were dispatched: the waits always
-// end. They are also bounded: after kSpinLimit polls a B block stops waiting,
-// raises the sticky error word and finishes (its output is then garbage; the
-// host can read the word with logan_hip_moe_sync_errors()).
+// Progress: A blocks never wait on another block. Workgroups are dispatched in
+// ID order, and every A block precedes every B block, so a B block can only be
+// resident after all A blocks were dispatched: the waits always end. They are
+// also bounded: after kSpinLimit polls a B block stops waiting, raises the
+// sticky error word and finishes without writing its rows (the host can read
+// the word with logan_hip_moe_sync_errors()).
+//
+// Hand-off without L2 maintenance: h is written and read only with
+// device-scope (sc1) relaxed atomic stores/loads, which are coherent across
+// the XCDs' L2s; an A wave waits for its h stores to complete (s_waitcnt)
+// before its arrival atomic, and B reads h only after observing every
+// arrival. An agent-scope release/acquire fence would instead write back /
+// invalidate the whole L2 of each XCD per wave (buffer_wbl2 / buffer_inv),
+// which measured tens of microseconds per launch here.
 //
 // The arrival counters live in module-scope device memory (zero when the code
 // object loads) and the last B block to finish puts them back to zero, so each
@@ -36,16 +45,32 @@
 
 namespace lh {
 
+// Arrivals are spread over kArrivalCtrs counters (A block b arrives on
+// counter b % kArrivalCtrs), each on its own 256-byte line: same-address
+// atomics serialise at the memory side (~40 ns each measured here), so one
+// shared counter for every arrival would take tens of microseconds. B waits
+// until each counter in use holds its expected count.
+constexpr int kArrivalCtrs = 64;
+constexpr int kLine = 64;  // u32 per 256-byte line
 struct FusedSync {
-  uint32_t a_done;
-  uint32_t b_done;
-  uint32_t error;
-  uint32_t launches;
+  uint32_t ctr[kArrivalCtrs][kLine];
+  uint32_t b_done[kLine];
+  uint32_t error[kLine];
 };
 __device__ FusedSync g_fused_sync;
 
 constexpr int kFusedMaxSlots = 12;  // k + 1 (routed + shared)
-constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit data format
+constexpr int kCpolSc1 = 16;           // cache policy: device scope (sc1)
+typedef float float4v __attribute__((ext_vector_type(4)));
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+__device__ __forceinline__ uint32_t ld_agent(uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // ---------------------------------------------------------------- DPP helpers
 
@@ -168,14 +193,22 @@ struct FusedGeom {
   int nA_waves;
   int nA_blocks;
   int nB_blocks;
+  int nctr;        // arrival counters in use
 };
 
+constexpr int kWaves = 8;              // waves per block (512 threads)
+constexpr int kHalfSlots = (kFusedMaxSlots + 1) / 2;
+
 template <int BITS, int CPLA, int LANESB, int KPL>
-__global__ __launch_bounds__(256) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
+__global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
   constexpr int UA = BITS == 8 ? 2 : 4;      // rows of gate (and of up) per A wave
-  constexpr int ROWS_B = 64 / LANESB;        // output rows per B wave
+  constexpr int ROWS_W = 64 / LANESB;        // output rows per B wave
+  constexpr int ROWS_B = 4 * ROWS_W;         // output rows per B block (4 row groups x 2 slot halves)
   constexpr int XDW = 36;                    // LDS dwords per (slot, chunk): 16 hi, 16 lo, xs, xsp
   __shared__ __align__(16) uint32_t s_h[kFusedMaxSlots * LANESB * XDW];
+  __shared__ float s_y[ROWS_B][kFusedMaxSlots];
+  __shared__ uint32_t s_timeout;
+  __shared__ float s_gsig;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -186,8 +219,9 @@ __global__ __launch_bounds__(256) void moe_fused_b1_kernel(MoeArgs a, FusedGeom 
 
   if ((int)blockIdx.x < g.nA_blocks) {
     // ------------------------------------------------------------ phase A
-    const int item = blockIdx.x * 4 + wave;
-    if (item >= g.nA_waves) return;
+    const int item_raw = blockIdx.x * kWaves + wave;
+    const bool active = item_raw < g.nA_waves;
+    const int item = active ? item_raw : g.nA_waves - 1;  // idle waves mirror a valid item
     const bool shared = item >= g.k * g.wpr;
     const int slot = shared ? g.k : item / g.wpr;
     const int jb = shared ? item - g.k * g.wpr : item % g.wpr;
@@ -283,125 +317,135 @@ __global__ __launch_bounds__(256) void moe_fused_b1_kernel(MoeArgs a, FusedGeom 
       hv[u] = silu(gv) * uv;  // logan-qwen4/src/lib.rs:8807-8809
     }
     float *hrow = reinterpret_cast<float *>(a.ws) + (size_t)slot * hmax;
-    if (lane < UA && j0 + lane < rows) {
+    if (active && lane < UA && j0 + lane < rows) {
       float v = hv[0];
 #pragma unroll
       for (int u = 1; u < UA; ++u) v = lane == u ? hv[u] : v;
-      hrow[j0 + lane] = v;
+      __hip_atomic_store(&hrow[j0 + lane], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    if (lane == 0) __hip_atomic_fetch_add(&g_fused_sync.a_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // h stores complete before the arrival
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(&g_fused_sync.ctr[blockIdx.x % kArrivalCtrs][0], 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
   // -------------------------------------------------------------- phase B
+  // wave w: row group w % 4 (ROWS_W rows), slot half w / 4
   const int bb = blockIdx.x - g.nA_blocks;
   const int lb = lane % LANESB;           // chunk of a down row
-  const int rsub = lane / LANESB;
-  const int d = (bb * 4 + wave) * ROWS_B + rsub;
+  const int rloc = (wave & 3) * ROWS_W + lane / LANESB;
+  const int d = bb * ROWS_B + rloc;
   const bool drow = d < a.D;
+  const int half = wave >> 2;
+  const int s_lo = half ? (g.slots + 1) / 2 : 0;
+  const int s_hi = half ? g.slots : (g.slots + 1) / 2;
   const bool has_shared = a.sdown.m.w != nullptr;
 
   uint32_t sel[kFusedMaxSlots];
   wave_route_bf16<KPL>(logits, a.E, g.k, sel);
-  float wr[kFusedMaxSlots];
-  {
-    const float l0 = sel_logit(sel[0]);
-    float ws = 0.f;
-#pragma unroll
-    for (int r = 0; r < kFusedMaxSlots; ++r) {
-      wr[r] = 0.f;
-      if (r < g.k) {
-        wr[r] = __expf(sel_logit(sel[r]) - l0);
-        ws += wr[r];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < kFusedMaxSlots; ++r) wr[r] = wr[r] / ws;
-  }
-  if (bb == 0 && threadIdx.x == 0) {
-    for (int r = 0; r < g.k; ++r) {
-      if (a.idx_out) a.idx_out[r] = sel_expert(sel[r]);
-      if (a.w_out) a.w_out[r] = wr[r];
-    }
-  }
 
-  // issue every slot's down-row loads now
-  uint32_t wv[kFusedMaxSlots][BITS];
-  float sc[kFusedMaxSlots], bi[kFusedMaxSlots];
+  // issue this wave's down-row loads (slots s_lo .. s_hi-1) now
+  uint32_t wv[kHalfSlots][BITS];
+  float sc[kHalfSlots], bi[kHalfSlots];
 #pragma unroll
-  for (int s = 0; s < kFusedMaxSlots; ++s) {
+  for (int t = 0; t < kHalfSlots; ++t) {
+    const int s = s_lo + t;
     const bool sh = s == g.k;
-    const bool live = s < g.slots;
     const DevBank &bd = sh ? a.sdown : a.down;
-    const int e = sh ? 0 : sel_expert(sel[s < g.k ? s : 0]);
+    uint32_t key = sel[0];
+#pragma unroll
+    for (int r = 1; r < kFusedMaxSlots; ++r) key = r == s ? sel[r] : key;
+    const int e = sh ? 0 : sel_expert(key);
     const int K = sh ? a.sinter : a.inter;
-    if (live && drow && lb < (K >> 5)) {
-      load_chunk<BITS>(wv[s], bd.m.w + (size_t)e * bd.w_stride + (size_t)d * bd.m.row_bytes +
+    if (s < s_hi && drow && lb < (K >> 5)) {
+      load_chunk<BITS>(wv[t], bd.m.w + (size_t)e * bd.w_stride + (size_t)d * bd.m.row_bytes +
                                   (size_t)lb * (4 * BITS));
-    } else {
-#pragma unroll
-      for (int t = 0; t < BITS; ++t) wv[s][t] = 0;
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < kFusedMaxSlots; ++s) {
-    const bool sh = s == g.k;
-    const bool live = s < g.slots;
-    const DevBank &bd = sh ? a.sdown : a.down;
-    const int e = sh ? 0 : sel_expert(sel[s < g.k ? s : 0]);
-    const int K = sh ? a.sinter : a.inter;
-    if (live && drow && lb < (K >> 5)) {
       const size_t p = (size_t)e * bd.p_stride + (size_t)d * bd.m.ng + lb / (bd.m.gs >> 5);
-      sc[s] = aux_to_f32(bd.m.sc[p], bd.m.fp16);
-      bi[s] = aux_to_f32(bd.m.bi[p], bd.m.fp16);
+      sc[t] = aux_to_f32(bd.m.sc[p], bd.m.fp16);
+      bi[t] = aux_to_f32(bd.m.bi[p], bd.m.fp16);
     } else {
-      sc[s] = bi[s] = 0.f;
+#pragma unroll
+      for (int q = 0; q < BITS; ++q) wv[t][q] = 0;
+      sc[t] = bi[t] = 0.f;
     }
-  }
-  // shared-expert scalar gate (logan-qwen4/src/lib.rs:7602-7604)
-  float gsig = 1.0f;
-  if (has_shared && a.se_gate_vec) {
-    float acc = 0.f;
-    for (int j = lane; j < a.D; j += 64)
-      acc = fmaf(bf16_to_f32(a.se_gate_vec[j]), bf16_to_f32(a.x[j]), acc);
-    acc = wave_sum_f32(acc);
-    gsig = 1.0f / (1.0f + __expf(-acc));
   }
 
-  // wait for every A wave
-  __shared__ uint32_t s_timeout;
-  if (threadIdx.x == 0) {
+  // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604):
+  // wave 0 reads se_g and x as 16-byte loads, all in flight at once
+  if (wave == 0) {
+    float gsig = 1.0f;
+    if (has_shared && a.se_gate_vec) {
+      float gd = 0.f;
+      const int C = a.D >> 5;
+#pragma unroll
+      for (int i = 0; i < CPLA; ++i) {
+        const int c = lane + 64 * i;
+        if (c < C) {
+          const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec + 32 * c);
+          const uint4 *xv = reinterpret_cast<const uint4 *>(a.x + 32 * c);
+          uint4 gq[4], xq[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            gq[v] = gv[v];
+            xq[v] = xv[v];
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            gd = dot2(gq[v].x, xq[v].x, gd);
+            gd = dot2(gq[v].y, xq[v].y, gd);
+            gd = dot2(gq[v].z, xq[v].z, gd);
+            gd = dot2(gq[v].w, xq[v].w, gd);
+          }
+        }
+      }
+      gd = wave_sum_f32(gd);
+      gsig = 1.0f / (1.0f + __expf(-gd));
+    }
+    if (lane == 0) s_gsig = gsig;
+  }
+
+  // wait until every arrival counter in use holds its expected count
+  if (wave == 0) {
     uint32_t spins = 0, to = 0;
-    while (__hip_atomic_load(&g_fused_sync.a_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-           (uint32_t)g.nA_waves) {
-      __builtin_amdgcn_s_sleep(1);
+    const int need = lane < g.nctr
+                         ? g.nA_blocks / kArrivalCtrs + (lane < g.nA_blocks % kArrivalCtrs ? 1 : 0)
+                         : 0;
+    bool done = lane >= g.nctr || ld_agent(&g_fused_sync.ctr[lane][0]) == (uint32_t)need;
+    while (!__all(done)) {
+      __builtin_amdgcn_s_sleep(2);
+      if (!done) done = ld_agent(&g_fused_sync.ctr[lane][0]) == (uint32_t)need;
       if (++spins > kSpinLimit) {
         to = 1;
-        __hip_atomic_fetch_or(&g_fused_sync.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_fetch_or(&g_fused_sync.error[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    s_timeout = to;
+    if (lane == 0) s_timeout = to;
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // stage h of every slot as x-operands in LDS
   {
     const int CI = hmax >> 5;
     const int items = g.slots * LANESB;
-    for (int it = threadIdx.x; it < items; it += 256) {
+    const __amdgpu_buffer_rsrc_t hrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws, (short)0, g.slots * hmax * 4, kBufWord3);
+    for (int it = threadIdx.x; it < items; it += kWaves * 64) {
       const int s = it / LANESB, c = it % LANESB;
       const int K = (has_shared && s == g.k) ? a.sinter : a.inter;
       float xf[32];
       if (c < (K >> 5) && c < CI) {
-        const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(a.ws) +
-                                                             (size_t)s * hmax + 32 * c);
+        // device-scope (sc1) 16-byte loads: coherent with A's sc1 stores
+        const int off = (s * hmax + 32 * c) * 4;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-          const float4 t = src[v];
+          const float4v t = __builtin_bit_cast(
+              float4v, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, off + 16 * v, 0, kCpolSc1));
           xf[4 * v + 0] = t.x; xf[4 * v + 1] = t.y; xf[4 * v + 2] = t.z; xf[4 * v + 3] = t.w;
         }
       } else {
@@ -422,10 +466,10 @@ __global__ __launch_bounds__(256) void moe_fused_b1_kernel(MoeArgs a, FusedGeom 
   }
   __syncthreads();
 
-  float acc_out = 0.f, y_sh = 0.f;
 #pragma unroll
-  for (int s = 0; s < kFusedMaxSlots; ++s) {
-    if (s < g.slots) {
+  for (int t = 0; t < kHalfSlots; ++t) {
+    const int s = s_lo + t;
+    if (s < s_hi) {
       const uint32_t *src = s_h + (size_t)(s * LANESB + lb) * XDW;
       uint32_t hp[16], lp[16];
 #pragma unroll
@@ -437,33 +481,58 @@ __global__ __launch_bounds__(256) void moe_fused_b1_kernel(MoeArgs a, FusedGeom 
       }
       const float xs = __uint_as_float(src[32]), xsp = __uint_as_float(src[33]);
       uint32_t q[16];
-      unpack_chunk<BITS>(q, wv[s], kc);
+      unpack_chunk<BITS>(q, wv[t], kc);
       const float acc = pairs_dot(q, hp) + pairs_dot(q, lp);
-      float v = chunk_fold<BITS>(acc, sc[s], bi[s], xs, xsp);
+      float v = chunk_fold<BITS>(acc, sc[t], bi[t], xs, xsp);
       v = group_sum_f32<LANESB>(v);
-      if (s < g.k)
-        acc_out = fmaf(v, wr[s], acc_out);  // rank order, as lib.rs:8692-8698
-      else
-        y_sh = v;
+      if (lb == 0) s_y[rloc][s] = v;
     }
   }
-  const float o = has_shared ? fmaf(y_sh, gsig, acc_out) : acc_out;
-  if (lb == 0 && drow && !s_timeout) {
-    if (a.out_f32)
-      reinterpret_cast<float *>(a.out)[d] = o;
-    else
-      reinterpret_cast<uint16_t *>(a.out)[d] = (uint16_t)f32_to_bf16_rne(o);
+  __syncthreads();
+
+  // rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711) by the first ROWS_B threads
+  if ((int)threadIdx.x < ROWS_B) {
+    const int r = threadIdx.x;
+    const int dd = bb * ROWS_B + r;
+    float wr[kFusedMaxSlots];
+    const float l0 = sel_logit(sel[0]);
+    float wsum = 0.f;
+#pragma unroll
+    for (int q = 0; q < kFusedMaxSlots; ++q) {
+      wr[q] = 0.f;
+      if (q < g.k) {
+        wr[q] = __expf(sel_logit(sel[q]) - l0);
+        wsum += wr[q];
+      }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < kFusedMaxSlots; ++q)
+      if (q < g.k) acc = fmaf(s_y[r][q], wr[q] / wsum, acc);
+    float o = acc;
+    if (has_shared) o = fmaf(s_y[r][g.k], s_gsig, acc);
+    if (dd < a.D && !s_timeout) {
+      if (a.out_f32)
+        reinterpret_cast<float *>(a.out)[dd] = o;
+      else
+        reinterpret_cast<uint16_t *>(a.out)[dd] = (uint16_t)f32_to_bf16_rne(o);
+    }
+    if (bb == 0 && r == 0) {
+      for (int q = 0; q < g.k; ++q) {
+        if (a.idx_out) a.idx_out[q] = sel_expert(sel[q]);
+        if (a.w_out) a.w_out[q] = wr[q] / wsum;
+      }
+    }
   }
 
   // last B block resets the arrival counters for the next launch
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
-        __hip_atomic_fetch_add(&g_fused_sync.b_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&g_fused_sync.b_done[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (uint32_t)g.nB_blocks - 1) {
-      __hip_atomic_store(&g_fused_sync.a_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&g_fused_sync.b_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(&g_fused_sync.launches, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int c = 0; c < kArrivalCtrs; ++c) st_agent(&g_fused_sync.ctr[c][0], 0u);
+      st_agent(&g_fused_sync.b_done[0], 0u);
     }
   }
 }
@@ -478,7 +547,7 @@ size_t moe_fused_workspace_bytes(int slots, int inter, int sinter) {
 template <int BITS, int CPLA, int LANESB, int KPL>
 static int fused_launch(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
   auto kern = moe_fused_b1_kernel<BITS, CPLA, LANESB, KPL>;
-  hipLaunchKernelGGL(kern, dim3(g.nA_blocks + g.nB_blocks), dim3(256), 0, st, a, g);
+  hipLaunchKernelGGL(kern, dim3(g.nA_blocks + g.nB_blocks), dim3(kWaves * 64), 0, st, a, g);
   return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
@@ -508,13 +577,15 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   if (a.ws_bytes < moe_fused_workspace_bytes(slots, a.inter, a.sinter)) return 0;
   if ((reinterpret_cast<uintptr_t>(a.ws) & 15) != 0 || (hmax & 3) != 0) return 0;
   const int UA = a.gate.m.bits == 8 ? 2 : 4;
+  if (a.se_gate_vec && (reinterpret_cast<uintptr_t>(a.se_gate_vec) & 15) != 0) return 0;
   FusedGeom g;
   g.k = a.k;
   g.slots = slots;
   g.wpr = (a.inter + UA - 1) / UA;
   g.wps = a.sdown.m.w ? (a.sinter + UA - 1) / UA : 0;
   g.nA_waves = g.k * g.wpr + g.wps;
-  g.nA_blocks = (g.nA_waves + 3) / 4;
+  g.nA_blocks = (g.nA_waves + kWaves - 1) / kWaves;
+  g.nctr = g.nA_blocks < kArrivalCtrs ? g.nA_blocks : kArrivalCtrs;
   const int Ci = hmax >> 5;
   const int lanesb = Ci <= 16 ? 16 : 32;
   const int rows_per_block = 4 * (64 / lanesb);
@@ -529,11 +600,13 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
 }
 
 uint32_t moe_fused_sync_errors() {
-  FusedSync s{};
+  static FusedSync s;
   if (hipMemcpyFromSymbol(&s, HIP_SYMBOL(g_fused_sync), sizeof(s), 0, hipMemcpyDeviceToHost) !=
       hipSuccess)
     return 0xffffffffu;
-  return s.error | (s.a_done ? 2u : 0u) | (s.b_done ? 4u : 0u);
+  uint32_t busy = 0;
+  for (int c = 0; c < kArrivalCtrs; ++c) busy |= s.ctr[c][0];
+  return s.error[0] | (busy ? 2u : 0u) | (s.b_done[0] ? 4u : 0u);
 }
 
 }  // namespace lh
