@@ -108,8 +108,9 @@ def bench_moe(torch, device, synth, args):
                 device.moe_block(layers[l], xs[i, l], logits[i, l], out=out[l], workspace=ws)
         graphs.append(gr)
     torch.cuda.synchronize()
-    for i in range(args.warmup):
-        graphs[i].replay()
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            graphs[i].replay()
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps x {L} layers")
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -154,17 +155,19 @@ def bench_gemv(torch, device, synth, args):
             for j in range(per_graph):
                 device.affine_gemv(mats[(gi * per_graph + j) % copies], x, out=y)
         graphs.append(gr)
-    graphs[0].replay()
+    with torch.cuda.stream(stream):
+        graphs[0].replay()
     torch.cuda.synchronize()
     launches = len(graphs) * per_graph
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for gr in graphs:
-        gr.replay()
-    ev1.record(stream)
-    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for gr in graphs:
+            gr.replay()
+        ev1.record(stream)
+        torch.cuda.synchronize()
     us = ev0.elapsed_time(ev1) * 1e3 / launches
     gbps = GEMV_BYTES / (us * 1e-6) / 1e9
     log(f"gemv q4 4096x2048: {us:.2f} us/launch, {gbps:.0f} GB/s")

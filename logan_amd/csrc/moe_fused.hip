@@ -7,13 +7,14 @@
 //   h[slot][j] = silu(gate_j . x) * (up_j . x) for them; once the block's h
 //   stores have completed, the block makes one atomic arrival.
 //
-//   B blocks: a block owns ROWS_B output rows d; wave w covers a quarter of
-//   them for one half of the k+1 slots. Each wave issues the loads of its
-//   down-projection weights right after routing (so they stream from HBM
-//   while A runs); wave 0 computes the shared-expert scalar gate
-//   sigmoid(se_g . x). After every A arrival the block stages all h (as bf16
-//   hi/lo x-operands) in LDS, each wave forms its per-slot down products, and
-//   the block combines them per row in rank order:
+//   B blocks: a block owns ROWS_B output rows d; wave w covers half of them
+//   for a quarter of the k+1 slots. Each wave issues the shared slot's
+//   down-row loads and the shared-expert gate loads before routing and the
+//   routed down rows right after it, so they stream from HBM while A runs;
+//   wave 0 computes the shared-expert scalar gate sigmoid(se_g . x). After
+//   every A arrival the block stages all h (as bf16 hi/lo x-operands) in LDS,
+//   each wave forms its per-slot down products, and the block combines them
+//   per row in rank order:
 //   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
 //
@@ -36,8 +37,10 @@
 // invalidate the whole L2 of each XCD per wave (buffer_wbl2 / buffer_inv),
 // which measured tens of microseconds per launch here.
 //
-// The arrival counters live in module-scope device memory (zero when the code
-// object loads) and the last B block to finish puts them back to zero, so each
+// The arrival and completion counters live in module-scope device memory
+// (zero when the code object loads). B blocks count their completion over
+// kDoneCtrs counters and then one top counter; the block that completes the
+// count puts every counter back to zero, so each
 // launch starts from zero without a memset. Launches of this kernel on one
 // device must therefore not overlap (one stream, or serialised streams).
 #include "affine_dev.hpp"
@@ -52,9 +55,11 @@ namespace lh {
 // until each counter in use holds its expected count.
 constexpr int kArrivalCtrs = 64;
 constexpr int kLine = 64;  // u32 per 256-byte line
+constexpr int kDoneCtrs = 16;  // B completion: block b -> bctr[b % 16], then btop
 struct FusedSync {
   uint32_t ctr[kArrivalCtrs][kLine];
-  uint32_t b_done[kLine];
+  uint32_t bctr[kDoneCtrs][kLine];
+  uint32_t btop[kLine];
   uint32_t error[kLine];
 };
 __device__ FusedSync g_fused_sync;
@@ -151,19 +156,29 @@ __device__ __forceinline__ void sort_desc(uint32_t (&v)[N]) {
       }
 }
 
-// Top-`rounds` of E bf16 logits by one wave. sel[r] = 32-bit key of rank r:
-// high half = ordered logit, low half = 0xffff - expert.
+// Routing by one wave, in two steps so the caller can put other loads in
+// flight between them: route_keys issues the logit loads (lane l holds
+// experts l + 64 i); route_select sorts each lane's keys and runs `rounds`
+// rounds of a wave max. sel[r] = 32-bit key of rank r: high half = ordered
+// logit, low half = 0xffff - expert.
 template <int KPL>
-__device__ __forceinline__ void wave_route_bf16(const uint16_t *logits, int E, int rounds,
-                                                uint32_t (&sel)[kFusedMaxSlots]) {
+__device__ __forceinline__ void route_keys(const uint16_t *logits, int E, uint32_t (&key)[KPL]) {
   const int lane = threadIdx.x & 63;
-  uint32_t key[KPL];
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int e = i * 64 + lane;
-    const bool ok = e < E;
-    const uint32_t b = logits[ok ? e : 0];
-    key[i] = ok ? ((ord16(b) << 16) | (0xffffu - (uint32_t)e)) : 0u;
+    key[i] = logits[e < E ? e : 0];
+  }
+}
+
+template <int KPL>
+__device__ __forceinline__ void route_select(uint32_t (&key)[KPL], int E, int rounds,
+                                             uint32_t (&sel)[kFusedMaxSlots]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int e = i * 64 + lane;
+    key[i] = e < E ? ((ord16(key[i]) << 16) | (0xffffu - (uint32_t)e)) : 0u;
   }
   sort_desc<KPL>(key);
 #pragma unroll
@@ -196,14 +211,31 @@ struct FusedGeom {
   int nctr;        // arrival counters in use
 };
 
-constexpr int kWaves = 8;              // waves per block (512 threads)
-constexpr int kHalfSlots = (kFusedMaxSlots + 1) / 2;
+constexpr int kWaves = 8;   // waves per block (512 threads)
+constexpr int kQSlots = 3;  // slots per B wave (a quarter of kFusedMaxSlots)
+
+// one slot's down-row chunk and its scale/bias
+template <int BITS>
+__device__ __forceinline__ void load_down(uint32_t (&w)[BITS], float &sc, float &bi,
+                                          const DevBank &bd, int e, int d, int lb, bool live) {
+  if (live) {
+    load_chunk<BITS>(w, bd.m.w + (size_t)e * bd.w_stride + (size_t)d * bd.m.row_bytes +
+                            (size_t)lb * (4 * BITS));
+    const size_t p = (size_t)e * bd.p_stride + (size_t)d * bd.m.ng + lb / (bd.m.gs >> 5);
+    sc = aux_to_f32(bd.m.sc[p], bd.m.fp16);
+    bi = aux_to_f32(bd.m.bi[p], bd.m.fp16);
+  } else {
+#pragma unroll
+    for (int q = 0; q < BITS; ++q) w[q] = 0;
+    sc = bi = 0.f;
+  }
+}
 
 template <int BITS, int CPLA, int LANESB, int KPL>
 __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
   constexpr int UA = BITS == 8 ? 2 : 4;      // rows of gate (and of up) per A wave
   constexpr int ROWS_W = 64 / LANESB;        // output rows per B wave
-  constexpr int ROWS_B = 4 * ROWS_W;         // output rows per B block (4 row groups x 2 slot halves)
+  constexpr int ROWS_B = 2 * ROWS_W;         // output rows per B block (2 row groups x 4 slot quarters)
   constexpr int XDW = 36;                    // LDS dwords per (slot, chunk): 16 hi, 16 lo, xs, xsp
   __shared__ __align__(16) uint32_t s_h[kFusedMaxSlots * LANESB * XDW];
   __shared__ float s_y[ROWS_B][kFusedMaxSlots];
@@ -214,6 +246,7 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
   const int wave = threadIdx.x >> 6;
   const uint16_t *logits = reinterpret_cast<const uint16_t *>(a.logits);
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  const int C = a.D >> 5;
   UnpackConsts kc;
   kc.init();
 
@@ -226,10 +259,22 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     const int slot = shared ? g.k : item / g.wpr;
     const int jb = shared ? item - g.k * g.wpr : item % g.wpr;
     const int rows = shared ? a.sinter : a.inter;
+
+    uint32_t key[KPL];
+    if (!shared) route_keys<KPL>(logits, a.E, key);
+    // x does not depend on the route: in flight together with the logits
+    uint4 xq[CPLA][4];
+#pragma unroll
+    for (int i = 0; i < CPLA; ++i) {
+      const int c = lane + 64 * i;
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.x + 32 * (c < C ? c : 0));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) xq[i][v] = src[v];
+    }
     int e = 0;
     if (!shared) {
       uint32_t sel[kFusedMaxSlots];
-      wave_route_bf16<KPL>(logits, a.E, slot + 1, sel);
+      route_select<KPL>(key, a.E, slot + 1, sel);
       uint32_t mine = sel[0];
 #pragma unroll
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
@@ -244,7 +289,6 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     const uint16_t *usc = buk.m.sc + (size_t)e * buk.p_stride;
     const uint16_t *ubi = buk.m.bi + (size_t)e * buk.p_stride;
     const int j0 = jb * UA;
-    const int C = a.D >> 5;
     const int gsc_chunks = bgk.m.gs >> 5;
 
     uint32_t wg[UA][CPLA][BITS], wu[UA][CPLA][BITS];
@@ -284,19 +328,14 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     for (int i = 0; i < CPLA; ++i) {
       const int c = lane + 64 * i;
       uint32_t xb[32];
-      if (c < C) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + 32 * c);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint4 q = src[v];
-          xb[8 * v + 0] = q.x & 0xffffu; xb[8 * v + 1] = q.x >> 16;
-          xb[8 * v + 2] = q.y & 0xffffu; xb[8 * v + 3] = q.y >> 16;
-          xb[8 * v + 4] = q.z & 0xffffu; xb[8 * v + 5] = q.z >> 16;
-          xb[8 * v + 6] = q.w & 0xffffu; xb[8 * v + 7] = q.w >> 16;
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) xb[v] = 0;
+      for (int v = 0; v < 4; ++v) {
+        const uint4 q = xq[i][v];
+        const bool ok = c < C;
+        xb[8 * v + 0] = ok ? q.x & 0xffffu : 0u; xb[8 * v + 1] = ok ? q.x >> 16 : 0u;
+        xb[8 * v + 2] = ok ? q.y & 0xffffu : 0u; xb[8 * v + 3] = ok ? q.y >> 16 : 0u;
+        xb[8 * v + 4] = ok ? q.z & 0xffffu : 0u; xb[8 * v + 5] = ok ? q.z >> 16 : 0u;
+        xb[8 * v + 6] = ok ? q.w & 0xffffu : 0u; xb[8 * v + 7] = ok ? q.w >> 16 : 0u;
       }
       XChunk xc;
       make_xchunk_bf16<BITS>(xc, xb);
@@ -333,71 +372,71 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
   }
 
   // -------------------------------------------------------------- phase B
-  // wave w: row group w % 4 (ROWS_W rows), slot half w / 4
+  // wave w: row group w % 2 (ROWS_W rows), slot quarter w / 2
   const int bb = blockIdx.x - g.nA_blocks;
-  const int lb = lane % LANESB;           // chunk of a down row
-  const int rloc = (wave & 3) * ROWS_W + lane / LANESB;
+  const int lb = lane % LANESB;  // chunk of a down row
+  const int rloc = (wave & 1) * ROWS_W + lane / LANESB;
   const int d = bb * ROWS_B + rloc;
   const bool drow = d < a.D;
-  const int half = wave >> 2;
-  const int s_lo = half ? (g.slots + 1) / 2 : 0;
-  const int s_hi = half ? g.slots : (g.slots + 1) / 2;
+  const int sq = wave >> 1;
+  const int s_lo = (g.slots * sq) / 4;
+  const int s_hi = (g.slots * (sq + 1)) / 4;
   const bool has_shared = a.sdown.m.w != nullptr;
 
-  uint32_t sel[kFusedMaxSlots];
-  wave_route_bf16<KPL>(logits, a.E, g.k, sel);
+  uint32_t key[KPL];
+  route_keys<KPL>(logits, a.E, key);
 
-  // issue this wave's down-row loads (slots s_lo .. s_hi-1) now
-  uint32_t wv[kHalfSlots][BITS];
-  float sc[kHalfSlots], bi[kHalfSlots];
+  // route-independent loads first: the shared slot's down rows, x and se_g
+  uint32_t wv[kQSlots][BITS];
+  float sc[kQSlots], bi[kQSlots];
 #pragma unroll
-  for (int t = 0; t < kHalfSlots; ++t) {
+  for (int t = 0; t < kQSlots; ++t) {
     const int s = s_lo + t;
-    const bool sh = s == g.k;
-    const DevBank &bd = sh ? a.sdown : a.down;
-    uint32_t key = sel[0];
+    const bool live = has_shared && s == g.k && s < s_hi && drow && lb < (a.sinter >> 5);
+    load_down<BITS>(wv[t], sc[t], bi[t], a.sdown, 0, d, lb, live);
+  }
+  uint4 gq[CPLA][4], xq[CPLA][4];
+  const bool do_gate = wave == 0 && has_shared && a.se_gate_vec;
+  if (do_gate) {
 #pragma unroll
-    for (int r = 1; r < kFusedMaxSlots; ++r) key = r == s ? sel[r] : key;
-    const int e = sh ? 0 : sel_expert(key);
-    const int K = sh ? a.sinter : a.inter;
-    if (s < s_hi && drow && lb < (K >> 5)) {
-      load_chunk<BITS>(wv[t], bd.m.w + (size_t)e * bd.w_stride + (size_t)d * bd.m.row_bytes +
-                                  (size_t)lb * (4 * BITS));
-      const size_t p = (size_t)e * bd.p_stride + (size_t)d * bd.m.ng + lb / (bd.m.gs >> 5);
-      sc[t] = aux_to_f32(bd.m.sc[p], bd.m.fp16);
-      bi[t] = aux_to_f32(bd.m.bi[p], bd.m.fp16);
-    } else {
+    for (int i = 0; i < CPLA; ++i) {
+      const int c = lane + 64 * i;
+      const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec + 32 * (c < C ? c : 0));
+      const uint4 *xv = reinterpret_cast<const uint4 *>(a.x + 32 * (c < C ? c : 0));
 #pragma unroll
-      for (int q = 0; q < BITS; ++q) wv[t][q] = 0;
-      sc[t] = bi[t] = 0.f;
+      for (int v = 0; v < 4; ++v) {
+        gq[i][v] = gv[v];
+        xq[i][v] = xv[v];
+      }
     }
   }
-
-  // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604):
-  // wave 0 reads se_g and x as 16-byte loads, all in flight at once
+  uint32_t sel[kFusedMaxSlots];
+  route_select<KPL>(key, a.E, g.k, sel);
+#pragma unroll
+  for (int t = 0; t < kQSlots; ++t) {
+    const int s = s_lo + t;
+    if (s < g.k) {
+      uint32_t kk = sel[0];
+#pragma unroll
+      for (int r = 1; r < kFusedMaxSlots; ++r) kk = r == s ? sel[r] : kk;
+      const bool live = s < s_hi && drow && lb < (a.inter >> 5);
+      load_down<BITS>(wv[t], sc[t], bi[t], a.down, sel_expert(kk), d, lb, live);
+    }
+  }
+  // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604)
   if (wave == 0) {
     float gsig = 1.0f;
-    if (has_shared && a.se_gate_vec) {
+    if (do_gate) {
       float gd = 0.f;
-      const int C = a.D >> 5;
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
-        const int c = lane + 64 * i;
-        if (c < C) {
-          const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec + 32 * c);
-          const uint4 *xv = reinterpret_cast<const uint4 *>(a.x + 32 * c);
-          uint4 gq[4], xq[4];
+        if (lane + 64 * i < C) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            gq[v] = gv[v];
-            xq[v] = xv[v];
-          }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            gd = dot2(gq[v].x, xq[v].x, gd);
-            gd = dot2(gq[v].y, xq[v].y, gd);
-            gd = dot2(gq[v].z, xq[v].z, gd);
-            gd = dot2(gq[v].w, xq[v].w, gd);
+            gd = dot2(gq[i][v].x, xq[i][v].x, gd);
+            gd = dot2(gq[i][v].y, xq[i][v].y, gd);
+            gd = dot2(gq[i][v].z, xq[i][v].z, gd);
+            gd = dot2(gq[i][v].w, xq[i][v].w, gd);
           }
         }
       }
@@ -467,7 +506,7 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
   __syncthreads();
 
 #pragma unroll
-  for (int t = 0; t < kHalfSlots; ++t) {
+  for (int t = 0; t < kQSlots; ++t) {
     const int s = s_lo + t;
     if (s < s_hi) {
       const uint32_t *src = s_h + (size_t)(s * LANESB + lb) * XDW;
@@ -525,14 +564,23 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     }
   }
 
-  // last B block resets the arrival counters for the next launch
+  // completion: the last B block (two-level count) resets every counter
   __syncthreads();
   if (threadIdx.x == 0) {
+    const int nb = g.nB_blocks;
+    const int c = bb % kDoneCtrs;
+    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
+    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
     const uint32_t prev =
-        __hip_atomic_fetch_add(&g_fused_sync.b_done[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (uint32_t)g.nB_blocks - 1) {
-      for (int c = 0; c < kArrivalCtrs; ++c) st_agent(&g_fused_sync.ctr[c][0], 0u);
-      st_agent(&g_fused_sync.b_done[0], 0u);
+        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (uint32_t)needc - 1) {
+      const uint32_t top =
+          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (top == (uint32_t)nbc - 1) {
+        for (int q = 0; q < kArrivalCtrs; ++q) st_agent(&g_fused_sync.ctr[q][0], 0u);
+        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
+        st_agent(&g_fused_sync.btop[0], 0u);
+      }
     }
   }
 }
@@ -578,6 +626,7 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   if ((reinterpret_cast<uintptr_t>(a.ws) & 15) != 0 || (hmax & 3) != 0) return 0;
   const int UA = a.gate.m.bits == 8 ? 2 : 4;
   if (a.se_gate_vec && (reinterpret_cast<uintptr_t>(a.se_gate_vec) & 15) != 0) return 0;
+  if ((reinterpret_cast<uintptr_t>(a.x) & 15) != 0) return 0;
   FusedGeom g;
   g.k = a.k;
   g.slots = slots;
@@ -588,7 +637,7 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   g.nctr = g.nA_blocks < kArrivalCtrs ? g.nA_blocks : kArrivalCtrs;
   const int Ci = hmax >> 5;
   const int lanesb = Ci <= 16 ? 16 : 32;
-  const int rows_per_block = 4 * (64 / lanesb);
+  const int rows_per_block = 2 * (64 / lanesb);
   g.nB_blocks = (a.D + rows_per_block - 1) / rows_per_block;
   switch (a.gate.m.bits) {
     case 4: return fused_bits<4>(a, g, st);
@@ -604,9 +653,10 @@ uint32_t moe_fused_sync_errors() {
   if (hipMemcpyFromSymbol(&s, HIP_SYMBOL(g_fused_sync), sizeof(s), 0, hipMemcpyDeviceToHost) !=
       hipSuccess)
     return 0xffffffffu;
-  uint32_t busy = 0;
+  uint32_t busy = 0, bbusy = s.btop[0];
   for (int c = 0; c < kArrivalCtrs; ++c) busy |= s.ctr[c][0];
-  return s.error[0] | (busy ? 2u : 0u) | (s.b_done[0] ? 4u : 0u);
+  for (int c = 0; c < kDoneCtrs; ++c) bbusy |= s.bctr[c][0];
+  return s.error[0] | (busy ? 2u : 0u) | (bbusy ? 4u : 0u);
 }
 
 }  // namespace lh
