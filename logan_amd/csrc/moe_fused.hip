@@ -4,17 +4,20 @@
 //
 //   A blocks (first in the grid): each wave owns UA rows j of one expert slot
 //   (rank r < k of the route, or the shared expert) and computes
-//   h[slot][j] = silu(gate_j . x) * (up_j . x) for them; once the block's h
-//   stores have completed, the block makes one atomic arrival.
+//   h[slot][j] = silu(gate_j . x) * (up_j . x) for them. It stores each h as
+//   a 64-bit (value, tag) pair, where tag names the launch, and adds one
+//   arrival on the slot's counters right behind the stores. Nothing on the
+//   A side waits for its stores to land.
 //
-//   B blocks: a block owns ROWS_B output rows d; wave w covers half of them
-//   for a quarter of the k+1 slots. Each wave issues the shared slot's
-//   down-row loads and the shared-expert gate loads before routing and the
-//   routed down rows right after it, so they stream from HBM while A runs;
-//   wave 0 computes the shared-expert scalar gate sigmoid(se_g . x). After
-//   every A arrival the block stages all h (as bf16 hi/lo x-operands) in LDS,
-//   each wave forms its per-slot down products, and the block combines them
-//   per row in rank order:
+//   B blocks: a block owns ROWS_B output rows d; wave w owns slots w and
+//   w + 8 for all of them. Each wave issues the shared slot's down-row loads
+//   and the shared-expert gate loads before routing and the routed down rows
+//   right after it, so they stream from HBM while A runs; the last wave
+//   computes the shared-expert scalar gate sigmoid(se_g . x). Per slot, a wave waits
+//   for the slot's arrivals, reads the slot's h pairs until every tag is
+//   this launch's (an arrival can overtake the stores it counts), converts h
+//   to bf16 hi/lo x-operands and forms the down products of its rows. The
+//   block then combines them per row in rank order:
 //   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
 //
@@ -25,48 +28,54 @@
 // Progress: A blocks never wait on another block. Workgroups are dispatched in
 // ID order, and every A block precedes every B block, so a B block can only be
 // resident after all A blocks were dispatched: the waits always end. They are
-// also bounded: after kSpinLimit polls a B block stops waiting, raises the
-// sticky error word and finishes without writing its rows (the host can read
-// the word with logan_hip_moe_sync_errors()).
+// also bounded: after kSpinLimit polls a B wave stops waiting, raises the
+// sticky error word and its block finishes without writing its rows (the
+// host can read the word with logan_hip_moe_sync_errors(); results of later
+// launches are then not guaranteed either).
 //
-// Hand-off without L2 maintenance: h is written and read only with
-// device-scope (sc1) relaxed atomic stores/loads, which are coherent across
-// the XCDs' L2s; an A wave waits for its h stores to complete (s_waitcnt)
-// before its arrival atomic, and B reads h only after observing every
-// arrival. An agent-scope release/acquire fence would instead write back /
-// invalidate the whole L2 of each XCD per wave (buffer_wbl2 / buffer_inv),
-// which measured tens of microseconds per launch here.
+// Hand-off without L2 maintenance: h pairs, counters and the epoch are
+// written and read only with device-scope (sc1) relaxed atomics / loads,
+// which are coherent across the XCDs' L2s. Each launch's tag is derived from
+// the epoch word that the last B block of the previous launch advanced, so
+// pairs left by earlier launches never pass the tag check. An agent-scope
+// release/acquire fence would instead write back / invalidate the whole L2
+// of each XCD per wave (buffer_wbl2 / buffer_inv), which measured tens of
+// microseconds per launch here.
 //
-// The arrival and completion counters live in module-scope device memory
-// (zero when the code object loads). B blocks count their completion over
-// kDoneCtrs counters and then one top counter; the block that completes the
-// count puts every counter back to zero, so each
-// launch starts from zero without a memset. Launches of this kernel on one
-// device must therefore not overlap (one stream, or serialised streams).
+// The counters and the epoch live in module-scope device memory (zero when
+// the code object loads). B blocks count their completion over kDoneCtrs
+// counters and then one top counter; the block that completes the count
+// puts every counter back to zero and advances the epoch, so each launch
+// starts from zero without a memset. Launches of this kernel on one device
+// must therefore not overlap (one stream, or serialised streams).
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 
 namespace lh {
 
-// Arrivals are spread over kArrivalCtrs counters (A block b arrives on
-// counter b % kArrivalCtrs), each on its own 256-byte line: same-address
-// atomics serialise at the memory side (~40 ns each measured here), so one
-// shared counter for every arrival would take tens of microseconds. B waits
-// until each counter in use holds its expected count.
-constexpr int kArrivalCtrs = 64;
+constexpr int kFusedMaxSlots = 12;  // k + 1 (routed + shared)
+// Each slot's arrivals are spread over kSubCtrs counters (the i-th A block of
+// a slot arrives on counter i % kSubCtrs), each on its own 256-byte line:
+// same-address atomics serialise at the memory side (~40 ns each measured
+// here). B completion likewise goes over kDoneCtrs counters, then btop.
+constexpr int kSubCtrs = 4;
 constexpr int kLine = 64;  // u32 per 256-byte line
-constexpr int kDoneCtrs = 16;  // B completion: block b -> bctr[b % 16], then btop
+constexpr int kDoneCtrs = 16;
 struct FusedSync {
-  uint32_t ctr[kArrivalCtrs][kLine];
+  uint32_t ctr[kFusedMaxSlots][kSubCtrs][kLine];
   uint32_t bctr[kDoneCtrs][kLine];
   uint32_t btop[kLine];
+  uint32_t epoch[kLine];
   uint32_t error[kLine];
 };
 __device__ FusedSync g_fused_sync;
 
-constexpr int kFusedMaxSlots = 12;  // k + 1 (routed + shared)
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit data format
 constexpr int kCpolSc1 = 16;           // cache policy: device scope (sc1)
+// h pairs rotate over kSlices workspace slices (slice = epoch % kSlices), so
+// a line that an XCD's L2 still holds from an earlier launch is many launches
+// old; B reads pairs through L2 first and re-reads with sc1 on a stale tag.
+constexpr int kSlices = 16;
 typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr uint32_t kSpinLimit = 1u << 20;
 
@@ -205,45 +214,119 @@ struct FusedGeom {
   int slots;       // k + (shared ? 1 : 0)
   int wpr;         // A waves per routed slot
   int wps;         // A waves for the shared slot
-  int nA_waves;
   int nA_blocks;
   int nB_blocks;
-  int nctr;        // arrival counters in use
 };
 
-constexpr int kWaves = 8;   // waves per block (512 threads)
-constexpr int kQSlots = 3;  // slots per B wave (a quarter of kFusedMaxSlots)
+constexpr int kWaves = 8;  // waves per block (512 threads)
 
-// one slot's down-row chunk and its scale/bias
+// gate/up rows per A wave: fewer where a lane's weight registers would spill
+__host__ __device__ constexpr int fused_ua(int bits, int cpla) {
+  return (bits == 8 || (cpla == 2 && bits >= 5)) ? 2 : 4;
+}
+constexpr int kSlotsPerWave = (kFusedMaxSlots + kWaves - 1) / kWaves;  // B: slots w, w + 8
+
+// One down-row chunk and its raw scale/bias. Branch-free: a dead lane loads
+// row 0 / chunk 0 of the same expert, and its scale and bias are zeroed where
+// they are used, so the loads of all slots and passes stay in flight together.
 template <int BITS>
-__device__ __forceinline__ void load_down(uint32_t (&w)[BITS], float &sc, float &bi,
+__device__ __forceinline__ void load_down(uint32_t (&w)[BITS], uint32_t &scr, uint32_t &bir,
                                           const DevBank &bd, int e, int d, int lb, bool live) {
-  if (live) {
-    load_chunk<BITS>(w, bd.m.w + (size_t)e * bd.w_stride + (size_t)d * bd.m.row_bytes +
-                            (size_t)lb * (4 * BITS));
-    const size_t p = (size_t)e * bd.p_stride + (size_t)d * bd.m.ng + lb / (bd.m.gs >> 5);
-    sc = aux_to_f32(bd.m.sc[p], bd.m.fp16);
-    bi = aux_to_f32(bd.m.bi[p], bd.m.fp16);
-  } else {
+  const int dd = live ? d : 0, ll = live ? lb : 0;
+  load_chunk<BITS>(w, bd.m.w + (size_t)e * bd.w_stride + (size_t)dd * bd.m.row_bytes +
+                          (size_t)ll * (4 * BITS));
+  const size_t p = (size_t)e * bd.p_stride + (size_t)dd * bd.m.ng + ll / (bd.m.gs >> 5);
+  scr = bd.m.sc[p];
+  bir = bd.m.bi[p];
+}
+
+// sum_k code_k * h_k over one 32-code chunk (LSB-first BITS-bit codes)
+template <int BITS>
+__device__ __forceinline__ float codes_dot(const uint32_t (&w)[BITS], const float (&h)[32]) {
+  float a0 = 0.f, a1 = 0.f;
+  if constexpr (BITS == 4) {
 #pragma unroll
-    for (int q = 0; q < BITS; ++q) w[q] = 0;
-    sc = bi = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      // nibbles to bytes, then one v_cvt_f32_ubyteN per code (the empty asm
+      // keeps the compiler from folding the masks into per-code bfe's)
+      uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        a0 = fmaf((float)((lo >> (8 * b)) & 0xffu), h[8 * i + 2 * b], a0);
+        a1 = fmaf((float)((hi >> (8 * b)) & 0xffu), h[8 * i + 2 * b + 1], a1);
+      }
+    }
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a0 = fmaf((float)(w[i] & 0xffu), h[4 * i], a0);
+      a1 = fmaf((float)((w[i] >> 8) & 0xffu), h[4 * i + 1], a1);
+      a0 = fmaf((float)((w[i] >> 16) & 0xffu), h[4 * i + 2], a0);
+      a1 = fmaf((float)(w[i] >> 24), h[4 * i + 3], a1);
+    }
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const int bit = k * BITS, i = bit >> 5, sh = bit & 31;
+      uint32_t c = w[i] >> sh;
+      if (sh + BITS > 32) c |= w[i + 1] << (32 - sh);
+      if (k & 1)
+        a1 = fmaf((float)(c & mask), h[k], a1);
+      else
+        a0 = fmaf((float)(c & mask), h[k], a0);
+    }
   }
+  return a0 + a1;
+}
+
+// VPL consecutive (value, tag) pairs from byte offset off; positions at or
+// beyond n (n may be <= 0) read as 0 and are not checked. True when every
+// checked tag is `tag`.
+template <int VPL, int CPOL>
+__device__ __forceinline__ bool read_pairs(__amdgpu_buffer_rsrc_t rs, int off, int n,
+                                           uint32_t tag, float (&hv)[VPL]) {
+  bool ok = true;
+#pragma unroll
+  for (int v = 0; v < VPL / 2; ++v) {
+    const uint4 q =
+        __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * v, 0, CPOL));
+    ok = ok && (2 * v >= n || q.y == tag) && (2 * v + 1 >= n || q.w == tag);
+    hv[2 * v] = 2 * v < n ? __uint_as_float(q.x) : 0.f;
+    hv[2 * v + 1] = 2 * v + 1 < n ? __uint_as_float(q.z) : 0.f;
+  }
+  return ok;
+}
+
+// tag of this launch's h pairs: odd, so zeroed memory never passes
+__device__ __forceinline__ uint32_t launch_tag() {
+  return (ld_agent(&g_fused_sync.epoch[0]) << 1) | 1u;
+}
+
+// expected arrivals on sub-counter q of a slot with n A waves
+__device__ __forceinline__ uint32_t sub_need(int n, int q) {
+  return (uint32_t)(n / kSubCtrs + (q < n % kSubCtrs ? 1 : 0));
 }
 
 template <int BITS, int CPLA, int LANESB, int KPL>
 __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
-  constexpr int UA = BITS == 8 ? 2 : 4;      // rows of gate (and of up) per A wave
-  constexpr int ROWS_W = 64 / LANESB;        // output rows per B wave
-  constexpr int ROWS_B = 2 * ROWS_W;         // output rows per B block (2 row groups x 4 slot quarters)
-  constexpr int XDW = 36;                    // LDS dwords per (slot, chunk): 16 hi, 16 lo, xs, xsp
-  __shared__ __align__(16) uint32_t s_h[kFusedMaxSlots * LANESB * XDW];
+  constexpr int UA = fused_ua(BITS, CPLA);     // rows of gate (and of up) per A wave
+  constexpr int RPP = 64 / LANESB;            // B rows per pass of a wave
+  constexpr int PASSES = BITS == 8 ? 2 : 4;   // B passes (rows held per lane, per slot)
+  constexpr int ROWS_B = RPP * PASSES;        // output rows per B block
+  constexpr int VPL = LANESB / 2;             // h pairs per lane when reading a slot
+  __shared__ __align__(16) float s_hv[kWaves][32 * LANESB];
   __shared__ float s_y[ROWS_B][kFusedMaxSlots];
-  __shared__ uint32_t s_timeout;
+  __shared__ uint32_t s_to[kWaves];
+  __shared__ uint32_t s_sel[kFusedMaxSlots];  // route keys, computed once per block
+  __shared__ uint32_t s_left;                  // A: waves of the block still running
   __shared__ float s_gsig;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform for the compiler too, so per-slot bank selection and
+  // addressing stay scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint16_t *logits = reinterpret_cast<const uint16_t *>(a.logits);
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   const int C = a.D >> 5;
@@ -252,16 +335,15 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
 
   if ((int)blockIdx.x < g.nA_blocks) {
     // ------------------------------------------------------------ phase A
-    const int item_raw = blockIdx.x * kWaves + wave;
-    const bool active = item_raw < g.nA_waves;
-    const int item = active ? item_raw : g.nA_waves - 1;  // idle waves mirror a valid item
+    const int item = blockIdx.x * kWaves + wave;
     const bool shared = item >= g.k * g.wpr;
     const int slot = shared ? g.k : item / g.wpr;
     const int jb = shared ? item - g.k * g.wpr : item % g.wpr;
     const int rows = shared ? a.sinter : a.inter;
 
+    // every wave of an A block serves the same slot: wave 0 routes for all
     uint32_t key[KPL];
-    if (!shared) route_keys<KPL>(logits, a.E, key);
+    if (!shared && wave == 0) route_keys<KPL>(logits, a.E, key);
     // x does not depend on the route: in flight together with the logits
     uint4 xq[CPLA][4];
 #pragma unroll
@@ -271,15 +353,17 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
 #pragma unroll
       for (int v = 0; v < 4; ++v) xq[i][v] = src[v];
     }
-    int e = 0;
-    if (!shared) {
+    if (threadIdx.x == 0) s_left = kWaves;
+    if (!shared && wave == 0) {
       uint32_t sel[kFusedMaxSlots];
       route_select<KPL>(key, a.E, slot + 1, sel);
       uint32_t mine = sel[0];
 #pragma unroll
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
-      e = sel_expert(mine);
+      if (lane == 0) s_sel[0] = mine;
     }
+    __syncthreads();
+    const int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
     const DevBank &bgk = shared ? a.sgate : a.gate;
     const DevBank &buk = shared ? a.sup : a.up;
     const uint8_t *gw = bgk.m.w + (size_t)e * bgk.w_stride;
@@ -291,36 +375,31 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     const int j0 = jb * UA;
     const int gsc_chunks = bgk.m.gs >> 5;
 
+    // branch-free loads (clamped row / chunk; dead lanes get zero scale and
+    // bias where they are used)
     uint32_t wg[UA][CPLA][BITS], wu[UA][CPLA][BITS];
+    uint32_t rsg[UA][CPLA], rbg[UA][CPLA], rsu[UA][CPLA], rbu[UA][CPLA];
 #pragma unroll
     for (int u = 0; u < UA; ++u)
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
-        const int j = j0 + u, c = lane + 64 * i;
-        if (j < rows && c < C) {
-          load_chunk<BITS>(wg[u][i], gw + (size_t)j * bgk.m.row_bytes + (size_t)c * (4 * BITS));
-          load_chunk<BITS>(wu[u][i], uw + (size_t)j * buk.m.row_bytes + (size_t)c * (4 * BITS));
-        } else {
-#pragma unroll
-          for (int t = 0; t < BITS; ++t) wg[u][i][t] = wu[u][i][t] = 0;
-        }
+        const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+        load_chunk<BITS>(wg[u][i], gw + (size_t)j * bgk.m.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS>(wu[u][i], uw + (size_t)j * buk.m.row_bytes + (size_t)c * (4 * BITS));
       }
-    float sg[UA][CPLA], bg[UA][CPLA], su[UA][CPLA], bu[UA][CPLA];
 #pragma unroll
     for (int u = 0; u < UA; ++u)
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
-        const int j = j0 + u, c = lane + 64 * i;
-        if (j < rows && c < C) {
-          const size_t p = (size_t)j * bgk.m.ng + c / gsc_chunks;
-          sg[u][i] = aux_to_f32(gsc[p], bgk.m.fp16);
-          bg[u][i] = aux_to_f32(gbi[p], bgk.m.fp16);
-          su[u][i] = aux_to_f32(usc[p], buk.m.fp16);
-          bu[u][i] = aux_to_f32(ubi[p], buk.m.fp16);
-        } else {
-          sg[u][i] = bg[u][i] = su[u][i] = bu[u][i] = 0.f;
-        }
+        const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+        const size_t p = (size_t)j * bgk.m.ng + c / gsc_chunks;
+        rsg[u][i] = gsc[p];
+        rbg[u][i] = gbi[p];
+        rsu[u][i] = usc[p];
+        rbu[u][i] = ubi[p];
       }
+    // this launch's tag, loaded behind the weights (it is needed only at the end)
+    const uint32_t tag = launch_tag();
     float pg[UA], pu[UA];
 #pragma unroll
     for (int u = 0; u < UA; ++u) pg[u] = pu[u] = 0.f;
@@ -341,11 +420,16 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       make_xchunk_bf16<BITS>(xc, xb);
 #pragma unroll
       for (int u = 0; u < UA; ++u) {
+        const bool live = j0 + u < rows && c < C;
+        const float sg = live ? aux_to_f32(rsg[u][i], bgk.m.fp16) : 0.f;
+        const float bg = live ? aux_to_f32(rbg[u][i], bgk.m.fp16) : 0.f;
+        const float su = live ? aux_to_f32(rsu[u][i], buk.m.fp16) : 0.f;
+        const float bu = live ? aux_to_f32(rbu[u][i], buk.m.fp16) : 0.f;
         uint32_t q[16];
         unpack_chunk<BITS>(q, wg[u][i], kc);
-        pg[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), sg[u][i], bg[u][i], xc.xs, xc.xsp);
+        pg[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), sg, bg, xc.xs, xc.xsp);
         unpack_chunk<BITS>(q, wu[u][i], kc);
-        pu[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), su[u][i], bu[u][i], xc.xs, xc.xsp);
+        pu[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), su, bu, xc.xs, xc.xsp);
       }
     }
     float hv[UA];
@@ -355,48 +439,84 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       const float uv = wave_sum_f32(pu[u]);
       hv[u] = silu(gv) * uv;  // logan-qwen4/src/lib.rs:8807-8809
     }
-    float *hrow = reinterpret_cast<float *>(a.ws) + (size_t)slot * hmax;
-    if (active && lane < UA && j0 + lane < rows) {
+    const int slice = (int)((tag >> 1) % kSlices);
+    uint64_t *hrow = reinterpret_cast<uint64_t *>(a.ws) + ((size_t)slice * g.slots + slot) * hmax;
+    if (lane < UA && j0 + lane < rows) {
       float v = hv[0];
 #pragma unroll
       for (int u = 1; u < UA; ++u) v = lane == u ? hv[u] : v;
-      __hip_atomic_store(&hrow[j0 + lane], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t pr = ((uint64_t)tag << 32) | __float_as_uint(v);
+      __hip_atomic_store(&hrow[j0 + lane], pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // h stores complete before the arrival
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(&g_fused_sync.ctr[blockIdx.x % kArrivalCtrs][0], 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    // The block's last wave to get here adds the block's arrival, right
+    // behind the stores and without waiting for them (B checks the tags).
+    if (lane == 0 && atomicSub(&s_left, 1u) == 1u) {
+      const int first = shared ? g.k * g.wpr / kWaves : slot * (g.wpr / kWaves);
+      __hip_atomic_fetch_add(&g_fused_sync.ctr[slot][(blockIdx.x - first) % kSubCtrs][0], 1u,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
 
   // -------------------------------------------------------------- phase B
-  // wave w: row group w % 2 (ROWS_W rows), slot quarter w / 2
+  // lane: chunk lb of row rsub within each pass; wave: slots wave, wave + 8
   const int bb = blockIdx.x - g.nA_blocks;
-  const int lb = lane % LANESB;  // chunk of a down row
-  const int rloc = (wave & 1) * ROWS_W + lane / LANESB;
-  const int d = bb * ROWS_B + rloc;
-  const bool drow = d < a.D;
-  const int sq = wave >> 1;
-  const int s_lo = (g.slots * sq) / 4;
-  const int s_hi = (g.slots * (sq + 1)) / 4;
+  const int lb = lane % LANESB;
+  const int rsub = lane / LANESB;
+  const int d0 = bb * ROWS_B;
   const bool has_shared = a.sdown.m.w != nullptr;
 
+  // wave 0 routes for the block
   uint32_t key[KPL];
-  route_keys<KPL>(logits, a.E, key);
+  if (wave == 0) route_keys<KPL>(logits, a.E, key);
 
-  // route-independent loads first: the shared slot's down rows, x and se_g
-  uint32_t wv[kQSlots][BITS];
-  float sc[kQSlots], bi[kQSlots];
+  // route-independent loads first: the shared slot's down rows
+  uint32_t wv[kSlotsPerWave][PASSES][BITS];
+  uint32_t rsc[kSlotsPerWave][PASSES], rbi[kSlotsPerWave][PASSES];
 #pragma unroll
-  for (int t = 0; t < kQSlots; ++t) {
-    const int s = s_lo + t;
-    const bool live = has_shared && s == g.k && s < s_hi && drow && lb < (a.sinter >> 5);
-    load_down<BITS>(wv[t], sc[t], bi[t], a.sdown, 0, d, lb, live);
+  for (int t = 0; t < kSlotsPerWave; ++t) {
+    const int s = wave + t * kWaves;
+    if (has_shared && s == g.k) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int d = d0 + p * RPP + rsub;
+        const bool live = d < a.D && lb < (a.sinter >> 5);
+        load_down<BITS>(wv[t][p], rsc[t][p], rbi[t][p], a.sdown, 0, d, lb, live);
+      }
+    }
   }
+  if (wave == 0) {
+    uint32_t sel0[kFusedMaxSlots];
+    route_select<KPL>(key, a.E, g.k, sel0);
+    uint32_t mine = 0;
+#pragma unroll
+    for (int r = 0; r < kFusedMaxSlots; ++r) mine = lane == r ? sel0[r] : mine;
+    if (lane < kFusedMaxSlots) s_sel[lane] = mine;
+  }
+  __syncthreads();
+  uint32_t sel[kFusedMaxSlots];
+#pragma unroll
+  for (int r = 0; r < kFusedMaxSlots; ++r) sel[r] = __builtin_amdgcn_readfirstlane(s_sel[r]);
+#pragma unroll
+  for (int t = 0; t < kSlotsPerWave; ++t) {
+    const int s = wave + t * kWaves;
+    if (s < g.k) {
+      uint32_t kk = sel[0];
+#pragma unroll
+      for (int r = 1; r < kFusedMaxSlots; ++r) kk = r == s ? sel[r] : kk;
+      const int e = sel_expert(kk);
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int d = d0 + p * RPP + rsub;
+        const bool live = d < a.D && lb < (a.inter >> 5);
+        load_down<BITS>(wv[t][p], rsc[t][p], rbi[t][p], a.down, e, d, lb, live);
+      }
+    }
+  }
+  // shared-expert gate loads after the down rows, by the last wave (one slot
+  // fewer than wave 0 when slots > kWaves)
   uint4 gq[CPLA][4], xq[CPLA][4];
-  const bool do_gate = wave == 0 && has_shared && a.se_gate_vec;
+  const bool do_gate = wave == kWaves - 1 && has_shared && a.se_gate_vec;
   if (do_gate) {
 #pragma unroll
     for (int i = 0; i < CPLA; ++i) {
@@ -410,21 +530,9 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       }
     }
   }
-  uint32_t sel[kFusedMaxSlots];
-  route_select<KPL>(key, a.E, g.k, sel);
-#pragma unroll
-  for (int t = 0; t < kQSlots; ++t) {
-    const int s = s_lo + t;
-    if (s < g.k) {
-      uint32_t kk = sel[0];
-#pragma unroll
-      for (int r = 1; r < kFusedMaxSlots; ++r) kk = r == s ? sel[r] : kk;
-      const bool live = s < s_hi && drow && lb < (a.inter >> 5);
-      load_down<BITS>(wv[t], sc[t], bi[t], a.down, sel_expert(kk), d, lb, live);
-    }
-  }
+  const uint32_t tag = launch_tag();
   // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604)
-  if (wave == 0) {
+  if (wave == kWaves - 1) {
     float gsig = 1.0f;
     if (do_gate) {
       float gd = 0.f;
@@ -446,93 +554,134 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     if (lane == 0) s_gsig = gsig;
   }
 
-  // wait until every arrival counter in use holds its expected count
-  if (wave == 0) {
-    uint32_t spins = 0, to = 0;
-    const int need = lane < g.nctr
-                         ? g.nA_blocks / kArrivalCtrs + (lane < g.nA_blocks % kArrivalCtrs ? 1 : 0)
-                         : 0;
-    bool done = lane >= g.nctr || ld_agent(&g_fused_sync.ctr[lane][0]) == (uint32_t)need;
+  // Wait for the arrivals of this wave's slots (lane 4 t + q polls
+  // sub-counter q of slot wave + 8 t), read their tagged h together until
+  // every tag is this launch's, then form the down products slot by slot.
+  static_assert(kSlotsPerWave * kSubCtrs <= 64, "one poll lane per sub-counter");
+  uint32_t to = 0;
+  {
+    const int t = lane / kSubCtrs, q = lane % kSubCtrs;
+    const int s = wave + t * kWaves;
+    const bool mine = t < kSlotsPerWave && s < g.slots;
+    const int nb = ((has_shared && s == g.k) ? g.wps : g.wpr) / kWaves;  // A blocks of slot s
+    const uint32_t need = mine ? sub_need(nb, q) : 0u;
+    uint32_t *cp = &g_fused_sync.ctr[mine ? s : 0][q][0];
+    bool done = !mine || ld_agent(cp) >= need;
+    uint32_t spins = 0;
     while (!__all(done)) {
       __builtin_amdgcn_s_sleep(2);
-      if (!done) done = ld_agent(&g_fused_sync.ctr[lane][0]) == (uint32_t)need;
+      if (!done) done = ld_agent(cp) >= need;
       if (++spins > kSpinLimit) {
         to = 1;
-        if (lane == 0)
-          __hip_atomic_fetch_or(&g_fused_sync.error[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
-    if (lane == 0) s_timeout = to;
   }
-  __syncthreads();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-
-  // stage h of every slot as x-operands in LDS
-  {
-    const int CI = hmax >> 5;
-    const int items = g.slots * LANESB;
-    const __amdgpu_buffer_rsrc_t hrsrc = __builtin_amdgcn_make_buffer_rsrc(
-        a.ws, (short)0, g.slots * hmax * 4, kBufWord3);
-    for (int it = threadIdx.x; it < items; it += kWaves * 64) {
-      const int s = it / LANESB, c = it % LANESB;
-      const int K = (has_shared && s == g.k) ? a.sinter : a.inter;
+  // lane covers h[VPL*lane .. VPL*lane + VPL) of each slot: first through
+  // L2, then (stale or not yet landed) with device-scope loads
+  const int slice = (int)((tag >> 1) % kSlices);
+  const __amdgpu_buffer_rsrc_t hrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws, (short)0, kSlices * g.slots * hmax * 8, kBufWord3);
+  float hv[kSlotsPerWave][VPL];
+  bool ok = true;
+  if (!to) {
+#pragma unroll
+    for (int t = 0; t < kSlotsPerWave; ++t) {
+      const int s = wave + t * kWaves;
+      const int K = s < g.slots ? ((has_shared && s == g.k) ? a.sinter : a.inter) : 0;
+      const int off = ((slice * g.slots + (s < g.slots ? s : 0)) * hmax + VPL * lane) * 8;
+      ok = read_pairs<VPL, 0>(hrsrc, off, K - VPL * lane, tag, hv[t]) && ok;
+    }
+  }
+  for (uint32_t spins = 0; !to && !__all(ok);) {
+    __builtin_amdgcn_s_sleep(1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (++spins > kSpinLimit) {
+      to = 1;
+      break;
+    }
+    ok = true;
+#pragma unroll
+    for (int t = 0; t < kSlotsPerWave; ++t) {
+      const int s = wave + t * kWaves;
+      const int K = s < g.slots ? ((has_shared && s == g.k) ? a.sinter : a.inter) : 0;
+      const int off = ((slice * g.slots + (s < g.slots ? s : 0)) * hmax + VPL * lane) * 8;
+      ok = read_pairs<VPL, kCpolSc1>(hrsrc, off, K - VPL * lane, tag, hv[t]) && ok;
+    }
+  }
+  if (to && lane == 0)
+    __hip_atomic_fetch_or(&g_fused_sync.error[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int t = 0; t < kSlotsPerWave; ++t) {
+    const int s = wave + t * kWaves;
+    if (s < g.slots && !to) {
+      const bool sh = has_shared && s == g.k;
+      const int K = sh ? a.sinter : a.inter;
+      // through this wave's LDS row to chunk-per-lane (h of chunk lb)
+      float *row = s_hv[wave];
+#pragma unroll
+      for (int v = 0; v < VPL; v += 4)
+        *reinterpret_cast<float4 *>(row + VPL * lane + v) =
+            make_float4(hv[t][v], hv[t][v + 1], hv[t][v + 2], hv[t][v + 3]);
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
       float xf[32];
-      if (c < (K >> 5) && c < CI) {
-        // device-scope (sc1) 16-byte loads: coherent with A's sc1 stores
-        const int off = (s * hmax + 32 * c) * 4;
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float4v t = __builtin_bit_cast(
-              float4v, __builtin_amdgcn_raw_buffer_load_b128(hrsrc, off + 16 * v, 0, kCpolSc1));
-          xf[4 * v + 0] = t.x; xf[4 * v + 1] = t.y; xf[4 * v + 2] = t.z; xf[4 * v + 3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) xf[v] = 0.f;
+      for (int v = 0; v < 32; v += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(row + 32 * lb + v);
+        xf[v] = f.x; xf[v + 1] = f.y; xf[v + 2] = f.z; xf[v + 3] = f.w;
       }
-      XChunk xh, xl;
-      make_xchunk_f32<BITS>(xh, xl, xf);
-      uint32_t *dst = s_h + (size_t)it * XDW;
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      float xs = 0.f;
 #pragma unroll
-      for (int p = 0; p < 16; ++p) {
-        dst[p] = xh.p[p];
-        dst[16 + p] = xl.p[p];
+      for (int v = 0; v < 32; ++v) xs += xf[v];
+      const DevBank &bd = sh ? a.sdown : a.down;
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const bool live = d0 + p * RPP + rsub < a.D && lb < (K >> 5);
+        const float sc = live ? aux_to_f32(rsc[t][p], bd.m.fp16) : 0.f;
+        const float bi = live ? aux_to_f32(rbi[t][p], bd.m.fp16) : 0.f;
+        // sum_k (code_k * sc + bi) * h_k = sc * sum_k code_k h_k + bi * sum_k h_k
+        float v = fmaf(sc, codes_dot<BITS>(wv[t][p], xf), bi * xs);
+        v = group_sum_f32<LANESB>(v);
+        if (lb == 0) s_y[p * RPP + rsub][s] = v;
       }
-      dst[32] = __float_as_uint(xh.xs);
-      dst[33] = __float_as_uint(xh.xsp);
     }
   }
+  if (lane == 0) s_to[wave] = to;
   __syncthreads();
 
-#pragma unroll
-  for (int t = 0; t < kQSlots; ++t) {
-    const int s = s_lo + t;
-    if (s < s_hi) {
-      const uint32_t *src = s_h + (size_t)(s * LANESB + lb) * XDW;
-      uint32_t hp[16], lp[16];
-#pragma unroll
-      for (int p = 0; p < 16; p += 4) {
-        const uint4 t0 = *reinterpret_cast<const uint4 *>(src + p);
-        const uint4 t1 = *reinterpret_cast<const uint4 *>(src + 16 + p);
-        hp[p] = t0.x; hp[p + 1] = t0.y; hp[p + 2] = t0.z; hp[p + 3] = t0.w;
-        lp[p] = t1.x; lp[p + 1] = t1.y; lp[p + 2] = t1.z; lp[p + 3] = t1.w;
+  // Completion, counted as soon as every wave of the block has read its h
+  // (counters and pairs are no longer needed): the block completing the
+  // two-level count resets every counter and advances the epoch.
+  if (threadIdx.x == 64) {  // a thread outside the combine below
+    const int nb = g.nB_blocks;
+    const int c = bb % kDoneCtrs;
+    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
+    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (uint32_t)needc - 1) {
+      const uint32_t top =
+          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (top == (uint32_t)nbc - 1) {
+        for (int s = 0; s < kFusedMaxSlots; ++s)
+          for (int q = 0; q < kSubCtrs; ++q) st_agent(&g_fused_sync.ctr[s][q][0], 0u);
+        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
+        st_agent(&g_fused_sync.btop[0], 0u);
+        st_agent(&g_fused_sync.epoch[0], ld_agent(&g_fused_sync.epoch[0]) + 1u);
       }
-      const float xs = __uint_as_float(src[32]), xsp = __uint_as_float(src[33]);
-      uint32_t q[16];
-      unpack_chunk<BITS>(q, wv[t], kc);
-      const float acc = pairs_dot(q, hp) + pairs_dot(q, lp);
-      float v = chunk_fold<BITS>(acc, sc[t], bi[t], xs, xsp);
-      v = group_sum_f32<LANESB>(v);
-      if (lb == 0) s_y[rloc][s] = v;
     }
   }
-  __syncthreads();
 
   // rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711) by the first ROWS_B threads
   if ((int)threadIdx.x < ROWS_B) {
     const int r = threadIdx.x;
-    const int dd = bb * ROWS_B + r;
+    const int dd = d0 + r;
+    uint32_t anyto = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) anyto |= s_to[w];
     float wr[kFusedMaxSlots];
     const float l0 = sel_logit(sel[0]);
     float wsum = 0.f;
@@ -550,7 +699,7 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       if (q < g.k) acc = fmaf(s_y[r][q], wr[q] / wsum, acc);
     float o = acc;
     if (has_shared) o = fmaf(s_y[r][g.k], s_gsig, acc);
-    if (dd < a.D && !s_timeout) {
+    if (dd < a.D && !anyto) {
       if (a.out_f32)
         reinterpret_cast<float *>(a.out)[dd] = o;
       else
@@ -564,32 +713,13 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     }
   }
 
-  // completion: the last B block (two-level count) resets every counter
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int nb = g.nB_blocks;
-    const int c = bb % kDoneCtrs;
-    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
-    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
-    const uint32_t prev =
-        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (uint32_t)needc - 1) {
-      const uint32_t top =
-          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (top == (uint32_t)nbc - 1) {
-        for (int q = 0; q < kArrivalCtrs; ++q) st_agent(&g_fused_sync.ctr[q][0], 0u);
-        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
-        st_agent(&g_fused_sync.btop[0], 0u);
-      }
-    }
-  }
 }
 
 // ---------------------------------------------------------------- launch
 
 size_t moe_fused_workspace_bytes(int slots, int inter, int sinter) {
   const size_t hmax = (size_t)(inter > sinter ? inter : sinter);
-  return (size_t)slots * hmax * sizeof(float);
+  return (size_t)kSlices * slots * hmax * sizeof(uint64_t);  // (value, tag) pairs
 }
 
 template <int BITS, int CPLA, int LANESB, int KPL>
@@ -624,7 +754,7 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   if (a.ws_bytes < moe_fused_workspace_bytes(slots, a.inter, a.sinter)) return 0;
   if ((reinterpret_cast<uintptr_t>(a.ws) & 15) != 0 || (hmax & 3) != 0) return 0;
-  const int UA = a.gate.m.bits == 8 ? 2 : 4;
+  const int UA = fused_ua(a.gate.m.bits, (a.D >> 5) <= 64 ? 1 : 2);
   if (a.se_gate_vec && (reinterpret_cast<uintptr_t>(a.se_gate_vec) & 15) != 0) return 0;
   if ((reinterpret_cast<uintptr_t>(a.x) & 15) != 0) return 0;
   FusedGeom g;
@@ -632,12 +762,12 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   g.slots = slots;
   g.wpr = (a.inter + UA - 1) / UA;
   g.wps = a.sdown.m.w ? (a.sinter + UA - 1) / UA : 0;
-  g.nA_waves = g.k * g.wpr + g.wps;
-  g.nA_blocks = (g.nA_waves + kWaves - 1) / kWaves;
-  g.nctr = g.nA_blocks < kArrivalCtrs ? g.nA_blocks : kArrivalCtrs;
+  // whole A blocks per slot (inter and sinter are multiples of 32)
+  if (g.wpr % kWaves != 0 || g.wps % kWaves != 0) return 0;
+  g.nA_blocks = (g.k * g.wpr + g.wps) / kWaves;
   const int Ci = hmax >> 5;
   const int lanesb = Ci <= 16 ? 16 : 32;
-  const int rows_per_block = 2 * (64 / lanesb);
+  const int rows_per_block = (64 / lanesb) * (a.gate.m.bits == 8 ? 2 : 4);
   g.nB_blocks = (a.D + rows_per_block - 1) / rows_per_block;
   switch (a.gate.m.bits) {
     case 4: return fused_bits<4>(a, g, st);
@@ -654,7 +784,8 @@ uint32_t moe_fused_sync_errors() {
       hipSuccess)
     return 0xffffffffu;
   uint32_t busy = 0, bbusy = s.btop[0];
-  for (int c = 0; c < kArrivalCtrs; ++c) busy |= s.ctr[c][0];
+  for (int c = 0; c < kFusedMaxSlots; ++c)
+    for (int q = 0; q < kSubCtrs; ++q) busy |= s.ctr[c][q][0];
   for (int c = 0; c < kDoneCtrs; ++c) bbusy |= s.bctr[c][0];
   return s.error[0] | (busy ? 2u : 0u) | (bbusy ? 4u : 0u);
 }
