@@ -62,6 +62,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (5 times), to calibrate "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes, then exit")
     return ap.parse_args()
 
 
@@ -174,6 +177,16 @@ def bench_gemv(torch, device, synth, args):
     return dict(us_per_launch=us, gbps=gbps, launches=launches)
 
 
+def measured_traffic():
+    """HBM bytes per fused-MoE launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy of known
+    size), or None when the summary is absent."""
+    f = ROOT / "profiles" / "moe_fused_b1_config3_traffic.json"
+    if not f.exists():
+        return None
+    return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+
+
 def cpu_baseline(torch, layer, seconds):
     """The oracle (single thread) on tokens of layer 0 until `seconds` pass."""
     import numpy as np
@@ -222,6 +235,15 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     assert backend.hip_init(), "logan-hip failed to initialise"
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src = torch.ones(n // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_mib} MiB x 5")
+        return
     moe = bench_moe(torch, device, synth, args)
     gemv = None if args.no_gemv else bench_gemv(torch, device, synth, args)
     cpu = None
@@ -254,9 +276,11 @@ def main():
         "us_per_token_layer": round(moe["layer_us"], 3),
         "roofline": {
             "bound": "hbm", "achieved": round(moe["gbps"], 2), "peak": PEAK_GBPS, "unit": "GB/s",
-            "frac": round(moe["gbps"] / PEAK_GBPS, 4), "traffic": None,
-            "kernel": "moe_block B=1 (route/group + gate-up + down + combine launches), "
-                      f"{LAYER_BYTES_B1} algorithmic B per layer over the event-timed layer time",
+            "frac": round(moe["gbps"] / PEAK_GBPS, 4), "traffic": measured_traffic(),
+            "kernel": "moe_fused_b1_kernel: one launch per layer (routing, gate/up + SwiGLU, "
+                      "down, rank-ordered combine, shared expert); "
+                      f"{LAYER_BYTES_B1} algorithmic B per launch over the event-timed "
+                      "average launch interval",
         },
         "cpu_baseline": cpu,
     }
