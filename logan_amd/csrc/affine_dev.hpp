@@ -301,11 +301,49 @@ __device__ __forceinline__ void load_chunk(uint32_t (&w)[BITS], const uint8_t *p
 }
 
 // Sum over `WIDTH` consecutive lanes (WIDTH a power of two <= 64).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_src_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xF, false));
+}
+
+// Sum over each aligned group of WIDTH lanes (16, 32 or 64), returned in
+// every lane of the group. DPP within 16-lane rows (quad xor 1, xor 2, row
+// rotate 4, 8), then row broadcasts across rows and readlane, instead of
+// LDS-routed shuffles. Callers keep every lane of the wave active.
 template <int WIDTH>
 __device__ __forceinline__ float team_sum(float v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
-  return v;
+  static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "team width");
+  v += dpp_src_f32<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_src_f32<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_src_f32<0x124, 0xF>(v);  // row_ror 4
+  v += dpp_src_f32<0x128, 0xF>(v);  // row_ror 8: every lane holds its row's sum
+  if constexpr (WIDTH == 16) return v;
+  v += dpp_src_f32<0x142, 0xA>(v);  // row_bcast 15: rows 1, 3 += rows 0, 2
+  if constexpr (WIDTH == 32) {
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (threadIdx.x & 32) ? hi : lo;
+  }
+  v += dpp_src_f32<0x143, 0xC>(v);  // row_bcast 31: row 3 += rows 0 + 1
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sums four values over all 64 lanes of a wave at once. On return every
+// lane of 16-lane row r (r = lane / 16) holds the wave total of the r-th
+// argument. permlane32_swap exchanges the wave halves (a with c, b with d),
+// permlane16_swap the odd and even rows, then four DPP steps finish each row.
+__device__ __forceinline__ float wave_reduce4(float a, float b, float c, float d) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(c), false, false);
+  const float s1 = __uint_as_float(p[0]) + __uint_as_float(p[1]);  // rows 0-1: a, rows 2-3: c
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(b), __float_as_uint(d), false, false);
+  const float s2 = __uint_as_float(q[0]) + __uint_as_float(q[1]);  // rows 0-1: b, rows 2-3: d
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s1), __float_as_uint(s2), false, false);
+  float t = __uint_as_float(r[0]) + __uint_as_float(r[1]);  // row 0: a, 1: b, 2: c, 3: d
+  t += dpp_src_f32<0xB1, 0xF>(t);
+  t += dpp_src_f32<0x4E, 0xF>(t);
+  t += dpp_src_f32<0x124, 0xF>(t);
+  t += dpp_src_f32<0x128, 0xF>(t);
+  return t;
 }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }

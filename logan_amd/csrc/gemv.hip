@@ -25,6 +25,7 @@ struct GemvParams {
   void *y;
   long long row_bytes;
   int I, O, ng, gsc;  // gsc = chunks per group
+  int gsc_shift;      // log2(gsc) when gsc is a power of two, else -1
   int fp16, x_stride, M, y_stride, y_bf16;
 };
 
@@ -44,74 +45,87 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
   kc.init();
   __shared__ float s_part[SPLIT > 1 ? TEAMS * U * MT : 1];
 
+  // Loads are branch-free (row and chunk clamped into the matrix, x rows
+  // clamped to M) and issued x first, then every weight chunk, then the raw
+  // scale/bias words, so they are all in flight together; the values of
+  // dead lanes are masked where they are used. In-order vmcnt lets the x
+  // conversion wait for the x loads alone.
   int gidx[CPL];
   bool cval[CPL];
+  int cc[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = cbase + lane + LANES * j;
     cval[j] = c < C;
-    gidx[j] = c / a.gsc;
+    cc[j] = cval[j] ? c : C - 1;
+    gidx[j] = a.gsc_shift >= 0 ? cc[j] >> a.gsc_shift : cc[j] / a.gsc;
   }
 
-  XChunk xc[MT][CPL];
+  uint4 xr[MT][CPL][4];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
+    const int mm = m < a.M ? m : a.M - 1;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = cbase + lane + LANES * j;
-      uint32_t xb[32];
-      if (cval[j] && m < a.M) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)m * a.x_stride + 32 * c);
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)mm * a.x_stride + 32 * cc[j]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const uint4 t = src[v];
-          xb[8 * v + 0] = t.x & 0xffffu; xb[8 * v + 1] = t.x >> 16;
-          xb[8 * v + 2] = t.y & 0xffffu; xb[8 * v + 3] = t.y >> 16;
-          xb[8 * v + 4] = t.z & 0xffffu; xb[8 * v + 5] = t.z >> 16;
-          xb[8 * v + 6] = t.w & 0xffffu; xb[8 * v + 7] = t.w >> 16;
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) xb[v] = 0;
-      }
-      make_xchunk_bf16<BITS>(xc[m][j], xb);
+      for (int v = 0; v < 4; ++v) xr[m][j][v] = src[v];
     }
   }
 
-  const int rows_per_block = ROWTEAMS * U;
-  for (int base = blockIdx.x * rows_per_block; base < a.O; base += gridDim.x * rows_per_block) {
-    const int r0 = base + rteam * U;
+  // the grid covers O exactly once: block b owns rows [b*ROWTEAMS*U, ...)
+  {
+    const int r0 = blockIdx.x * (ROWTEAMS * U) + rteam * U;
     uint32_t wv[U][CPL][BITS];
+    uint32_t scr[U][CPL], bir[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = min(r0 + u, a.O - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = min(r0 + u, a.O - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const size_t pi = (size_t)row * a.ng + gidx[j];
+        scr[u][j] = a.sc[pi];
+        bir[u][j] = a.bi[pi];
+      }
+    }
+    // keep every load above issued before any of their consumers
+    __builtin_amdgcn_sched_barrier(0);
+    XChunk xc[MT][CPL];
+    {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const bool ok = cval[j] && m < a.M;
+          uint32_t xb[32];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const uint4 t = xr[m][j][v];
+            xb[8 * v + 0] = ok ? t.x & 0xffffu : 0u; xb[8 * v + 1] = ok ? t.x >> 16 : 0u;
+            xb[8 * v + 2] = ok ? t.y & 0xffffu : 0u; xb[8 * v + 3] = ok ? t.y >> 16 : 0u;
+            xb[8 * v + 4] = ok ? t.z & 0xffffu : 0u; xb[8 * v + 5] = ok ? t.z >> 16 : 0u;
+            xb[8 * v + 6] = ok ? t.w & 0xffffu : 0u; xb[8 * v + 7] = ok ? t.w >> 16 : 0u;
+          }
+          make_xchunk_bf16<BITS>(xc[m][j], xb);
+        }
+      }
+    }
     float scv[U][CPL], biv[U][CPL];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = r0 + u;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        const int c = cbase + lane + LANES * j;
-        if (row < a.O && cval[j]) {
-          load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)c * (4 * BITS));
-        } else {
-#pragma unroll
-          for (int t = 0; t < BITS; ++t) wv[u][j][t] = 0;
-        }
+        const bool live = r0 + u < a.O && cval[j];
+        scv[u][j] = live ? aux_to_f32(scr[u][j], a.fp16) : 0.f;
+        biv[u][j] = live ? aux_to_f32(bir[u][j], a.fp16) : 0.f;
       }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = r0 + u;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        if (row < a.O && cval[j]) {
-          const size_t pi = (size_t)row * a.ng + gidx[j];
-          scv[u][j] = aux_to_f32(a.sc[pi], a.fp16);
-          biv[u][j] = aux_to_f32(a.bi[pi], a.fp16);
-        } else {
-          scv[u][j] = 0.f;
-          biv[u][j] = 0.f;
-        }
-      }
-    }
     float part[U][MT];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -130,44 +144,71 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
         }
       }
     }
-    float tot[U][MT];
+    if constexpr (LANES == 64 && SPLIT == 1 && U * MT >= 2) {
+      // four (row, token) sums per wave_reduce4; row r of lanes gets value r
+      constexpr int NV = U * MT;
+      float vals[NV];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int m = 0; m < MT; ++m) tot[u][m] = team_sum<LANES>(part[u][m]);
-    if constexpr (SPLIT > 1) {
-      if (lane == 0) {
+        for (int m = 0; m < MT; ++m) vals[u * MT + m] = part[u][m];
+      const int rr = lane >> 4;
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int m = 0; m < MT; ++m) s_part[(team * U + u) * MT + m] = tot[u][m];
-      }
-      __syncthreads();
-      if (seg == 0 && lane == 0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int m = 0; m < MT; ++m) {
-            float v = tot[u][m];
-#pragma unroll
-            for (int s = 1; s < SPLIT; ++s) v += s_part[((team + s) * U + u) * MT + m];
-            tot[u][m] = v;
-          }
-      }
-      __syncthreads();
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = r0 + u;
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float v = tot[u][m];
-        if (seg == 0 && lane == 0 && row < a.O && m < a.M) {
+      for (int g0 = 0; g0 < NV; g0 += 4) {
+        const float t = wave_reduce4(vals[g0], g0 + 1 < NV ? vals[g0 + 1] : 0.f,
+                                     g0 + 2 < NV ? vals[g0 + 2] : 0.f,
+                                     g0 + 3 < NV ? vals[g0 + 3] : 0.f);
+        const int idx = g0 + rr;
+        const int u = idx / MT, m = idx % MT;
+        const int row = r0 + u;
+        if ((lane & 15) == 0 && idx < NV && row < a.O && m < a.M) {
           if (a.y_bf16)
             reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
-                (uint16_t)f32_to_bf16_rne(v);
+                (uint16_t)f32_to_bf16_rne(t);
           else
-            reinterpret_cast<float *>(a.y)[(size_t)m * a.y_stride + row] = v;
+            reinterpret_cast<float *>(a.y)[(size_t)m * a.y_stride + row] = t;
+        }
+      }
+    } else {
+      float tot[U][MT];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) tot[u][m] = team_sum<LANES>(part[u][m]);
+      if constexpr (SPLIT > 1) {
+        if (lane == 0) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) s_part[(team * U + u) * MT + m] = tot[u][m];
+        }
+        __syncthreads();
+        if (seg == 0 && lane == 0) {
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+              float v = tot[u][m];
+#pragma unroll
+              for (int s = 1; s < SPLIT; ++s) v += s_part[((team + s) * U + u) * MT + m];
+              tot[u][m] = v;
+            }
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int row = r0 + u;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const float v = tot[u][m];
+          if (seg == 0 && lane == 0 && row < a.O && m < a.M) {
+            if (a.y_bf16)
+              reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
+                  (uint16_t)f32_to_bf16_rne(v);
+            else
+              reinterpret_cast<float *>(a.y)[(size_t)m * a.y_stride + row] = v;
+          }
         }
       }
     }
@@ -232,6 +273,7 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
   p.O = m.O;
   p.ng = m.ng;
   p.gsc = m.gs / 32;
+  p.gsc_shift = (p.gsc & (p.gsc - 1)) == 0 ? __builtin_ctz(p.gsc) : -1;
   p.fp16 = m.fp16;
   p.x_stride = x_stride;
   p.y_stride = y_stride;

@@ -400,6 +400,8 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       }
     // this launch's tag, loaded behind the weights (it is needed only at the end)
     const uint32_t tag = launch_tag();
+    // keep every load above issued before any of their consumers
+    __builtin_amdgcn_sched_barrier(0);
     float pg[UA], pu[UA];
 #pragma unroll
     for (int u = 0; u < UA; ++u) pg[u] = pu[u] = 0.f;
@@ -531,6 +533,7 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
     }
   }
   const uint32_t tag = launch_tag();
+  __builtin_amdgcn_sched_barrier(0);
   // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604)
   if (wave == kWaves - 1) {
     float gsig = 1.0f;
