@@ -310,17 +310,20 @@ __device__ __forceinline__ uint32_t sub_need(int n, int q) {
 }
 
 template <int BITS, int CPLA, int LANESB, int KPL>
-__global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
+// Two 8-wave blocks per CU (4 waves per SIMD, <= 128 VGPRs) so all A and B
+// blocks of a config-3 launch are resident at once; the D > 2048 variants
+// hold two x chunks per lane and would spill there.
+__global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
   constexpr int UA = fused_ua(BITS, CPLA);     // rows of gate (and of up) per A wave
   constexpr int RPP = 64 / LANESB;            // B rows per pass of a wave
-  constexpr int PASSES = BITS == 8 ? 2 : 4;   // B passes (rows held per lane, per slot)
+  constexpr int PASSES = 2;                   // B passes (rows held per lane, per slot)
   constexpr int ROWS_B = RPP * PASSES;        // output rows per B block
   constexpr int VPL = LANESB / 2;             // h pairs per lane when reading a slot
   __shared__ __align__(16) float s_hv[kWaves][32 * LANESB];
   __shared__ float s_y[ROWS_B][kFusedMaxSlots];
   __shared__ uint32_t s_to[kWaves];
   __shared__ uint32_t s_sel[kFusedMaxSlots];  // route keys, computed once per block
-  __shared__ uint32_t s_left;                  // A: waves of the block still running
+  __shared__ uint32_t s_left;  // A: waves of the block still running; B: waves done polling
   __shared__ float s_gsig;
 
   const int lane = threadIdx.x & 63;
@@ -470,6 +473,7 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
 
   // wave 0 routes for the block
   uint32_t key[KPL];
+  if (threadIdx.x == 0) s_left = 0;
   if (wave == 0) route_keys<KPL>(logits, a.E, key);
 
   // route-independent loads first: the shared slot's down rows
@@ -580,6 +584,30 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       }
     }
   }
+  // Completion, counted once every wave of the block has seen its slots'
+  // arrivals (the counters are not read again; the epoch is already in every
+  // wave's tag): the last wave of the block to get here counts the block, and
+  // the block completing the two-level count resets every counter and
+  // advances the epoch, while the other waves go on reading h.
+  if (lane == 0 && atomicAdd(&s_left, 1u) == kWaves - 1) {
+    const int nb = g.nB_blocks;
+    const int c = bb % kDoneCtrs;
+    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
+    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (uint32_t)needc - 1) {
+      const uint32_t top =
+          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (top == (uint32_t)nbc - 1) {
+        for (int s = 0; s < kFusedMaxSlots; ++s)
+          for (int q = 0; q < kSubCtrs; ++q) st_agent(&g_fused_sync.ctr[s][q][0], 0u);
+        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
+        st_agent(&g_fused_sync.btop[0], 0u);
+        st_agent(&g_fused_sync.epoch[0], ld_agent(&g_fused_sync.epoch[0]) + 1u);
+      }
+    }
+  }
   // lane covers h[VPL*lane .. VPL*lane + VPL) of each slot: first through
   // L2, then (stale or not yet landed) with device-scope loads
   const int slice = (int)((tag >> 1) % kSlices);
@@ -636,9 +664,14 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
       }
       __builtin_amdgcn_wave_barrier();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      float xs = 0.f;
+      float xt[16];
 #pragma unroll
-      for (int v = 0; v < 32; ++v) xs += xf[v];
+      for (int v = 0; v < 16; ++v) xt[v] = xf[v] + xf[v + 16];
+#pragma unroll
+      for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+        for (int v = 0; v < w; ++v) xt[v] += xt[v + w];
+      const float xs = xt[0];
       const DevBank &bd = sh ? a.sdown : a.down;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
@@ -654,29 +687,6 @@ __global__ __launch_bounds__(kWaves * 64) void moe_fused_b1_kernel(MoeArgs a, Fu
   }
   if (lane == 0) s_to[wave] = to;
   __syncthreads();
-
-  // Completion, counted as soon as every wave of the block has read its h
-  // (counters and pairs are no longer needed): the block completing the
-  // two-level count resets every counter and advances the epoch.
-  if (threadIdx.x == 64) {  // a thread outside the combine below
-    const int nb = g.nB_blocks;
-    const int c = bb % kDoneCtrs;
-    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
-    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
-    const uint32_t prev =
-        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (uint32_t)needc - 1) {
-      const uint32_t top =
-          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (top == (uint32_t)nbc - 1) {
-        for (int s = 0; s < kFusedMaxSlots; ++s)
-          for (int q = 0; q < kSubCtrs; ++q) st_agent(&g_fused_sync.ctr[s][q][0], 0u);
-        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
-        st_agent(&g_fused_sync.btop[0], 0u);
-        st_agent(&g_fused_sync.epoch[0], ld_agent(&g_fused_sync.epoch[0]) + 1u);
-      }
-    }
-  }
 
   // rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711) by the first ROWS_B threads
   if ((int)threadIdx.x < ROWS_B) {
@@ -770,7 +780,7 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   g.nA_blocks = (g.k * g.wpr + g.wps) / kWaves;
   const int Ci = hmax >> 5;
   const int lanesb = Ci <= 16 ? 16 : 32;
-  const int rows_per_block = (64 / lanesb) * (a.gate.m.bits == 8 ? 2 : 4);
+  const int rows_per_block = (64 / lanesb) * 2;  // RPP * PASSES
   g.nB_blocks = (a.D + rows_per_block - 1) / rows_per_block;
   switch (a.gate.m.bits) {
     case 4: return fused_bits<4>(a, g, st);
