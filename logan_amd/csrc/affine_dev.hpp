@@ -48,6 +48,12 @@ __device__ __forceinline__ float aux_to_f32(uint32_t b, bool fp16) {
   return fp16 ? f16_to_f32(b) : bf16_to_f32(b);
 }
 
+// Same value, both conversions computed and one selected (no branch).
+__device__ __forceinline__ float aux_to_f32_sel(uint32_t b, bool fp16) {
+  const float h = f16_to_f32(b), f = bf16_to_f32(b);
+  return fp16 ? h : f;
+}
+
 // Round-to-nearest-even f32 -> bf16 bits (logan-core/src/math.rs:279-283).
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -133,6 +139,20 @@ __device__ __forceinline__ void make_xchunk_bf16(XChunk &xc, const uint32_t (&xb
   }
   xc.xs = s;
   xc.xsp = sp;
+}
+
+// One pair word of make_xchunk_bf16 (pair p), with its two terms of xs and
+// xsp, for callers that split a chunk's conversion across lanes or waves.
+template <int BITS>
+__device__ __forceinline__ void xpair_bf16(const uint32_t (&xb)[32], int p, uint32_t &word,
+                                           float &s, float &sp) {
+  const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
+  const float vl = bf16_to_f32(xb[kl]), vh = bf16_to_f32(xb[kh]);
+  const float xl = vl * xscale(PairMap<BITS>::slo(p));
+  const float xh = vh * xscale(PairMap<BITS>::shi(p));
+  word = f32_hi16(xl) | (f32_hi16(xh) << 16);
+  s = vl + vh;
+  sp = xl + xh;
 }
 
 // f32 activations: x' = hi + lo (both bf16, RNE) so the pair dot keeps ~16

@@ -323,6 +323,9 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __shared__ float s_y[ROWS_B][kFusedMaxSlots];
   __shared__ uint32_t s_to[kWaves];
   __shared__ uint32_t s_sel[kFusedMaxSlots];  // route keys, computed once per block
+  __shared__ __align__(16) uint32_t s_xp[64 * CPLA][16];  // A: x pairs per chunk
+  __shared__ __align__(16) float s_xs[64 * CPLA][kWaves];  // A: partial sums of x
+  __shared__ __align__(16) float s_xsp[64 * CPLA][kWaves]; // A: partial sums of x' (pairs)
   __shared__ uint32_t s_left;  // A: waves of the block still running; B: waves done polling
   __shared__ float s_gsig;
 
@@ -357,6 +360,36 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       for (int v = 0; v < 4; ++v) xq[i][v] = src[v];
     }
     if (threadIdx.x == 0) s_left = kWaves;
+    // x as pre-scaled bf16 pairs, converted once per block: wave w converts
+    // pairs 2w and 2w+1 of every chunk into LDS, with its partial sums
+#pragma unroll
+    for (int i = 0; i < CPLA; ++i) {
+      const int c = lane + 64 * i;
+      const bool ok = c < C;
+      uint32_t xb[32];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint4 q = xq[i][v];
+        xb[8 * v + 0] = q.x & 0xffffu; xb[8 * v + 1] = q.x >> 16;
+        xb[8 * v + 2] = q.y & 0xffffu; xb[8 * v + 3] = q.y >> 16;
+        xb[8 * v + 4] = q.z & 0xffffu; xb[8 * v + 5] = q.z >> 16;
+        xb[8 * v + 6] = q.w & 0xffffu; xb[8 * v + 7] = q.w >> 16;
+      }
+      // (pair index compile-time in each unrolled body: no dynamic register indexing)
+#pragma unroll
+      for (int pp = 0; pp < 16; pp += 2) {
+        if ((pp >> 1) == wave) {
+          uint32_t w0, w1;
+          float s0, sp0, s1, sp1;
+          xpair_bf16<BITS>(xb, pp, w0, s0, sp0);
+          xpair_bf16<BITS>(xb, pp + 1, w1, s1, sp1);
+          s_xp[c][pp] = ok ? w0 : 0u;
+          s_xp[c][pp + 1] = ok ? w1 : 0u;
+          s_xs[c][wave] = ok ? s0 + s1 : 0.f;
+          s_xsp[c][wave] = ok ? sp0 + sp1 : 0.f;
+        }
+      }
+    }
     if (!shared && wave == 0) {
       uint32_t sel[kFusedMaxSlots];
       route_select<KPL>(key, a.E, slot + 1, sel);
@@ -367,16 +400,21 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
     __syncthreads();
     const int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
-    const DevBank &bgk = shared ? a.sgate : a.gate;
-    const DevBank &buk = shared ? a.sup : a.up;
-    const uint8_t *gw = bgk.m.w + (size_t)e * bgk.w_stride;
-    const uint8_t *uw = buk.m.w + (size_t)e * buk.w_stride;
-    const uint16_t *gsc = bgk.m.sc + (size_t)e * bgk.p_stride;
-    const uint16_t *gbi = bgk.m.bi + (size_t)e * bgk.p_stride;
-    const uint16_t *usc = buk.m.sc + (size_t)e * buk.p_stride;
-    const uint16_t *ubi = buk.m.bi + (size_t)e * buk.p_stride;
+    // bank fields copied once (scalar) rather than re-read per use
+    const DevMat gm = shared ? a.sgate.m : a.gate.m;
+    const DevMat um = shared ? a.sup.m : a.up.m;
+    const long long gws = shared ? a.sgate.w_stride : a.gate.w_stride;
+    const long long uws = shared ? a.sup.w_stride : a.up.w_stride;
+    const long long gps = shared ? a.sgate.p_stride : a.gate.p_stride;
+    const long long ups = shared ? a.sup.p_stride : a.up.p_stride;
+    const uint8_t *gw = gm.w + (size_t)e * gws;
+    const uint8_t *uw = um.w + (size_t)e * uws;
+    const uint16_t *gsc = gm.sc + (size_t)e * gps;
+    const uint16_t *gbi = gm.bi + (size_t)e * gps;
+    const uint16_t *usc = um.sc + (size_t)e * ups;
+    const uint16_t *ubi = um.bi + (size_t)e * ups;
     const int j0 = jb * UA;
-    const int gsc_chunks = bgk.m.gs >> 5;
+    const int gsh = __builtin_ctz(gm.gs >> 5);  // group sizes are 32 * 2^n
 
     // branch-free loads (clamped row / chunk; dead lanes get zero scale and
     // bias where they are used)
@@ -387,15 +425,15 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
         const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-        load_chunk<BITS>(wg[u][i], gw + (size_t)j * bgk.m.row_bytes + (size_t)c * (4 * BITS));
-        load_chunk<BITS>(wu[u][i], uw + (size_t)j * buk.m.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS>(wg[u][i], gw + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS>(wu[u][i], uw + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
       }
 #pragma unroll
     for (int u = 0; u < UA; ++u)
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
         const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-        const size_t p = (size_t)j * bgk.m.ng + c / gsc_chunks;
+        const size_t p = (size_t)j * gm.ng + (c >> gsh);
         rsg[u][i] = gsc[p];
         rbg[u][i] = gbi[p];
         rsu[u][i] = usc[p];
@@ -411,47 +449,51 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 #pragma unroll
     for (int i = 0; i < CPLA; ++i) {
       const int c = lane + 64 * i;
-      uint32_t xb[32];
+      uint32_t xp[16];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint4 q = xq[i][v];
-        const bool ok = c < C;
-        xb[8 * v + 0] = ok ? q.x & 0xffffu : 0u; xb[8 * v + 1] = ok ? q.x >> 16 : 0u;
-        xb[8 * v + 2] = ok ? q.y & 0xffffu : 0u; xb[8 * v + 3] = ok ? q.y >> 16 : 0u;
-        xb[8 * v + 4] = ok ? q.z & 0xffffu : 0u; xb[8 * v + 5] = ok ? q.z >> 16 : 0u;
-        xb[8 * v + 6] = ok ? q.w & 0xffffu : 0u; xb[8 * v + 7] = ok ? q.w >> 16 : 0u;
+      for (int v = 0; v < 16; v += 4) {
+        const uint4 t = *reinterpret_cast<const uint4 *>(&s_xp[c][v]);
+        xp[v] = t.x; xp[v + 1] = t.y; xp[v + 2] = t.z; xp[v + 3] = t.w;
       }
-      XChunk xc;
-      make_xchunk_bf16<BITS>(xc, xb);
+      const float4 s0 = *reinterpret_cast<const float4 *>(&s_xs[c][0]);
+      const float4 s1 = *reinterpret_cast<const float4 *>(&s_xs[c][4]);
+      const float4 q0 = *reinterpret_cast<const float4 *>(&s_xsp[c][0]);
+      const float4 q1 = *reinterpret_cast<const float4 *>(&s_xsp[c][4]);
+      const float xs = ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w));
+      const float xsp = ((q0.x + q0.y) + (q0.z + q0.w)) + ((q1.x + q1.y) + (q1.z + q1.w));
 #pragma unroll
       for (int u = 0; u < UA; ++u) {
         const bool live = j0 + u < rows && c < C;
-        const float sg = live ? aux_to_f32(rsg[u][i], bgk.m.fp16) : 0.f;
-        const float bg = live ? aux_to_f32(rbg[u][i], bgk.m.fp16) : 0.f;
-        const float su = live ? aux_to_f32(rsu[u][i], buk.m.fp16) : 0.f;
-        const float bu = live ? aux_to_f32(rbu[u][i], buk.m.fp16) : 0.f;
+        const float sg = live ? aux_to_f32_sel(rsg[u][i], gm.fp16) : 0.f;
+        const float bg = live ? aux_to_f32_sel(rbg[u][i], gm.fp16) : 0.f;
+        const float su = live ? aux_to_f32_sel(rsu[u][i], um.fp16) : 0.f;
+        const float bu = live ? aux_to_f32_sel(rbu[u][i], um.fp16) : 0.f;
         uint32_t q[16];
         unpack_chunk<BITS>(q, wg[u][i], kc);
-        pg[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), sg, bg, xc.xs, xc.xsp);
+        pg[u] += chunk_fold<BITS>(pairs_dot(q, xp), sg, bg, xs, xsp);
         unpack_chunk<BITS>(q, wu[u][i], kc);
-        pu[u] += chunk_fold<BITS>(pairs_dot(q, xc.p), su, bu, xc.xs, xc.xsp);
+        pu[u] += chunk_fold<BITS>(pairs_dot(q, xp), su, bu, xs, xsp);
       }
     }
-    float hv[UA];
-#pragma unroll
-    for (int u = 0; u < UA; ++u) {
-      const float gv = wave_sum_f32(pg[u]);
-      const float uv = wave_sum_f32(pu[u]);
-      hv[u] = silu(gv) * uv;  // logan-qwen4/src/lib.rs:8807-8809
+    // wave totals: lane row r (r = lane / 16) ends up with row j0 + r's h
+    // (logan-qwen4/src/lib.rs:8807-8809: h = silu(gate) * up)
+    float hval;
+    if constexpr (UA == 4) {
+      const float gv = wave_reduce4(pg[0], pg[1], pg[2], pg[3]);
+      const float uv = wave_reduce4(pu[0], pu[1], pu[2], pu[3]);
+      hval = silu(gv) * uv;
+    } else {
+      static_assert(UA == 2, "A rows per wave");
+      const float t = wave_reduce4(pg[0], pg[1], pu[0], pu[1]);  // rows: g0, g1, u0, u1
+      const float up = __int_as_float(__builtin_amdgcn_ds_bpermute((lane + 32) << 2, __float_as_int(t)));
+      hval = silu(t) * up;
     }
     const int slice = (int)((tag >> 1) % kSlices);
     uint64_t *hrow = reinterpret_cast<uint64_t *>(a.ws) + ((size_t)slice * g.slots + slot) * hmax;
-    if (lane < UA && j0 + lane < rows) {
-      float v = hv[0];
-#pragma unroll
-      for (int u = 1; u < UA; ++u) v = lane == u ? hv[u] : v;
-      const uint64_t pr = ((uint64_t)tag << 32) | __float_as_uint(v);
-      __hip_atomic_store(&hrow[j0 + lane], pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && r < UA && j0 + r < rows) {
+      const uint64_t pr = ((uint64_t)tag << 32) | __float_as_uint(hval);
+      __hip_atomic_store(&hrow[j0 + r], pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // The block's last wave to get here adds the block's arrival, right
     // behind the stores and without waiting for them (B checks the tags).
@@ -500,16 +542,11 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     if (lane < kFusedMaxSlots) s_sel[lane] = mine;
   }
   __syncthreads();
-  uint32_t sel[kFusedMaxSlots];
-#pragma unroll
-  for (int r = 0; r < kFusedMaxSlots; ++r) sel[r] = __builtin_amdgcn_readfirstlane(s_sel[r]);
 #pragma unroll
   for (int t = 0; t < kSlotsPerWave; ++t) {
     const int s = wave + t * kWaves;
     if (s < g.k) {
-      uint32_t kk = sel[0];
-#pragma unroll
-      for (int r = 1; r < kFusedMaxSlots; ++r) kk = r == s ? sel[r] : kk;
+      const uint32_t kk = __builtin_amdgcn_readfirstlane(s_sel[s]);
       const int e = sel_expert(kk);
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
@@ -696,6 +733,9 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) anyto |= s_to[w];
     float wr[kFusedMaxSlots];
+    uint32_t sel[kFusedMaxSlots];  // the route, kept in LDS until here
+#pragma unroll
+    for (int q = 0; q < kFusedMaxSlots; ++q) sel[q] = s_sel[q];
     const float l0 = sel_logit(sel[0]);
     float wsum = 0.f;
 #pragma unroll
@@ -770,6 +810,8 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   const int UA = fused_ua(a.gate.m.bits, (a.D >> 5) <= 64 ? 1 : 2);
   if (a.se_gate_vec && (reinterpret_cast<uintptr_t>(a.se_gate_vec) & 15) != 0) return 0;
   if ((reinterpret_cast<uintptr_t>(a.x) & 15) != 0) return 0;
+  const int gs32 = a.gate.m.gs >> 5;  // A indexes groups with a shift
+  if ((gs32 & (gs32 - 1)) != 0) return 0;
   FusedGeom g;
   g.k = a.k;
   g.slots = slots;
