@@ -623,27 +623,15 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   }
   // Completion, counted once every wave of the block has seen its slots'
   // arrivals (the counters are not read again; the epoch is already in every
-  // wave's tag): the last wave of the block to get here counts the block, and
-  // the block completing the two-level count resets every counter and
-  // advances the epoch, while the other waves go on reading h.
+  // wave's tag): the last wave of the block to get here counts the block on
+  // bctr[bb % kDoneCtrs]. The returned count is looked at only after the
+  // combine, so the atomic's round trip overlaps the h reads and the math.
+  bool counted = false;
+  uint32_t done_prev = 0;
   if (lane == 0 && atomicAdd(&s_left, 1u) == kWaves - 1) {
-    const int nb = g.nB_blocks;
-    const int c = bb % kDoneCtrs;
-    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
-    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
-    const uint32_t prev =
-        __hip_atomic_fetch_add(&g_fused_sync.bctr[c][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (uint32_t)needc - 1) {
-      const uint32_t top =
-          __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (top == (uint32_t)nbc - 1) {
-        for (int s = 0; s < kFusedMaxSlots; ++s)
-          for (int q = 0; q < kSubCtrs; ++q) st_agent(&g_fused_sync.ctr[s][q][0], 0u);
-        for (int q = 0; q < kDoneCtrs; ++q) st_agent(&g_fused_sync.bctr[q][0], 0u);
-        st_agent(&g_fused_sync.btop[0], 0u);
-        st_agent(&g_fused_sync.epoch[0], ld_agent(&g_fused_sync.epoch[0]) + 1u);
-      }
-    }
+    counted = true;
+    done_prev = __hip_atomic_fetch_add(&g_fused_sync.bctr[bb % kDoneCtrs][0], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
   }
   // lane covers h[VPL*lane .. VPL*lane + VPL) of each slot: first through
   // L2, then (stale or not yet landed) with device-scope loads
@@ -762,6 +750,30 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       for (int q = 0; q < g.k; ++q) {
         if (a.idx_out) a.idx_out[q] = sel_expert(sel[q]);
         if (a.w_out) a.w_out[q] = wr[q] / wsum;
+      }
+    }
+  }
+
+  // the block completing its bctr counts on btop; the block completing btop
+  // resets every counter (one store per lane) and advances the epoch
+  if (__builtin_amdgcn_readfirstlane(counted ? 1 : 0)) {
+    const uint32_t prev = __builtin_amdgcn_readfirstlane(done_prev);
+    const int nb = g.nB_blocks;
+    const int c = bb % kDoneCtrs;
+    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
+    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
+    if (prev == (uint32_t)needc - 1) {
+      uint32_t top = 0;
+      if (lane == 0)
+        top = __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readfirstlane(top) == (uint32_t)nbc - 1) {
+        static_assert(kFusedMaxSlots * kSubCtrs <= 64 && kDoneCtrs <= 64, "one lane per counter");
+        if (lane < kFusedMaxSlots * kSubCtrs) st_agent(&g_fused_sync.ctr[lane / kSubCtrs][lane % kSubCtrs][0], 0u);
+        if (lane < kDoneCtrs) st_agent(&g_fused_sync.bctr[lane][0], 0u);
+        if (lane == 0) {
+          st_agent(&g_fused_sync.btop[0], 0u);
+          __hip_atomic_fetch_add(&g_fused_sync.epoch[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   }
