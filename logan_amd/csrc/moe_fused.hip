@@ -218,6 +218,9 @@ struct FusedGeom {
   int nB_blocks;
 };
 
+#ifndef FUSED_PASSES
+#define FUSED_PASSES 2
+#endif
 constexpr int kWaves = 8;  // waves per block (512 threads)
 
 // gate/up rows per A wave: fewer where a lane's weight registers would spill
@@ -316,13 +319,14 @@ template <int BITS, int CPLA, int LANESB, int KPL>
 __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_kernel(MoeArgs a, FusedGeom g) {
   constexpr int UA = fused_ua(BITS, CPLA);     // rows of gate (and of up) per A wave
   constexpr int RPP = 64 / LANESB;            // B rows per pass of a wave
-  constexpr int PASSES = 2;                   // B passes (rows held per lane, per slot)
+  constexpr int PASSES = FUSED_PASSES;        // B passes (rows held per lane, per slot)
   constexpr int ROWS_B = RPP * PASSES;        // output rows per B block
   constexpr int VPL = LANESB / 2;             // h pairs per lane when reading a slot
   __shared__ __align__(16) float s_hv[kWaves][32 * LANESB];
   __shared__ float s_y[ROWS_B][kFusedMaxSlots];
   __shared__ uint32_t s_to[kWaves];
   __shared__ uint32_t s_sel[kFusedMaxSlots];  // route keys, computed once per block
+  __shared__ float s_w[kFusedMaxSlots];       // B: combine weights by rank
   __shared__ __align__(16) uint32_t s_xp[64 * CPLA][16];  // A: x pairs per chunk
   __shared__ __align__(16) float s_xs[64 * CPLA][kWaves];  // A: partial sums of x
   __shared__ __align__(16) float s_xsp[64 * CPLA][kWaves]; // A: partial sums of x' (pairs)
@@ -540,6 +544,15 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 #pragma unroll
     for (int r = 0; r < kFusedMaxSlots; ++r) mine = lane == r ? sel0[r] : mine;
     if (lane < kFusedMaxSlots) s_sel[lane] = mine;
+    // combine weights, one rank per lane (logan-qwen4/src/lib.rs:8694):
+    // w_r = exp(l_r - l_0) / sum_{r<k} exp(l_r - l_0)
+    const float ev = lane < g.k ? __expf(sel_logit(mine) - sel_logit(sel0[0])) : 0.f;
+    const float wr = ev / wave_sum_f32(ev);
+    if (lane < kFusedMaxSlots) s_w[lane] = wr;
+    if (bb == 0 && lane < g.k) {
+      if (a.idx_out) a.idx_out[lane] = sel_expert(mine);
+      if (a.w_out) a.w_out[lane] = wr;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -720,24 +733,10 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     uint32_t anyto = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) anyto |= s_to[w];
-    float wr[kFusedMaxSlots];
-    uint32_t sel[kFusedMaxSlots];  // the route, kept in LDS until here
-#pragma unroll
-    for (int q = 0; q < kFusedMaxSlots; ++q) sel[q] = s_sel[q];
-    const float l0 = sel_logit(sel[0]);
-    float wsum = 0.f;
-#pragma unroll
-    for (int q = 0; q < kFusedMaxSlots; ++q) {
-      wr[q] = 0.f;
-      if (q < g.k) {
-        wr[q] = __expf(sel_logit(sel[q]) - l0);
-        wsum += wr[q];
-      }
-    }
     float acc = 0.f;
 #pragma unroll
     for (int q = 0; q < kFusedMaxSlots; ++q)
-      if (q < g.k) acc = fmaf(s_y[r][q], wr[q] / wsum, acc);
+      if (q < g.k) acc = fmaf(s_y[r][q], s_w[q], acc);
     float o = acc;
     if (has_shared) o = fmaf(s_y[r][g.k], s_gsig, acc);
     if (dd < a.D && !anyto) {
@@ -745,12 +744,6 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
         reinterpret_cast<float *>(a.out)[dd] = o;
       else
         reinterpret_cast<uint16_t *>(a.out)[dd] = (uint16_t)f32_to_bf16_rne(o);
-    }
-    if (bb == 0 && r == 0) {
-      for (int q = 0; q < g.k; ++q) {
-        if (a.idx_out) a.idx_out[q] = sel_expert(sel[q]);
-        if (a.w_out) a.w_out[q] = wr[q] / wsum;
-      }
     }
   }
 
@@ -834,7 +827,7 @@ int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
   g.nA_blocks = (g.k * g.wpr + g.wps) / kWaves;
   const int Ci = hmax >> 5;
   const int lanesb = Ci <= 16 ? 16 : 32;
-  const int rows_per_block = (64 / lanesb) * 2;  // RPP * PASSES
+  const int rows_per_block = (64 / lanesb) * FUSED_PASSES;  // RPP * PASSES
   g.nB_blocks = (a.D + rows_per_block - 1) / rows_per_block;
   switch (a.gate.m.bits) {
     case 4: return fused_bits<4>(a, g, st);
