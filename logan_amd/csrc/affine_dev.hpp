@@ -366,6 +366,47 @@ __device__ __forceinline__ float wave_reduce4(float a, float b, float c, float d
   return t;
 }
 
+// sum_k code_k * h_k over one 32-code chunk (LSB-first BITS-bit codes)
+template <int BITS>
+__device__ __forceinline__ float codes_dot(const uint32_t (&w)[BITS], const float (&h)[32]) {
+  float a0 = 0.f, a1 = 0.f;
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // nibbles to bytes, then one v_cvt_f32_ubyteN per code (the empty asm
+      // keeps the compiler from folding the masks into per-code bfe's)
+      uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        a0 = fmaf((float)((lo >> (8 * b)) & 0xffu), h[8 * i + 2 * b], a0);
+        a1 = fmaf((float)((hi >> (8 * b)) & 0xffu), h[8 * i + 2 * b + 1], a1);
+      }
+    }
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a0 = fmaf((float)(w[i] & 0xffu), h[4 * i], a0);
+      a1 = fmaf((float)((w[i] >> 8) & 0xffu), h[4 * i + 1], a1);
+      a0 = fmaf((float)((w[i] >> 16) & 0xffu), h[4 * i + 2], a0);
+      a1 = fmaf((float)(w[i] >> 24), h[4 * i + 3], a1);
+    }
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      const int bit = k * BITS, i = bit >> 5, sh = bit & 31;
+      uint32_t c = w[i] >> sh;
+      if (sh + BITS > 32) c |= w[i + 1] << (32 - sh);
+      if (k & 1)
+        a1 = fmaf((float)(c & mask), h[k], a1);
+      else
+        a0 = fmaf((float)(c & mask), h[k], a0);
+    }
+  }
+  return a0 + a1;
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 }  // namespace lh

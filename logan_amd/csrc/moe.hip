@@ -27,105 +27,37 @@
 
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
+#include "route_dev.hpp"
 
 namespace lh {
-
-__device__ __forceinline__ uint32_t ord32(float f) {
-  uint32_t u = __float_as_uint(f);
-  if (u == 0x80000000u) u = 0;  // -0 == +0, as the reference's comparison
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float unord32(uint32_t o) {
-  const uint32_t u = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
-  return __uint_as_float(u);
-}
-
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ __forceinline__ float load_logit(const void *p, int f32, size_t i) {
-  return f32 ? reinterpret_cast<const float *>(p)[i]
-             : bf16_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
-}
 
 constexpr int kMaxE = 1024;  // 16 keys per lane
 constexpr int kMaxK = 32;
 
-// One wave selects the top-k of one row of E logits. Rank r's expert and
-// logit land in sel_idx[r] / sel_l[r] (LDS, written by lane 0); weights
-// w_r = exp(l_r - l_0) / sum_{j<k} exp(l_j - l_0) are written to sel_w[r].
-template <bool F32>
-__device__ __forceinline__ void wave_topk_t(const void *logits, size_t row_off, int E, int k,
-                                            int *sel_idx, float *sel_l, float *sel_w) {
-  const int lane = threadIdx.x & 63;
-  uint64_t key[16];
-  // branch-free loads: out-of-range lanes read element 0 and get key 0
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int e = i * 64 + lane;
-    const bool ok = e < E;
-    const size_t ei = row_off + (ok ? e : 0);
-    const float l = F32 ? reinterpret_cast<const float *>(logits)[ei]
-                        : bf16_to_f32(reinterpret_cast<const uint16_t *>(logits)[ei]);
-    const uint64_t kk = ((uint64_t)ord32(l) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
-    key[i] = ok ? kk : 0ull;
-  }
-#pragma unroll 1
-  for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) best = key[i] > best ? key[i] : best;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const uint64_t other = shfl_xor_u64(best, o);
-      best = other > best ? other : best;
-    }
-    const int e = (int)(0xffffffffu - (uint32_t)best);
-    if (lane == 0) {
-      sel_idx[r] = e;
-      sel_l[r] = unord32((uint32_t)(best >> 32));
-    }
-    // keys are unique (the index is part of the key): clear the winner
-#pragma unroll
-    for (int i = 0; i < 16; ++i) key[i] = key[i] == best ? 0ull : key[i];
-  }
-  if (lane == 0) {
-    float wsum = 0.f;
-    const float l0 = sel_l[0];
-    for (int r = 0; r < k; ++r) {
-      const float ex = __expf(sel_l[r] - l0);
-      sel_w[r] = ex;
-      wsum += ex;
-    }
-    for (int r = 0; r < k; ++r) sel_w[r] = sel_w[r] / wsum;
-  }
-}
-
+// One wave: top-k of one token's logits; lane r < k ends with rank r's
+// expert and weight (route_dev.hpp: wave_topk_lanes).
 __device__ __forceinline__ void wave_topk(const void *logits, int f32, size_t row_off, int E,
-                                          int k, int *sel_idx, float *sel_l, float *sel_w) {
-  if (f32)
-    wave_topk_t<true>(logits, row_off, E, k, sel_idx, sel_l, sel_w);
-  else
-    wave_topk_t<false>(logits, row_off, E, k, sel_idx, sel_l, sel_w);
+                                          int k, int &idx, float &w) {
+  if (f32) {
+    if (E <= 512) wave_topk_lanes<8, true>(logits, row_off, E, k, idx, w);
+    else wave_topk_lanes<16, true>(logits, row_off, E, k, idx, w);
+  } else {
+    if (E <= 512) wave_topk_lanes<8, false>(logits, row_off, E, k, idx, w);
+    else wave_topk_lanes<16, false>(logits, row_off, E, k, idx, w);
+  }
 }
 
 __global__ __launch_bounds__(256) void route_topk_kernel(const void *logits, int f32, int B, int E,
                                                          int k, int32_t *idx, float *w) {
-  __shared__ int s_idx[4][kMaxK];
-  __shared__ float s_l[4][kMaxK], s_w[4][kMaxK];
-  const int wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= B) return;
-  wave_topk(logits, f32, (size_t)t * E, E, k, s_idx[wave], s_l[wave], s_w[wave]);
-  if ((threadIdx.x & 63) == 0) {
-    for (int r = 0; r < k; ++r) {
-      idx[(size_t)t * k + r] = s_idx[wave][r];
-      w[(size_t)t * k + r] = s_w[wave][r];
-    }
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= B) return;  // whole waves leave together
+  int id;
+  float wt;
+  wave_topk(logits, f32, (size_t)t * E, E, k, id, wt);
+  if (lane < k) {
+    idx[(size_t)t * k + lane] = id;
+    w[(size_t)t * k + lane] = wt;
   }
 }
 
@@ -148,6 +80,8 @@ struct MoeWs {
   int32_t *topk_idx;  // [B*k]
   float *topk_w;      // [B*k]
   float *gs;          // [B]
+  uint32_t *xp;       // [B][C][16] x of every token as pre-scaled bf16 pairs
+  float *xps;         // [B][C][2]  per chunk: sum x, sum of the paired values
   float *h;           // [(B*k+B) * hmax]
   float *y;           // [(B*k+B) * D]
   size_t total;
@@ -174,6 +108,8 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
   w.topk_idx = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * (size_t)B * k));
   w.topk_w = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B * k));
   w.gs = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B));
+  w.xp = reinterpret_cast<uint32_t *>(take(sizeof(uint32_t) * (size_t)B * (D / 32) * 16));
+  w.xps = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B * (D / 32) * 2));
   w.h = reinterpret_cast<float *>(take(sizeof(float) * slots * hmax));
   w.y = reinterpret_cast<float *>(take(sizeof(float) * slots * (size_t)D));
   w.total = off;
@@ -204,13 +140,40 @@ static bool fused_enabled() {
 constexpr int kGroupThreads = 1024;
 constexpr int kMaxB = 64;
 
+// xp[t][c] = make_xchunk_bf16 of chunk c of token t (pairs, sum x, sum x')
+template <int BITS>
+__device__ __forceinline__ void convert_x_pairs(const MoeArgs &a, const MoeWs &w, int tid, int nthr) {
+  const int C = a.D >> 5;
+  for (int it = tid; it < a.B * C; it += nthr) {
+    const int t = it / C, c = it % C;
+    const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D + 32 * c);
+    uint32_t xb[32];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 q = src[v];
+      xb[8 * v + 0] = q.x & 0xffffu; xb[8 * v + 1] = q.x >> 16;
+      xb[8 * v + 2] = q.y & 0xffffu; xb[8 * v + 3] = q.y >> 16;
+      xb[8 * v + 4] = q.z & 0xffffu; xb[8 * v + 5] = q.z >> 16;
+      xb[8 * v + 6] = q.w & 0xffffu; xb[8 * v + 7] = q.w >> 16;
+    }
+    XChunk xc;
+    make_xchunk_bf16<BITS>(xc, xb);
+    uint4 *dst = reinterpret_cast<uint4 *>(w.xp + (size_t)it * 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      dst[v] = make_uint4(xc.p[4 * v], xc.p[4 * v + 1], xc.p[4 * v + 2], xc.p[4 * v + 3]);
+    w.xps[(size_t)it * 2] = xc.xs;
+    w.xps[(size_t)it * 2 + 1] = xc.xsp;
+  }
+}
+
+template <int KPL, bool F32>
 __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs a, MoeWs w) {
   __shared__ int s_idx[kMaxB * kMaxK];
   __shared__ int s_cnt[kMaxE];
   __shared__ int s_start[kMaxE];
   __shared__ int s_gid[kMaxE];
   __shared__ int s_wave_tot[kGroupThreads / 64];
-  __shared__ float s_l[kGroupThreads / 64][kMaxK], s_w[kGroupThreads / 64][kMaxK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = kGroupThreads / 64;
   const int nslots = a.B * a.k;
@@ -218,17 +181,15 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
   for (int e = tid; e < a.E; e += kGroupThreads) s_cnt[e] = 0;
 
   for (int t = wave; t < a.B; t += nwaves) {
-    wave_topk(a.logits, a.logits_f32, (size_t)t * a.E, a.E, a.k, &s_idx[t * a.k], s_l[wave],
-              s_w[wave]);
-    if (lane == 0) {
-      for (int r = 0; r < a.k; ++r) {
-        const int si = s_idx[t * a.k + r];
-        const float sw = s_w[wave][r];
-        w.topk_idx[t * a.k + r] = si;
-        w.topk_w[t * a.k + r] = sw;
-        if (a.idx_out) a.idx_out[t * a.k + r] = si;
-        if (a.w_out) a.w_out[t * a.k + r] = sw;
-      }
+    int id;
+    float wt;
+    wave_topk_lanes<KPL, F32>(a.logits, (size_t)t * a.E, a.E, a.k, id, wt);
+    if (lane < a.k) {
+      s_idx[t * a.k + lane] = id;
+      w.topk_idx[t * a.k + lane] = id;
+      w.topk_w[t * a.k + lane] = wt;
+      if (a.idx_out) a.idx_out[t * a.k + lane] = id;
+      if (a.w_out) a.w_out[t * a.k + lane] = wt;
     }
     // shared-expert scalar gate: sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604)
     if (a.sgate.m.w) {
@@ -243,6 +204,13 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
       }
       if (lane == 0) w.gs[t] = g;
     }
+  }
+  // x of every token as the gate/up kernels' operand (one chunk per thread)
+  switch (a.gate.m.bits) {
+    case 4: convert_x_pairs<4>(a, w, tid, kGroupThreads); break;
+    case 5: convert_x_pairs<5>(a, w, tid, kGroupThreads); break;
+    case 6: convert_x_pairs<6>(a, w, tid, kGroupThreads); break;
+    default: convert_x_pairs<8>(a, w, tid, kGroupThreads); break;
   }
   __syncthreads();
   for (int i = tid; i < nslots; i += kGroupThreads) atomicAdd(&s_cnt[s_idx[i]], 1);
@@ -324,211 +292,202 @@ __device__ __forceinline__ bool moe_item_group(const MoeArgs &a, const MoeWs &w,
   return false;
 }
 
-template <int BITS, int LANES, int CPL, int U>
-__global__ __launch_bounds__(256) void moe_gateup_kernel(MoeArgs a, MoeWs w, int ipg, int ipg_s) {
-  constexpr int TEAMS = 256 / LANES;
-  constexpr int RPB = TEAMS * U;  // rows per block
-  const int lane = threadIdx.x & (LANES - 1);
-  const int team = threadIdx.x / LANES;
+// One block: RPB = 16 rows of gate and of up (4 per wave, a wave spans the
+// whole row: CPL chunks per lane) of one expert group, applied to every token
+// of the group. Loads are issued together, branch-free; x comes pre-paired.
+template <int BITS, int CPL>
+__global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, int ipg, int ipg_s) {
+  constexpr int U = 4;
+  constexpr int RPB = 4 * U;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int C = a.D >> 5;
-  const int ng = *w.n_groups;
-  const int n_items = ng * ipg + (a.sgate.m.w ? ipg_s : 0);
   UnpackConsts kc;
   kc.init();
-  int gidx[CPL];
-  bool cval[CPL];
+  const int item = blockIdx.x;
+  const bool shared = item >= ipg * (a.B * a.k < a.E ? a.B * a.k : a.E);
+  const int g = shared ? -1 : item / ipg;
+  const int rb = shared ? item - ipg * (a.B * a.k < a.E ? a.B * a.k : a.E) : item % ipg;
+  const int ng = *w.n_groups;
+  const int ge = shared ? 0 : w.group_expert[g < 0 ? 0 : g];
+  const int s0 = shared ? 0 : w.group_off[g < 0 ? 0 : g];
+  const int s1 = shared ? a.B : w.group_off[(g < 0 ? 0 : g) + 1];
+  if (shared ? (a.sgate.m.w == nullptr || rb >= ipg_s) : g >= ng) return;
+  const DevMat gm = shared ? a.sgate.m : a.gate.m;
+  const DevMat um = shared ? a.sup.m : a.up.m;
+  const long long gws = shared ? a.sgate.w_stride : a.gate.w_stride;
+  const long long uws = shared ? a.sup.w_stride : a.up.w_stride;
+  const long long gps = shared ? a.sgate.p_stride : a.gate.p_stride;
+  const long long ups = shared ? a.sup.p_stride : a.up.p_stride;
+  const int e = __builtin_amdgcn_readfirstlane(ge);
+  const int rows = shared ? a.sinter : a.inter;
+  const uint8_t *gwb = gm.w + (size_t)e * gws;
+  const uint8_t *uwb = um.w + (size_t)e * uws;
+  const uint16_t *gsc = gm.sc + (size_t)e * gps;
+  const uint16_t *gbi = gm.bi + (size_t)e * gps;
+  const uint16_t *usc = um.sc + (size_t)e * ups;
+  const uint16_t *ubi = um.bi + (size_t)e * ups;
+  const int j0 = rb * RPB + wave * U;
+  const int gshift = __builtin_ctz(gm.gs >> 5);
+
+  uint32_t wg[U][CPL][BITS], wu[U][CPL][BITS];
+  uint32_t rsg[U][CPL], rbg[U][CPL], rsu[U][CPL], rbu[U][CPL];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane + LANES * j;
-    cval[j] = c < C;
-    gidx[j] = c / (a.gate.m.gs >> 5);
-  }
-
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    int g, rb;
-    if (!moe_item_group(a, w, ng, ipg, ipg_s, item, g, rb)) break;
-    const bool shared = g < 0;
-    const DevBank &bg = shared ? a.sgate : a.gate;
-    const DevBank &bu = shared ? a.sup : a.up;
-    const int e = shared ? 0 : w.group_expert[g];
-    const int rows = shared ? a.sinter : a.inter;
-    const int s0 = shared ? 0 : w.group_off[g];
-    const int s1 = shared ? a.B : w.group_off[g + 1];
-    const uint8_t *gwb = bg.m.w + (size_t)e * bg.w_stride;
-    const uint8_t *uwb = bu.m.w + (size_t)e * bu.w_stride;
-    const uint16_t *gsc = bg.m.sc + (size_t)e * bg.p_stride;
-    const uint16_t *gbi = bg.m.bi + (size_t)e * bg.p_stride;
-    const uint16_t *usc = bu.m.sc + (size_t)e * bu.p_stride;
-    const uint16_t *ubi = bu.m.bi + (size_t)e * bu.p_stride;
-    const int j0 = rb * RPB + team * U;
-
-    uint32_t wg[U][CPL][BITS], wu[U][CPL][BITS];
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+      load_chunk<BITS>(wg[u][i], gwb + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+      load_chunk<BITS>(wu[u][i], uwb + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+      const size_t p = (size_t)j * gm.ng + (c >> gshift);
+      rsg[u][i] = gsc[p];
+      rbg[u][i] = gbi[p];
+      rsu[u][i] = usc[p];
+      rbu[u][i] = ubi[p];
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  // the packed rows stay in registers; each token unpacks them again (groups
+  // hold one or two tokens in the common case)
+  float sg[U][CPL], bg[U][CPL], su[U][CPL], bu[U][CPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const bool live = j0 + u < rows && lane + 64 * i < C;
+      sg[u][i] = live ? aux_to_f32_sel(rsg[u][i], gm.fp16) : 0.f;
+      bg[u][i] = live ? aux_to_f32_sel(rbg[u][i], gm.fp16) : 0.f;
+      su[u][i] = live ? aux_to_f32_sel(rsu[u][i], um.fp16) : 0.f;
+      bu[u][i] = live ? aux_to_f32_sel(rbu[u][i], um.fp16) : 0.f;
+    }
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  for (int si = s0; si < s1; ++si) {
+    // keep the unpack inside the loop (not hoisted into 128 live registers)
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int row = j0 + u, c = lane + LANES * j;
-        if (row < rows && cval[j]) {
-          load_chunk<BITS>(wg[u][j], gwb + (size_t)row * bg.m.row_bytes + (size_t)c * (4 * BITS));
-          load_chunk<BITS>(wu[u][j], uwb + (size_t)row * bu.m.row_bytes + (size_t)c * (4 * BITS));
-        } else {
+      for (int i = 0; i < CPL; ++i)
 #pragma unroll
-          for (int t = 0; t < BITS; ++t) wg[u][j][t] = wu[u][j][t] = 0;
-        }
+        for (int q = 0; q < BITS; ++q) asm volatile("" : "+v"(wg[u][i][q]), "+v"(wu[u][i][q]));
+    const int slot = shared ? a.B * a.k + si : w.entries[si];
+    const int t = shared ? si : slot / a.k;
+    float pg[U], pu[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) pg[u] = pu[u] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      const size_t xo = (size_t)t * C + c;
+      uint32_t xp[16];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint4 q = reinterpret_cast<const uint4 *>(w.xp + xo * 16)[v];
+        xp[4 * v] = q.x; xp[4 * v + 1] = q.y; xp[4 * v + 2] = q.z; xp[4 * v + 3] = q.w;
       }
-    float sg[U][CPL], bg_[U][CPL], su[U][CPL], bu_[U][CPL];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int row = j0 + u;
-        if (row < rows && cval[j]) {
-          const size_t pg = (size_t)row * bg.m.ng + gidx[j];
-          const size_t pu = (size_t)row * bu.m.ng + gidx[j];
-          sg[u][j] = aux_to_f32(gsc[pg], bg.m.fp16);
-          bg_[u][j] = aux_to_f32(gbi[pg], bg.m.fp16);
-          su[u][j] = aux_to_f32(usc[pu], bu.m.fp16);
-          bu_[u][j] = aux_to_f32(ubi[pu], bu.m.fp16);
-        } else {
-          sg[u][j] = bg_[u][j] = su[u][j] = bu_[u][j] = 0.f;
-        }
-      }
-    uint32_t qg[U][CPL][16], qu[U][CPL][16];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        unpack_chunk<BITS>(qg[u][j], wg[u][j], kc);
-        unpack_chunk<BITS>(qu[u][j], wu[u][j], kc);
-      }
-
-    for (int si = s0; si < s1; ++si) {
-      const int slot = shared ? a.B * a.k + si : w.entries[si];
-      const int t = shared ? si : slot / a.k;
-      float pg[U], pu[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) pg[u] = pu[u] = 0.f;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + LANES * j;
-        uint32_t xb[32];
-        if (cval[j]) {
-          const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D + 32 * c);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const uint4 q = src[v];
-            xb[8 * v + 0] = q.x & 0xffffu; xb[8 * v + 1] = q.x >> 16;
-            xb[8 * v + 2] = q.y & 0xffffu; xb[8 * v + 3] = q.y >> 16;
-            xb[8 * v + 4] = q.z & 0xffffu; xb[8 * v + 5] = q.z >> 16;
-            xb[8 * v + 6] = q.w & 0xffffu; xb[8 * v + 7] = q.w >> 16;
-          }
-        } else {
-#pragma unroll
-          for (int v = 0; v < 32; ++v) xb[v] = 0;
-        }
-        XChunk xc;
-        make_xchunk_bf16<BITS>(xc, xb);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          pg[u] += chunk_fold<BITS>(pairs_dot(qg[u][j], xc.p), sg[u][j], bg_[u][j], xc.xs, xc.xsp);
-          pu[u] += chunk_fold<BITS>(pairs_dot(qu[u][j], xc.p), su[u][j], bu_[u][j], xc.xs, xc.xsp);
-        }
-      }
-      const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+      const float2 xsum = reinterpret_cast<const float2 *>(w.xps)[xo];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float gv = team_sum<LANES>(pg[u]);
-        const float uv = team_sum<LANES>(pu[u]);
-        const int row = j0 + u;
-        // logan-qwen4/src/lib.rs:8807-8809: h = silu(gate) * up
-        if (lane == 0 && row < rows) w.h[(size_t)slot * hmax + row] = silu(gv) * uv;
+        uint32_t q[16];
+        unpack_chunk<BITS>(q, wg[u][i], kc);
+        pg[u] += chunk_fold<BITS>(pairs_dot(q, xp), sg[u][i], bg[u][i], xsum.x, xsum.y);
+        unpack_chunk<BITS>(q, wu[u][i], kc);
+        pu[u] += chunk_fold<BITS>(pairs_dot(q, xp), su[u][i], bu[u][i], xsum.x, xsum.y);
       }
     }
+    // lane row r (lane / 16) gets row j0 + r: h = silu(gate) * up
+    // (logan-qwen4/src/lib.rs:8807-8809)
+    const float gv = wave_reduce4(pg[0], pg[1], pg[2], pg[3]);
+    const float uv = wave_reduce4(pu[0], pu[1], pu[2], pu[3]);
+    const int r = lane >> 4;
+    if ((lane & 15) == 0 && j0 + r < rows) w.h[(size_t)slot * hmax + j0 + r] = silu(gv) * uv;
   }
 }
 
 // ---------------------------------------------------------------------------
 // 3. down projection of h for every slot of a group
 
-template <int BITS, int LANES, int U>
+// One block: 32 output rows d of one expert group's down projection (a row
+// per LANES lanes, PASSES rows per lane), applied to h of every slot of the
+// group with f32 FMAs: y = scale * sum code*h + bias * sum h.
+template <int BITS, int LANES>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int ipg) {
-  constexpr int TEAMS = 256 / LANES;
-  constexpr int RPB = TEAMS * U;
-  const int lane = threadIdx.x & (LANES - 1);
-  const int team = threadIdx.x / LANES;
+  constexpr int RPP = 256 / LANES;  // rows per pass of the block
+  constexpr int PASSES = 32 / RPP;
+  const int lane = threadIdx.x & 63;
+  const int lb = threadIdx.x % LANES;
+  const int rsub = threadIdx.x / LANES;
+  const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
+  const int item = blockIdx.x;
+  const bool shared = item >= G * ipg;
+  const int g = shared ? -1 : item / ipg;
+  const int rb = shared ? item - G * ipg : item % ipg;
   const int ng = *w.n_groups;
-  const int n_items = (ng + (a.sdown.m.w ? 1 : 0)) * ipg;
+  const int ge = shared ? 0 : w.group_expert[g < 0 ? 0 : g];
+  const int s0 = shared ? 0 : w.group_off[g < 0 ? 0 : g];
+  const int s1 = shared ? a.B : w.group_off[(g < 0 ? 0 : g) + 1];
+  if (shared ? a.sdown.m.w == nullptr : g >= ng) return;
+  const DevMat dm = shared ? a.sdown.m : a.down.m;
+  const long long dws = shared ? a.sdown.w_stride : a.down.w_stride;
+  const long long dps = shared ? a.sdown.p_stride : a.down.p_stride;
+  const int e = __builtin_amdgcn_readfirstlane(ge);
+  const int K = shared ? a.sinter : a.inter;  // columns of down
+  const int Ck = K >> 5;
+  const uint8_t *wb = dm.w + (size_t)e * dws;
+  const uint16_t *scb = dm.sc + (size_t)e * dps;
+  const uint16_t *bib = dm.bi + (size_t)e * dps;
+  const int d0 = rb * 32;
+  const int cl = min(lb, Ck - 1);
+  const int gi = cl / (dm.gs >> 5);
+
+  uint32_t wv[PASSES][BITS];
+  uint32_t rs[PASSES], rbi[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int d = min(d0 + p * RPP + rsub, a.D - 1);
+    load_chunk<BITS>(wv[p], wb + (size_t)d * dm.row_bytes + (size_t)cl * (4 * BITS));
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int d = min(d0 + p * RPP + rsub, a.D - 1);
+    rs[p] = scb[(size_t)d * dm.ng + gi];
+    rbi[p] = bib[(size_t)d * dm.ng + gi];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float sc[PASSES], bi[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const bool live = d0 + p * RPP + rsub < a.D && lb < Ck;
+    sc[p] = live ? aux_to_f32_sel(rs[p], dm.fp16) : 0.f;
+    bi[p] = live ? aux_to_f32_sel(rbi[p], dm.fp16) : 0.f;
+  }
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
-  UnpackConsts kc;
-  kc.init();
-
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int g = item / ipg, rb = item % ipg;
-    const bool shared = g >= ng;
-    const DevBank &bd = shared ? a.sdown : a.down;
-    const int e = shared ? 0 : w.group_expert[g];
-    const int K = shared ? a.sinter : a.inter;  // columns of down
-    const int C = K >> 5;
-    const int s0 = shared ? 0 : w.group_off[g];
-    const int s1 = shared ? a.B : w.group_off[g + 1];
-    const uint8_t *wb = bd.m.w + (size_t)e * bd.w_stride;
-    const uint16_t *scb = bd.m.sc + (size_t)e * bd.p_stride;
-    const uint16_t *bib = bd.m.bi + (size_t)e * bd.p_stride;
-    const int d0 = rb * RPB + team * U;
-    const bool cval = lane < C;
-    const int gi = lane / (bd.m.gs >> 5);
-
-    uint32_t wv[U][BITS];
-    float sc[U], bi[U];
+  for (int si = s0; si < s1; ++si) {
+    const int slot = shared ? a.B * a.k + si : w.entries[si];
+    float xf[32];
+    const float4 *src = reinterpret_cast<const float4 *>(w.h + (size_t)slot * hmax + 32 * cl);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int d = d0 + u;
-      if (d < a.D && cval) {
-        load_chunk<BITS>(wv[u], wb + (size_t)d * bd.m.row_bytes + (size_t)lane * (4 * BITS));
-      } else {
-#pragma unroll
-        for (int t = 0; t < BITS; ++t) wv[u][t] = 0;
-      }
+    for (int v = 0; v < 8; ++v) {
+      const float4 t = src[v];
+      xf[4 * v + 0] = t.x; xf[4 * v + 1] = t.y; xf[4 * v + 2] = t.z; xf[4 * v + 3] = t.w;
     }
+    float xt[16];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int d = d0 + u;
-      if (d < a.D && cval) {
-        const size_t p = (size_t)d * bd.m.ng + gi;
-        sc[u] = aux_to_f32(scb[p], bd.m.fp16);
-        bi[u] = aux_to_f32(bib[p], bd.m.fp16);
-      } else {
-        sc[u] = bi[u] = 0.f;
-      }
-    }
-    uint32_t q[U][16];
+    for (int v = 0; v < 16; ++v) xt[v] = xf[v] + xf[v + 16];
 #pragma unroll
-    for (int u = 0; u < U; ++u) unpack_chunk<BITS>(q[u], wv[u], kc);
-
-    for (int si = s0; si < s1; ++si) {
-      const int slot = shared ? a.B * a.k + si : w.entries[si];
-      float xf[32];
-      if (cval) {
-        const float4 *src = reinterpret_cast<const float4 *>(w.h + (size_t)slot * hmax + 32 * lane);
+    for (int q = 8; q > 0; q >>= 1)
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float4 t = src[v];
-          xf[4 * v + 0] = t.x; xf[4 * v + 1] = t.y; xf[4 * v + 2] = t.z; xf[4 * v + 3] = t.w;
-        }
-      } else {
+      for (int v = 0; v < q; ++v) xt[v] += xt[v + q];
 #pragma unroll
-        for (int v = 0; v < 32; ++v) xf[v] = 0.f;
-      }
-      XChunk xh, xl;
-      make_xchunk_f32<BITS>(xh, xl, xf);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float acc = pairs_dot(q[u], xh.p) + pairs_dot(q[u], xl.p);
-        float v = chunk_fold<BITS>(acc, sc[u], bi[u], xh.xs, xh.xsp);
-        v = team_sum<LANES>(v);
-        const int d = d0 + u;
-        if (lane == 0 && d < a.D) w.y[(size_t)slot * a.D + d] = v;
-      }
+    for (int p = 0; p < PASSES; ++p) {
+      float v = fmaf(sc[p], codes_dot<BITS>(wv[p], xf), bi[p] * xt[0]);
+      v = team_sum<LANES>(v);
+      const int d = d0 + p * RPP + rsub;
+      if (lb == 0 && d < a.D) w.y[(size_t)slot * a.D + d] = v;
     }
   }
 }
@@ -563,41 +522,29 @@ template <int BITS>
 static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
   const int Cd = a.D >> 5;
   const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
-  // gate/up
+  // gate/up: 16 rows per block, every possible group (blocks of groups that
+  // did not form leave at once)
   {
-    constexpr int U = 2;
-    int lanes, cpl;
-    if (Cd <= 16) { lanes = 16; cpl = 1; }
-    else if (Cd <= 32) { lanes = 32; cpl = 1; }
-    else if (Cd <= 64) { lanes = 64; cpl = 1; }
-    else if (Cd <= 128) { lanes = 64; cpl = 2; }
-    else return 0;
-    const int rpb = (256 / lanes) * U;
-    const int ipg = (a.inter + rpb - 1) / rpb;
-    const int ipg_s = a.sgate.m.w ? (a.sinter + rpb - 1) / rpb : 0;
+    const int ipg = (a.inter + 15) / 16;
+    const int ipg_s = a.sgate.m.w ? (a.sinter + 15) / 16 : 0;
     const int grid = G * ipg + ipg_s;
-    if (lanes == 16) hipLaunchKernelGGL((moe_gateup_kernel<BITS, 16, 1, U>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
-    else if (lanes == 32) hipLaunchKernelGGL((moe_gateup_kernel<BITS, 32, 1, U>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
-    else if (cpl == 1) hipLaunchKernelGGL((moe_gateup_kernel<BITS, 64, 1, U>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
-    else hipLaunchKernelGGL((moe_gateup_kernel<BITS, 64, 2, U>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
+    if (Cd <= 64)
+      hipLaunchKernelGGL((moe_gateup_kernel<BITS, 1>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
+    else if (Cd <= 128)
+      hipLaunchKernelGGL((moe_gateup_kernel<BITS, 2>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
+    else
+      return 0;
     if (hipGetLastError() != hipSuccess) return -1;
   }
-  // down
+  // down: 32 rows per block
   {
-    constexpr int U = 2;
     const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
     const int Ci = kmax >> 5;
-    int lanes;
-    if (Ci <= 16) lanes = 16;
-    else if (Ci <= 32) lanes = 32;
-    else if (Ci <= 64) lanes = 64;
-    else return -1;
-    const int rpb = (256 / lanes) * U;
-    const int ipg = (a.D + rpb - 1) / rpb;
+    const int ipg = (a.D + 31) / 32;
     const int grid = (G + (a.sdown.m.w ? 1 : 0)) * ipg;
-    if (lanes == 16) hipLaunchKernelGGL((moe_down_kernel<BITS, 16, U>), dim3(grid), dim3(256), 0, st, a, w, ipg);
-    else if (lanes == 32) hipLaunchKernelGGL((moe_down_kernel<BITS, 32, U>), dim3(grid), dim3(256), 0, st, a, w, ipg);
-    else hipLaunchKernelGGL((moe_down_kernel<BITS, 64, U>), dim3(grid), dim3(256), 0, st, a, w, ipg);
+    if (Ci <= 16) hipLaunchKernelGGL((moe_down_kernel<BITS, 16>), dim3(grid), dim3(256), 0, st, a, w, ipg);
+    else if (Ci <= 32) hipLaunchKernelGGL((moe_down_kernel<BITS, 32>), dim3(grid), dim3(256), 0, st, a, w, ipg);
+    else return -1;
     if (hipGetLastError() != hipSuccess) return -1;
   }
   {
@@ -625,6 +572,7 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
   if (a.B <= 0 || a.B > kMaxB || a.E <= 0 || a.E > kMaxE || a.k <= 0 || a.k > kMaxK || a.k > a.E)
     return 0;
   if (a.D <= 0 || a.D % 32 != 0 || a.inter <= 0 || a.inter % 32 != 0) return 0;
+  if (a.D > 4096 || a.inter > 1024 || a.sinter > 1024) return 0;  // kernel shapes below
   if (!a.x || !a.logits || !a.out || !a.ws) return 0;
   if ((reinterpret_cast<uintptr_t>(a.x) & 15) != 0) return 0;
   const int bits = a.gate.m.bits, gs = a.gate.m.gs;
@@ -647,7 +595,17 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
     if (rc != 0) return rc;
   }
   MoeWs w = moe_ws_layout(a.ws, a.B, a.D, a.inter, sinter, a.E, a.k);
-  hipLaunchKernelGGL(moe_route_group_kernel, dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+  if (a.logits_f32) {
+    if (a.E <= 512)
+      hipLaunchKernelGGL((moe_route_group_kernel<8, true>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+    else
+      hipLaunchKernelGGL((moe_route_group_kernel<16, true>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+  } else {
+    if (a.E <= 512)
+      hipLaunchKernelGGL((moe_route_group_kernel<8, false>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+    else
+      hipLaunchKernelGGL((moe_route_group_kernel<16, false>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+  }
   if (hipGetLastError() != hipSuccess) return -1;
   switch (bits) {
     case 4: return moe_launch_bits<4>(aa, w, st);

@@ -50,6 +50,7 @@
 // must therefore not overlap (one stream, or serialised streams).
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
+#include "route_dev.hpp"
 
 namespace lh {
 
@@ -86,127 +87,6 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---------------------------------------------------------------- DPP helpers
-
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xF, false);
-}
-
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xF, false));
-}
-
-// max over all 64 lanes, returned uniformly
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, dpp_u32<0xB1, 0xF>(v));   // quad_perm [1,0,3,2]
-  v = max(v, dpp_u32<0x4E, 0xF>(v));   // quad_perm [2,3,0,1]
-  v = max(v, dpp_u32<0x124, 0xF>(v));  // row_ror 4
-  v = max(v, dpp_u32<0x128, 0xF>(v));  // row_ror 8
-  v = max(v, dpp_u32<0x142, 0xA>(v));  // row_bcast 15 -> rows 1, 3
-  v = max(v, dpp_u32<0x143, 0xC>(v));  // row_bcast 31 -> rows 2, 3
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
-// sum over all 64 lanes, returned uniformly
-__device__ __forceinline__ float wave_sum_f32(float v) {
-  v += dpp_f32<0xB1, 0xF>(v);
-  v += dpp_f32<0x4E, 0xF>(v);
-  v += dpp_f32<0x124, 0xF>(v);
-  v += dpp_f32<0x128, 0xF>(v);
-  v += dpp_f32<0x142, 0xA>(v);
-  v += dpp_f32<0x143, 0xC>(v);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// sum over each aligned group of W lanes (W = 16, 32 or 64); every lane of
-// the group gets the group sum
-template <int W>
-__device__ __forceinline__ float group_sum_f32(float v) {
-  v += dpp_f32<0xB1, 0xF>(v);
-  v += dpp_f32<0x4E, 0xF>(v);
-  v += dpp_f32<0x124, 0xF>(v);
-  v += dpp_f32<0x128, 0xF>(v);
-  if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
-// ---------------------------------------------------------------- routing
-
-__device__ __forceinline__ uint32_t ord16(uint32_t b) {
-  if (b == 0x8000u) b = 0;  // -0 == +0
-  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-}
-
-__device__ __forceinline__ float unord16(uint32_t o) {
-  const uint32_t b = (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
-  return bf16_to_f32(b);
-}
-
-template <int N>
-__device__ __forceinline__ void sort_desc(uint32_t (&v)[N]) {
-  // bitonic network, descending
-#pragma unroll
-  for (int k = 2; k <= N; k <<= 1)
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1)
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        const int l = i ^ j;
-        if (l > i) {
-          const bool desc = (i & k) == 0;
-          const uint32_t a = v[i], b = v[l];
-          const uint32_t hi = max(a, b), lo = min(a, b);
-          v[i] = desc ? hi : lo;
-          v[l] = desc ? lo : hi;
-        }
-      }
-}
-
-// Routing by one wave, in two steps so the caller can put other loads in
-// flight between them: route_keys issues the logit loads (lane l holds
-// experts l + 64 i); route_select sorts each lane's keys and runs `rounds`
-// rounds of a wave max. sel[r] = 32-bit key of rank r: high half = ordered
-// logit, low half = 0xffff - expert.
-template <int KPL>
-__device__ __forceinline__ void route_keys(const uint16_t *logits, int E, uint32_t (&key)[KPL]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int e = i * 64 + lane;
-    key[i] = logits[e < E ? e : 0];
-  }
-}
-
-template <int KPL>
-__device__ __forceinline__ void route_select(uint32_t (&key)[KPL], int E, int rounds,
-                                             uint32_t (&sel)[kFusedMaxSlots]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int e = i * 64 + lane;
-    key[i] = e < E ? ((ord16(key[i]) << 16) | (0xffffu - (uint32_t)e)) : 0u;
-  }
-  sort_desc<KPL>(key);
-#pragma unroll
-  for (int r = 0; r < kFusedMaxSlots; ++r) {
-    sel[r] = 0;
-    if (r < rounds) {
-      const uint32_t m = wave_max_u32(key[0]);
-      sel[r] = m;
-      const bool mine = key[0] == m;  // keys are unique
-#pragma unroll
-      for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
-      key[KPL - 1] = mine ? 0u : key[KPL - 1];
-    }
-  }
-}
-
-__device__ __forceinline__ int sel_expert(uint32_t key) { return (int)(0xffffu - (key & 0xffffu)); }
-__device__ __forceinline__ float sel_logit(uint32_t key) { return unord16(key >> 16); }
-
 // ---------------------------------------------------------------- kernel
 
 struct FusedGeom {
@@ -241,47 +121,6 @@ __device__ __forceinline__ void load_down(uint32_t (&w)[BITS], uint32_t &scr, ui
   const size_t p = (size_t)e * bd.p_stride + (size_t)dd * bd.m.ng + ll / (bd.m.gs >> 5);
   scr = bd.m.sc[p];
   bir = bd.m.bi[p];
-}
-
-// sum_k code_k * h_k over one 32-code chunk (LSB-first BITS-bit codes)
-template <int BITS>
-__device__ __forceinline__ float codes_dot(const uint32_t (&w)[BITS], const float (&h)[32]) {
-  float a0 = 0.f, a1 = 0.f;
-  if constexpr (BITS == 4) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // nibbles to bytes, then one v_cvt_f32_ubyteN per code (the empty asm
-      // keeps the compiler from folding the masks into per-code bfe's)
-      uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
-      asm volatile("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        a0 = fmaf((float)((lo >> (8 * b)) & 0xffu), h[8 * i + 2 * b], a0);
-        a1 = fmaf((float)((hi >> (8 * b)) & 0xffu), h[8 * i + 2 * b + 1], a1);
-      }
-    }
-  } else if constexpr (BITS == 8) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a0 = fmaf((float)(w[i] & 0xffu), h[4 * i], a0);
-      a1 = fmaf((float)((w[i] >> 8) & 0xffu), h[4 * i + 1], a1);
-      a0 = fmaf((float)((w[i] >> 16) & 0xffu), h[4 * i + 2], a0);
-      a1 = fmaf((float)(w[i] >> 24), h[4 * i + 3], a1);
-    }
-  } else {
-    constexpr uint32_t mask = (1u << BITS) - 1u;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      const int bit = k * BITS, i = bit >> 5, sh = bit & 31;
-      uint32_t c = w[i] >> sh;
-      if (sh + BITS > 32) c |= w[i + 1] << (32 - sh);
-      if (k & 1)
-        a1 = fmaf((float)(c & mask), h[k], a1);
-      else
-        a0 = fmaf((float)(c & mask), h[k], a0);
-    }
-  }
-  return a0 + a1;
 }
 
 // VPL consecutive (value, tag) pairs from byte offset off; positions at or
