@@ -195,8 +195,26 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
     if (a.sgate.m.w) {
       float g = 0.f;
       if (a.se_gate_vec) {
-        for (int j = lane; j < a.D; j += 64)
-          g = fmaf(bf16_to_f32(a.se_gate_vec[j]), bf16_to_f32(a.x[(size_t)t * a.D + j]), g);
+        // 16-byte loads, all in flight (chunk c = 8 bf16 per lane per step)
+        const int n8 = a.D >> 3;
+        for (int c0 = 0; c0 < n8; c0 += 256) {
+          uint4 gq[4], xq[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int c = min(c0 + v * 64 + lane, n8 - 1);
+            gq[v] = reinterpret_cast<const uint4 *>(a.se_gate_vec)[c];
+            xq[v] = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D)[c];
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            if (c0 + v * 64 + lane < n8) {
+              g = dot2(gq[v].x, xq[v].x, g);
+              g = dot2(gq[v].y, xq[v].y, g);
+              g = dot2(gq[v].z, xq[v].z, g);
+              g = dot2(gq[v].w, xq[v].w, g);
+            }
+          }
+        }
         g = team_sum<64>(g);
         g = 1.0f / (1.0f + __expf(-g));
       } else {
@@ -256,12 +274,13 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
     for (int q = 0; q < nwaves; ++q) ng += s_wave_tot[q] & 2047;
     w.group_off[ng] = nslots;
   }
-  // stable placement: position among equal experts follows slot order
+  // placement within a group in arrival order: every slot's arithmetic is
+  // independent of its position, so the results do not depend on it
+  for (int e = tid; e < a.E; e += kGroupThreads) s_cnt[e] = 0;
+  __syncthreads();
   for (int i = tid; i < nslots; i += kGroupThreads) {
     const int e = s_idx[i];
-    int before = 0;
-    for (int j = 0; j < i; ++j) before += (s_idx[j] == e);
-    w.entries[s_start[e] + before] = i;
+    w.entries[s_start[e] + atomicAdd(&s_cnt[e], 1)] = i;
   }
 }
 
@@ -466,15 +485,21 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
     bi[p] = live ? aux_to_f32_sel(rbi[p], dm.fp16) : 0.f;
   }
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  __shared__ __align__(16) float s_h[32 * LANES];
   for (int si = s0; si < s1; ++si) {
     const int slot = shared ? a.B * a.k + si : w.entries[si];
+    // h of the slot through LDS once per block (each of the RPP row groups
+    // needs all of it)
+    for (int v = threadIdx.x; v < 8 * Ck; v += 256)
+      reinterpret_cast<float4 *>(s_h)[v] = reinterpret_cast<const float4 *>(w.h + (size_t)slot * hmax)[v];
+    __syncthreads();
     float xf[32];
-    const float4 *src = reinterpret_cast<const float4 *>(w.h + (size_t)slot * hmax + 32 * cl);
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const float4 t = src[v];
+      const float4 t = reinterpret_cast<const float4 *>(s_h)[8 * cl + v];
       xf[4 * v + 0] = t.x; xf[4 * v + 1] = t.y; xf[4 * v + 2] = t.z; xf[4 * v + 3] = t.w;
     }
+    __syncthreads();
     float xt[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) xt[v] = xf[v] + xf[v + 16];
