@@ -14,15 +14,20 @@
 //
 // Launch structure (all on one stream):
 //   1. moe_route_group_kernel   one block: route every token, shared-expert
-//                               gate, group (token, rank) slots by expert
-//   2. moe_gateup_kernel        per (expert group, row block): gate and up
-//                               rows unpacked once, applied to every token of
-//                               the group, SwiGLU fused -> h[slot][j] (f32)
-//   3. moe_down_kernel          per (expert group, row block): down rows
-//                               unpacked once, applied to h of every slot
-//                               -> y[slot][d] (f32)
-//   4. moe_combine_kernel       out[t][d] = sum_r w_r y[t,r][d] (rank order)
-//                               + gs_t * y[t,shared][d] -> bf16
+//                               gate, x of every token as bf16 pairs, group
+//                               the (token, rank) slots by expert: one record
+//                               per group (expert, first row, rows, first
+//                               tokens) and a grouped row per slot
+//   2. moe_gateup_kernel        per (group, 16 rows): gate and up rows loaded
+//                               once, applied to every token of the group,
+//                               SwiGLU fused -> h[grouped row][j] (f32)
+//   3. moe_down_kernel          per (group, 32 rows): down rows loaded once,
+//                               applied to h of every row of the group
+//                               -> y[grouped row][d] (f32)
+//   4. moe_combine_kernel       out[t][d] = sum_r w_r y[row(t,r)][d] (rank
+//                               order) + gs_t * y[shared row t][d] -> bf16
+// A group's record carries what its blocks need first, so each block starts
+// its weight and activation loads after one dependent load.
 #include <cstdlib>
 
 #include "affine_dev.hpp"
@@ -72,11 +77,15 @@ hipError_t launch_route_topk(const void *logits, int logits_f32, int B, int E, i
 // ---------------------------------------------------------------------------
 // Workspace layout (all offsets 256-byte aligned).
 
+// Grouped order: the B*k routed (token, rank) slots sorted by expert (one
+// group per distinct expert), then the B shared-expert slots. h and y rows
+// are stored in grouped order, so a group's rows are contiguous.
+constexpr int kRecInts = 8;  // group record: expert, first grouped row, rows, tokens[0..3], 0
 struct MoeWs {
   int *n_groups;      // [1]  routed groups
-  int *group_expert;  // [G]
-  int *group_off;     // [G+1] into entries
-  int *entries;       // [B*k] routed slot ids, grouped by expert
+  int *rec;           // [G+1][kRecInts]; rec[G] is the shared expert's
+  int *tok;           // [B*k] token of each grouped routed row
+  int *gpos;          // [B*k] grouped row of slot t*k + r
   int32_t *topk_idx;  // [B*k]
   float *topk_w;      // [B*k]
   float *gs;          // [B]
@@ -102,9 +111,9 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
     return p;
   };
   w.n_groups = reinterpret_cast<int *>(take(sizeof(int)));
-  w.group_expert = reinterpret_cast<int *>(take(sizeof(int) * (G + 1)));
-  w.group_off = reinterpret_cast<int *>(take(sizeof(int) * (G + 2)));
-  w.entries = reinterpret_cast<int *>(take(sizeof(int) * (size_t)B * k));
+  w.rec = reinterpret_cast<int *>(take(sizeof(int) * (G + 1) * kRecInts));
+  w.tok = reinterpret_cast<int *>(take(sizeof(int) * (size_t)B * k));
+  w.gpos = reinterpret_cast<int *>(take(sizeof(int) * (size_t)B * k));
   w.topk_idx = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * (size_t)B * k));
   w.topk_w = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B * k));
   w.gs = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B));
@@ -173,6 +182,8 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
   __shared__ int s_cnt[kMaxE];
   __shared__ int s_start[kMaxE];
   __shared__ int s_gid[kMaxE];
+  __shared__ int s_fill[kMaxE];
+  __shared__ int s_tok[kMaxB * kMaxK];
   __shared__ int s_wave_tot[kGroupThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = kGroupThreads / 64;
@@ -260,56 +271,39 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
       *w.n_groups = tot & 2047;
     }
   }
-  __syncthreads();
-  for (int e = tid; e < a.E; e += kGroupThreads) {
-    if (s_cnt[e] > 0) {
-      const int g = s_gid[e];
-      w.group_expert[g] = e;
-      w.group_off[g] = s_start[e];
-    }
-  }
-  if (tid == 0) {
-    // group_off[n_groups] = nslots (the routed entries end)
-    int ng = 0;
-    for (int q = 0; q < nwaves; ++q) ng += s_wave_tot[q] & 2047;
-    w.group_off[ng] = nslots;
-  }
-  // placement within a group in arrival order: every slot's arithmetic is
+  // placement within a group in arrival order: every row's arithmetic is
   // independent of its position, so the results do not depend on it
-  for (int e = tid; e < a.E; e += kGroupThreads) s_cnt[e] = 0;
+  for (int e = tid; e < a.E; e += kGroupThreads) s_fill[e] = 0;
   __syncthreads();
   for (int i = tid; i < nslots; i += kGroupThreads) {
     const int e = s_idx[i];
-    w.entries[s_start[e] + atomicAdd(&s_cnt[e], 1)] = i;
+    const int gp = s_start[e] + atomicAdd(&s_fill[e], 1);
+    s_tok[gp] = i / a.k;
+    w.tok[gp] = i / a.k;
+    w.gpos[i] = gp;
+  }
+  __syncthreads();
+  // one record per group (and the shared expert's at index G)
+  const int G = nslots < a.E ? nslots : a.E;
+  for (int e = tid; e < a.E; e += kGroupThreads) {
+    const int c = s_cnt[e];
+    if (c > 0) {
+      const int off = s_start[e];
+      int4 *r = reinterpret_cast<int4 *>(w.rec + (size_t)s_gid[e] * kRecInts);
+      r[0] = make_int4(e, off, c, s_tok[off]);
+      r[1] = make_int4(c > 1 ? s_tok[off + 1] : 0, c > 2 ? s_tok[off + 2] : 0,
+                       c > 3 ? s_tok[off + 3] : 0, 0);
+    }
+  }
+  if (tid == 0) {
+    int4 *r = reinterpret_cast<int4 *>(w.rec + (size_t)G * kRecInts);
+    r[0] = make_int4(0, nslots, a.B, 0);
+    r[1] = make_int4(1, 2, 3, 0);
   }
 }
 
 // ---------------------------------------------------------------------------
 // 2. gate/up + SwiGLU
-
-struct GroupView {
-  const uint8_t *gw, *uw;
-  const uint16_t *gsc, *gbi, *usc, *ubi;
-  int rows;       // inter of this expert
-  int slot_begin, slot_end;
-  bool shared;
-};
-
-__device__ __forceinline__ bool moe_item_group(const MoeArgs &a, const MoeWs &w, int ng, int ipg,
-                                               int ipg_s, int item, int &g, int &rb) {
-  if (item < ng * ipg) {
-    g = item / ipg;
-    rb = item % ipg;
-    return true;
-  }
-  const int si = item - ng * ipg;
-  if (a.sgate.m.w && si < ipg_s) {
-    g = -1;
-    rb = si;
-    return true;
-  }
-  return false;
-}
 
 // One block: RPB = 16 rows of gate and of up (4 per wave, a wave spans the
 // whole row: CPL chunks per lane) of one expert group, applied to every token
@@ -323,15 +317,19 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
   const int C = a.D >> 5;
   UnpackConsts kc;
   kc.init();
+  const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
   const int item = blockIdx.x;
-  const bool shared = item >= ipg * (a.B * a.k < a.E ? a.B * a.k : a.E);
-  const int g = shared ? -1 : item / ipg;
-  const int rb = shared ? item - ipg * (a.B * a.k < a.E ? a.B * a.k : a.E) : item % ipg;
+  const bool shared = item >= ipg * G;
+  const int g = shared ? G : item / ipg;
+  const int rb = shared ? item - ipg * G : item % ipg;
+  // one load round for the group: its record carries the first tokens
   const int ng = *w.n_groups;
-  const int ge = shared ? 0 : w.group_expert[g < 0 ? 0 : g];
-  const int s0 = shared ? 0 : w.group_off[g < 0 ? 0 : g];
-  const int s1 = shared ? a.B : w.group_off[(g < 0 ? 0 : g) + 1];
+  const int4 rc0 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[0];
+  const int4 rc1 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[1];
   if (shared ? (a.sgate.m.w == nullptr || rb >= ipg_s) : g >= ng) return;
+  const int ge = rc0.x;
+  const int off = __builtin_amdgcn_readfirstlane(rc0.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(rc0.z);
   const DevMat gm = shared ? a.sgate.m : a.gate.m;
   const DevMat um = shared ? a.sup.m : a.up.m;
   const long long gws = shared ? a.sgate.w_stride : a.gate.w_stride;
@@ -370,6 +368,22 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
       rsu[u][i] = usc[p];
       rbu[u][i] = ubi[p];
     }
+  // token 0's x pairs ride with the weights
+  uint32_t xpn[CPL][16];
+  float2 xsn[CPL];
+  auto load_x = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const size_t xo = (size_t)t * C + min(lane + 64 * i, C - 1);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint4 q = reinterpret_cast<const uint4 *>(w.xp + xo * 16)[v];
+        xpn[i][4 * v] = q.x; xpn[i][4 * v + 1] = q.y; xpn[i][4 * v + 2] = q.z; xpn[i][4 * v + 3] = q.w;
+      }
+      xsn[i] = reinterpret_cast<const float2 *>(w.xps)[xo];
+    }
+  };
+  load_x(__builtin_amdgcn_readfirstlane(rc0.w));
   __builtin_amdgcn_sched_barrier(0);
   // the packed rows stay in registers; each token unpacks them again (groups
   // hold one or two tokens in the common case)
@@ -385,7 +399,7 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
       bu[u][i] = live ? aux_to_f32_sel(rbu[u][i], um.fp16) : 0.f;
     }
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
-  for (int si = s0; si < s1; ++si) {
+  for (int i_t = 0; i_t < cnt; ++i_t) {
     // keep the unpack inside the loop (not hoisted into 128 live registers)
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -393,29 +407,24 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
       for (int i = 0; i < CPL; ++i)
 #pragma unroll
         for (int q = 0; q < BITS; ++q) asm volatile("" : "+v"(wg[u][i][q]), "+v"(wu[u][i][q]));
-    const int slot = shared ? a.B * a.k + si : w.entries[si];
-    const int t = shared ? si : slot / a.k;
+    if (i_t > 0) {
+      const int t = shared ? i_t
+                           : (i_t == 1 ? rc1.x
+                                       : i_t == 2 ? rc1.y : i_t == 3 ? rc1.z : w.tok[off + i_t]);
+      load_x(__builtin_amdgcn_readfirstlane(t));
+    }
     float pg[U], pu[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) pg[u] = pu[u] = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = min(lane + 64 * i, C - 1);
-      const size_t xo = (size_t)t * C + c;
-      uint32_t xp[16];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint4 q = reinterpret_cast<const uint4 *>(w.xp + xo * 16)[v];
-        xp[4 * v] = q.x; xp[4 * v + 1] = q.y; xp[4 * v + 2] = q.z; xp[4 * v + 3] = q.w;
-      }
-      const float2 xsum = reinterpret_cast<const float2 *>(w.xps)[xo];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         uint32_t q[16];
         unpack_chunk<BITS>(q, wg[u][i], kc);
-        pg[u] += chunk_fold<BITS>(pairs_dot(q, xp), sg[u][i], bg[u][i], xsum.x, xsum.y);
+        pg[u] += chunk_fold<BITS>(pairs_dot(q, xpn[i]), sg[u][i], bg[u][i], xsn[i].x, xsn[i].y);
         unpack_chunk<BITS>(q, wu[u][i], kc);
-        pu[u] += chunk_fold<BITS>(pairs_dot(q, xp), su[u][i], bu[u][i], xsum.x, xsum.y);
+        pu[u] += chunk_fold<BITS>(pairs_dot(q, xpn[i]), su[u][i], bu[u][i], xsn[i].x, xsn[i].y);
       }
     }
     // lane row r (lane / 16) gets row j0 + r: h = silu(gate) * up
@@ -423,33 +432,37 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
     const float gv = wave_reduce4(pg[0], pg[1], pg[2], pg[3]);
     const float uv = wave_reduce4(pu[0], pu[1], pu[2], pu[3]);
     const int r = lane >> 4;
-    if ((lane & 15) == 0 && j0 + r < rows) w.h[(size_t)slot * hmax + j0 + r] = silu(gv) * uv;
+    if ((lane & 15) == 0 && j0 + r < rows) w.h[(size_t)(off + i_t) * hmax + j0 + r] = silu(gv) * uv;
   }
 }
 
 // ---------------------------------------------------------------------------
 // 3. down projection of h for every slot of a group
 
-// One block: 32 output rows d of one expert group's down projection (a row
+constexpr int kDownRows = 32;  // output rows per down block
+
+// One block: kDownRows output rows d of one expert group's down projection (a row
 // per LANES lanes, PASSES rows per lane), applied to h of every slot of the
 // group with f32 FMAs: y = scale * sum code*h + bias * sum h.
 template <int BITS, int LANES>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int ipg) {
+  constexpr int kHq = LANES / 8;     // float4 of one h row per thread (K <= 32 * LANES)
   constexpr int RPP = 256 / LANES;  // rows per pass of the block
-  constexpr int PASSES = 32 / RPP;
+  constexpr int PASSES = kDownRows / RPP;
   const int lane = threadIdx.x & 63;
   const int lb = threadIdx.x % LANES;
   const int rsub = threadIdx.x / LANES;
   const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
   const int item = blockIdx.x;
   const bool shared = item >= G * ipg;
-  const int g = shared ? -1 : item / ipg;
+  const int g = shared ? G : item / ipg;
   const int rb = shared ? item - G * ipg : item % ipg;
   const int ng = *w.n_groups;
-  const int ge = shared ? 0 : w.group_expert[g < 0 ? 0 : g];
-  const int s0 = shared ? 0 : w.group_off[g < 0 ? 0 : g];
-  const int s1 = shared ? a.B : w.group_off[(g < 0 ? 0 : g) + 1];
+  const int4 rc0 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[0];
   if (shared ? a.sdown.m.w == nullptr : g >= ng) return;
+  const int ge = rc0.x;
+  const int off = __builtin_amdgcn_readfirstlane(rc0.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(rc0.z);
   const DevMat dm = shared ? a.sdown.m : a.down.m;
   const long long dws = shared ? a.sdown.w_stride : a.down.w_stride;
   const long long dps = shared ? a.sdown.p_stride : a.down.p_stride;
@@ -459,7 +472,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   const uint8_t *wb = dm.w + (size_t)e * dws;
   const uint16_t *scb = dm.sc + (size_t)e * dps;
   const uint16_t *bib = dm.bi + (size_t)e * dps;
-  const int d0 = rb * 32;
+  const int d0 = rb * kDownRows;
   const int cl = min(lb, Ck - 1);
   const int gi = cl / (dm.gs >> 5);
 
@@ -476,6 +489,19 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
     rs[p] = scb[(size_t)d * dm.ng + gi];
     rbi[p] = bib[(size_t)d * dm.ng + gi];
   }
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  // the group's first h row (K floats, 2 per thread for K <= 512) rides with
+  // the weights
+  auto load_h = [&](int row, float4 (&hq)[kHq]) {
+#pragma unroll
+    for (int v = 0; v < kHq; ++v) {
+      const int o = threadIdx.x + 256 * v;
+      hq[v] = o < 8 * Ck ? reinterpret_cast<const float4 *>(w.h + (size_t)row * hmax)[o]
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float4 hq[kHq];
+  load_h(off, hq);
   __builtin_amdgcn_sched_barrier(0);
   float sc[PASSES], bi[PASSES];
 #pragma unroll
@@ -484,14 +510,16 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
     sc[p] = live ? aux_to_f32_sel(rs[p], dm.fp16) : 0.f;
     bi[p] = live ? aux_to_f32_sel(rbi[p], dm.fp16) : 0.f;
   }
-  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   __shared__ __align__(16) float s_h[32 * LANES];
-  for (int si = s0; si < s1; ++si) {
-    const int slot = shared ? a.B * a.k + si : w.entries[si];
-    // h of the slot through LDS once per block (each of the RPP row groups
+  for (int i_t = 0; i_t < cnt; ++i_t) {
+    // h of the row through LDS once per block (each of the RPP row groups
     // needs all of it)
-    for (int v = threadIdx.x; v < 8 * Ck; v += 256)
-      reinterpret_cast<float4 *>(s_h)[v] = reinterpret_cast<const float4 *>(w.h + (size_t)slot * hmax)[v];
+    if (i_t > 0) load_h(off + i_t, hq);
+#pragma unroll
+    for (int v = 0; v < kHq; ++v) {
+      const int o = threadIdx.x + 256 * v;
+      if (o < 8 * Ck) reinterpret_cast<float4 *>(s_h)[o] = hq[v];
+    }
     __syncthreads();
     float xf[32];
 #pragma unroll
@@ -512,7 +540,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
       float v = fmaf(sc[p], codes_dot<BITS>(wv[p], xf), bi[p] * xt[0]);
       v = team_sum<LANES>(v);
       const int d = d0 + p * RPP + rsub;
-      if (lb == 0 && d < a.D) w.y[(size_t)slot * a.D + d] = v;
+      if (lb == 0 && d < a.D) w.y[(size_t)(off + i_t) * a.D + d] = v;
     }
   }
 }
@@ -527,12 +555,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a, MoeWs w) {
     float acc = 0.f;
     for (int r = 0; r < a.k; ++r) {
       const int slot = t * a.k + r;
-      acc = fmaf(w.y[(size_t)slot * a.D + d], w.topk_w[slot], acc);
+      acc = fmaf(w.y[(size_t)w.gpos[slot] * a.D + d], w.topk_w[slot], acc);
     }
     float o = acc;
     if (a.sdown.m.w) {
-      const int slot = a.B * a.k + t;
-      o = fmaf(w.y[(size_t)slot * a.D + d], w.gs[t], acc);
+      const int row = a.B * a.k + t;  // shared rows follow the routed ones
+      o = fmaf(w.y[(size_t)row * a.D + d], w.gs[t], acc);
     }
     if (a.out_f32)
       reinterpret_cast<float *>(a.out)[i] = o;
@@ -561,11 +589,11 @@ static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
       return 0;
     if (hipGetLastError() != hipSuccess) return -1;
   }
-  // down: 32 rows per block
+  // down: kDownRows rows per block
   {
     const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
     const int Ci = kmax >> 5;
-    const int ipg = (a.D + 31) / 32;
+    const int ipg = (a.D + kDownRows - 1) / kDownRows;
     const int grid = (G + (a.sdown.m.w ? 1 : 0)) * ipg;
     if (Ci <= 16) hipLaunchKernelGGL((moe_down_kernel<BITS, 16>), dim3(grid), dim3(256), 0, st, a, w, ipg);
     else if (Ci <= 32) hipLaunchKernelGGL((moe_down_kernel<BITS, 32>), dim3(grid), dim3(256), 0, st, a, w, ipg);
