@@ -157,6 +157,16 @@ typedef struct LoganHipAffine {
 int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                           int y_stride, int y_dtype, void *stream);
 
+/* Prefill / large-batch form of the same product on MFMA, with the
+ * reference QMM's numerics (logan-metal/metal/backend_metal.mm:1480-1560,
+ * spark_qmm_affine8_t16o8): every dequantised weight code*scale + bias is
+ * rounded to bf16 (RNE) before bf16 x bf16 products are accumulated in f32.
+ * x bf16 [M][x_stride], y bf16 (RNE) or f32. I must be a multiple of 64 and
+ * group_size a multiple of 32. 1 ok, 0 unsupported geometry, -1 launch
+ * failure. */
+int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
+                         int y_stride, int y_dtype, void *stream);
+
 /* Same product with f32 activations and f32 output, exact per-element
  * dequantisation (any group size dividing I). */
 int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,

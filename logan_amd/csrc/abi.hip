@@ -565,6 +565,18 @@ int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_s
                                       reinterpret_cast<hipStream_t>(stream)));
 }
 
+int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
+                         int y_stride, int y_dtype, void *stream) {
+  if (!affine_ok(w) || !x || !y || M <= 0 || x_stride < w->I || y_stride < w->O) return 0;
+  if (y_dtype != LOGAN_HIP_F32 && y_dtype != LOGAN_HIP_BF16) return 0;
+  const lh::DevMat m = devmat(*w);
+  if (!lh::affine_qmm_supported(m)) return 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return 0;
+  return rc_from(lh::launch_affine_qmm(m, reinterpret_cast<const uint16_t *>(x), x_stride, M, y,
+                                       y_stride, y_dtype == LOGAN_HIP_BF16,
+                                       reinterpret_cast<hipStream_t>(stream)));
+}
+
 int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,
                               float *y, int y_stride, void *stream) {
   if (!affine_ok(w) || !x || !y || M <= 0 || x_stride < w->I || y_stride < w->O) return 0;

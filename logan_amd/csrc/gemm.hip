@@ -1,0 +1,174 @@
+// Prefill / large-batch product with MLX-affine weights on MFMA (gfx950):
+//   y[m][n] = sum_k x[m][k] * bf16(code[n][k] * scale[n][k/gs] + bias[n][k/gs])
+// the semantics of logan-metal's QMM (backend_metal.mm:1480-1560: each
+// dequantised weight rounded to bf16 in threadgroup memory, bf16 x bf16
+// products accumulated in f32, bf16 output).
+//
+// One block computes a 64 x 64 tile of y (4 waves, each a 32 x 32 tile with
+// v_mfma_f32_32x32x16_bf16). Per 64-wide k step the block dequantises its 64
+// weight rows into LDS (codes -> f32 fma -> v_cvt_pk_bf16_f32), while every
+// lane loads its x operands straight from global memory (x rows are re-read
+// by the N/64 blocks of a row block and stay in L2). Operand layout of the
+// 32x32x16 instruction (checked on the device): lane l holds row (col) l % 32
+// and 8 consecutive k at offset 8 * (l / 32) of each 16-wide k slice; the
+// result's element i of lane l is row 8 * (i / 4) + 4 * (l / 32) + i % 4,
+// column l % 32.
+#include "affine_dev.hpp"
+#include "lh_internal.hpp"
+
+namespace lh {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct GemmParams {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  const uint16_t *x;
+  void *y;
+  long long row_bytes;
+  int M, N, K, ng, gs, fp16, x_stride, y_stride, y_bf16;
+};
+
+constexpr int kTile = 64;        // block tile (m and n) and k step
+constexpr int kLdsStride = 72;   // bf16 per LDS row: 64 + 8 pad (no bank conflicts)
+
+// Codes per dequantising thread: 16 (4 per row of 64) for widths whose
+// 16-code runs start on a dword boundary; 5-bit runs of 32 codes (2 per row).
+template <int BITS>
+struct DeqGeom {
+  static constexpr int CPT = BITS == 5 ? 32 : 16;
+  static constexpr int THREADS = kTile * (kTile / CPT);  // 256 or 128
+  static constexpr int DW = CPT * BITS / 32;             // dwords of codes
+};
+
+template <int BITS>
+__device__ __forceinline__ uint32_t code_of(const uint32_t (&w)[DeqGeom<BITS>::DW], int j) {
+  const int bit = j * BITS, i = bit >> 5, sh = bit & 31;
+  uint32_t c = w[i] >> sh;
+  if (sh + BITS > 32) c |= w[i + 1] << (32 - sh);
+  return c & ((1u << BITS) - 1u);
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
+  using G = DeqGeom<BITS>;
+  __shared__ __align__(16) __bf16 sW[kTile * kLdsStride];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bm0 = blockIdx.x * kTile, bn0 = blockIdx.y * kTile;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  // dequantising role: row n = tid / (64 / CPT), codes [kq, kq + CPT)
+  const int dn = tid / (kTile / G::CPT);
+  const int kq = (tid % (kTile / G::CPT)) * G::CPT;
+  const bool deq = tid < G::THREADS;
+  const int nrow = min(bn0 + dn, p.N - 1);
+  const uint8_t *wrow = p.w + (size_t)nrow * p.row_bytes;
+  const uint16_t *srow = p.sc + (size_t)nrow * p.ng;
+  const uint16_t *brow = p.bi + (size_t)nrow * p.ng;
+
+  // x operand row of this lane (clamped; rows past M are never stored)
+  const int xm = min(bm0 + wm * 32 + l32, p.M - 1);
+  const uint16_t *xrow = p.x + (size_t)xm * p.x_stride;
+
+  f32x16 acc = {};
+  for (int k0 = 0; k0 < p.K; k0 += kTile) {
+    // issue this step's loads: codes, scale/bias, x operands
+    uint32_t wv[G::DW];
+    uint32_t sraw = 0, braw = 0;
+    if (deq) {
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(wrow + (size_t)(k0 + kq) * BITS / 8);
+#pragma unroll
+      for (int i = 0; i < G::DW; ++i) wv[i] = src[i];
+      const int gidx = (k0 + kq) / p.gs;
+      sraw = srow[gidx];
+      braw = brow[gidx];
+    }
+    uint4 xa[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      xa[ks] = *reinterpret_cast<const uint4 *>(xrow + k0 + 16 * ks + 8 * half);
+    __builtin_amdgcn_sched_barrier(0);
+    if (deq) {
+      const float s = aux_to_f32_sel(sraw, p.fp16), b = aux_to_f32_sel(braw, p.fp16);
+      uint32_t packed[G::CPT / 2];
+#pragma unroll
+      for (int j = 0; j < G::CPT; j += 2) {
+        bf16x2 v;
+        v[0] = (__bf16)fmaf((float)code_of<BITS>(wv, j), s, b);
+        v[1] = (__bf16)fmaf((float)code_of<BITS>(wv, j + 1), s, b);
+        packed[j / 2] = __builtin_bit_cast(uint32_t, v);
+      }
+      uint4 *dst = reinterpret_cast<uint4 *>(sW + dn * kLdsStride + kq);
+#pragma unroll
+      for (int v = 0; v < G::CPT / 8; ++v)
+        dst[v] = make_uint4(packed[4 * v], packed[4 * v + 1], packed[4 * v + 2], packed[4 * v + 3]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = __builtin_bit_cast(bf16x8, xa[ks]);
+      const bf16x8 b = *reinterpret_cast<const bf16x8 *>(sW + (wn * 32 + l32) * kLdsStride + 16 * ks +
+                                                        8 * half);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // store: element i of this lane is (row 8*(i/4) + 4*half + i%4, col l32)
+  const int n = bn0 + wn * 32 + l32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int m = bm0 + wm * 32 + 8 * (i / 4) + 4 * half + (i % 4);
+    if (m < p.M && n < p.N) {
+      if (p.y_bf16)
+        reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)acc[i];
+      else
+        reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = acc[i];
+    }
+  }
+}
+
+bool affine_qmm_supported(const DevMat &m) {
+  if (!(m.bits == 4 || m.bits == 5 || m.bits == 6 || m.bits == 8)) return false;
+  if (m.I <= 0 || m.I % kTile != 0 || m.O <= 0) return false;
+  if (m.gs <= 0 || m.gs % 32 != 0 || m.I % m.gs != 0) return false;
+  if (m.row_bytes != (long long)m.I * m.bits / 8) return false;
+  if ((m.row_bytes & 3) != 0 || (reinterpret_cast<uintptr_t>(m.w) & 3) != 0) return false;
+  return true;
+}
+
+hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                             int y_stride, int y_bf16, hipStream_t st) {
+  if (!affine_qmm_supported(m) || M <= 0) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  GemmParams p;
+  p.w = m.w;
+  p.sc = m.sc;
+  p.bi = m.bi;
+  p.x = x;
+  p.y = y;
+  p.row_bytes = m.row_bytes;
+  p.M = M;
+  p.N = m.O;
+  p.K = m.I;
+  p.ng = m.ng;
+  p.gs = m.gs;
+  p.fp16 = m.fp16;
+  p.x_stride = x_stride;
+  p.y_stride = y_stride;
+  p.y_bf16 = y_bf16;
+  const dim3 grid((M + kTile - 1) / kTile, (m.O + kTile - 1) / kTile);
+  switch (m.bits) {
+    case 4: hipLaunchKernelGGL(affine_qmm_kernel<4>, grid, dim3(256), 0, st, p); break;
+    case 5: hipLaunchKernelGGL(affine_qmm_kernel<5>, grid, dim3(256), 0, st, p); break;
+    case 6: hipLaunchKernelGGL(affine_qmm_kernel<6>, grid, dim3(256), 0, st, p); break;
+    case 8: hipLaunchKernelGGL(affine_qmm_kernel<8>, grid, dim3(256), 0, st, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lh

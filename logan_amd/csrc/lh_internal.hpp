@@ -24,6 +24,12 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
                             void *y, int y_stride, int y_bf16, hipStream_t st);
 bool gemv_bf16_supported(const DevMat &m);
 
+// ---- prefill / large-batch product on MFMA: bf16-rounded dequantised
+// weights (the reference QMM semantics), x bf16 [M, I], y [M, O] ----
+hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                             int y_stride, int y_bf16, hipStream_t st);
+bool affine_qmm_supported(const DevMat &m);
+
 // ---- generic GEMV over up to 16 descriptors, f32 activations ----
 struct GenDesc {
   const uint8_t *w;

@@ -104,6 +104,26 @@ def affine_gemv(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = 
     return out
 
 
+def affine_qmm(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+               out_dtype: torch.dtype = torch.bfloat16, stream=None) -> torch.Tensor:
+    """Prefill product on MFMA with the reference QMM numerics: y[M, O] =
+    x[M, I] . bf16(W)^T (logan-metal/metal/backend_metal.mm:1480-1560)."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    x2 = x.reshape(-1, w.I)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((M, w.O), dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("out must be bf16 or f32")
+    yd = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    a = w.c()
+    rc = L.lib().logan_hip_affine_qmm(C.byref(a), _dev(x2, "x"), M, w.I, _dev(out, "out"), w.O,
+                                      yd, _stream(stream))
+    _check(rc, "affine_qmm")
+    return out
+
+
 def affine_gemv_f32(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                     stream=None) -> torch.Tensor:
     """f32 activations, exact per-element dequantisation, f32 output."""

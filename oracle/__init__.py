@@ -57,6 +57,8 @@ def lib() -> C.CDLL:
         h.lo_affine_gemv_mt.argtypes = [P, P, P, P, P, SZ, SZ, I, SZ, I, I]
         h.lo_spark_affine8_gemv.restype = None
         h.lo_spark_affine8_gemv.argtypes = [P, P, P, P, SZ, SZ]
+        h.lo_affine_qmm_bf16.restype = None
+        h.lo_affine_qmm_bf16.argtypes = [P, P, P, P, P, SZ, SZ, SZ, I, SZ, I]
         h.lo_silu.restype = C.c_float
         h.lo_silu.argtypes = [C.c_float]
         h.lo_softmax_row.restype = None
@@ -110,6 +112,19 @@ def affine_gemv(x: np.ndarray, w, sc, bi, O, I, bits, gs, fp16=False, nthreads=N
         lib().lo_affine_gemv(_p(y), _p(x), _p(w), _p(sc), _p(bi), O, I, bits, gs, int(fp16))
     else:
         lib().lo_affine_gemv_mt(_p(y), _p(x), _p(w), _p(sc), _p(bi), O, I, bits, gs, int(fp16), t)
+    return y
+
+
+def affine_qmm_bf16(x: np.ndarray, w, sc, bi, O, I, bits, gs, fp16=False) -> np.ndarray:
+    """Y[M, O] = X[M, I] . bf16(W)^T, f32 accumulation
+    (logan-metal/metal/backend_metal.mm:1480-1560)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, I)
+    M = x.shape[0]
+    y = np.empty((M, O), np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(sc).view(np.uint8)
+    bi = np.ascontiguousarray(bi).view(np.uint8)
+    lib().lo_affine_qmm_bf16(_p(y), _p(x), _p(w), _p(sc), _p(bi), M, O, I, bits, gs, int(fp16))
     return y
 
 

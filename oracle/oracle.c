@@ -141,6 +141,39 @@ void lo_affine_gemv(float *y, const float *x, const uint8_t *w,
                             fp16);
 }
 
+/* logan-metal/metal/backend_metal.mm:1480-1560 (spark_qmm_affine8_t16o8):
+ * the prefill product with every dequantised weight rounded to bf16 (RNE,
+ * logan-core/src/math.rs:279-283) before the products, accumulated in f32.
+ * x[m * i + k] are the (bf16-valued) activations; y[m * o + n] f32 before the
+ * caller's bf16 rounding. Sequential k order. */
+void lo_affine_qmm_bf16(float *y, const float *x, const uint8_t *w,
+                        const uint8_t *scales, const uint8_t *biases, size_t m,
+                        size_t o, size_t i, int bits, size_t group_size,
+                        int fp16) {
+  size_t row_bytes = i * (size_t)bits / 8;
+  size_t groups = i / group_size;
+  float *wq = (float *)malloc(sizeof(float) * i);
+  for (size_t n = 0; n < o; ++n) {
+    const uint8_t *wr = w + n * row_bytes;
+    for (size_t k = 0; k < i; ++k) {
+      size_t group = n * groups + k / group_size;
+      float value = (float)lo_affine_code(wr, k, bits) *
+                    lo_affine_param(scales, group, fp16);
+      value = value + lo_affine_param(biases, group, fp16);
+      wq[k] = lo_bf16_to_f32(lo_f32_to_bf16(value));
+    }
+    for (size_t r = 0; r < m; ++r) {
+      float sum = 0.0f;
+      for (size_t k = 0; k < i; ++k) {
+        float prod = wq[k] * x[r * i + k];
+        sum = sum + prod;
+      }
+      y[r * o + n] = sum;
+    }
+  }
+  free(wq);
+}
+
 typedef struct gemv_job {
   float *y;
   const float *x;

@@ -58,6 +58,13 @@ void lo_affine_gemv_mt(float *y, const float *x, const uint8_t *w,
 void lo_spark_affine8_gemv(float *y, const float *x, const uint8_t *w,
                            const uint8_t *aux, size_t o, size_t i);
 
+/* logan-metal/metal/backend_metal.mm:1480-1560: prefill product with the
+ * dequantised weights rounded to bf16, f32 accumulation; y[m][o]. */
+void lo_affine_qmm_bf16(float *y, const float *x, const uint8_t *w,
+                        const uint8_t *scales, const uint8_t *biases, size_t m,
+                        size_t o, size_t i, int bits, size_t group_size,
+                        int fp16);
+
 /* logan-qwen4/src/lib.rs:4516-4518. */
 float lo_silu(float x);
 /* logan-qwen4/src/lib.rs:4558-4574 (= logan-qwen/src/lib.rs:260-276). */

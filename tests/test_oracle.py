@@ -253,3 +253,40 @@ def test_moe_expert_source_closed_form():
             assert np.all(out == 0.0)
         else:
             assert np.all(np.abs(out - want) <= abs(want) * c["rel_tol"])
+
+
+def _bf16_round_torch(a: np.ndarray) -> np.ndarray:
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def test_qmm_closed_form():
+    """Constant code 3, scale bf16(0.1), bias 0: every weight is bf16(3 * 0.1)
+    (not 3 * 0.1) and y = 64 * that weight for x = 1 (exact in f32)."""
+    M, O, I, bits, gs = 2, 4, 64, 8, 64
+    w = np.full((O, I), 3, np.uint8)
+    sc = bf16_bits(np.full(O * (I // gs), 0.1, np.float32))
+    bi = bf16_bits(np.zeros(O * (I // gs), np.float32))
+    y = oracle.affine_qmm_bf16(np.ones((M, I), np.float32), w, sc, bi, O, I, bits, gs)
+    wq = _bf16_round_torch(np.float32(3.0) * bf16_to_f32(sc[:1]))[0]
+    assert wq != np.float32(3.0) * bf16_to_f32(sc[:1])[0]  # the rounding is visible
+    np.testing.assert_array_equal(y, np.full((M, O), 64 * wq, np.float32))
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (5, 32), (6, 128), (8, 64)])
+def test_qmm_against_float64_of_bf16_weights(bits, gs):
+    """The prefill oracle equals a float64 product of the bf16-rounded
+    (torch RNE) float64 dequantisation, to f32 accumulation error; without
+    the rounding it would sit ~1e-3 away."""
+    rng = np.random.default_rng(bits * 13 + gs)
+    M, O, I = 5, 48, 512
+    w, sc, bi = make_affine(rng, O, I, bits, gs)
+    x = bf16_to_f32(make_x(rng, M, I)).reshape(M, I)
+    y = oracle.affine_qmm_bf16(x, w, sc, bi, O, I, bits, gs)
+    wd = dequant_f64(w, sc, bi, O, I, bits, gs)
+    wq = _bf16_round_torch(wd.astype(np.float32)).astype(np.float64)
+    ref = x.astype(np.float64) @ wq.T
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-5
+    unrounded = x.astype(np.float64) @ wd.T
+    assert np.abs(unrounded - ref).max() / np.abs(ref).max() > 1e-4
