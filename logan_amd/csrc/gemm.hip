@@ -75,11 +75,14 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
   const int xm = min(bm0 + wm * 32 + l32, p.M - 1);
   const uint16_t *xrow = p.x + (size_t)xm * p.x_stride;
 
-  f32x16 acc = {};
-  for (int k0 = 0; k0 < p.K; k0 += kTile) {
-    // issue this step's loads: codes, scale/bias, x operands
-    uint32_t wv[G::DW];
-    uint32_t sraw = 0, braw = 0;
+  // software pipeline: the loads of step k0 + 64 are issued before step k0 is
+  // dequantised and multiplied
+  // (two register buffers with compile-time indices: the loop body is
+  // unrolled by two steps)
+  uint32_t wv0[G::DW], wv1[G::DW];
+  uint32_t sr0 = 0, br0 = 0, sr1 = 0, br1 = 0;
+  uint4 xa0[4], xa1[4];
+  auto issue = [&](int k0, uint32_t (&wv)[G::DW], uint32_t &sraw, uint32_t &braw, uint4 (&xa)[4]) {
     if (deq) {
       const uint32_t *src = reinterpret_cast<const uint32_t *>(wrow + (size_t)(k0 + kq) * BITS / 8);
 #pragma unroll
@@ -88,11 +91,12 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
       sraw = srow[gidx];
       braw = brow[gidx];
     }
-    uint4 xa[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       xa[ks] = *reinterpret_cast<const uint4 *>(xrow + k0 + 16 * ks + 8 * half);
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  f32x16 acc = {};
+  auto step = [&](const uint32_t (&wv)[G::DW], uint32_t sraw, uint32_t braw, const uint4 (&xa)[4]) {
     if (deq) {
       const float s = aux_to_f32_sel(sraw, p.fp16), b = aux_to_f32_sel(braw, p.fp16);
       uint32_t packed[G::CPT / 2];
@@ -117,6 +121,17 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
       acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
     }
     __syncthreads();
+  };
+  issue(0, wv0, sr0, br0, xa0);
+  for (int k0 = 0; k0 < p.K; k0 += 2 * kTile) {
+    if (k0 + kTile < p.K) issue(k0 + kTile, wv1, sr1, br1, xa1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(wv0, sr0, br0, xa0);
+    if (k0 + kTile < p.K) {
+      if (k0 + 2 * kTile < p.K) issue(k0 + 2 * kTile, wv0, sr0, br0, xa0);
+      __builtin_amdgcn_sched_barrier(0);
+      step(wv1, sr1, br1, xa1);
+    }
   }
   // store: element i of this lane is (row 8*(i/4) + 4*half + i%4, col l32)
   const int n = bn0 + wn * 32 + l32;
