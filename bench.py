@@ -19,6 +19,24 @@ layer. The config-1 q4 GEMV (4096x2048) is timed as a secondary leg over 64
 rotated weight copies (302 MB). The CPU baseline is the oracle's
 single-threaded restatement of the reference CPU path on a bounded sample
 of the same workload.
+
+Secondary legs (reported under "secondary", same synthetic scheme, every
+one a HIP graph of the product entry points timed with HIP events):
+  * config 1: q4 GEMV 4096x2048 over 64 rotated weight copies;
+  * config 2: dense 8-bit g64 decode layer (QKV 4096->6144, O 4096->4096,
+    gate/up 4096->14336, SwiGLU, down 14336->4096) at M = 1, 4, 8 over 4
+    rotated layers (927 MB);
+  * config 3 at B = 16 (and 32) over the 48 resident layers, distinct
+    experts U counted from the routes;
+  * config 4: 5-bit and 6-bit layers with Zipf(1.1) router logits at B = 1
+    and B = 32 over 16 resident layers per width;
+  * config 5: the 48-layer Qwen3-Next-80B-A3B stack (12 full-attention
+    layers with q/k/v/o projections, 36 linear-attention layers with
+    qkvz/ba/out projections, every layer with its MoE block), decode B = 1
+    and B = 32, and a prefill chunk of M = 512 (projections on the MFMA
+    product, MoE block in chunks of 64 tokens). The attention / recurrence
+    math between the projections is outside the path: its inputs are
+    synthetic activations of the right shape.
 """
 from __future__ import annotations
 
@@ -61,7 +79,10 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip every secondary leg (configs 1, 2, 3 at B>1, 4, 5)")
+    ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times), to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against known bytes, then exit")
@@ -86,10 +107,8 @@ def build_layers(torch, device, synth, L):
     return layers
 
 
-def bench_moe(torch, device, synth, args):
+def bench_moe(torch, device, synth, args, layers):
     L = args.layers
-    log(f"building {L} resident MoE layers ({L * 0.906:.1f} GB)")
-    layers = build_layers(torch, device, synth, L)
     n = args.warmup + args.steps
     g = torch.Generator(device="cuda")
     g.manual_seed(12345)
@@ -133,9 +152,266 @@ def bench_moe(torch, device, synth, args):
     layer_us = ms_per_step * 1e3 / L
     gbps = LAYER_BYTES_B1 * L / (ms_per_step * 1e-3) / 1e9
     del graphs
-    cpu_layer = layers[0]
-    return dict(ms_per_step=ms_per_step, layer_us=layer_us, gbps=gbps, wall_ms=wall * 1e3 / args.steps,
-                layer0=cpu_layer)
+    return dict(ms_per_step=ms_per_step, layer_us=layer_us, gbps=gbps, wall_ms=wall * 1e3 / args.steps)
+
+
+def graph_us(torch, step, reps):
+    """Capture step() (launches on the current stream) once into a HIP graph,
+    replay it once untimed, then `reps` times between two HIP events on the
+    capture stream; microseconds per replay."""
+    step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        step()
+    with torch.cuda.stream(stream):
+        gr.replay()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(reps):
+            gr.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    del gr
+    return ev0.elapsed_time(ev1) * 1e3 / reps
+
+
+def distinct_experts(logits_bf16_bits, k):
+    """Distinct experts over a batch's top-k routes (softmax is monotone, so
+    the top-k of the logits with lower-index ties; stable sort)."""
+    import numpy as np
+
+    lg = (logits_bf16_bits.astype(np.uint32) << 16).view(np.float32)
+    top = np.argsort(-lg, axis=-1, kind="stable")[..., :k]
+    return len(np.unique(top))
+
+
+def dev_bf16(torch, bits):
+    import numpy as np
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def moe_batch_leg(torch, device, synth, layers, B, bits, per_expert, zipf, reps, seed):
+    """One graph step = B tokens through every layer of `layers` (fresh x and
+    logits per layer); algorithmic bytes per layer = (U + 1) experts (U
+    distinct routed, plus the shared one) + logits + x + out + gate row."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    n = len(layers)
+    lgb = [synth.make_logits(rng, B, E, zipf) for _ in range(n)]
+    xs = [dev_bf16(torch, synth.make_x(rng, B, D)) for _ in range(n)]
+    lg = [dev_bf16(torch, a) for a in lgb]
+    out = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(layers[0].workspace_bytes(B), dtype=torch.uint8, device="cuda")
+
+    def step():
+        for l in range(n):
+            device.moe_block(layers[l], xs[l], lg[l], out=out, workspace=ws)
+
+    us = graph_us(torch, step, reps) / n
+    U = float(np.mean([distinct_experts(a, TOPK) for a in lgb]))
+    nbytes = (U + 1) * per_expert + B * (E * 2 + 3 * D * 2)
+    return dict(B=B, bits=bits, us_per_layer=round(us, 2), us_per_token_layer=round(us / B, 3),
+                distinct_experts=round(U, 1), bytes_per_layer=int(nbytes),
+                gbps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                frac_of_peak=round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBPS, 4), layers=n,
+                router="Zipf(%.1f)" % zipf if zipf else "N(0,1)")
+
+
+def build_moe_layers(torch, device, synth, n, bits, seed0):
+    per = []
+    for l in range(n):
+        s = seed0 + 1000 * l
+
+        def bank(O, I, ne, seed):
+            w, sc, bi = synth.torch_affine(O, I, bits, GS, E=ne, seed=seed)
+            return device.AffineBank(w, sc, bi, ne, O, I, bits, GS)
+
+        g = torch.Generator(device="cuda")
+        g.manual_seed(s + 7)
+        se_g = (torch.randn(D, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+        per.append(device.MoeLayer(bank(INTER, D, E, s + 1), bank(INTER, D, E, s + 2),
+                                   bank(D, INTER, E, s + 3), TOPK, bank(INTER, D, 1, s + 4),
+                                   bank(INTER, D, 1, s + 5), bank(D, INTER, 1, s + 6), se_g))
+    return per
+
+
+def bench_config4(torch, device, synth, args):
+    res = {}
+    for bits in (5, 6):
+        per_expert = expert_bytes([(INTER, D), (INTER, D), (D, INTER)], bits)
+        n = 16
+        log(f"config 4: building {n} {bits}-bit layers")
+        layers = build_moe_layers(torch, device, synth, n, bits, 7_000_000 * bits)
+        for B in (1, 32):
+            r = moe_batch_leg(torch, device, synth, layers, B, bits, per_expert, 1.1, args.reps,
+                              seed=bits * 100 + B)
+            log(f"config 4 {bits}-bit B={B}: {r['us_per_layer']} us/layer, {r['gbps']} GB/s, "
+                f"U={r['distinct_experts']}")
+            res[f"b{bits}_B{B}"] = r
+        del layers
+        torch.cuda.empty_cache()
+    return res
+
+
+DENSE_H, DENSE_Q, DENSE_F = 4096, 6144, 14336
+DENSE8_LAYER_BYTES = expert_bytes([(DENSE_Q, DENSE_H), (DENSE_H, DENSE_H), (DENSE_F, DENSE_H),
+                                   (DENSE_F, DENSE_H), (DENSE_H, DENSE_F)], 8)  # 231,735,296 B
+
+
+def bench_config2(torch, device, synth, args):
+    """Dense 8-bit decode layer: QKV, O, gate, up, SwiGLU, down. The O input
+    stands in for the attention output (outside the path)."""
+    nl = 4
+    log(f"config 2: building {nl} dense 8-bit layers ({nl * DENSE8_LAYER_BYTES / 1e9:.2f} GB)")
+    shapes = (("qkv", DENSE_Q, DENSE_H), ("o", DENSE_H, DENSE_H), ("gate", DENSE_F, DENSE_H),
+              ("up", DENSE_F, DENSE_H), ("down", DENSE_H, DENSE_F))
+    layers = []
+    for l in range(nl):
+        m = {}
+        for j, (name, O, I) in enumerate(shapes):
+            w, sc, bi = synth.torch_affine(O, I, 8, GS, seed=900_000 + 10 * l + j)
+            m[name] = device.AffineMatrix(w, sc, bi, O, I, 8, GS)
+        layers.append(m)
+    res = {}
+    for M in getattr(args, "dense_m", (1, 4, 8)):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(M)
+        x = torch.randn((M, DENSE_H), device="cuda", generator=g).to(torch.bfloat16)
+        att = torch.randn((M, DENSE_H), device="cuda", generator=g).to(torch.bfloat16)
+        qkv = torch.empty((M, DENSE_Q), dtype=torch.bfloat16, device="cuda")
+        o = torch.empty((M, DENSE_H), dtype=torch.bfloat16, device="cuda")
+        gt = torch.empty((M, DENSE_F), dtype=torch.bfloat16, device="cuda")
+        up = torch.empty((M, DENSE_F), dtype=torch.bfloat16, device="cuda")
+        y = torch.empty((M, DENSE_H), dtype=torch.bfloat16, device="cuda")
+
+        def step():
+            for L in layers:
+                device.affine_gemv(L["qkv"], x, out=qkv)
+                device.affine_gemv(L["o"], att, out=o)
+                device.affine_gemv(L["gate"], o, out=gt)
+                device.affine_gemv(L["up"], o, out=up)
+                device.silu_mul(gt, up)
+                device.affine_gemv(L["down"], gt, out=y)
+
+        us = graph_us(torch, step, args.reps) / nl
+        nbytes = DENSE8_LAYER_BYTES + 139_264 * M
+        gbps = nbytes / (us * 1e-6) / 1e9
+        log(f"config 2 M={M}: {us:.2f} us/layer, {gbps:.0f} GB/s")
+        res[f"M{M}"] = dict(us_per_layer=round(us, 2), bytes_per_layer=nbytes, gbps=round(gbps, 1),
+                            frac_of_peak=round(gbps / PEAK_GBPS, 4))
+    res["layers_rotated"] = nl
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
+# Qwen3-Next-80B-A3B projections per layer (hidden 2048; 16 q heads x 256 with
+# the output gate, 2 kv heads x 256; linear attention 16 k heads x 128,
+# 32 v heads x 128): (name, O, I)
+FULL_ATTN = (("q", 8192, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 4096))
+LIN_ATTN = (("qkvz", 12288, 2048), ("ba", 64, 2048), ("out", 2048, 4096))
+FULL_EVERY = 4
+
+
+def bench_config5(torch, device, synth, args, moe_layers):
+    """48-layer stack: per layer its attention projections (4-bit g64) plus
+    its MoE block. Layers l % 4 == 3 are full attention."""
+    import numpy as np
+
+    nl = len(moe_layers)
+    log(f"config 5: building {nl} layers of attention projections")
+    proj = []
+    pbytes = 0
+    pflop_per_tok = 0
+    for l in range(nl):
+        shapes = FULL_ATTN if l % FULL_EVERY == FULL_EVERY - 1 else LIN_ATTN
+        m = []
+        for j, (name, O, I) in enumerate(shapes):
+            w, sc, bi = synth.torch_affine(O, I, BITS, GS, seed=5_000_000 + 10 * l + j)
+            m.append(device.AffineMatrix(w, sc, bi, O, I, BITS, GS))
+            pbytes += expert_bytes([(O, I)])
+            pflop_per_tok += 2 * O * I
+        proj.append(m)
+    moe_bytes_b1 = nl * (TOPK + 1) * PER_EXPERT
+    res = {"layers": nl, "projection_bytes": pbytes}
+    rng = np.random.default_rng(55)
+    for B in (1, 32):
+        x = dev_bf16(torch, synth.make_x(rng, B, D))
+        att = dev_bf16(torch, synth.make_x(rng, B, 4096))
+        lgb = [synth.make_logits(rng, B, E) for _ in range(nl)]
+        lg = [dev_bf16(torch, a) for a in lgb]
+        outs = {}
+        for shapes in (FULL_ATTN, LIN_ATTN):
+            for name, O, I in shapes:
+                outs[name] = torch.empty((B, O), dtype=torch.bfloat16, device="cuda")
+        mo = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(moe_layers[0].workspace_bytes(B), dtype=torch.uint8, device="cuda")
+        prod = device.affine_gemv
+
+        def step():
+            for l in range(nl):
+                shapes = FULL_ATTN if l % FULL_EVERY == FULL_EVERY - 1 else LIN_ATTN
+                for (name, O, I), m in zip(shapes, proj[l]):
+                    prod(m, x if I == D else att, out=outs[name])
+                device.moe_block(moe_layers[l], x, lg[l], out=mo, workspace=ws)
+
+        us = graph_us(torch, step, args.reps)
+        U = [distinct_experts(a, TOPK) for a in lgb]
+        nbytes = pbytes + sum((u + 1) * PER_EXPERT for u in U)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        log(f"config 5 decode B={B}: {us:.1f} us/step, {us / B:.2f} us/token, {gbps:.0f} GB/s")
+        res[f"decode_B{B}"] = dict(us_per_step=round(us, 1), us_per_token=round(us / B, 2),
+                                   bytes_per_step=int(nbytes), gbps=round(gbps, 1),
+                                   frac_of_peak=round(gbps / PEAK_GBPS, 4),
+                                   projections="affine_gemv")
+    # prefill chunk: M = 512 tokens
+    M = 512
+    x = dev_bf16(torch, synth.make_x(rng, M, D))
+    att = dev_bf16(torch, synth.make_x(rng, M, 4096))
+    outs = {}
+    for shapes in (FULL_ATTN, LIN_ATTN):
+        for name, O, I in shapes:
+            outs[name] = torch.empty((M, O), dtype=torch.bfloat16, device="cuda")
+
+    def proj_step():
+        for l in range(nl):
+            shapes = FULL_ATTN if l % FULL_EVERY == FULL_EVERY - 1 else LIN_ATTN
+            for (name, O, I), m in zip(shapes, proj[l]):
+                device.affine_qmm(m, x if I == D else att, out=outs[name])
+
+    us_p = graph_us(torch, proj_step, args.reps)
+    tflops = pflop_per_tok * M / (us_p * 1e-6) / 1e12
+    chunk = 64
+    lgb = [synth.make_logits(rng, M, E) for _ in range(nl)]
+    lg = [dev_bf16(torch, a) for a in lgb]
+    mo = torch.empty((M, D), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(moe_layers[0].workspace_bytes(chunk), dtype=torch.uint8, device="cuda")
+
+    def moe_step():
+        for l in range(nl):
+            for c0 in range(0, M, chunk):
+                device.moe_block(moe_layers[l], x[c0:c0 + chunk], lg[l][c0:c0 + chunk],
+                                 out=mo[c0:c0 + chunk], workspace=ws)
+
+    us_m = graph_us(torch, moe_step, max(1, args.reps // 2))
+    log(f"config 5 prefill M={M}: projections {us_p:.0f} us ({tflops:.1f} TFLOP/s), "
+        f"MoE {us_m:.0f} us")
+    res["prefill_M512"] = dict(
+        projections_us=round(us_p, 1), projections_tflops=round(tflops, 2),
+        projections_frac_of_bf16_mfma_peak=round(tflops / 2500.0, 4),
+        projection_flop=pflop_per_tok * M, moe_us=round(us_m, 1), moe_chunk_tokens=chunk,
+        us_per_chunk=round(us_p + us_m, 1), tokens_per_s=round(M / ((us_p + us_m) * 1e-6), 1))
+    res["moe_bytes_b1_ideal"] = moe_bytes_b1
+    del proj
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_gemv(torch, device, synth, args):
@@ -244,12 +520,33 @@ def main():
         torch.cuda.synchronize()
         log(f"copied {args.copy_mib} MiB x 5")
         return
-    moe = bench_moe(torch, device, synth, args)
-    gemv = None if args.no_gemv else bench_gemv(torch, device, synth, args)
+    log(f"building {args.layers} resident MoE layers ({args.layers * 0.906:.1f} GB)")
+    layers = build_layers(torch, device, synth, args.layers)
+    moe = bench_moe(torch, device, synth, args, layers)
+    secondary = {}
+    if not args.no_secondary:
+        if not args.no_gemv:
+            gemv = bench_gemv(torch, device, synth, args)
+            secondary["gemv_q4_config1"] = {
+                "shape": "M=1 K=2048 N=4096 4-bit g64", "bytes_per_launch": GEMV_BYTES,
+                "us_per_launch": round(gemv["us_per_launch"], 3), "gbps": round(gemv["gbps"], 1),
+                "frac_of_peak": round(gemv["gbps"] / PEAK_GBPS, 4), "launches": gemv["launches"],
+                "rotation": "64 weight copies (302 MB) > 256 MB MALL"}
+        secondary["dense8_config2"] = bench_config2(torch, device, synth, args)
+        c3 = {}
+        for B in (16, 32):
+            r = moe_batch_leg(torch, device, synth, layers, B, BITS, PER_EXPERT, None, args.reps,
+                              seed=300 + B)
+            log(f"config 3 B={B}: {r['us_per_layer']} us/layer, {r['gbps']} GB/s, "
+                f"U={r['distinct_experts']}")
+            c3[f"B{B}"] = r
+        secondary["moe_config3"] = c3
+        secondary["stack_config5"] = bench_config5(torch, device, synth, args, layers)
+        secondary["moe_config4"] = bench_config4(torch, device, synth, args)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
-        cpu = cpu_baseline(torch, moe["layer0"], args.cpu_seconds)
+        cpu = cpu_baseline(torch, layers[0], args.cpu_seconds)
         log(f"cpu: {cpu['us_per_token_layer']:.0f} us/token-layer")
     res = {
         "metric": METRIC,
@@ -284,12 +581,8 @@ def main():
         },
         "cpu_baseline": cpu,
     }
-    if gemv:
-        res["secondary"] = {"gemv_q4_config1": {
-            "shape": "M=1 K=2048 N=4096 4-bit g64", "bytes_per_launch": GEMV_BYTES,
-            "us_per_launch": round(gemv["us_per_launch"], 3), "gbps": round(gemv["gbps"], 1),
-            "frac_of_peak": round(gemv["gbps"] / PEAK_GBPS, 4), "launches": gemv["launches"],
-            "rotation": "64 weight copies (302 MB) > 256 MB MALL"}}
+    if secondary:
+        res["secondary"] = secondary
     print(json.dumps(res), flush=True)
 
 

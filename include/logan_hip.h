@@ -167,6 +167,14 @@ int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_s
 int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                          int y_stride, int y_dtype, void *stream);
 
+/* SwiGLU between a dense gate/up pair and the down projection, in place:
+ * g[i] = silu(g[i]) * u[i], silu(v) = v / (1 + exp(-v)), f32 arithmetic
+ * (replaces coli_metal_silu_mul, logan-metal/metal/backend_metal.mm
+ * :2187-2203, kernel moe_silu :698-699). dtype LOGAN_HIP_F32 or
+ * LOGAN_HIP_BF16 (bf16 result rounded RNE); g and u 16-byte aligned device
+ * pointers of n elements. 1 ok, 0 bad arguments, -1 launch failure. */
+int logan_hip_silu_mul(void *g, const void *u, long long n, int dtype, void *stream);
+
 /* Same product with f32 activations and f32 output, exact per-element
  * dequantisation (any group size dividing I). */
 int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,

@@ -101,6 +101,7 @@ SIGNATURES = {
     "logan_hip_affine_gemv": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
     "logan_hip_affine_gemv_f32": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _P]),
     "logan_hip_affine_qmm": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
+    "logan_hip_silu_mul": (_I, [_P, _P, C.c_longlong, _I, _P]),
     "logan_hip_affine_dequant": (_I, [C.POINTER(Affine), _I, _I, _P, _P]),
     "logan_hip_route_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "logan_hip_moe_workspace_bytes": (_SZ, [C.POINTER(MoeBlock), _I]),

@@ -577,6 +577,14 @@ int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_st
                                        reinterpret_cast<hipStream_t>(stream)));
 }
 
+int logan_hip_silu_mul(void *g, const void *u, long long n, int dtype, void *stream) {
+  if (!g || !u || n <= 0) return 0;
+  if (dtype != LOGAN_HIP_F32 && dtype != LOGAN_HIP_BF16) return 0;
+  if (((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u)) & 15) != 0) return 0;
+  return rc_from(lh::launch_silu_mul(g, u, n, dtype == LOGAN_HIP_BF16,
+                                     reinterpret_cast<hipStream_t>(stream)));
+}
+
 int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, int x_stride,
                               float *y, int y_stride, void *stream) {
   if (!affine_ok(w) || !x || !y || M <= 0 || x_stride < w->I || y_stride < w->O) return 0;

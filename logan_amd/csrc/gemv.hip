@@ -278,6 +278,18 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
   p.x_stride = x_stride;
   p.y_stride = y_stride;
   p.y_bf16 = y_bf16;
+  // three or more activation rows: the MFMA path reads each weight once per
+  // 32 rows (4- and 8-bit codes, groups of 64k)
+  if (M >= 3 && affine_skinny_supported(m)) {
+    for (int m0 = 0; m0 < M; m0 += 32) {
+      void *ym = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
+                        : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
+      hipError_t e = launch_affine_skinny(m, x + (size_t)m0 * x_stride, x_stride, min(32, M - m0), ym,
+                                          y_stride, y_bf16, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   // token blocks of at most 2 rows of x per launch
   for (int m0 = 0; m0 < M; m0 += 2) {
     const int mt = M - m0 >= 2 ? 2 : 1;

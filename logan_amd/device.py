@@ -124,6 +124,19 @@ def affine_qmm(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = N
     return out
 
 
+def silu_mul(g: torch.Tensor, u: torch.Tensor, stream=None) -> torch.Tensor:
+    """In place g = silu(g) * u (f32 or bf16 device tensors of equal size;
+    logan-metal/metal/backend_metal.mm:2187-2203). Returns g."""
+    if g.dtype != u.dtype or g.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("g and u must both be bf16 or both f32")
+    if g.numel() != u.numel():
+        raise LoganHipError("g and u differ in size")
+    dt = L.LOGAN_HIP_BF16 if g.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    rc = L.lib().logan_hip_silu_mul(_dev(g, "g"), _dev(u, "u"), g.numel(), dt, _stream(stream))
+    _check(rc, "silu_mul")
+    return g
+
+
 def affine_gemv_f32(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
                     stream=None) -> torch.Tensor:
     """f32 activations, exact per-element dequantisation, f32 output."""

@@ -61,6 +61,8 @@ def lib() -> C.CDLL:
         h.lo_affine_qmm_bf16.argtypes = [P, P, P, P, P, SZ, SZ, SZ, I, SZ, I]
         h.lo_silu.restype = C.c_float
         h.lo_silu.argtypes = [C.c_float]
+        h.lo_silu_mul.restype = None
+        h.lo_silu_mul.argtypes = [P, P, SZ]
         h.lo_softmax_row.restype = None
         h.lo_softmax_row.argtypes = [P, SZ]
         h.lo_topk.restype = C.c_float
@@ -135,6 +137,15 @@ def spark_affine8_gemv(x, w, aux, O, I) -> np.ndarray:
     aux = np.ascontiguousarray(aux).view(np.uint8)
     lib().lo_spark_affine8_gemv(_p(y), _p(x), _p(w), _p(aux), O, I)
     return y
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """silu(g) * u element-wise in f32 (returns a new array)."""
+    out = np.ascontiguousarray(g, np.float32).copy()
+    uu = np.ascontiguousarray(u, np.float32)
+    assert out.size == uu.size
+    lib().lo_silu_mul(_p(out), _p(uu), out.size)
+    return out
 
 
 def softmax_row(x: np.ndarray) -> np.ndarray:

@@ -263,6 +263,12 @@ float lo_silu(float x) {
   return x / d;
 }
 
+/* Dense SwiGLU in place, g[i] = silu(g[i]) * u[i]
+ * (logan-metal/metal/backend_metal.mm:698-699, moe_silu). */
+void lo_silu_mul(float *g, const float *u, size_t n) {
+  for (size_t i = 0; i < n; ++i) g[i] = lo_silu(g[i]) * u[i];
+}
+
 /* logan-qwen4/src/lib.rs:4558-4574 */
 void lo_softmax_row(float *x, size_t n) {
   float m = -1e30f;

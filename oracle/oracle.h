@@ -67,6 +67,7 @@ void lo_affine_qmm_bf16(float *y, const float *x, const uint8_t *w,
 
 /* logan-qwen4/src/lib.rs:4516-4518. */
 float lo_silu(float x);
+void lo_silu_mul(float *g, const float *u, size_t n);
 /* logan-qwen4/src/lib.rs:4558-4574 (= logan-qwen/src/lib.rs:260-276). */
 void lo_softmax_row(float *x, size_t n);
 /* logan-qwen4/src/lib.rs:7993-8043 (= logan-qwen/src/lib.rs:545-557):

@@ -65,7 +65,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("O,I,bits,gs", SHAPES)
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 8, 17])
 def test_gemv_bf16_matches_oracle(gpu, O, I, bits, gs, M):
     import torch
     from logan_amd.device import affine_gemv

@@ -290,3 +290,20 @@ def test_qmm_against_float64_of_bf16_weights(bits, gs):
     assert np.abs(y - ref).max() / np.abs(ref).max() < 1e-5
     unrounded = x.astype(np.float64) @ wd.T
     assert np.abs(unrounded - ref).max() / np.abs(ref).max() > 1e-4
+
+
+def test_silu_mul_closed_form():
+    """silu(g) * u against the float64 closed form g / (1 + e^-g) * u, and
+    the values the formula fixes exactly: silu(0) = 0, silu(v) -> v for large
+    v, silu(v) -> -0 for very negative v, u = 0 gives 0."""
+    rng = np.random.default_rng(3)
+    g = (rng.standard_normal(4096) * 4).astype(np.float32)
+    u = rng.standard_normal(4096).astype(np.float32)
+    got = oracle.silu_mul(g, u)
+    g64 = g.astype(np.float64)
+    ref = g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 4e-7 * np.abs(ref) + 1e-30)
+    special = oracle.silu_mul(np.array([0.0, 100.0, -200.0, 3.0], np.float32),
+                              np.array([5.0, 2.0, 1.0, 0.0], np.float32))
+    assert special[0] == 0.0 and special[1] == 200.0
+    assert special[2] == 0.0 and special[3] == 0.0
