@@ -388,17 +388,14 @@ def bench_config5(torch, device, synth, args, moe_layers):
 
     us_p = graph_us(torch, proj_step, args.reps)
     tflops = pflop_per_tok * M / (us_p * 1e-6) / 1e12
-    chunk = 64
     lgb = [synth.make_logits(rng, M, E) for _ in range(nl)]
     lg = [dev_bf16(torch, a) for a in lgb]
     mo = torch.empty((M, D), dtype=torch.bfloat16, device="cuda")
-    ws = torch.empty(moe_layers[0].workspace_bytes(chunk), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(moe_layers[0].workspace_bytes(M), dtype=torch.uint8, device="cuda")
 
     def moe_step():
         for l in range(nl):
-            for c0 in range(0, M, chunk):
-                device.moe_block(moe_layers[l], x[c0:c0 + chunk], lg[l][c0:c0 + chunk],
-                                 out=mo[c0:c0 + chunk], workspace=ws)
+            device.moe_block(moe_layers[l], x, lg[l], out=mo, workspace=ws)
 
     us_m = graph_us(torch, moe_step, max(1, args.reps // 2))
     log(f"config 5 prefill M={M}: projections {us_p:.0f} us ({tflops:.1f} TFLOP/s), "
@@ -406,7 +403,8 @@ def bench_config5(torch, device, synth, args, moe_layers):
     res["prefill_M512"] = dict(
         projections_us=round(us_p, 1), projections_tflops=round(tflops, 2),
         projections_frac_of_bf16_mfma_peak=round(tflops / 2500.0, 4),
-        projection_flop=pflop_per_tok * M, moe_us=round(us_m, 1), moe_chunk_tokens=chunk,
+        projection_flop=pflop_per_tok * M, moe_us=round(us_m, 1),
+        moe_bytes=int(sum((distinct_experts(a, TOPK) + 1) * PER_EXPERT for a in lgb)),
         us_per_chunk=round(us_p + us_m, 1), tokens_per_s=round(M / ((us_p + us_m) * 1e-6), 1))
     res["moe_bytes_b1_ideal"] = moe_bytes_b1
     del proj

@@ -228,8 +228,9 @@ size_t logan_hip_moe_workspace_bytes(const LoganHipMoeBlock *blk, int B);
  * (RNE of the f32 result) or LOGAN_HIP_F32. idx_out [B][k] and w_out [B][k]
  * are optional (NULL) copies of the routing. workspace: device memory of at
  * least logan_hip_moe_workspace_bytes(blk, B) bytes (256-byte aligned), or
- * NULL to use a library-owned buffer (allocated on growth). B <= 64,
- * E <= 1024, k <= 32. 1 ok, 0 unsupported geometry, -1 failure. */
+ * NULL to use a library-owned buffer (allocated on growth). B <= 4096,
+ * B * k <= 65536, E <= 1024, k <= 32. 1 ok, 0 unsupported geometry,
+ * -1 failure. */
 int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *logits,
                         int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
                         float *w_out, void *workspace, size_t workspace_bytes, void *stream);
@@ -245,6 +246,16 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
  * rest between launches. */
 void logan_hip_set_moe_fused(int on);
 uint32_t logan_hip_moe_sync_errors(void);
+
+/* Batches of at least this many tokens take the routed-MoE block's MFMA
+ * path (4/8-bit codes with group sizes that are multiples of 64; each
+ * expert's weights read once per 16 of its tokens); smaller batches and
+ * other geometries take the per-token dot-product path in passes of up to
+ * 64 tokens. Default 96, or LOGAN_HIP_MOE_MFMA_MIN_B from the environment.
+ * Both paths follow the same reference semantics (logan-qwen4/src/lib.rs
+ * :8692-8711, :8759-8815); this control has no counterpart in the
+ * reference (its batched path is host-side, lib.rs:9714-9721). */
+void logan_hip_set_moe_mfma_min_batch(int b);
 
 /* Library version string. */
 const char *logan_hip_version(void);

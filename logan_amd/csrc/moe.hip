@@ -125,10 +125,27 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
   return w;
 }
 
+constexpr int kMaxB = 64;  // tokens per launch of the dot2 path (larger batches go in chunks)
+
 size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k) {
-  const size_t general = moe_ws_layout(nullptr, B, D, inter, sinter, E, k).total;
+  const size_t general = moe_ws_layout(nullptr, B < kMaxB ? B : kMaxB, D, inter, sinter, E, k).total;
   const size_t fused = moe_fused_workspace_bytes(k + 1, inter, sinter);
-  return general > fused ? general : fused;
+  const size_t mfma = moe_mfma_workspace_bytes(B, D, inter, sinter, E, k);
+  size_t m = general > fused ? general : fused;
+  return m > mfma ? m : mfma;
+}
+
+static int g_mfma_min_b = -1;
+
+void set_moe_mfma_min_batch(int b) { g_mfma_min_b = b; }
+
+static int mfma_min_batch() {
+  if (g_mfma_min_b < 0) {
+    const char *v = getenv("LOGAN_HIP_MOE_MFMA_MIN_B");
+    g_mfma_min_b = v ? atoi(v) : kMfmaMinBatchDefault;
+    if (g_mfma_min_b < 1) g_mfma_min_b = 1;
+  }
+  return g_mfma_min_b;
 }
 
 static int g_fused_enabled = -1;
@@ -147,7 +164,6 @@ static bool fused_enabled() {
 // 1. route + shared gate + grouping (one block of 1024 threads, B <= 64)
 
 constexpr int kGroupThreads = 1024;
-constexpr int kMaxB = 64;
 
 // xp[t][c] = make_xchunk_bf16 of chunk c of token t (pairs, sum x, sum x')
 template <int BITS>
@@ -622,8 +638,9 @@ static bool bank_ok(const DevBank &b, int O, int I, int bits, int gs) {
 }
 
 int launch_moe_block(const MoeArgs &a, hipStream_t st) {
-  if (a.B <= 0 || a.B > kMaxB || a.E <= 0 || a.E > kMaxE || a.k <= 0 || a.k > kMaxK || a.k > a.E)
+  if (a.B <= 0 || a.B > kMaxBatch || a.E <= 0 || a.E > kMaxE || a.k <= 0 || a.k > kMaxK || a.k > a.E)
     return 0;
+  if ((long long)a.B * a.k > kMaxBatchSlots) return 0;
   if (a.D <= 0 || a.D % 32 != 0 || a.inter <= 0 || a.inter % 32 != 0) return 0;
   if (a.D > 4096 || a.inter > 1024 || a.sinter > 1024) return 0;  // kernel shapes below
   if (!a.x || !a.logits || !a.out || !a.ws) return 0;
@@ -647,26 +664,43 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
     const int rc = launch_moe_fused_b1(aa, st);
     if (rc != 0) return rc;
   }
-  MoeWs w = moe_ws_layout(a.ws, a.B, a.D, a.inter, sinter, a.E, a.k);
-  if (a.logits_f32) {
-    if (a.E <= 512)
-      hipLaunchKernelGGL((moe_route_group_kernel<8, true>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
-    else
-      hipLaunchKernelGGL((moe_route_group_kernel<16, true>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
-  } else {
-    if (a.E <= 512)
-      hipLaunchKernelGGL((moe_route_group_kernel<8, false>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
-    else
-      hipLaunchKernelGGL((moe_route_group_kernel<16, false>), dim3(1), dim3(kGroupThreads), 0, st, aa, w);
+  if (a.B >= mfma_min_batch()) {
+    const int rc = launch_moe_mfma(aa, st);
+    if (rc != 0) return rc;
   }
-  if (hipGetLastError() != hipSuccess) return -1;
-  switch (bits) {
-    case 4: return moe_launch_bits<4>(aa, w, st);
-    case 5: return moe_launch_bits<5>(aa, w, st);
-    case 6: return moe_launch_bits<6>(aa, w, st);
-    case 8: return moe_launch_bits<8>(aa, w, st);
+  // dot2 path, at most kMaxB tokens per pass (the passes reuse the workspace
+  // in stream order)
+  for (int b0 = 0; b0 < a.B; b0 += kMaxB) {
+    MoeArgs c = aa;
+    c.B = a.B - b0 < kMaxB ? a.B - b0 : kMaxB;
+    c.x = a.x + (size_t)b0 * a.D;
+    c.logits = reinterpret_cast<const char *>(a.logits) + (size_t)b0 * a.E * (a.logits_f32 ? 4 : 2);
+    c.out = reinterpret_cast<char *>(a.out) + (size_t)b0 * a.D * (a.out_f32 ? 4 : 2);
+    if (a.idx_out) c.idx_out = a.idx_out + (size_t)b0 * a.k;
+    if (a.w_out) c.w_out = a.w_out + (size_t)b0 * a.k;
+    MoeWs w = moe_ws_layout(a.ws, c.B, a.D, a.inter, sinter, a.E, a.k);
+    if (a.logits_f32) {
+      if (a.E <= 512)
+        hipLaunchKernelGGL((moe_route_group_kernel<8, true>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
+      else
+        hipLaunchKernelGGL((moe_route_group_kernel<16, true>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
+    } else {
+      if (a.E <= 512)
+        hipLaunchKernelGGL((moe_route_group_kernel<8, false>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
+      else
+        hipLaunchKernelGGL((moe_route_group_kernel<16, false>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
+    }
+    if (hipGetLastError() != hipSuccess) return -1;
+    int rc = 0;
+    switch (bits) {
+      case 4: rc = moe_launch_bits<4>(c, w, st); break;
+      case 5: rc = moe_launch_bits<5>(c, w, st); break;
+      case 6: rc = moe_launch_bits<6>(c, w, st); break;
+      case 8: rc = moe_launch_bits<8>(c, w, st); break;
+    }
+    if (rc != 1) return rc;
   }
-  return 0;
+  return 1;
 }
 
 }  // namespace lh

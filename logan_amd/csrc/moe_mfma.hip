@@ -1,0 +1,603 @@
+// Routed-MoE block for token batches on MFMA (prefill chunks, large decode
+// batches): the same semantics as moe.hip (logan-qwen/src/lib.rs:535-593,
+// logan-qwen4/src/lib.rs:8692-8711, :8759-8815, :7597-7759), with the
+// per-expert products on v_mfma_f32_16x16x32_bf16 so that an expert's
+// weights are read once for up to 16 of its tokens at a time.
+//
+// Launches (one stream):
+//   1. moe_mroute_kernel       one wave per token: top-k (lower-index ties),
+//                              normalised weights, shared-expert gate
+//   2. moe_mgroup_kernel       one block: group the (token, rank) slots by
+//                              expert and cut each group into tiles of at most
+//                              16 slots; the shared expert gets tiles of 16
+//                              tokens after the routed ones
+//   3. moe_gateup_mfma_kernel  per (tile, 64 rows): the tile's x rows staged
+//                              in LDS, gate and up rows of 16 per wave, SwiGLU
+//                              fused; h stored as two bf16 planes (hi, lo with
+//                              h = hi + lo to 2^-17) in grouped row order
+//   4. moe_down_mfma_kernel    per (tile, 128 rows): h hi/lo staged in LDS,
+//                              two MFMA passes (hi, lo), y in grouped order
+//   5. moe_mcombine_kernel     out[t] = sum_r w_r y[row(t, r)] (rank order)
+//                              + gs_t y[shared row t]
+// Numerics: codes exact, activations exact (x bf16; h to 2^-17), f32
+// accumulation, per-group scale/bias folded after each 64-code step (the
+// group sizes are multiples of 64).
+#include "lh_internal.hpp"
+#include "mfma_dev.hpp"
+#include "route_dev.hpp"
+
+namespace lh {
+
+constexpr int kMTok = 16;          // slots per tile
+constexpr int kMChunk = 1024;      // x codes staged in LDS at a time (gate/up)
+constexpr int kMDownK = 512;       // largest down K (expert intermediate size)
+constexpr int kMMaxSlots = 65536;  // B * k
+constexpr int kMMaxE = 1024;
+constexpr int kMGroupThreads = 1024;
+
+struct MoeMWs {
+  int *n_tiles;       // [1]
+  int4 *tiles;        // [max_tiles] (expert or -1 for shared, first grouped row, slots, 0)
+  int *tok;           // [B*k] token of each grouped routed row
+  int *gpos;          // [B*k] grouped row of slot t*k + r
+  int32_t *topk_idx;  // [B*k]
+  float *topk_w;      // [B*k]
+  float *gs;          // [B]
+  uint16_t *h_hi;     // [(B*k + B) * hmax] bf16
+  uint16_t *h_lo;     // [(B*k + B) * hmax] bf16
+  float *y;           // [(B*k + B) * D]
+  int max_tiles;
+  size_t total;
+};
+
+static inline size_t al256m(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static MoeMWs moe_mws_layout(void *base, int B, int D, int inter, int sinter, int E, int k) {
+  MoeMWs w{};
+  const size_t nsl = (size_t)B * k;
+  const size_t slots = nsl + B;
+  const size_t hmax = (size_t)(inter > sinter ? inter : sinter);
+  const int G = (int)(nsl < (size_t)E ? nsl : (size_t)E);
+  w.max_tiles = (int)((nsl + kMTok - 1) / kMTok) + G + (B + kMTok - 1) / kMTok;
+  size_t off = 0;
+  char *b = reinterpret_cast<char *>(base);
+  auto take = [&](size_t bytes) {
+    char *p = b ? b + off : nullptr;
+    off += al256m(bytes);
+    return p;
+  };
+  w.n_tiles = reinterpret_cast<int *>(take(sizeof(int)));
+  w.tiles = reinterpret_cast<int4 *>(take(sizeof(int4) * (size_t)w.max_tiles));
+  w.tok = reinterpret_cast<int *>(take(sizeof(int) * nsl));
+  w.gpos = reinterpret_cast<int *>(take(sizeof(int) * nsl));
+  w.topk_idx = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * nsl));
+  w.topk_w = reinterpret_cast<float *>(take(sizeof(float) * nsl));
+  w.gs = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B));
+  w.h_hi = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * slots * hmax));
+  w.h_lo = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * slots * hmax));
+  w.y = reinterpret_cast<float *>(take(sizeof(float) * slots * (size_t)D));
+  w.total = off;
+  return w;
+}
+
+size_t moe_mfma_workspace_bytes(int B, int D, int inter, int sinter, int E, int k) {
+  return moe_mws_layout(nullptr, B, D, inter, sinter, E, k).total;
+}
+
+// ---------------------------------------------------------------------------
+// 1. routing and the shared-expert gate, one wave per token
+
+template <int KPL, bool F32>
+__global__ __launch_bounds__(256) void moe_mroute_kernel(MoeArgs a, MoeMWs w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= a.B) return;  // whole waves leave together
+  int id;
+  float wt;
+  wave_topk_lanes<KPL, F32>(a.logits, (size_t)t * a.E, a.E, a.k, id, wt);
+  if (lane < a.k) {
+    const size_t s = (size_t)t * a.k + lane;
+    w.topk_idx[s] = id;
+    w.topk_w[s] = wt;
+    if (a.idx_out) a.idx_out[s] = id;
+    if (a.w_out) a.w_out[s] = wt;
+  }
+  if (a.sgate.m.w) {
+    // sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604), 8 bf16 per lane per load
+    float g = 1.0f;
+    if (a.se_gate_vec) {
+      float acc = 0.f;
+      const int n8 = a.D >> 3;
+      const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec);
+      const uint4 *xv = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D);
+      for (int c = lane; c < n8; c += 64) {
+        const uint4 gq = gv[c], xq = xv[c];
+        acc = dot2(gq.x, xq.x, acc);
+        acc = dot2(gq.y, xq.y, acc);
+        acc = dot2(gq.z, xq.z, acc);
+        acc = dot2(gq.w, xq.w, acc);
+      }
+      acc = wave_sum_f32(acc);
+      g = 1.0f / (1.0f + __expf(-acc));
+    }
+    if (lane == 0) w.gs[t] = g;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. grouping into tiles (one block)
+
+__global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, MoeMWs w) {
+  __shared__ int s_cnt[kMMaxE];
+  __shared__ int s_start[kMMaxE];
+  __shared__ int s_tbase[kMMaxE];
+  __shared__ int s_fill[kMMaxE];
+  __shared__ int s_wave_tot[kMGroupThreads / 64];
+  __shared__ int s_routed_tiles;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nslots = a.B * a.k;
+  for (int e = tid; e < kMMaxE; e += kMGroupThreads) {
+    s_cnt[e] = 0;
+    s_fill[e] = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < nslots; i += kMGroupThreads) atomicAdd(&s_cnt[w.topk_idx[i]], 1);
+  __syncthreads();
+  {
+    // exclusive scan over experts of (slots << 14 | tiles): slots <= 2^16,
+    // tiles <= 2^12 + 2^10
+    const int e = tid;
+    const int c = e < a.E ? s_cnt[e] : 0;
+    const int v = (c << 14) | ((c + kMTok - 1) / kMTok);
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int n = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += n;
+    }
+    if (lane == 63) s_wave_tot[wave] = incl;
+    __syncthreads();
+    int prefix = 0;
+    for (int q = 0; q < wave; ++q) prefix += s_wave_tot[q];
+    const int excl = prefix + incl - v;
+    if (e < a.E) {
+      s_start[e] = excl >> 14;
+      s_tbase[e] = excl & 16383;
+    }
+    if (tid == kMGroupThreads - 1) s_routed_tiles = (prefix + incl) & 16383;
+  }
+  __syncthreads();
+  // placement in arrival order (each row's arithmetic is independent of it)
+  for (int i = tid; i < nslots; i += kMGroupThreads) {
+    const int e = w.topk_idx[i];
+    const int gp = s_start[e] + atomicAdd(&s_fill[e], 1);
+    w.tok[gp] = i / a.k;
+    w.gpos[i] = gp;
+  }
+  for (int e = tid; e < a.E; e += kMGroupThreads) {
+    const int c = s_cnt[e];
+    for (int tt = 0; tt * kMTok < c; ++tt)
+      w.tiles[s_tbase[e] + tt] = make_int4(e, s_start[e] + kMTok * tt, min(kMTok, c - kMTok * tt), 0);
+  }
+  const int R = s_routed_tiles;
+  const int S = a.sgate.m.w ? (a.B + kMTok - 1) / kMTok : 0;
+  for (int tt = tid; tt < S; tt += kMGroupThreads)
+    w.tiles[R + tt] = make_int4(-1, nslots + kMTok * tt, min(kMTok, a.B - kMTok * tt), 0);
+  if (tid == 0) *w.n_tiles = R + S;
+}
+
+// ---------------------------------------------------------------------------
+// shared pieces of the MFMA kernels
+
+// LDS tile of 16 rows of bf16 in 16-byte granules; granule q of row m sits at
+// q ^ m inside its aligned run of 16 granules, so the 16 rows of one MFMA
+// operand read hit 16 different bank groups.
+__device__ __forceinline__ int swz(int m, int q) { return q ^ (m & 15); }
+
+template <int BITS>
+struct MfmaStep {
+  // operand of one 64-code step: two 8-k slices per lane
+  static __device__ __forceinline__ void a_ops(const uint16_t *rowp, int q0, int m, bf16x8_t &a0,
+                                               bf16x8_t &a1) {
+    const uint4 v0 = *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0));
+    const uint4 v1 = *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0 + 1));
+    if constexpr (BITS == 4) {
+      a0 = a_nibble_order(v0);
+      a1 = a_nibble_order(v1);
+    } else {
+      a0 = __builtin_bit_cast(bf16x8_t, v0);
+      a1 = __builtin_bit_cast(bf16x8_t, v1);
+    }
+  }
+  static __device__ __forceinline__ void b_ops(const SkRaw<BITS> &r, const UnpackConsts &kc,
+                                               bf16x8_t &b0, bf16x8_t &b1) {
+    if constexpr (BITS == 4) {
+      b0 = b_from_nibbles(r.v.x, kc);
+      b1 = b_from_nibbles(r.v.y, kc);
+    } else {
+      b0 = b_from_bytes(r.v.x, r.v.y);
+      b1 = b_from_bytes(r.v.z, r.v.w);
+    }
+  }
+  static __device__ __forceinline__ void load_raw(SkRaw<BITS> &r, const uint8_t *row, int k) {
+    if constexpr (BITS == 4)
+      r.v = *reinterpret_cast<const uint2 *>(row + (k >> 1));
+    else
+      r.v = *reinterpret_cast<const uint4 *>(row + k);
+  }
+  // y += s' D + b' X (4-bit D = X + sum(c x)/16, 8-bit D = sum(c x))
+  static __device__ __forceinline__ void fold(f32x4_t &acc, const f32x4_t &d, const f32x4_t &xs,
+                                              float s, float b) {
+    const float s2 = BITS == 4 ? 16.f * s : s;
+    const float b2 = BITS == 4 ? b - 16.f * s : b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(b2, xs[i], fmaf(s2, d[i], acc[i]));
+  }
+};
+
+__device__ __forceinline__ const bf16x8_t mfma_ones() {
+  return as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+}
+
+// ---------------------------------------------------------------------------
+// 3. gate/up + SwiGLU: block = (tile, 64 rows), wave = 16 rows of gate and up
+
+template <int BITS>
+struct GuBatch {
+  SkRaw<BITS> g[2], u[2];
+  uint32_t sg[2], bg[2], su[2], bu[2];
+};
+
+template <int BITS>
+__global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
+  __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
+  using S = MfmaStep<BITS>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
+  if (tile >= *w.n_tiles) return;
+  const int4 tr = w.tiles[tile];
+  const int e = __builtin_amdgcn_readfirstlane(tr.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
+  const bool shared = e < 0;
+  const int rows = shared ? a.sinter : a.inter;
+  if (rb * 64 >= rows) return;
+  const DevBank &gbk = shared ? a.sgate : a.gate;
+  const DevBank &ubk = shared ? a.sup : a.up;
+  const size_t eo = shared ? 0 : (size_t)e;
+  const int j = min(rb * 64 + wave * 16 + r16, rows - 1);
+  const uint8_t *gw = gbk.m.w + eo * gbk.w_stride + (size_t)j * gbk.m.row_bytes;
+  const uint8_t *uw = ubk.m.w + eo * ubk.w_stride + (size_t)j * ubk.m.row_bytes;
+  const uint16_t *gsr = gbk.m.sc + eo * gbk.p_stride + (size_t)j * gbk.m.ng;
+  const uint16_t *gbr = gbk.m.bi + eo * gbk.p_stride + (size_t)j * gbk.m.ng;
+  const uint16_t *usr = ubk.m.sc + eo * ubk.p_stride + (size_t)j * ubk.m.ng;
+  const uint16_t *ubr = ubk.m.bi + eo * ubk.p_stride + (size_t)j * ubk.m.ng;
+  const int gsteps = gbk.m.gs >> 6;
+  const int nslots = a.B * a.k;
+  const int chunk = a.D < kMChunk ? a.D : kMChunk;
+  const int nch = a.D / chunk;
+  const int spc = chunk >> 6;  // steps per chunk (even)
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](int st, GuBatch<BITS> &B) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = (st + u) * 64 + 16 * g;
+      S::load_raw(B.g[u], gw, k);
+      S::load_raw(B.u[u], uw, k);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int gi = (st + u) / gsteps;
+      B.sg[u] = gsr[gi];
+      B.bg[u] = gbr[gi];
+      B.su[u] = usr[gi];
+      B.bu[u] = ubr[gi];
+    }
+  };
+  auto step = [&](int stc, const GuBatch<BITS> &B) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      bf16x8_t a0, a1, b0, b1;
+      S::a_ops(sx + r16 * chunk, ((stc + u) * 64 + 16 * g) >> 3, r16, a0, a1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      S::b_ops(B.g[u], kc, b0, b1);
+      f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      S::fold(accg, d, xs, aux_to_f32_sel(B.sg[u], gbk.m.fp16), aux_to_f32_sel(B.bg[u], gbk.m.fp16));
+      S::b_ops(B.u[u], kc, b0, b1);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      S::fold(accu, d, xs, aux_to_f32_sel(B.su[u], ubk.m.fp16), aux_to_f32_sel(B.bu[u], ubk.m.fp16));
+    }
+  };
+
+  for (int c = 0; c < nch; ++c) {
+    const int s0 = c * spc;
+    GuBatch<BITS> B0, B1;
+    issue(s0, B0);
+    // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk)
+    if (c > 0) __syncthreads();
+    {
+      // every load issued before any store (at most 8 granules per thread;
+      // threads past the tile re-read its last granule)
+      const int gpr = chunk >> 3;  // granules per row
+      const int lim = cnt * gpr;
+      uint4 v[kMTok * kMChunk / 8 / 256];
+#pragma unroll
+      for (int i = 0; i < kMTok * kMChunk / 8 / 256; ++i) {
+        const int q = min(tid + 256 * i, lim - 1);
+        const int m = q / gpr, qq = q % gpr;
+        const int t = shared ? row0 - nslots + m : w.tok[row0 + m];
+        v[i] = *reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D + c * chunk + 8 * qq);
+      }
+#pragma unroll
+      for (int i = 0; i < kMTok * kMChunk / 8 / 256; ++i) {
+        const int q = tid + 256 * i;
+        if (q < lim) {
+          const int m = q / gpr, qq = q % gpr;
+          *reinterpret_cast<uint4 *>(sx + m * chunk + 8 * swz(m, qq)) = v[i];
+        }
+      }
+    }
+    __syncthreads();
+    // batches of two steps; issues past the chunk end reload its last batch
+    // (unconditional, so the in-order vmcnt stays exact)
+    for (int b = 0; b < spc; b += 4) {
+      issue(s0 + min(b + 2, spc - 2), B1);
+      __builtin_amdgcn_sched_barrier(0);
+      step(b, B0);
+      issue(s0 + min(b + 4, spc - 2), B0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b + 2 < spc) step(b + 2, B1);
+    }
+  }
+  // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16
+  const int jj = rb * 64 + wave * 16 + r16;
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  if (jj < rows) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * g + i;
+      if (m < cnt) {
+        const float h = silu(accg[i]) * accu[i];
+        const uint32_t hi = f32_to_bf16_rne(h);
+        const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
+        const size_t o = (size_t)(row0 + m) * hmax + jj;
+        w.h_hi[o] = (uint16_t)hi;
+        w.h_lo[o] = (uint16_t)lo;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512
+
+template <int BITS>
+struct DnBatch {
+  SkRaw<BITS> w[2][2];  // [step][row tile]
+  uint32_t s[2][2], b[2][2];
+};
+
+template <int BITS>
+__global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
+  __shared__ __align__(16) uint16_t shi[kMTok * kMDownK];
+  __shared__ __align__(16) uint16_t slo[kMTok * kMDownK];
+  using S = MfmaStep<BITS>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
+  if (tile >= *w.n_tiles) return;
+  const int4 tr = w.tiles[tile];
+  const int e = __builtin_amdgcn_readfirstlane(tr.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
+  const bool shared = e < 0;
+  const DevBank &dbk = shared ? a.sdown : a.down;
+  const int K = shared ? a.sinter : a.inter;
+  const size_t eo = shared ? 0 : (size_t)e;
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  const uint8_t *wr[2];
+  const uint16_t *sr[2], *br[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int d = min(rb * 128 + wave * 32 + 16 * r + r16, a.D - 1);
+    wr[r] = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
+    sr[r] = dbk.m.sc + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
+    br[r] = dbk.m.bi + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
+  }
+  const int gsteps = dbk.m.gs >> 6;
+  const int steps = K >> 6;  // even
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+
+  auto issue = [&](int st, DnBatch<BITS> &B) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) S::load_raw(B.w[u][r], wr[r], (st + u) * 64 + 16 * g);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int gi = (st + u) / gsteps;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        B.s[u][r] = sr[r][gi];
+        B.b[u][r] = br[r][gi];
+      }
+    }
+  };
+  auto step = [&](int st, const DnBatch<BITS> &B) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int q0 = ((st + u) * 64 + 16 * g) >> 3;
+      bf16x8_t h0, h1, l0, l1;
+      S::a_ops(shi + r16 * K, q0, r16, h0, h1);
+      S::a_ops(slo + r16 * K, q0, r16, l0, l1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, ones, xs, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, ones, xs, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, ones, xs, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        bf16x8_t b0, b1;
+        S::b_ops(B.w[u][r], kc, b0, b1);
+        f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, b0, z, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, b1, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, b0, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, b1, d, 0, 0, 0);
+        S::fold(acc[r], d, xs, aux_to_f32_sel(B.s[u][r], dbk.m.fp16), aux_to_f32_sel(B.b[u][r], dbk.m.fp16));
+      }
+    }
+  };
+
+  DnBatch<BITS> B0, B1;
+  issue(0, B0);
+  {
+    // stage h (hi, lo) of the tile's rows
+    constexpr int NQ = kMTok * kMDownK / 8 / 256;
+    const int gpr = K >> 3;
+    const int lim = cnt * gpr;
+    uint4 vh[NQ], vl[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q = min(tid + 256 * i, lim - 1);
+      const size_t o = (size_t)(row0 + q / gpr) * hmax + 8 * (q % gpr);
+      vh[i] = *reinterpret_cast<const uint4 *>(w.h_hi + o);
+      vl[i] = *reinterpret_cast<const uint4 *>(w.h_lo + o);
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q = tid + 256 * i;
+      if (q < lim) {
+        const int m = q / gpr, qq = q % gpr;
+        *reinterpret_cast<uint4 *>(shi + m * K + 8 * swz(m, qq)) = vh[i];
+        *reinterpret_cast<uint4 *>(slo + m * K + 8 * swz(m, qq)) = vl[i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int st = 0; st < steps; st += 4) {
+    issue(min(st + 2, steps - 2), B1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(st, B0);
+    issue(min(st + 4, steps - 2), B0);  // unconditional: exact vmcnt
+    __builtin_amdgcn_sched_barrier(0);
+    if (st + 2 < steps) step(st + 2, B1);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int d = rb * 128 + wave * 32 + 16 * r + r16;
+    if (d >= a.D) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * g + i;
+      if (m < cnt) w.y[(size_t)(row0 + m) * a.D + d] = acc[r][i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 5. rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711)
+
+__global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) {
+  const long long n = (long long)a.B * a.D;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+    const int t = (int)(i / a.D), d = (int)(i % a.D);
+    float acc = 0.f;
+    for (int r = 0; r < a.k; ++r) {
+      const int slot = t * a.k + r;
+      acc = fmaf(w.y[(size_t)w.gpos[slot] * a.D + d], w.topk_w[slot], acc);
+    }
+    float o = acc;
+    if (a.sdown.m.w) o = fmaf(w.y[((size_t)a.B * a.k + t) * a.D + d], w.gs[t], acc);
+    if (a.out_f32)
+      reinterpret_cast<float *>(a.out)[i] = o;
+    else
+      reinterpret_cast<uint16_t *>(a.out)[i] = (uint16_t)f32_to_bf16_rne(o);
+  }
+}
+
+// ---------------------------------------------------------------------------
+
+static bool mbank_ok(const DevBank &b) {
+  const DevMat &m = b.m;
+  if (m.bits != 4 && m.bits != 8) return false;
+  if (m.gs <= 0 || m.gs % 64 != 0 || m.I % m.gs != 0) return false;
+  const uintptr_t need = m.bits == 4 ? 7 : 15;
+  if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
+  if ((b.w_stride & (long long)need) != 0) return false;
+  return true;
+}
+
+bool moe_mfma_supported(const MoeArgs &a) {
+  if (a.B <= 0 || (long long)a.B * a.k > kMMaxSlots || a.E > kMMaxE) return false;
+  if (a.D % 128 != 0 || (a.D > kMChunk && a.D % kMChunk != 0)) return false;
+  if (a.inter % 128 != 0 || a.inter > kMDownK) return false;
+  if (!mbank_ok(a.gate) || !mbank_ok(a.up) || !mbank_ok(a.down)) return false;
+  if (a.up.m.bits != a.gate.m.bits || a.down.m.bits != a.gate.m.bits) return false;
+  if (a.sgate.m.w) {
+    if (a.sinter % 128 != 0 || a.sinter > kMDownK) return false;
+    if (!mbank_ok(a.sgate) || !mbank_ok(a.sup) || !mbank_ok(a.sdown)) return false;
+    if (a.sgate.m.bits != a.gate.m.bits || a.sup.m.bits != a.gate.m.bits ||
+        a.sdown.m.bits != a.gate.m.bits)
+      return false;
+  }
+  return true;
+}
+
+template <int BITS>
+static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
+  const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
+  {
+    const int ipt = (kmax + 63) / 64;
+    hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  {
+    const int ipt = (a.D + 127) / 128;
+    hipLaunchKernelGGL((moe_down_mfma_kernel<BITS>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  {
+    long long n = (long long)a.B * a.D;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(moe_mcombine_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a, w);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  return 1;
+}
+
+// a.sinter is 0 when there is no shared expert; the caller has validated the
+// banks against the block geometry.
+int launch_moe_mfma(const MoeArgs &a, hipStream_t st) {
+  if (!moe_mfma_supported(a)) return 0;
+  if (a.ws_bytes < moe_mfma_workspace_bytes(a.B, a.D, a.inter, a.sinter, a.E, a.k)) return 0;
+  const MoeMWs w = moe_mws_layout(a.ws, a.B, a.D, a.inter, a.sinter, a.E, a.k);
+  const dim3 rgrid((a.B + 3) / 4);
+  if (a.logits_f32) {
+    if (a.E <= 512) hipLaunchKernelGGL((moe_mroute_kernel<8, true>), rgrid, dim3(256), 0, st, a, w);
+    else hipLaunchKernelGGL((moe_mroute_kernel<16, true>), rgrid, dim3(256), 0, st, a, w);
+  } else {
+    if (a.E <= 512) hipLaunchKernelGGL((moe_mroute_kernel<8, false>), rgrid, dim3(256), 0, st, a, w);
+    else hipLaunchKernelGGL((moe_mroute_kernel<16, false>), rgrid, dim3(256), 0, st, a, w);
+  }
+  if (hipGetLastError() != hipSuccess) return -1;
+  hipLaunchKernelGGL(moe_mgroup_kernel, dim3(1), dim3(kMGroupThreads), 0, st, a, w);
+  if (hipGetLastError() != hipSuccess) return -1;
+  return a.gate.m.bits == 4 ? moe_mfma_launch_bits<4>(a, w, st) : moe_mfma_launch_bits<8>(a, w, st);
+}
+
+}  // namespace lh

@@ -287,3 +287,106 @@ def test_moe_fused_agrees_with_multi_launch(gpu):
     np.testing.assert_allclose(wa, wb, rtol=1e-6)
     assert normwise_rel(a.cpu().numpy(), b.cpu().numpy()) < 2e-5
     assert _lib.lib().logan_hip_moe_sync_errors() == 0
+
+
+@pytest.fixture
+def mfma_min_b(request):
+    """Set the smallest batch that takes the MFMA path for one test, restore
+    the default after."""
+    from logan_amd import _lib
+
+    b = getattr(request, "param", 1)
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(b)
+    yield b
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(96)
+
+
+def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
+    xf, lf = bf16_to_f32(xb), bf16_to_f32(lb)
+    for t in tokens:
+        ref, ridx, rw = layer.ref(xf[t], lf[t])
+        np.testing.assert_array_equal(idx[t], ridx)
+        np.testing.assert_allclose(w[t], rw, rtol=1e-5)
+        err = normwise_rel(out32[t], ref)
+        assert err <= 5e-5, f"token {t}: {err:.3e} (expected f32-accumulation level)"
+
+
+@pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
+@pytest.mark.parametrize("bits,B,zipf,shared", [(4, 2, False, True), (4, 16, False, True),
+                                                (8, 5, False, True), (4, 40, True, True),
+                                                (8, 33, True, False)])
+def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
+    """The token-batch MFMA path (forced for every B) against the oracle:
+    routing bit-exact, outputs at f32-accumulation level; Zipf routes put
+    more than 16 tokens on the popular experts (several tiles per expert)."""
+    import torch
+
+    print(f"moe mfma bits={bits} B={B} zipf={zipf} shared={shared}", flush=True)
+    layer = Layer(torch, 512, 10, 2048, 512, bits, 64, seed=bits * 7 + B, shared=shared)
+    rng = np.random.default_rng(2000 + B)
+    xb = make_x(rng, B, 2048)
+    lb = make_logits(rng, B, 512, zipf_s=1.1 if zipf else None)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    out16, idx2, _ = run_layer(torch, layer, xb, lb, torch.bfloat16)
+    out32 = out32.cpu().numpy()
+    np.testing.assert_array_equal(idx, idx2)
+    np.testing.assert_array_equal(out16.view(torch.int16).cpu().numpy().view(np.uint16),
+                                  bf16_bits(out32))
+    if zipf:
+        assert np.bincount(idx.reshape(-1)).max() > 16
+    _check_tokens(layer, xb, lb, out32, idx, w, range(B))
+
+
+@pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
+def test_moe_mfma_shapes_and_group_sizes(gpu, mfma_min_b):
+    """Smaller shapes through the MFMA path: D = 512 (one LDS chunk), inter =
+    256, a shared expert of 384 rows, group size 128."""
+    import torch
+
+    layer = Layer(torch, 64, 6, 512, 256, 4, 128, seed=31, sinter=384)
+    rng = np.random.default_rng(32)
+    B = 24
+    xb = make_x(rng, B, 512)
+    lb = make_logits(rng, B, 64, zipf_s=1.1)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(B))
+
+
+def test_moe_prefill_chunk_sampled(gpu):
+    """A prefill-sized batch (B = 512, the config-5 chunk) with the default
+    threshold (MFMA path), checked against the oracle on a sample of tokens,
+    and against the per-token path on every token."""
+    import torch
+    from logan_amd import _lib
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=41)
+    rng = np.random.default_rng(42)
+    B = 512
+    xb = make_x(rng, B, 2048)
+    lb = make_logits(rng, B, 512)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    out32 = out32.cpu().numpy()
+    _check_tokens(layer, xb, lb, out32, idx, w, range(0, B, 37))
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(1 << 20)
+    try:
+        out_d, idx_d, _ = run_layer(torch, layer, xb, lb, torch.float32)
+    finally:
+        _lib.lib().logan_hip_set_moe_mfma_min_batch(96)
+    np.testing.assert_array_equal(idx, idx_d)
+    out_d = out_d.cpu().numpy()
+    for t in range(B):
+        assert normwise_rel(out32[t], out_d[t]) <= 5e-5
+
+
+def test_moe_large_batch_without_mfma_kernels(gpu):
+    """5-bit codes have no MFMA kernel: B = 100 runs the per-token path in
+    passes of 64 tokens, every token against the oracle."""
+    import torch
+
+    layer = Layer(torch, 512, 10, 2048, 512, 5, 64, seed=51)
+    rng = np.random.default_rng(52)
+    B = 100
+    xb = make_x(rng, B, 2048)
+    lb = make_logits(rng, B, 512, zipf_s=1.1)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(0, B, 3))
