@@ -29,7 +29,7 @@
 namespace lh {
 
 constexpr int kMTok = 16;          // slots per tile
-constexpr int kMChunk = 1024;      // x codes staged in LDS at a time (gate/up)
+constexpr int kMChunk = 2048;      // x codes staged in LDS at a time (gate/up)
 constexpr int kMDownK = 512;       // largest down K (expert intermediate size)
 constexpr int kMMaxSlots = 65536;  // B * k
 constexpr int kMMaxE = 1024;
@@ -43,7 +43,8 @@ struct MoeMWs {
   int32_t *topk_idx;  // [B*k]
   float *topk_w;      // [B*k]
   float *gs;          // [B]
-  uint16_t *h_hi;     // [(B*k + B) * hmax] bf16
+  uint16_t *xop;      // [B * D] x in the 4-bit operand order (a_nibble_order per 8)
+  uint16_t *h_hi;     // [(B*k + B) * hmax] bf16, stored in the operand order
   uint16_t *h_lo;     // [(B*k + B) * hmax] bf16
   float *y;           // [(B*k + B) * D]
   int max_tiles;
@@ -73,6 +74,7 @@ static MoeMWs moe_mws_layout(void *base, int B, int D, int inter, int sinter, in
   w.topk_idx = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * nsl));
   w.topk_w = reinterpret_cast<float *>(take(sizeof(float) * nsl));
   w.gs = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B));
+  w.xop = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * (size_t)B * D));
   w.h_hi = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * slots * hmax));
   w.h_lo = reinterpret_cast<uint16_t *>(take(sizeof(uint16_t) * slots * hmax));
   w.y = reinterpret_cast<float *>(take(sizeof(float) * slots * (size_t)D));
@@ -101,6 +103,12 @@ __global__ __launch_bounds__(256) void moe_mroute_kernel(MoeArgs a, MoeMWs w) {
     w.topk_w[s] = wt;
     if (a.idx_out) a.idx_out[s] = id;
     if (a.w_out) a.w_out[s] = wt;
+  }
+  if (a.gate.m.bits == 4) {
+    // x in the operand order of 4-bit codes: pairs (x_p, x_{p+4}) of every 8
+    const uint4 *xs = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D);
+    uint4 *xd = reinterpret_cast<uint4 *>(w.xop + (size_t)t * a.D);
+    for (int c = lane; c < (a.D >> 3); c += 64) xd[c] = __builtin_bit_cast(uint4, a_nibble_order(xs[c]));
   }
   if (a.sgate.m.w) {
     // sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604), 8 bf16 per lane per load
@@ -196,17 +204,20 @@ __device__ __forceinline__ int swz(int m, int q) { return q ^ (m & 15); }
 
 template <int BITS>
 struct MfmaStep {
-  // operand of one 64-code step: two 8-k slices per lane
+  // activation operand of one 64-code step (two 8-k slices per lane) from an
+  // LDS tile already in the operand order of BITS-bit codes
   static __device__ __forceinline__ void a_ops(const uint16_t *rowp, int q0, int m, bf16x8_t &a0,
                                                bf16x8_t &a1) {
-    const uint4 v0 = *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0));
-    const uint4 v1 = *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0 + 1));
+    a0 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0)));
+    a1 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0 + 1)));
+  }
+  // position of activation k inside its run of 8 in the operand order
+  static __device__ __forceinline__ int op_pos(int k) {
     if constexpr (BITS == 4) {
-      a0 = a_nibble_order(v0);
-      a1 = a_nibble_order(v1);
+      const int i = k & 7;
+      return (k & ~7) | (i < 4 ? 2 * i : 2 * (i - 4) + 1);
     } else {
-      a0 = __builtin_bit_cast(bf16x8_t, v0);
-      a1 = __builtin_bit_cast(bf16x8_t, v1);
+      return k;
     }
   }
   static __device__ __forceinline__ void b_ops(const SkRaw<BITS> &r, const UnpackConsts &kc,
@@ -235,22 +246,80 @@ struct MfmaStep {
   }
 };
 
+template <bool FP16>
+__device__ __forceinline__ float aux_f32(uint32_t b) {
+  if constexpr (FP16) return f16_to_f32(b);
+  else return bf16_to_f32(b);
+}
+
 __device__ __forceinline__ const bf16x8_t mfma_ones() {
   return as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 }
 
 // ---------------------------------------------------------------------------
-// 3. gate/up + SwiGLU: block = (tile, 64 rows), wave = 16 rows of gate and up
+// 3. gate/up + SwiGLU: block = (tile, 16 * WAVES rows), wave = 16 rows of gate
+//    and up; batches of GU 64-code steps double-buffered in registers
 
-template <int BITS>
-struct GuBatch {
-  SkRaw<BITS> g[2], u[2];
-  uint32_t sg[2], bg[2], su[2], bu[2];
+#ifndef MOE_GU
+#define MOE_GU 4
+#endif
+#ifndef MOE_GU_WAVES
+#define MOE_GU_WAVES 8
+#endif
+#ifndef MOE_GU_MINW
+#define MOE_GU_MINW 1  // minimum waves per SIMD (register cap)
+#endif
+
+// scale/bias words of GU steps for one lane's row: with 64-code groups the GU
+// consecutive u16 come in one load
+template <int GU, bool GS64>
+struct AuxRun {
+  uint32_t s[GS64 ? GU / 2 : GU], b[GS64 ? GU / 2 : GU];
+  __device__ __forceinline__ void load(const uint16_t *sr, const uint16_t *br, int st, int gsteps) {
+    if constexpr (GS64) {
+      static_assert(GU == 2 || GU == 4 || GU == 8, "aux run of 2, 4 or 8 steps");
+      if constexpr (GU == 8) {
+        const uint4 vs = *reinterpret_cast<const uint4 *>(sr + st);
+        const uint4 vb = *reinterpret_cast<const uint4 *>(br + st);
+        s[0] = vs.x; s[1] = vs.y; s[2] = vs.z; s[3] = vs.w;
+        b[0] = vb.x; b[1] = vb.y; b[2] = vb.z; b[3] = vb.w;
+      } else if constexpr (GU == 4) {
+        const uint2 vs = *reinterpret_cast<const uint2 *>(sr + st);
+        const uint2 vb = *reinterpret_cast<const uint2 *>(br + st);
+        s[0] = vs.x; s[1] = vs.y; b[0] = vb.x; b[1] = vb.y;
+      } else {
+        s[0] = *reinterpret_cast<const uint32_t *>(sr + st);
+        b[0] = *reinterpret_cast<const uint32_t *>(br + st);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < GU; ++u) {
+        s[u] = sr[(st + u) / gsteps];
+        b[u] = br[(st + u) / gsteps];
+      }
+    }
+  }
+  __device__ __forceinline__ uint32_t sw(int u) const {
+    if constexpr (GS64) return (s[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+    else return s[u];
+  }
+  __device__ __forceinline__ uint32_t bw(int u) const {
+    if constexpr (GS64) return (b[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+    else return b[u];
+  }
 };
 
-template <int BITS>
-__global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
+template <int BITS, int GU, bool GS64>
+struct GuBatch {
+  SkRaw<BITS> g[GU], u[GU];
+  AuxRun<GU, GS64> ag, au;
+};
+
+template <int BITS, int GU, int WAVES, bool GS64, bool FP16>
+__global__ __launch_bounds__(WAVES * 64, MOE_GU_MINW) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
   __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
+  constexpr int NT = WAVES * 64;
+  constexpr int RPB = 16 * WAVES;
   using S = MfmaStep<BITS>;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -263,11 +332,11 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
   const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
   const bool shared = e < 0;
   const int rows = shared ? a.sinter : a.inter;
-  if (rb * 64 >= rows) return;
+  if (rb * RPB >= rows) return;
   const DevBank &gbk = shared ? a.sgate : a.gate;
   const DevBank &ubk = shared ? a.sup : a.up;
   const size_t eo = shared ? 0 : (size_t)e;
-  const int j = min(rb * 64 + wave * 16 + r16, rows - 1);
+  const int j = min(rb * RPB + wave * 16 + r16, rows - 1);
   const uint8_t *gw = gbk.m.w + eo * gbk.w_stride + (size_t)j * gbk.m.row_bytes;
   const uint8_t *uw = ubk.m.w + eo * ubk.w_stride + (size_t)j * ubk.m.row_bytes;
   const uint16_t *gsr = gbk.m.sc + eo * gbk.p_stride + (size_t)j * gbk.m.ng;
@@ -278,31 +347,26 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
   const int nslots = a.B * a.k;
   const int chunk = a.D < kMChunk ? a.D : kMChunk;
   const int nch = a.D / chunk;
-  const int spc = chunk >> 6;  // steps per chunk (even)
+  const int bpc = (chunk >> 6) / GU;  // batches per chunk
+  const uint16_t *xsrc = BITS == 4 ? w.xop : a.x;  // x in the operand order
   UnpackConsts kc;
   kc.init();
   const bf16x8_t ones = mfma_ones();
   f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 
-  auto issue = [&](int st, GuBatch<BITS> &B) {
+  auto issue = [&](int st, GuBatch<BITS, GU, GS64> &B) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < GU; ++u) {
       const int k = (st + u) * 64 + 16 * g;
       S::load_raw(B.g[u], gw, k);
       S::load_raw(B.u[u], uw, k);
     }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int gi = (st + u) / gsteps;
-      B.sg[u] = gsr[gi];
-      B.bg[u] = gbr[gi];
-      B.su[u] = usr[gi];
-      B.bu[u] = ubr[gi];
-    }
+    B.ag.load(gsr, gbr, st, gsteps);
+    B.au.load(usr, ubr, st, gsteps);
   };
-  auto step = [&](int stc, const GuBatch<BITS> &B) {
+  auto step = [&](int stc, const GuBatch<BITS, GU, GS64> &B) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < GU; ++u) {
       bf16x8_t a0, a1, b0, b1;
       S::a_ops(sx + r16 * chunk, ((stc + u) * 64 + 16 * g) >> 3, r16, a0, a1);
       const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
@@ -311,36 +375,36 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
       S::b_ops(B.g[u], kc, b0, b1);
       f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
-      S::fold(accg, d, xs, aux_to_f32_sel(B.sg[u], gbk.m.fp16), aux_to_f32_sel(B.bg[u], gbk.m.fp16));
+      S::fold(accg, d, xs, aux_f32<FP16>(B.ag.sw(u)), aux_f32<FP16>(B.ag.bw(u)));
       S::b_ops(B.u[u], kc, b0, b1);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
-      S::fold(accu, d, xs, aux_to_f32_sel(B.su[u], ubk.m.fp16), aux_to_f32_sel(B.bu[u], ubk.m.fp16));
+      S::fold(accu, d, xs, aux_f32<FP16>(B.au.sw(u)), aux_f32<FP16>(B.au.bw(u)));
     }
   };
 
   for (int c = 0; c < nch; ++c) {
-    const int s0 = c * spc;
-    GuBatch<BITS> B0, B1;
+    const int s0 = c * chunk >> 6;
+    GuBatch<BITS, GU, GS64> B0, B1;
     issue(s0, B0);
-    // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk)
+    // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk): every load
+    // issued before any store; threads past the tile re-read its last granule
     if (c > 0) __syncthreads();
     {
-      // every load issued before any store (at most 8 granules per thread;
-      // threads past the tile re-read its last granule)
+      constexpr int NV = kMTok * kMChunk / 8 / NT;
       const int gpr = chunk >> 3;  // granules per row
       const int lim = cnt * gpr;
-      uint4 v[kMTok * kMChunk / 8 / 256];
+      uint4 v[NV];
 #pragma unroll
-      for (int i = 0; i < kMTok * kMChunk / 8 / 256; ++i) {
-        const int q = min(tid + 256 * i, lim - 1);
+      for (int i = 0; i < NV; ++i) {
+        const int q = min(tid + NT * i, lim - 1);
         const int m = q / gpr, qq = q % gpr;
         const int t = shared ? row0 - nslots + m : w.tok[row0 + m];
-        v[i] = *reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D + c * chunk + 8 * qq);
+        v[i] = *reinterpret_cast<const uint4 *>(xsrc + (size_t)t * a.D + c * chunk + 8 * qq);
       }
 #pragma unroll
-      for (int i = 0; i < kMTok * kMChunk / 8 / 256; ++i) {
-        const int q = tid + 256 * i;
+      for (int i = 0; i < NV; ++i) {
+        const int q = tid + NT * i;
         if (q < lim) {
           const int m = q / gpr, qq = q % gpr;
           *reinterpret_cast<uint4 *>(sx + m * chunk + 8 * swz(m, qq)) = v[i];
@@ -348,19 +412,20 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
       }
     }
     __syncthreads();
-    // batches of two steps; issues past the chunk end reload its last batch
-    // (unconditional, so the in-order vmcnt stays exact)
-    for (int b = 0; b < spc; b += 4) {
-      issue(s0 + min(b + 2, spc - 2), B1);
+    // issues past the chunk end reload its last batch (unconditional, so the
+    // in-order vmcnt stays exact)
+    for (int b = 0; b < bpc; b += 2) {
+      issue(s0 + GU * min(b + 1, bpc - 1), B1);
       __builtin_amdgcn_sched_barrier(0);
-      step(b, B0);
-      issue(s0 + min(b + 4, spc - 2), B0);
+      step(GU * b, B0);
+      issue(s0 + GU * min(b + 2, bpc - 1), B0);
       __builtin_amdgcn_sched_barrier(0);
-      if (b + 2 < spc) step(b + 2, B1);
+      if (b + 1 < bpc) step(GU * (b + 1), B1);
     }
   }
-  // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16
-  const int jj = rb * 64 + wave * 16 + r16;
+  // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16,
+  // each at its place in the down pass's operand order
+  const int jj = rb * RPB + wave * 16 + r16;
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   if (jj < rows) {
 #pragma unroll
@@ -370,7 +435,7 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
         const float h = silu(accg[i]) * accu[i];
         const uint32_t hi = f32_to_bf16_rne(h);
         const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
-        const size_t o = (size_t)(row0 + m) * hmax + jj;
+        const size_t o = (size_t)(row0 + m) * hmax + S::op_pos(jj);
         w.h_hi[o] = (uint16_t)hi;
         w.h_lo[o] = (uint16_t)lo;
       }
@@ -379,16 +444,12 @@ __global__ __launch_bounds__(256) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs 
 }
 
 // ---------------------------------------------------------------------------
-// 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512
+// 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512: every
+//    weight and scale/bias load of the wave is issued before h is staged
 
-template <int BITS>
-struct DnBatch {
-  SkRaw<BITS> w[2][2];  // [step][row tile]
-  uint32_t s[2][2], b[2][2];
-};
-
-template <int BITS>
+template <int BITS, bool FP16>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
+  constexpr int NS = kMDownK / 64;  // steps at most
   __shared__ __align__(16) uint16_t shi[kMTok * kMDownK];
   __shared__ __align__(16) uint16_t slo[kMTok * kMDownK];
   using S = MfmaStep<BITS>;
@@ -406,66 +467,44 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
   const int K = shared ? a.sinter : a.inter;
   const size_t eo = shared ? 0 : (size_t)e;
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
-  const uint8_t *wr[2];
-  const uint16_t *sr[2], *br[2];
+  const int steps = K >> 6;
+  const int gsteps = dbk.m.gs >> 6;
+  // scale/bias as dwords of two steps when every step is its own group
+  const bool pair_aux = gsteps == 1 && (dbk.m.ng & 1) == 0;
+  SkRaw<BITS> wr[2][NS];
+  uint32_t sr[2][NS], br[2][NS];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int d = min(rb * 128 + wave * 32 + 16 * r + r16, a.D - 1);
-    wr[r] = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
-    sr[r] = dbk.m.sc + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
-    br[r] = dbk.m.bi + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
+    const uint8_t *wrow = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) S::load_raw(wr[r][u], wrow, min(u, steps - 1) * 64 + 16 * g);
   }
-  const int gsteps = dbk.m.gs >> 6;
-  const int steps = K >> 6;  // even
-  UnpackConsts kc;
-  kc.init();
-  const bf16x8_t ones = mfma_ones();
-  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-
-  auto issue = [&](int st, DnBatch<BITS> &B) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+  for (int r = 0; r < 2; ++r) {
+    const int d = min(rb * 128 + wave * 32 + 16 * r + r16, a.D - 1);
+    const uint16_t *srow = dbk.m.sc + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
+    const uint16_t *brow = dbk.m.bi + eo * dbk.p_stride + (size_t)d * dbk.m.ng;
+    if (pair_aux) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) S::load_raw(B.w[u][r], wr[r], (st + u) * 64 + 16 * g);
+      for (int u = 0; u < NS; u += 2) {
+        const int q = min(u, steps - 2);
+        const uint32_t vs = *reinterpret_cast<const uint32_t *>(srow + q);
+        const uint32_t vb = *reinterpret_cast<const uint32_t *>(brow + q);
+        sr[r][u] = vs & 0xffffu; sr[r][u + 1] = vs >> 16;
+        br[r][u] = vb & 0xffffu; br[r][u + 1] = vb >> 16;
+      }
+    } else {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int gi = (st + u) / gsteps;
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        B.s[u][r] = sr[r][gi];
-        B.b[u][r] = br[r][gi];
+      for (int u = 0; u < NS; ++u) {
+        const int gi = min(u, steps - 1) / gsteps;
+        sr[r][u] = srow[gi];
+        br[r][u] = brow[gi];
       }
     }
-  };
-  auto step = [&](int st, const DnBatch<BITS> &B) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int q0 = ((st + u) * 64 + 16 * g) >> 3;
-      bf16x8_t h0, h1, l0, l1;
-      S::a_ops(shi + r16 * K, q0, r16, h0, h1);
-      S::a_ops(slo + r16 * K, q0, r16, l0, l1);
-      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, ones, z, 0, 0, 0);
-      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, ones, xs, 0, 0, 0);
-      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, ones, xs, 0, 0, 0);
-      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, ones, xs, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        bf16x8_t b0, b1;
-        S::b_ops(B.w[u][r], kc, b0, b1);
-        f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, b0, z, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, b1, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, b0, d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, b1, d, 0, 0, 0);
-        S::fold(acc[r], d, xs, aux_to_f32_sel(B.s[u][r], dbk.m.fp16), aux_to_f32_sel(B.b[u][r], dbk.m.fp16));
-      }
-    }
-  };
-
-  DnBatch<BITS> B0, B1;
-  issue(0, B0);
+  }
   {
-    // stage h (hi, lo) of the tile's rows
+    // stage h (hi, lo) of the tile's rows; every load before any store
     constexpr int NQ = kMTok * kMDownK / 8 / 256;
     const int gpr = K >> 3;
     const int lim = cnt * gpr;
@@ -488,13 +527,33 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
     }
   }
   __syncthreads();
-  for (int st = 0; st < steps; st += 4) {
-    issue(min(st + 2, steps - 2), B1);
-    __builtin_amdgcn_sched_barrier(0);
-    step(st, B0);
-    issue(min(st + 4, steps - 2), B0);  // unconditional: exact vmcnt
-    __builtin_amdgcn_sched_barrier(0);
-    if (st + 2 < steps) step(st + 2, B1);
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (u < steps) {
+      const int q0 = (u * 64 + 16 * g) >> 3;
+      bf16x8_t h0, h1, l0, l1;
+      S::a_ops(shi + r16 * K, q0, r16, h0, h1);
+      S::a_ops(slo + r16 * K, q0, r16, l0, l1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, ones, xs, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, ones, xs, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, ones, xs, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        bf16x8_t b0, b1;
+        S::b_ops(wr[r][u], kc, b0, b1);
+        f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, b0, z, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, b1, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, b0, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, b1, d, 0, 0, 0);
+        S::fold(acc[r], d, xs, aux_f32<FP16>(sr[r][u]), aux_f32<FP16>(br[r][u]));
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -512,20 +571,38 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
 // 5. rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711)
 
 __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) {
-  const long long n = (long long)a.B * a.D;
+  // four consecutive outputs per thread (D % 4 == 0)
+  const int D4 = a.D >> 2;
+  const long long n = (long long)a.B * D4;
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
-    const int t = (int)(i / a.D), d = (int)(i % a.D);
-    float acc = 0.f;
+    const int t = (int)(i / D4), d = 4 * (int)(i % D4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int r = 0; r < a.k; ++r) {
       const int slot = t * a.k + r;
-      acc = fmaf(w.y[(size_t)w.gpos[slot] * a.D + d], w.topk_w[slot], acc);
+      const float wr = w.topk_w[slot];
+      const float4 v = *reinterpret_cast<const float4 *>(w.y + (size_t)w.gpos[slot] * a.D + d);
+      acc.x = fmaf(v.x, wr, acc.x);
+      acc.y = fmaf(v.y, wr, acc.y);
+      acc.z = fmaf(v.z, wr, acc.z);
+      acc.w = fmaf(v.w, wr, acc.w);
     }
-    float o = acc;
-    if (a.sdown.m.w) o = fmaf(w.y[((size_t)a.B * a.k + t) * a.D + d], w.gs[t], acc);
-    if (a.out_f32)
-      reinterpret_cast<float *>(a.out)[i] = o;
-    else
-      reinterpret_cast<uint16_t *>(a.out)[i] = (uint16_t)f32_to_bf16_rne(o);
+    if (a.sdown.m.w) {
+      const float gs = w.gs[t];
+      const float4 v = *reinterpret_cast<const float4 *>(w.y + ((size_t)a.B * a.k + t) * a.D + d);
+      acc.x = fmaf(v.x, gs, acc.x);
+      acc.y = fmaf(v.y, gs, acc.y);
+      acc.z = fmaf(v.z, gs, acc.z);
+      acc.w = fmaf(v.w, gs, acc.w);
+    }
+    const size_t o = (size_t)t * a.D + d;
+    if (a.out_f32) {
+      *reinterpret_cast<float4 *>(reinterpret_cast<float *>(a.out) + o) = acc;
+    } else {
+      uint2 p;
+      p.x = f32_to_bf16_rne(acc.x) | (f32_to_bf16_rne(acc.y) << 16);
+      p.y = f32_to_bf16_rne(acc.z) | (f32_to_bf16_rne(acc.w) << 16);
+      *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(a.out) + o) = p;
+    }
   }
 }
 
@@ -538,14 +615,26 @@ static bool mbank_ok(const DevBank &b) {
   const uintptr_t need = m.bits == 4 ? 7 : 15;
   if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
   if ((b.w_stride & (long long)need) != 0) return false;
+  // scale/bias runs are read as 4- or 8-byte words
+  if (((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 7) != 0) return false;
+  if ((b.p_stride & 7) != 0) return false;
   return true;
 }
 
 bool moe_mfma_supported(const MoeArgs &a) {
   if (a.B <= 0 || (long long)a.B * a.k > kMMaxSlots || a.E > kMMaxE) return false;
-  if (a.D % 128 != 0 || (a.D > kMChunk && a.D % kMChunk != 0)) return false;
+  // the combine writes four outputs per store
+  if ((reinterpret_cast<uintptr_t>(a.out) & (a.out_f32 ? 15 : 7)) != 0) return false;
+  // whole batches of MOE_GU steps per LDS chunk
+  if (a.D % (64 * MOE_GU) != 0 || (a.D > kMChunk && a.D % kMChunk != 0)) return false;
   if (a.inter % 128 != 0 || a.inter > kMDownK) return false;
   if (!mbank_ok(a.gate) || !mbank_ok(a.up) || !mbank_ok(a.down)) return false;
+  // one scale/bias type per pass (gate/up and the shared gate/up; down and
+  // the shared down)
+  if (a.up.m.fp16 != a.gate.m.fp16) return false;
+  if (a.sgate.m.w && (a.sgate.m.fp16 != a.gate.m.fp16 || a.sup.m.fp16 != a.gate.m.fp16 ||
+                      a.sdown.m.fp16 != a.down.m.fp16))
+    return false;
   if (a.up.m.bits != a.gate.m.bits || a.down.m.bits != a.gate.m.bits) return false;
   if (a.sgate.m.w) {
     if (a.sinter % 128 != 0 || a.sinter > kMDownK) return false;
@@ -561,17 +650,31 @@ template <int BITS>
 static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
   const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
   {
-    const int ipt = (kmax + 63) / 64;
-    hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+    constexpr int WV = MOE_GU_WAVES;
+    const int ipt = (kmax + 16 * WV - 1) / (16 * WV);
+    // one aligned load of GU consecutive u16 scale (bias) words per batch
+    const bool gs64 = a.gate.m.gs == 64 && (!a.sgate.m.w || a.sgate.m.gs == 64) &&
+                      a.gate.m.ng % (MOE_GU < 4 ? 4 : MOE_GU) == 0;
+    const dim3 grid(w.max_tiles * ipt), block(WV * 64);
+    if (a.gate.m.fp16) {
+      if (gs64) hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, true, true>), grid, block, 0, st, a, w, ipt);
+      else hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, false, true>), grid, block, 0, st, a, w, ipt);
+    } else {
+      if (gs64) hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, true, false>), grid, block, 0, st, a, w, ipt);
+      else hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, false, false>), grid, block, 0, st, a, w, ipt);
+    }
     if (hipGetLastError() != hipSuccess) return -1;
   }
   {
     const int ipt = (a.D + 127) / 128;
-    hipLaunchKernelGGL((moe_down_mfma_kernel<BITS>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+    if (a.down.m.fp16)
+      hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, true>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+    else
+      hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, false>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   {
-    long long n = (long long)a.B * a.D;
+    long long n = (long long)a.B * (a.D >> 2);
     long long blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(moe_mcombine_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a, w);

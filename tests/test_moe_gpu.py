@@ -91,29 +91,31 @@ def test_route_negative_zero_and_equal_logits(gpu):
 class Layer:
     """Seeded MoE layer in the benchmark scheme, host copies + device banks."""
 
-    def __init__(self, torch, E, k, D, inter, bits, gs, shared=True, seed=0, sinter=None):
+    def __init__(self, torch, E, k, D, inter, bits, gs, shared=True, seed=0, sinter=None,
+                 fp16=False):
         from logan_amd.device import AffineBank, MoeLayer
 
         rng = np.random.default_rng(seed)
         self.E, self.k, self.D, self.inter, self.bits, self.gs = E, k, D, inter, bits, gs
+        self.fp16 = fp16
         self.sinter = inter if sinter is None else sinter
-        self.gate = make_affine(rng, inter, D, bits, gs, E=E)
-        self.up = make_affine(rng, inter, D, bits, gs, E=E)
-        self.down = make_affine(rng, D, inter, bits, gs, E=E)
+        self.gate = make_affine(rng, inter, D, bits, gs, fp16, E=E)
+        self.up = make_affine(rng, inter, D, bits, gs, fp16, E=E)
+        self.down = make_affine(rng, D, inter, bits, gs, fp16, E=E)
 
         def bank(t, O, I, n):
             w, sc, bi = t
             return AffineBank(to_dev(w, torch), to_dev(sc.view(np.int16), torch),
-                              to_dev(bi.view(np.int16), torch), n, O, I, bits, gs)
+                              to_dev(bi.view(np.int16), torch), n, O, I, bits, gs, fp16)
 
         kw = {}
         self.shared = None
         self.se_g = None
         if shared:
             si = self.sinter
-            sg = make_affine(rng, si, D, bits, gs, E=1)
-            su = make_affine(rng, si, D, bits, gs, E=1)
-            sd = make_affine(rng, D, si, bits, gs, E=1)
+            sg = make_affine(rng, si, D, bits, gs, fp16, E=1)
+            su = make_affine(rng, si, D, bits, gs, fp16, E=1)
+            sd = make_affine(rng, D, si, bits, gs, fp16, E=1)
             self.shared = tuple(tuple(a[0] for a in t) for t in (sg, su, sd))
             self.se_g_bits = bf16_bits(rng.standard_normal(D).astype(np.float32) * np.float32(0.05))
             self.se_g = bf16_to_f32(self.se_g_bits)
@@ -125,7 +127,8 @@ class Layer:
 
     def ref(self, xf, lf):
         return oracle.moe_token(xf, lf, self.k, self.D, self.inter, self.bits, self.gs, self.gate,
-                                self.up, self.down, self.shared, self.se_g, sinter=self.sinter)
+                                self.up, self.down, self.shared, self.se_g, sinter=self.sinter,
+                                fp16=self.fp16)
 
 
 def run_layer(torch, layer, xb, lb, out_dtype):
@@ -335,6 +338,21 @@ def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
     if zipf:
         assert np.bincount(idx.reshape(-1)).max() > 16
     _check_tokens(layer, xb, lb, out32, idx, w, range(B))
+
+
+@pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_moe_mfma_fp16_sidecars(gpu, mfma_min_b, bits):
+    """fp16 scale/bias sidecars through the MFMA path (both passes)."""
+    import torch
+
+    layer = Layer(torch, 128, 8, 1024, 256, bits, 64, seed=61 + bits, fp16=True)
+    rng = np.random.default_rng(62)
+    B = 20
+    xb = make_x(rng, B, 1024)
+    lb = make_logits(rng, B, 128)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(B))
 
 
 @pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
