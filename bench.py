@@ -79,9 +79,11 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4",
+                    help="secondary legs to run (comma list of gemv, dense8, moe3, stack5, moe4; "
+                         "'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
-    ap.add_argument("--no-secondary", action="store_true",
-                    help="skip every secondary leg (configs 1, 2, 3 at B>1, 4, 5)")
+    ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (5 times), to calibrate "
@@ -522,25 +524,32 @@ def main():
     layers = build_layers(torch, device, synth, args.layers)
     moe = bench_moe(torch, device, synth, args, layers)
     secondary = {}
-    if not args.no_secondary:
-        if not args.no_gemv:
+    legs = set() if args.no_secondary or args.legs == "none" else set(args.legs.split(","))
+    if args.no_gemv:
+        legs.discard("gemv")
+    if legs:
+        if "gemv" in legs:
             gemv = bench_gemv(torch, device, synth, args)
             secondary["gemv_q4_config1"] = {
                 "shape": "M=1 K=2048 N=4096 4-bit g64", "bytes_per_launch": GEMV_BYTES,
                 "us_per_launch": round(gemv["us_per_launch"], 3), "gbps": round(gemv["gbps"], 1),
                 "frac_of_peak": round(gemv["gbps"] / PEAK_GBPS, 4), "launches": gemv["launches"],
                 "rotation": "64 weight copies (302 MB) > 256 MB MALL"}
-        secondary["dense8_config2"] = bench_config2(torch, device, synth, args)
-        c3 = {}
-        for B in (16, 32):
-            r = moe_batch_leg(torch, device, synth, layers, B, BITS, PER_EXPERT, None, args.reps,
-                              seed=300 + B)
-            log(f"config 3 B={B}: {r['us_per_layer']} us/layer, {r['gbps']} GB/s, "
-                f"U={r['distinct_experts']}")
-            c3[f"B{B}"] = r
-        secondary["moe_config3"] = c3
-        secondary["stack_config5"] = bench_config5(torch, device, synth, args, layers)
-        secondary["moe_config4"] = bench_config4(torch, device, synth, args)
+        if "dense8" in legs:
+            secondary["dense8_config2"] = bench_config2(torch, device, synth, args)
+        if "moe3" in legs:
+            c3 = {}
+            for B in (16, 32):
+                r = moe_batch_leg(torch, device, synth, layers, B, BITS, PER_EXPERT, None, args.reps,
+                                  seed=300 + B)
+                log(f"config 3 B={B}: {r['us_per_layer']} us/layer, {r['gbps']} GB/s, "
+                    f"U={r['distinct_experts']}")
+                c3[f"B{B}"] = r
+            secondary["moe_config3"] = c3
+        if "stack5" in legs:
+            secondary["stack_config5"] = bench_config5(torch, device, synth, args, layers)
+        if "moe4" in legs:
+            secondary["moe_config4"] = bench_config4(torch, device, synth, args)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
