@@ -355,13 +355,17 @@ def bench_config5(torch, device, synth, args, moe_layers):
                 outs[name] = torch.empty((B, O), dtype=torch.bfloat16, device="cuda")
         mo = torch.empty((B, D), dtype=torch.bfloat16, device="cuda")
         ws = torch.empty(moe_layers[0].workspace_bytes(B), dtype=torch.uint8, device="cuda")
-        prod = device.affine_gemv
-
         def step():
             for l in range(nl):
                 shapes = FULL_ATTN if l % FULL_EVERY == FULL_EVERY - 1 else LIN_ATTN
+                # the projections that read the hidden state share one launch
+                # (q/k/v, qkvz/ba); the output projection reads the attention
+                # output
+                grp = [(m, outs[name]) for (name, O, I), m in zip(shapes, proj[l]) if I == D]
+                device.affine_gemv_multi([m for m, _ in grp], x, outs=[o for _, o in grp])
                 for (name, O, I), m in zip(shapes, proj[l]):
-                    prod(m, x if I == D else att, out=outs[name])
+                    if I != D:
+                        device.affine_gemv(m, att, out=outs[name])
                 device.moe_block(moe_layers[l], x, lg[l], out=mo, workspace=ws)
 
         us = graph_us(torch, step, args.reps)
@@ -372,7 +376,7 @@ def bench_config5(torch, device, synth, args, moe_layers):
         res[f"decode_B{B}"] = dict(us_per_step=round(us, 1), us_per_token=round(us / B, 2),
                                    bytes_per_step=int(nbytes), gbps=round(gbps, 1),
                                    frac_of_peak=round(gbps / PEAK_GBPS, 4),
-                                   projections="affine_gemv")
+                                   projections="affine_gemv_multi (q/k/v, qkvz/ba) + affine_gemv")
     # prefill chunk: M = 512 tokens
     M = 512
     x = dev_bf16(torch, synth.make_x(rng, M, D))

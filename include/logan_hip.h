@@ -157,6 +157,17 @@ typedef struct LoganHipAffine {
 int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                           int y_stride, int y_dtype, void *stream);
 
+/* Up to 8 matrices that read the same activation (q/k/v, gate/up, ...) in
+ * one launch: ys[i][M][O_i] = x[M][x_stride] . W_i^T, each as
+ * logan_hip_affine_gemv. The reference encodes its batch of GEMVs into one
+ * command buffer (coli_metal_matmul_multi,
+ * logan-metal/metal/backend_metal.mm:2290-2493, up to 16 descriptors each
+ * with its own x); here the shared x is read once per block and the
+ * matrices' row blocks form one grid. Every matrix has the same I, bits,
+ * group_size and aux type. 1 ok, 0 unsupported, -1 launch failure. */
+int logan_hip_affine_gemv_multi(const LoganHipAffine *ws, int count, const void *x, int M,
+                                int x_stride, void *const *ys, int y_dtype, void *stream);
+
 /* Prefill / large-batch form of the same product on MFMA, with the
  * reference QMM's numerics (logan-metal/metal/backend_metal.mm:1480-1560,
  * spark_qmm_affine8_t16o8): every dequantised weight code*scale + bias is

@@ -33,7 +33,7 @@ struct GemvParams {
 // LANES*CPL chunks; their partial sums meet in LDS and are added in segment
 // order.
 template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
-__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
+__device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   constexpr int TEAMS = 256 / LANES;
   constexpr int ROWTEAMS = TEAMS / SPLIT;
   const int lane = threadIdx.x & (LANES - 1);
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
 
   // the grid covers O exactly once: block b owns rows [b*ROWTEAMS*U, ...)
   {
-    const int r0 = blockIdx.x * (ROWTEAMS * U) + rteam * U;
+    const int r0 = bid * (ROWTEAMS * U) + rteam * U;
     uint32_t wv[U][CPL][BITS];
     uint32_t scr[U][CPL], bir[U][CPL];
 #pragma unroll
@@ -215,10 +215,58 @@ __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
   }
 }
 
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+__global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
+  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT>(a, blockIdx.x);
+}
+
+// Up to kMultiMax matrices sharing one activation in one launch: block b
+// serves the matrix whose block range holds it.
+constexpr int kMultiMax = 8;
+struct GemvMultiDesc {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  void *y;
+  long long row_bytes;
+  int O, ng;
+};
+struct GemvMultiParams {
+  GemvParams common;  // I, gsc, gsc_shift, fp16, x, x_stride, M, y_bf16
+  GemvMultiDesc d[kMultiMax];
+  int block_start[kMultiMax + 1];
+  int n;
+};
+
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+__global__ __launch_bounds__(256) void gemv_bf16_multi_kernel(GemvMultiParams mp) {
+  int i = 0;
+  while (i + 1 < mp.n && (int)blockIdx.x >= mp.block_start[i + 1]) ++i;
+  GemvParams a = mp.common;
+  a.w = mp.d[i].w;
+  a.sc = mp.d[i].sc;
+  a.bi = mp.d[i].bi;
+  a.y = mp.d[i].y;
+  a.row_bytes = mp.d[i].row_bytes;
+  a.O = mp.d[i].O;
+  a.ng = mp.d[i].ng;
+  a.y_stride = mp.d[i].O;
+  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT>(a, blockIdx.x - mp.block_start[i]);
+}
+
 template <int BITS, int LANES, int CPL, int MT, int SPLIT = 1>
-static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st) {
+static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiParams *mp = nullptr) {
   constexpr int U = CPL == 1 ? 4 : (CPL == 2 ? 2 : 1);
   constexpr int rows_per_block = (256 / LANES / SPLIT) * U;
+  if (mp) {
+    mp->block_start[0] = 0;
+    for (int i = 0; i < mp->n; ++i)
+      mp->block_start[i + 1] = mp->block_start[i] + (mp->d[i].O + rows_per_block - 1) / rows_per_block;
+    for (int i = mp->n + 1; i <= kMultiMax; ++i) mp->block_start[i] = mp->block_start[mp->n];
+    hipLaunchKernelGGL((gemv_bf16_multi_kernel<BITS, LANES, CPL, U, MT, SPLIT>),
+                       dim3(mp->block_start[mp->n]), dim3(256), 0, st, *mp);
+    return hipGetLastError();
+  }
   const int blocks = (p.O + rows_per_block - 1) / rows_per_block;
   hipLaunchKernelGGL((gemv_bf16_kernel<BITS, LANES, CPL, U, MT, SPLIT>), dim3(blocks), dim3(256), 0,
                      st, p);
@@ -226,24 +274,25 @@ static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st) {
 }
 
 template <int BITS, int MT>
-static hipError_t gemv_dispatch_shape(const GemvParams &p, hipStream_t st) {
+static hipError_t gemv_dispatch_shape(const GemvParams &p, hipStream_t st, GemvMultiParams *mp) {
   const int C = p.I >> 5;
-  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT>(p, st);
-  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT>(p, st);
-  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT>(p, st);
-  if (C <= 128) return gemv_launch_t<BITS, 64, 2, MT>(p, st);
-  if (C <= 256) return gemv_launch_t<BITS, 64, 4, MT>(p, st);
-  if (C <= 512) return gemv_launch_t<BITS, 64, 4, MT, 2>(p, st);
+  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT>(p, st, mp);
+  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT>(p, st, mp);
+  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT>(p, st, mp);
+  if (C <= 128) return gemv_launch_t<BITS, 64, 2, MT>(p, st, mp);
+  if (C <= 256) return gemv_launch_t<BITS, 64, 4, MT>(p, st, mp);
+  if (C <= 512) return gemv_launch_t<BITS, 64, 4, MT, 2>(p, st, mp);
   return hipErrorInvalidValue;
 }
 
 template <int MT>
-static hipError_t gemv_dispatch_bits(const GemvParams &p, int bits, hipStream_t st) {
+static hipError_t gemv_dispatch_bits(const GemvParams &p, int bits, hipStream_t st,
+                                     GemvMultiParams *mp = nullptr) {
   switch (bits) {
-    case 4: return gemv_dispatch_shape<4, MT>(p, st);
-    case 5: return gemv_dispatch_shape<5, MT>(p, st);
-    case 6: return gemv_dispatch_shape<6, MT>(p, st);
-    case 8: return gemv_dispatch_shape<8, MT>(p, st);
+    case 4: return gemv_dispatch_shape<4, MT>(p, st, mp);
+    case 5: return gemv_dispatch_shape<5, MT>(p, st, mp);
+    case 6: return gemv_dispatch_shape<6, MT>(p, st, mp);
+    case 8: return gemv_dispatch_shape<8, MT>(p, st, mp);
   }
   return hipErrorInvalidValue;
 }
@@ -298,6 +347,55 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
     p.y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
                  : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
     hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st) : gemv_dispatch_bits<1>(p, m.bits, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// Matrices sharing x (same I, bits, group size, aux type): one launch per
+// token pair through the dot2 kernel; three or more tokens run the MFMA path
+// matrix by matrix.
+hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
+                                  int x_stride, int M, int y_bf16, hipStream_t st) {
+  if (n <= 0 || n > kMultiMax || M <= 0) return hipErrorInvalidValue;
+  for (int i = 0; i < n; ++i) {
+    if (!gemv_bf16_supported(ms[i]) || ms[i].I != ms[0].I || ms[i].bits != ms[0].bits ||
+        ms[i].gs != ms[0].gs || ms[i].fp16 != ms[0].fp16 || !ys[i])
+      return hipErrorInvalidValue;
+  }
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  if (M >= 3 && affine_skinny_supported(ms[0])) {
+    for (int i = 0; i < n; ++i) {
+      hipError_t e = launch_gemv_bf16(ms[i], x, x_stride, M, ys[i], ms[i].O, y_bf16, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  GemvMultiParams mp{};
+  GemvParams &p = mp.common;
+  p.I = ms[0].I;
+  p.gsc = ms[0].gs / 32;
+  p.gsc_shift = (p.gsc & (p.gsc - 1)) == 0 ? __builtin_ctz(p.gsc) : -1;
+  p.fp16 = ms[0].fp16;
+  p.x_stride = x_stride;
+  p.y_bf16 = y_bf16;
+  mp.n = n;
+  for (int m0 = 0; m0 < M; m0 += 2) {
+    const int mt = M - m0 >= 2 ? 2 : 1;
+    p.x = x + (size_t)m0 * x_stride;
+    p.M = mt;
+    for (int i = 0; i < n; ++i) {
+      mp.d[i].w = ms[i].w;
+      mp.d[i].sc = ms[i].sc;
+      mp.d[i].bi = ms[i].bi;
+      mp.d[i].row_bytes = ms[i].row_bytes;
+      mp.d[i].O = ms[i].O;
+      mp.d[i].ng = ms[i].ng;
+      mp.d[i].y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(ys[i]) + (size_t)m0 * ms[i].O)
+                         : (void *)(reinterpret_cast<float *>(ys[i]) + (size_t)m0 * ms[i].O);
+    }
+    hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, ms[0].bits, st, &mp)
+                           : gemv_dispatch_bits<1>(p, ms[0].bits, st, &mp);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -23,6 +23,10 @@ struct DevMat {
 hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, int M,
                             void *y, int y_stride, int y_bf16, hipStream_t st);
 bool gemv_bf16_supported(const DevMat &m);
+// up to 8 matrices sharing x (same I, bits, group size, aux type); ys[i] is
+// [M][O_i]
+hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
+                                  int x_stride, int M, int y_bf16, hipStream_t st);
 
 // ---- prefill / large-batch product on MFMA: bf16-rounded dequantised
 // weights (the reference QMM semantics), x bf16 [M, I], y [M, O] ----
