@@ -147,6 +147,139 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large tiles: 128 x 128 output per 256-thread block (each wave 64 x 64 as
+// 2 x 2 MFMA tiles), so every weight is dequantised once per 128 tokens. Per
+// 64-k step the block writes the x tile and the dequantised W tile into LDS;
+// the next step's global loads are issued into registers before the current
+// step's MFMAs. Blocks are numbered so that the M tiles of one N tile share an
+// XCD (block id mod 8) and meet the weight tile in that XCD's L2.
+constexpr int kQ2 = 128;     // tile rows (m) and columns (n)
+constexpr int kQ2Ld = 72;    // bf16 per LDS row: 64 + 8 pad
+#ifndef QMM_MIN_TILES
+#define QMM_MIN_TILES 192
+#endif
+constexpr int kQ2MinTiles = QMM_MIN_TILES;
+
+template <int BITS>
+__global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mtiles, int ntiles) {
+  __shared__ __align__(16) __bf16 sA[kQ2 * kQ2Ld];
+  __shared__ __align__(16) __bf16 sB[kQ2 * kQ2Ld];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+  // XCD-grouped tile order
+  const int L = blockIdx.x;
+  const int grp = L / (8 * mtiles), rem = L % (8 * mtiles);
+  const int nt = grp * 8 + rem % 8, mt = rem / 8;
+  if (nt >= ntiles) return;
+  const int bm0 = mt * kQ2, bn0 = nt * kQ2;
+
+  // loader role: row lr of both tiles, codes / activations [32 lh, 32 lh + 32)
+  const int lr = tid >> 1, lh = tid & 1;
+  const uint16_t *xrow = p.x + (size_t)min(bm0 + lr, p.M - 1) * p.x_stride + 32 * lh;
+  const int wrw = min(bn0 + lr, p.N - 1);
+  const uint8_t *wrow = p.w + (size_t)wrw * p.row_bytes;
+  const uint16_t *srow = p.sc + (size_t)wrw * p.ng;
+  const uint16_t *brow = p.bi + (size_t)wrw * p.ng;
+  struct Loads {
+    uint4 x0, x1, x2, x3;
+    uint32_t w[BITS];
+    uint32_t s, b;
+  };
+  auto issue = [&](int k0) {
+    Loads r;
+    const uint4 *xs = reinterpret_cast<const uint4 *>(xrow + k0);
+    r.x0 = xs[0];
+    r.x1 = xs[1];
+    r.x2 = xs[2];
+    r.x3 = xs[3];
+    load_chunk<BITS>(r.w, wrow + (size_t)(k0 + 32 * lh) * BITS / 8);
+    const int gi = (k0 + 32 * lh) / p.gs;
+    r.s = srow[gi];
+    r.b = brow[gi];
+    return r;
+  };
+  auto commit = [&](const Loads &r) {
+    uint4 *da = reinterpret_cast<uint4 *>(sA + lr * kQ2Ld + 32 * lh);
+    da[0] = r.x0;
+    da[1] = r.x1;
+    da[2] = r.x2;
+    da[3] = r.x3;
+    const float s = aux_to_f32_sel(r.s, p.fp16), b = aux_to_f32_sel(r.b, p.fp16);
+    uint32_t pk[16];
+#pragma unroll
+    for (int j = 0; j < 32; j += 2) {
+      // codes j, j + 1 of the 32-code chunk (LSB-first stream)
+      uint32_t c[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int bit = (j + q) * BITS, i = bit >> 5, sh = bit & 31;
+        uint32_t v = r.w[i] >> sh;
+        if (sh + BITS > 32) v |= r.w[i + 1] << (32 - sh);
+        c[q] = v & ((1u << BITS) - 1u);
+      }
+      bf16x2 v;
+      v[0] = (__bf16)fmaf((float)c[0], s, b);
+      v[1] = (__bf16)fmaf((float)c[1], s, b);
+      pk[j / 2] = __builtin_bit_cast(uint32_t, v);
+    }
+    uint4 *db = reinterpret_cast<uint4 *>(sB + lr * kQ2Ld + 32 * lh);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) db[v] = make_uint4(pk[4 * v], pk[4 * v + 1], pk[4 * v + 2], pk[4 * v + 3]);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  auto mfma_step = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      bf16x8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const bf16x8 *>(sA + (wm * 64 + 32 * i + l32) * kQ2Ld + 16 * ks + 8 * half);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b[j] = *reinterpret_cast<const bf16x8 *>(sB + (wn * 64 + 32 * j + l32) * kQ2Ld + 16 * ks + 8 * half);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  // one step of loads in flight (the last step reloads itself, so every
+  // issue is unconditional); a second stage measured slower
+  Loads cur = issue(0);
+  for (int k0 = 0; k0 < p.K; k0 += 64) {
+    __syncthreads();  // the previous step's operand reads are done
+    commit(cur);
+    __syncthreads();
+    cur = issue(min(k0 + 64, p.K - 64));
+    mfma_step();
+  }
+  // element e of tile (i, j): row 32 i + 8 (e / 4) + 4 half + e % 4, column 32 j + l32
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = bn0 + wn * 64 + 32 * j + l32;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = bm0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * half + (e % 4);
+        if (m < p.M && n < p.N) {
+          if (p.y_bf16)
+            reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)acc[i][j][e];
+          else
+            reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = acc[i][j][e];
+        }
+      }
+    }
+}
+
 bool affine_qmm_supported(const DevMat &m) {
   if (!(m.bits == 4 || m.bits == 5 || m.bits == 6 || m.bits == 8)) return false;
   if (m.I <= 0 || m.I % kTile != 0 || m.O <= 0) return false;
@@ -176,6 +309,19 @@ hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, i
   p.x_stride = x_stride;
   p.y_stride = y_stride;
   p.y_bf16 = y_bf16;
+  // large tiles when their grid alone keeps the chip busy; smaller grids
+  // take the 64 x 64 kernel (four times the blocks)
+  const int mt = (M + kQ2 - 1) / kQ2, nt = (m.O + kQ2 - 1) / kQ2;
+  if (M > kTile && mt * nt >= kQ2MinTiles) {
+    const int blocks = ((nt + 7) / 8) * 8 * mt;
+    switch (m.bits) {
+      case 4: hipLaunchKernelGGL(affine_qmm128_kernel<4>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
+      case 5: hipLaunchKernelGGL(affine_qmm128_kernel<5>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
+      case 6: hipLaunchKernelGGL(affine_qmm128_kernel<6>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
+      case 8: hipLaunchKernelGGL(affine_qmm128_kernel<8>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid((M + kTile - 1) / kTile, (m.O + kTile - 1) / kTile);
   switch (m.bits) {
     case 4: hipLaunchKernelGGL(affine_qmm_kernel<4>, grid, dim3(256), 0, st, p); break;

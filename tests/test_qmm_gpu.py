@@ -41,6 +41,8 @@ CASES = [
     (64, 512, 2048, 4, 64, False),   # config-5 attention projection shape, one tile of M
     (33, 192, 1024, 5, 32, True),
     (65, 130, 512, 8, 128, False),
+    (200, 96, 320, 5, 64, False),    # large-tile kernel: M > 64, partial tiles in M and N
+    (300, 257, 128, 4, 32, True),
 ]
 
 
@@ -82,6 +84,33 @@ def test_qmm_prefill_chunk(gpu):
     bis = bi.reshape(O, ng)[cols].reshape(-1)
     ref = oracle.affine_qmm_bf16(bf16_to_f32(xb).reshape(M, I), ws, scs, bis, len(cols), I, bits, gs)
     assert normwise_rel(y[:, cols], ref) <= 1e-5
+
+
+@pytest.mark.parametrize("bits,gs,fp16", [(4, 64, False), (5, 64, True), (8, 128, False)])
+def test_qmm_large_tiles_ragged(gpu, bits, gs, fp16):
+    """A grid of >= 192 tiles of 128 x 128 (the large-tile kernel) with
+    partial tiles in both M and N, against the oracle on a sample of output
+    columns (every column of the last, partial tile included)."""
+    import torch
+    from logan_amd.device import affine_qmm
+
+    rng = np.random.default_rng(bits * 3 + gs)
+    M, O, I = 500, 6337, 256
+    w, sc, bi = make_affine(rng, O, I, bits, gs, fp16)
+    xb = make_x(rng, M, I).reshape(M, I)
+    m = dev_matrix(torch, w, sc, bi, O, I, bits, gs, fp16)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    y = affine_qmm(m, x, out_dtype=torch.float32).cpu().numpy()
+    cols = np.concatenate([np.arange(0, O, 53), np.arange(O - 65, O)])
+    ng = I // gs
+    ws = w.reshape(O, -1)[cols]
+    scs = sc.reshape(O, ng)[cols].reshape(-1)
+    bis = bi.reshape(O, ng)[cols].reshape(-1)
+    ref = oracle.affine_qmm_bf16(bf16_to_f32(xb).reshape(M, I), ws, scs, bis, len(cols), I, bits, gs,
+                                 fp16)
+    assert normwise_rel(y[:, cols], ref) <= 1e-5
+    yb = affine_qmm(m, x, out_dtype=torch.bfloat16)
+    assert torch.equal(yb, torch.from_numpy(y).cuda().to(torch.bfloat16))
 
 
 def test_qmm_leaves_outside_untouched(gpu):
