@@ -259,10 +259,10 @@ void logan_hip_set_moe_fused(int on);
 uint32_t logan_hip_moe_sync_errors(void);
 
 /* Batches of at least this many tokens take the routed-MoE block's MFMA
- * path (4/8-bit codes with group sizes that are multiples of 64; each
+ * path (4/5/6/8-bit codes with group sizes that are multiples of 64; each
  * expert's weights read once per 16 of its tokens); smaller batches and
  * other geometries take the per-token dot-product path in passes of up to
- * 64 tokens. Default 96, or LOGAN_HIP_MOE_MFMA_MIN_B from the environment.
+ * 64 tokens. Default 24, or LOGAN_HIP_MOE_MFMA_MIN_B from the environment.
  * Both paths follow the same reference semantics (logan-qwen4/src/lib.rs
  * :8692-8711, :8759-8815); this control has no counterpart in the
  * reference (its batched path is host-side, lib.rs:9714-9721). */

@@ -237,11 +237,17 @@ bool affine_skinny_supported(const DevMat &m) {
 #define SKINNY_U 1
 #endif
 
+#ifndef SKINNY_WBIG
+#define SKINNY_WBIG 8
+#endif
+
 template <int BITS, int MT>
 static hipError_t skinny_launch(const SkinnyParams &p, hipStream_t st) {
-  constexpr int R = SKINNY_R, U = SKINNY_U;
+  constexpr int R = SKINNY_R, U = SKINNY_U, WB = SKINNY_WBIG;
   const dim3 grid((p.N + 16 * R - 1) / (16 * R));
-  if ((p.K >> 6) >= 32)
+  if ((p.K >> 6) >= 4 * WB)
+    hipLaunchKernelGGL((affine_skinny_kernel<BITS, MT, R, U, WB>), grid, dim3(64 * WB), 0, st, p);
+  else if ((p.K >> 6) >= 32)
     hipLaunchKernelGGL((affine_skinny_kernel<BITS, MT, R, U, 8>), grid, dim3(512), 0, st, p);
   else
     hipLaunchKernelGGL((affine_skinny_kernel<BITS, MT, R, U, 4>), grid, dim3(256), 0, st, p);

@@ -96,12 +96,12 @@ size_t moe_fused_workspace_bytes(int slots, int inter, int sinter);
 uint32_t moe_fused_sync_errors();
 // 0 disables the fused B = 1 path (LOGAN_HIP_MOE_FUSED=0); default on
 void set_moe_fused_enabled(int on);
-// token-batch path on MFMA (moe_mfma.hip): 4/8-bit codes, groups of 64k,
+// token-batch path on MFMA (moe_mfma.hip): 4/5/6/8-bit codes, groups of 64k,
 // D % 128 == 0, inter and sinter <= 512 and % 128 == 0; 1 launched, 0 not
 // applicable, -1 launch failure
 constexpr int kMaxBatch = 4096;         // tokens per moe_block call
 constexpr int kMaxBatchSlots = 65536;   // tokens * top_k
-constexpr int kMfmaMinBatchDefault = 96;
+constexpr int kMfmaMinBatchDefault = 24;
 bool moe_mfma_supported(const MoeArgs &a);
 int launch_moe_mfma(const MoeArgs &a, hipStream_t st);
 size_t moe_mfma_workspace_bytes(int B, int D, int inter, int sinter, int E, int k);

@@ -64,5 +64,42 @@ template <>
 struct SkRaw<8> {
   uint4 v;  // 16 codes
 };
+template <>
+struct SkRaw<5> {
+  uint32_t w[3];  // 96 bits holding 16 codes from bit 0 or 16 (lane group parity)
+};
+template <>
+struct SkRaw<6> {
+  uint32_t w[3];  // 16 codes, 96 bits
+};
+
+// B operand pairs (codes 2p, 2p + 1, natural order) of 5/6-bit codes as
+// 0x3F80 | code << S (S = 2: 1 + code/32; S = 1: 1 + code/64) from a 96-bit
+// window whose first code starts at bit `sh`.
+template <int BITS>
+__device__ __forceinline__ void b_from_window(const uint32_t (&w)[3], int sh, bf16x8_t &b0, bf16x8_t &b1) {
+  constexpr int S = BITS == 5 ? 2 : 1;
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  // shift the window so code 0 sits at bit 0 (sh is 0 or 16)
+  const uint32_t v0 = __builtin_amdgcn_alignbit(w[1], w[0], sh);
+  const uint32_t v1 = __builtin_amdgcn_alignbit(w[2], w[1], sh);
+  const uint32_t v2 = w[2] >> sh;
+  const uint32_t win[3] = {v0, v1, v2};
+  uint32_t q[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    uint32_t c[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int bit = (2 * p + t) * BITS, i = bit >> 5, o = bit & 31;
+      uint32_t v = win[i] >> o;
+      if (o + BITS > 32) v |= win[i + 1] << (32 - o);
+      c[t] = v & mask;
+    }
+    q[p] = 0x3F803F80u | (c[0] << S) | (c[1] << (16 + S));
+  }
+  b0 = as_bf16x8(q[0], q[1], q[2], q[3]);
+  b1 = as_bf16x8(q[4], q[5], q[6], q[7]);
+}
 
 }  // namespace lh

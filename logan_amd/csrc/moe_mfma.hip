@@ -225,22 +225,35 @@ struct MfmaStep {
     if constexpr (BITS == 4) {
       b0 = b_from_nibbles(r.v.x, kc);
       b1 = b_from_nibbles(r.v.y, kc);
-    } else {
+    } else if constexpr (BITS == 8) {
       b0 = b_from_bytes(r.v.x, r.v.y);
       b1 = b_from_bytes(r.v.z, r.v.w);
+    } else {
+      // 5-bit runs of 16 codes start at bit 0 or 16 of their first dword
+      b_from_window<BITS>(r.w, BITS == 5 ? 16 * ((threadIdx.x >> 4) & 1) : 0, b0, b1);
     }
   }
+  // the lane's 16 codes [k, k + 16) of a row (k a multiple of 16)
   static __device__ __forceinline__ void load_raw(SkRaw<BITS> &r, const uint8_t *row, int k) {
-    if constexpr (BITS == 4)
+    if constexpr (BITS == 4) {
       r.v = *reinterpret_cast<const uint2 *>(row + (k >> 1));
-    else
+    } else if constexpr (BITS == 8) {
       r.v = *reinterpret_cast<const uint4 *>(row + k);
+    } else {
+      // dword holding the first code: 5-bit (k * 5) / 32, 6-bit (k * 6) / 32
+      const uint32_t *p = reinterpret_cast<const uint32_t *>(row) + ((k * BITS) >> 5);
+      r.w[0] = p[0];
+      r.w[1] = p[1];
+      r.w[2] = p[2];
+    }
   }
-  // y += s' D + b' X (4-bit D = X + sum(c x)/16, 8-bit D = sum(c x))
+  // y += s' D + b' X: D = X + 2^(s-7) sum(c x) for codes at mantissa bit s
+  // (4-bit s = 3, 5-bit 2, 6-bit 1), D = sum(c x) for 8-bit
   static __device__ __forceinline__ void fold(f32x4_t &acc, const f32x4_t &d, const f32x4_t &xs,
                                               float s, float b) {
-    const float s2 = BITS == 4 ? 16.f * s : s;
-    const float b2 = BITS == 4 ? b - 16.f * s : b;
+    constexpr float F = BITS == 4 ? 16.f : BITS == 5 ? 32.f : BITS == 6 ? 64.f : 1.f;
+    const float s2 = BITS == 8 ? s : F * s;
+    const float b2 = BITS == 8 ? b : b - F * s;
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = fmaf(b2, xs[i], fmaf(s2, d[i], acc[i]));
   }
@@ -610,9 +623,9 @@ __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) 
 
 static bool mbank_ok(const DevBank &b) {
   const DevMat &m = b.m;
-  if (m.bits != 4 && m.bits != 8) return false;
+  if (m.bits < 4 || m.bits > 8 || m.bits == 7) return false;
   if (m.gs <= 0 || m.gs % 64 != 0 || m.I % m.gs != 0) return false;
-  const uintptr_t need = m.bits == 4 ? 7 : 15;
+  const uintptr_t need = m.bits == 4 ? 7 : m.bits == 8 ? 15 : 3;
   if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
   if ((b.w_stride & (long long)need) != 0) return false;
   // scale/bias runs are read as 4- or 8-byte words
@@ -700,7 +713,12 @@ int launch_moe_mfma(const MoeArgs &a, hipStream_t st) {
   if (hipGetLastError() != hipSuccess) return -1;
   hipLaunchKernelGGL(moe_mgroup_kernel, dim3(1), dim3(kMGroupThreads), 0, st, a, w);
   if (hipGetLastError() != hipSuccess) return -1;
-  return a.gate.m.bits == 4 ? moe_mfma_launch_bits<4>(a, w, st) : moe_mfma_launch_bits<8>(a, w, st);
+  switch (a.gate.m.bits) {
+    case 4: return moe_mfma_launch_bits<4>(a, w, st);
+    case 5: return moe_mfma_launch_bits<5>(a, w, st);
+    case 6: return moe_mfma_launch_bits<6>(a, w, st);
+    default: return moe_mfma_launch_bits<8>(a, w, st);
+  }
 }
 
 }  // namespace lh

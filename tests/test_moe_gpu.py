@@ -301,7 +301,7 @@ def mfma_min_b(request):
     b = getattr(request, "param", 1)
     _lib.lib().logan_hip_set_moe_mfma_min_batch(b)
     yield b
-    _lib.lib().logan_hip_set_moe_mfma_min_batch(96)
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(24)
 
 
 def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
@@ -317,7 +317,9 @@ def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
 @pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
 @pytest.mark.parametrize("bits,B,zipf,shared", [(4, 2, False, True), (4, 16, False, True),
                                                 (8, 5, False, True), (4, 40, True, True),
-                                                (8, 33, True, False)])
+                                                (8, 33, True, False), (5, 40, True, True),
+                                                (6, 32, True, True), (5, 3, False, False),
+                                                (6, 17, False, True)])
 def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
     """The token-batch MFMA path (forced for every B) against the oracle:
     routing bit-exact, outputs at f32-accumulation level; Zipf routes put
@@ -341,7 +343,7 @@ def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
 
 
 @pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 5, 6, 8])
 def test_moe_mfma_fp16_sidecars(gpu, mfma_min_b, bits):
     """fp16 scale/bias sidecars through the MFMA path (both passes)."""
     import torch
@@ -389,16 +391,17 @@ def test_moe_prefill_chunk_sampled(gpu):
     try:
         out_d, idx_d, _ = run_layer(torch, layer, xb, lb, torch.float32)
     finally:
-        _lib.lib().logan_hip_set_moe_mfma_min_batch(96)
+        _lib.lib().logan_hip_set_moe_mfma_min_batch(24)
     np.testing.assert_array_equal(idx, idx_d)
     out_d = out_d.cpu().numpy()
     for t in range(B):
         assert normwise_rel(out32[t], out_d[t]) <= 5e-5
 
 
-def test_moe_large_batch_without_mfma_kernels(gpu):
-    """5-bit codes have no MFMA kernel: B = 100 runs the per-token path in
-    passes of 64 tokens, every token against the oracle."""
+@pytest.mark.parametrize("mfma_min_b", [1 << 20], indirect=True)
+def test_moe_large_batch_per_token_passes(gpu, mfma_min_b):
+    """With the MFMA path off, B = 100 runs the per-token path in passes of
+    64 tokens; every third token against the oracle."""
     import torch
 
     layer = Layer(torch, 512, 10, 2048, 512, 5, 64, seed=51)
