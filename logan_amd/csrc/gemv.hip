@@ -327,26 +327,35 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
   p.x_stride = x_stride;
   p.y_stride = y_stride;
   p.y_bf16 = y_bf16;
-  // three or more activation rows: the MFMA path reads each weight once per
-  // 32 rows (4- and 8-bit codes, groups of 64k)
-  if (M >= 3 && affine_skinny_supported(m)) {
-    for (int m0 = 0; m0 < M; m0 += 32) {
-      void *ym = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
-                        : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
-      hipError_t e = launch_affine_skinny(m, x + (size_t)m0 * x_stride, x_stride, min(32, M - m0), ym,
-                                          y_stride, y_bf16, st);
+  // token blocks of at most 2 rows of x per launch of the dot2 kernel
+  auto dot2_rows = [&](int r0, int nr) -> hipError_t {
+    for (int m0 = r0; m0 < r0 + nr; m0 += 2) {
+      const int mt = r0 + nr - m0 >= 2 ? 2 : 1;
+      p.x = x + (size_t)m0 * x_stride;
+      p.M = mt;
+      p.y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
+                   : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
+      hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st) : gemv_dispatch_bits<1>(p, m.bits, st);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
-  }
-  // token blocks of at most 2 rows of x per launch
-  for (int m0 = 0; m0 < M; m0 += 2) {
-    const int mt = M - m0 >= 2 ? 2 : 1;
-    p.x = x + (size_t)m0 * x_stride;
-    p.M = mt;
-    p.y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
-                 : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
-    hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st) : gemv_dispatch_bits<1>(p, m.bits, st);
+  };
+  if (M < 3) return dot2_rows(0, M);
+  // three or more activation rows: MFMA paths that read each weight once per
+  // 32 rows of x (the K-split form shares each block's x rows across 128
+  // weight rows; the wave-private form needs 4/8-bit codes)
+  for (int m0 = 0; m0 < M; m0 += 32) {
+    const int mc = min(32, M - m0);
+    void *ym = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
+                      : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
+    const uint16_t *xm = x + (size_t)m0 * x_stride;
+    hipError_t e;
+    if (mc >= 3 && affine_splitk_supported(m, mc))
+      e = launch_affine_splitk(m, xm, x_stride, mc, ym, y_stride, y_bf16, st);
+    else if (affine_skinny_supported(m))
+      e = launch_affine_skinny(m, xm, x_stride, mc, ym, y_stride, y_bf16, st);
+    else
+      e = dot2_rows(m0, mc);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

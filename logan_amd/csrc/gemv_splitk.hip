@@ -1,0 +1,219 @@
+// Small-batch MLX-affine product on MFMA with K split across blocks:
+// y[m] = W x[m] for 3 <= M <= 32 activation rows (same numerics as
+// gemv_mfma.hip: exact codes, f32 accumulation, per-group scale and bias
+// folded after each 64-code step).
+//
+// Block (rb, ks) owns rows [128 rb, 128 rb + 128) (8 waves x 16 rows) and
+// codes [512 ks, 512 ks + 512). Its x rows for that K range are staged once
+// in LDS (in the operand order of the code width) and feed all 8 waves, so
+// the activation traffic is 1/8 of a wave-private load; every wave issues
+// all eight of its 64-code steps' weight loads before x is staged. Each block
+// writes its partial sums for its (token, row) pairs into a scratch slot, and
+// a second kernel adds the K partials in order (deterministic) into y.
+//
+// Scratch: kSkSlots module-scope slots of kSkSlotFloats floats; the host
+// picks slots round-robin, so launches that overlap on one device do not
+// share a slot unless more than kSkSlots of them are in flight at once.
+#include <atomic>
+
+#include "lh_internal.hpp"
+#include "mfma_dev.hpp"
+
+namespace lh {
+
+constexpr int kSkKc = 512;   // codes per block
+constexpr int kSkSteps = kSkKc / 64;
+constexpr int kSkRows = 128;  // rows per block
+constexpr int kSkSlots = 4;
+constexpr size_t kSkSlotFloats = size_t(1) << 21;  // 8 MB per slot
+
+static __device__ __align__(256) float g_sk_part[kSkSlots * kSkSlotFloats];
+
+struct SplitParams {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  const uint16_t *x;
+  long long row_bytes;
+  int N, K, ng, gsteps, x_stride, M, slot;
+};
+
+template <int BITS, int MT, bool FP16, bool AUX8>
+__global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
+  __shared__ __align__(16) uint16_t sx[16 * MT * kSkKc];
+  using S = MfmaStep<BITS>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int ks = blockIdx.y;
+  const int k0 = ks * kSkKc;
+  const int n = blockIdx.x * kSkRows + wave * 16 + r16;
+  const int row = min(n, p.N - 1);
+  const uint8_t *wrow = p.w + (size_t)row * p.row_bytes;
+  const uint16_t *srow = p.sc + (size_t)row * p.ng;
+  const uint16_t *brow = p.bi + (size_t)row * p.ng;
+
+  // every weight and scale/bias load of the wave first
+  SkRaw<BITS> wr[kSkSteps];
+#pragma unroll
+  for (int u = 0; u < kSkSteps; ++u) S::load_raw(wr[u], wrow, k0 + u * 64 + 16 * g);
+  uint32_t sr[kSkSteps], br[kSkSteps];
+  if constexpr (AUX8) {
+    // groups of 64: the 8 steps' u16 words are one aligned 16-byte run
+    const uint4 vs = *reinterpret_cast<const uint4 *>(srow + (k0 >> 6));
+    const uint4 vb = *reinterpret_cast<const uint4 *>(brow + (k0 >> 6));
+    const uint32_t ws[4] = {vs.x, vs.y, vs.z, vs.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (int u = 0; u < kSkSteps; ++u) {
+      sr[u] = (ws[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+      br[u] = (wb[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kSkSteps; ++u) {
+      const int gi = ((k0 >> 6) + u) / p.gsteps;
+      sr[u] = srow[gi];
+      br[u] = brow[gi];
+    }
+  }
+  {
+    // stage x rows m < M, codes [k0, k0 + 512): 64 granules of 8 per row
+    constexpr int NV = 16 * MT * (kSkKc / 8) / 512;
+    const int lim = p.M * (kSkKc / 8);
+    uint4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int q = min(tid + 512 * i, lim - 1);
+      const int m = q >> 6, qq = q & 63;
+      v[i] = *reinterpret_cast<const uint4 *>(p.x + (size_t)m * p.x_stride + k0 + 8 * qq);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int q = tid + 512 * i;
+      if (q < lim) {
+        const int m = q >> 6, qq = q & 63;
+        const uint4 o = BITS == 4 ? __builtin_bit_cast(uint4, a_nibble_order(v[i])) : v[i];
+        *reinterpret_cast<uint4 *>(sx + m * kSkKc + 8 * swz(m, qq)) = o;
+      }
+    }
+  }
+  __syncthreads();
+
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kSkSteps; ++u) {
+    bf16x8_t b0, b1;
+    S::b_ops(wr[u], kc, b0, b1);
+    const float s = aux_f32<FP16>(sr[u]), b = aux_f32<FP16>(br[u]);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      bf16x8_t a0, a1;
+      const int m = 16 * t + r16;
+      S::a_ops(sx + m * kSkKc, (u * 64 + 16 * g) >> 3, m, a0, a1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      S::fold(acc[t], d, xs, s, b);
+    }
+  }
+  if (n >= p.N) return;
+  float *part = g_sk_part + (size_t)p.slot * kSkSlotFloats + (size_t)ks * p.M * p.N;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * t + 4 * g + i;
+      if (m < p.M) part[(size_t)m * p.N + n] = acc[t][i];
+    }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, int M, int N, void *y,
+                                                            int y_stride, int y_bf16) {
+  const float *part = g_sk_part + (size_t)slot * kSkSlotFloats;
+  const size_t MN = (size_t)M * N;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int ks = 0; ks < KS; ++ks) s += part[(size_t)ks * MN + i];
+    const int m = (int)(i / N), n = (int)(i % N);
+    if (y_bf16)
+      reinterpret_cast<uint16_t *>(y)[(size_t)m * y_stride + n] = (uint16_t)f32_to_bf16_rne(s);
+    else
+      reinterpret_cast<float *>(y)[(size_t)m * y_stride + n] = s;
+  }
+}
+
+bool affine_splitk_supported(const DevMat &m, int M) {
+  if (m.bits < 4 || m.bits > 8 || m.bits == 7) return false;
+  if (M < 3 || M > 32 || m.I % kSkKc != 0) return false;
+  if (m.gs <= 0 || m.gs % 64 != 0 || m.I % m.gs != 0) return false;
+  if (m.row_bytes != (long long)m.I * m.bits / 8) return false;
+  const uintptr_t need = m.bits == 4 ? 7 : m.bits == 8 ? 15 : 3;
+  if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
+  const size_t KS = (size_t)m.I / kSkKc;
+  return KS * (size_t)M * (size_t)m.O <= kSkSlotFloats;
+}
+
+template <int BITS, int MT>
+static void splitk_launch_t(const SplitParams &p, bool fp16, bool aux8, hipStream_t st) {
+  const dim3 grid((p.N + kSkRows - 1) / kSkRows, p.K / kSkKc);
+  if (fp16) {
+    if (aux8) hipLaunchKernelGGL((skinny_splitk_kernel<BITS, MT, true, true>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((skinny_splitk_kernel<BITS, MT, true, false>), grid, dim3(512), 0, st, p);
+  } else {
+    if (aux8) hipLaunchKernelGGL((skinny_splitk_kernel<BITS, MT, false, true>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((skinny_splitk_kernel<BITS, MT, false, false>), grid, dim3(512), 0, st, p);
+  }
+}
+
+template <int BITS>
+static void splitk_launch_bits(const SplitParams &p, bool fp16, bool aux8, hipStream_t st) {
+  if (p.M <= 16) splitk_launch_t<BITS, 1>(p, fp16, aux8, st);
+  else splitk_launch_t<BITS, 2>(p, fp16, aux8, st);
+}
+
+static std::atomic<unsigned> g_sk_next{0};
+
+hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                                int y_stride, int y_bf16, hipStream_t st) {
+  if (!affine_splitk_supported(m, M)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  SplitParams p;
+  p.w = m.w;
+  p.sc = m.sc;
+  p.bi = m.bi;
+  p.x = x;
+  p.row_bytes = m.row_bytes;
+  p.N = m.O;
+  p.K = m.I;
+  p.ng = m.ng;
+  p.gsteps = m.gs / 64;
+  p.x_stride = x_stride;
+  p.M = M;
+  p.slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
+  // 16-byte runs of eight u16 scale/bias words per 512 codes
+  const bool aux8 = m.gs == 64 && (m.ng % 8) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 15) == 0;
+  switch (m.bits) {
+    case 4: splitk_launch_bits<4>(p, m.fp16, aux8, st); break;
+    case 5: splitk_launch_bits<5>(p, m.fp16, aux8, st); break;
+    case 6: splitk_launch_bits<6>(p, m.fp16, aux8, st); break;
+    default: splitk_launch_bits<8>(p, m.fp16, aux8, st); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t MN = (size_t)M * m.O;
+  size_t blocks = (MN + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.slot, m.I / kSkKc, M,
+                     m.O, y, y_stride, y_bf16);
+  return hipGetLastError();
+}
+
+}  // namespace lh

@@ -36,6 +36,11 @@ bool affine_qmm_supported(const DevMat &m);
 bool affine_skinny_supported(const DevMat &m);
 hipError_t launch_affine_skinny(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);
+// K split across blocks (gemv_splitk.hip): I % 512 == 0, groups of 64k,
+// 3 <= M <= 32; partial sums in module-scope scratch slots
+bool affine_splitk_supported(const DevMat &m, int M);
+hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                                int y_stride, int y_bf16, hipStream_t st);
 hipError_t launch_silu_mul(void *g, const void *u, long long n, bool bf16, hipStream_t st);
 
 // ---- generic GEMV over up to 16 descriptors, f32 activations ----

@@ -195,81 +195,6 @@ __global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, M
 }
 
 // ---------------------------------------------------------------------------
-// shared pieces of the MFMA kernels
-
-// LDS tile of 16 rows of bf16 in 16-byte granules; granule q of row m sits at
-// q ^ m inside its aligned run of 16 granules, so the 16 rows of one MFMA
-// operand read hit 16 different bank groups.
-__device__ __forceinline__ int swz(int m, int q) { return q ^ (m & 15); }
-
-template <int BITS>
-struct MfmaStep {
-  // activation operand of one 64-code step (two 8-k slices per lane) from an
-  // LDS tile already in the operand order of BITS-bit codes
-  static __device__ __forceinline__ void a_ops(const uint16_t *rowp, int q0, int m, bf16x8_t &a0,
-                                               bf16x8_t &a1) {
-    a0 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0)));
-    a1 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(rowp + 8 * swz(m, q0 + 1)));
-  }
-  // position of activation k inside its run of 8 in the operand order
-  static __device__ __forceinline__ int op_pos(int k) {
-    if constexpr (BITS == 4) {
-      const int i = k & 7;
-      return (k & ~7) | (i < 4 ? 2 * i : 2 * (i - 4) + 1);
-    } else {
-      return k;
-    }
-  }
-  static __device__ __forceinline__ void b_ops(const SkRaw<BITS> &r, const UnpackConsts &kc,
-                                               bf16x8_t &b0, bf16x8_t &b1) {
-    if constexpr (BITS == 4) {
-      b0 = b_from_nibbles(r.v.x, kc);
-      b1 = b_from_nibbles(r.v.y, kc);
-    } else if constexpr (BITS == 8) {
-      b0 = b_from_bytes(r.v.x, r.v.y);
-      b1 = b_from_bytes(r.v.z, r.v.w);
-    } else {
-      // 5-bit runs of 16 codes start at bit 0 or 16 of their first dword
-      b_from_window<BITS>(r.w, BITS == 5 ? 16 * ((threadIdx.x >> 4) & 1) : 0, b0, b1);
-    }
-  }
-  // the lane's 16 codes [k, k + 16) of a row (k a multiple of 16)
-  static __device__ __forceinline__ void load_raw(SkRaw<BITS> &r, const uint8_t *row, int k) {
-    if constexpr (BITS == 4) {
-      r.v = *reinterpret_cast<const uint2 *>(row + (k >> 1));
-    } else if constexpr (BITS == 8) {
-      r.v = *reinterpret_cast<const uint4 *>(row + k);
-    } else {
-      // dword holding the first code: 5-bit (k * 5) / 32, 6-bit (k * 6) / 32
-      const uint32_t *p = reinterpret_cast<const uint32_t *>(row) + ((k * BITS) >> 5);
-      r.w[0] = p[0];
-      r.w[1] = p[1];
-      r.w[2] = p[2];
-    }
-  }
-  // y += s' D + b' X: D = X + 2^(s-7) sum(c x) for codes at mantissa bit s
-  // (4-bit s = 3, 5-bit 2, 6-bit 1), D = sum(c x) for 8-bit
-  static __device__ __forceinline__ void fold(f32x4_t &acc, const f32x4_t &d, const f32x4_t &xs,
-                                              float s, float b) {
-    constexpr float F = BITS == 4 ? 16.f : BITS == 5 ? 32.f : BITS == 6 ? 64.f : 1.f;
-    const float s2 = BITS == 8 ? s : F * s;
-    const float b2 = BITS == 8 ? b : b - F * s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = fmaf(b2, xs[i], fmaf(s2, d[i], acc[i]));
-  }
-};
-
-template <bool FP16>
-__device__ __forceinline__ float aux_f32(uint32_t b) {
-  if constexpr (FP16) return f16_to_f32(b);
-  else return bf16_to_f32(b);
-}
-
-__device__ __forceinline__ const bf16x8_t mfma_ones() {
-  return as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-}
-
-// ---------------------------------------------------------------------------
 // 3. gate/up + SwiGLU: block = (tile, 16 * WAVES rows), wave = 16 rows of gate
 //    and up; batches of GU 64-code steps double-buffered in registers
 
