@@ -153,7 +153,11 @@ typedef struct LoganHipAffine {
 /* y[M][y_stride] = x[M][x_stride] . W^T  (matmul_mlx_affine_storage,
  * logan-qwen4/src/lib.rs:3729-3764, per activation row). x bf16, y bf16 or
  * f32 (y_dtype). f32 accumulation. 1 ok, 0 unsupported geometry, -1 launch
- * failure. */
+ * failure. With M >= 3 (I a multiple of 512, groups of 64k) the product is
+ * split over K and its partial sums pass through one of 4 library-owned
+ * scratch slots taken round-robin per call; calls on one device whose
+ * executions overlap (different streams) therefore stay correct while at
+ * most 4 of them are in flight. */
 int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                           int y_stride, int y_dtype, void *stream);
 
