@@ -137,11 +137,18 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, int M, int N, void *y,
                                                             int y_stride, int y_bf16) {
   const float *part = g_sk_part + (size_t)slot * kSkSlotFloats;
-  const size_t MN = (size_t)M * N;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+  const int MN = M * N;  // <= kSkSlotFloats
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < MN; i += gridDim.x * 256) {
+    // eight partials in flight at a time, added in K order
     float s = 0.f;
-    for (int ks = 0; ks < KS; ++ks) s += part[(size_t)ks * MN + i];
-    const int m = (int)(i / N), n = (int)(i % N);
+    for (int k0 = 0; k0 < KS; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = part[min(k0 + j, KS - 1) * MN + i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += k0 + j < KS ? v[j] : 0.f;
+    }
+    const int m = i / N, n = i - m * N;
     if (y_bf16)
       reinterpret_cast<uint16_t *>(y)[(size_t)m * y_stride + n] = (uint16_t)f32_to_bf16_rne(s);
     else

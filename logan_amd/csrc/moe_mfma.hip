@@ -29,7 +29,10 @@
 namespace lh {
 
 constexpr int kMTok = 16;          // slots per tile
-constexpr int kMChunk = 2048;      // x codes staged in LDS at a time (gate/up)
+#ifndef MOE_CHUNK
+#define MOE_CHUNK 2048
+#endif
+constexpr int kMChunk = MOE_CHUNK;  // x codes staged in LDS at a time (gate/up)
 constexpr int kMDownK = 512;       // largest down K (expert intermediate size)
 constexpr int kMMaxSlots = 65536;  // B * k
 constexpr int kMMaxE = 1024;
