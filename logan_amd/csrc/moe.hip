@@ -569,9 +569,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a, MoeWs w) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     const int t = (int)(i / a.D), d = (int)(i % a.D);
     float acc = 0.f;
-    for (int r = 0; r < a.k; ++r) {
-      const int slot = t * a.k + r;
-      acc = fmaf(w.y[(size_t)w.gpos[slot] * a.D + d], w.topk_w[slot], acc);
+    // eight ranks' rows and weights in flight at a time, added in rank order
+    for (int r0 = 0; r0 < a.k; r0 += 8) {
+      int gp[8];
+      float wt[8], yv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int slot = t * a.k + min(r0 + j, a.k - 1);
+        gp[j] = w.gpos[slot];
+        wt[j] = r0 + j < a.k ? w.topk_w[slot] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) yv[j] = w.y[(size_t)gp[j] * a.D + d];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (r0 + j < a.k) acc = fmaf(yv[j], wt[j], acc);
     }
     float o = acc;
     if (a.sdown.m.w) {

@@ -518,14 +518,28 @@ __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) 
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     const int t = (int)(i / D4), d = 4 * (int)(i % D4);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int r = 0; r < a.k; ++r) {
-      const int slot = t * a.k + r;
-      const float wr = w.topk_w[slot];
-      const float4 v = *reinterpret_cast<const float4 *>(w.y + (size_t)w.gpos[slot] * a.D + d);
-      acc.x = fmaf(v.x, wr, acc.x);
-      acc.y = fmaf(v.y, wr, acc.y);
-      acc.z = fmaf(v.z, wr, acc.z);
-      acc.w = fmaf(v.w, wr, acc.w);
+    // eight ranks' rows and weights in flight at a time, added in rank order
+    for (int r0 = 0; r0 < a.k; r0 += 8) {
+      int gp[8];
+      float wt[8];
+      float4 yv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int slot = t * a.k + min(r0 + j, a.k - 1);
+        gp[j] = w.gpos[slot];
+        wt[j] = w.topk_w[slot];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) yv[j] = *reinterpret_cast<const float4 *>(w.y + (size_t)gp[j] * a.D + d);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (r0 + j < a.k) {
+          acc.x = fmaf(yv[j].x, wt[j], acc.x);
+          acc.y = fmaf(yv[j].y, wt[j], acc.y);
+          acc.z = fmaf(yv[j].z, wt[j], acc.z);
+          acc.w = fmaf(yv[j].w, wt[j], acc.w);
+        }
+      }
     }
     if (a.sdown.m.w) {
       const float gs = w.gs[t];
