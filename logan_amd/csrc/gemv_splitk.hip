@@ -87,14 +87,15 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
       const int m = q >> 6, qq = q & 63;
       v[i] = *reinterpret_cast<const uint4 *>(p.x + (size_t)m * p.x_stride + k0 + 8 * qq);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every staging load issued first
+    // unconditional stores (granules past row M - 1 fill LDS rows no stored
+    // output depends on), so no load is sunk into a guarded store
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int q = tid + 512 * i;
-      if (q < lim) {
-        const int m = q >> 6, qq = q & 63;
-        const uint4 o = BITS == 4 ? __builtin_bit_cast(uint4, a_nibble_order(v[i])) : v[i];
-        *reinterpret_cast<uint4 *>(sx + m * kSkKc + 8 * swz(m, qq)) = o;
-      }
+      const int m = q >> 6, qq = q & 63;
+      const uint4 o = BITS == 4 ? __builtin_bit_cast(uint4, a_nibble_order(v[i])) : v[i];
+      *reinterpret_cast<uint4 *>(sx + m * kSkKc + 8 * swz(m, qq)) = o;
     }
   }
   __syncthreads();

@@ -109,6 +109,15 @@ __device__ __forceinline__ void b_from_window(const uint32_t (&w)[3], int sh, bf
 // operand read hit 16 different bank groups.
 __device__ __forceinline__ int swz(int m, int q) { return q ^ (m & 15); }
 
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l of the wave
+// writes the 16 bytes at src into lds_wave + 16 l, without passing through
+// VGPRs. lds_wave must be wave-uniform; completion is counted by vmcnt, so a
+// reader waits with lds_dma_wait() and a barrier.
+__device__ __forceinline__ void lds_dma16(const void *src, uint16_t *lds_wave) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int BITS>
 struct MfmaStep {
   // activation operand of one 64-code step (two 8-k slices per lane) from an

@@ -294,6 +294,12 @@ __global__ __launch_bounds__(WAVES * 64, MOE_GU_MINW) void moe_gateup_mfma_kerne
   kc.init();
   const bf16x8_t ones = mfma_ones();
   f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+  // the tile's token indices, read once (the x staging loads then depend on
+  // LDS only and are all in flight together); rows past the tile repeat its
+  // last token
+  __shared__ int s_tok[kMTok];
+  if (tid < kMTok) s_tok[tid] = shared ? row0 - nslots + min(tid, cnt - 1) : w.tok[row0 + min(tid, cnt - 1)];
+  __syncthreads();
 
   auto issue = [&](int st, GuBatch<BITS, GU, GS64> &B) {
 #pragma unroll
@@ -328,29 +334,29 @@ __global__ __launch_bounds__(WAVES * 64, MOE_GU_MINW) void moe_gateup_mfma_kerne
     const int s0 = c * chunk >> 6;
     GuBatch<BITS, GU, GS64> B0, B1;
     issue(s0, B0);
-    // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk): every load
-    // issued before any store; threads past the tile re-read its last granule
+    // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk), straight
+    // into LDS: lane granule pg of the 16-row tile is physical granule P of
+    // row m, which holds logical granule P ^ (m & 15); rows past the tile
+    // repeat its last token (no operand of a stored output reads them)
     if (c > 0) __syncthreads();
     {
       constexpr int NV = kMTok * kMChunk / 8 / NT;
-      const int gpr = chunk >> 3;  // granules per row
-      const int lim = cnt * gpr;
-      uint4 v[NV];
+      const int gpr = chunk >> 3;  // granules per row (>= 32)
+      auto dma = [&](int base) {
+        const int pg = base + lane;
+        const int m = pg / gpr, qq = swz(m, pg % gpr);
+        lds_dma16(xsrc + (size_t)s_tok[m] * a.D + c * chunk + 8 * qq, sx + 8 * base);
+      };
+      if (chunk == kMChunk) {
+        // full tile: every copy unconditional, all in flight together
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int q = min(tid + NT * i, lim - 1);
-        const int m = q / gpr, qq = q % gpr;
-        const int t = shared ? row0 - nslots + m : w.tok[row0 + m];
-        v[i] = *reinterpret_cast<const uint4 *>(xsrc + (size_t)t * a.D + c * chunk + 8 * qq);
-      }
+        for (int i = 0; i < NV; ++i) dma(NT * i + 64 * wave);
+      } else {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int q = tid + NT * i;
-        if (q < lim) {
-          const int m = q / gpr, qq = q % gpr;
-          *reinterpret_cast<uint4 *>(sx + m * chunk + 8 * swz(m, qq)) = v[i];
-        }
+        for (int i = 0; i < NV; ++i)
+          if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
       }
+      lds_dma_wait();
     }
     __syncthreads();
     // issues past the chunk end reload its last batch (unconditional, so the
@@ -411,7 +417,7 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
   const int steps = K >> 6;
   const int gsteps = dbk.m.gs >> 6;
   // scale/bias as dwords of two steps when every step is its own group
-  const bool pair_aux = gsteps == 1 && (dbk.m.ng & 1) == 0;
+  const bool pair_aux = __builtin_amdgcn_readfirstlane(gsteps == 1 && (dbk.m.ng & 1) == 0);
   SkRaw<BITS> wr[2][NS];
   uint32_t sr[2][NS], br[2][NS];
 #pragma unroll
@@ -420,6 +426,29 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
     const uint8_t *wrow = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
 #pragma unroll
     for (int u = 0; u < NS; ++u) S::load_raw(wr[r][u], wrow, min(u, steps - 1) * 64 + 16 * g);
+  }
+  {
+    // stage h (hi, lo) of the tile's rows straight into LDS, in flight with
+    // the weight loads (physical granule P of row m holds logical granule
+    // P ^ (m & 15)); rows past the tile repeat its last row, which no operand
+    // of a stored output reads
+    constexpr int NQ = kMTok * kMDownK / 8 / 256;
+    const int gpr = K >> 3;  // >= 16
+    auto dma = [&](int base) {
+      const int pg = base + lane;
+      const int m = pg / gpr, qq = swz(m, pg % gpr);
+      const size_t o = (size_t)(row0 + min(m, cnt - 1)) * hmax + 8 * qq;
+      lds_dma16(w.h_hi + o, shi + 8 * base);
+      lds_dma16(w.h_lo + o, slo + 8 * base);
+    };
+    if (K == kMDownK) {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) dma(256 * i + 64 * wave);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i)
+        if (256 * i + 64 * wave < kMTok * gpr) dma(256 * i + 64 * wave);
+    }
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -430,10 +459,11 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
 #pragma unroll
       for (int u = 0; u < NS; u += 2) {
         const int q = min(u, steps - 2);
-        const uint32_t vs = *reinterpret_cast<const uint32_t *>(srow + q);
-        const uint32_t vb = *reinterpret_cast<const uint32_t *>(brow + q);
-        sr[r][u] = vs & 0xffffu; sr[r][u + 1] = vs >> 16;
-        br[r][u] = vb & 0xffffu; br[r][u + 1] = vb >> 16;
+        // the dword of steps (u, u + 1) in slot u, split where it is used
+        sr[r][u] = *reinterpret_cast<const uint32_t *>(srow + q);
+        br[r][u] = *reinterpret_cast<const uint32_t *>(brow + q);
+        sr[r][u + 1] = 0;
+        br[r][u + 1] = 0;
       }
     } else {
 #pragma unroll
@@ -444,29 +474,7 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
       }
     }
   }
-  {
-    // stage h (hi, lo) of the tile's rows; every load before any store
-    constexpr int NQ = kMTok * kMDownK / 8 / 256;
-    const int gpr = K >> 3;
-    const int lim = cnt * gpr;
-    uint4 vh[NQ], vl[NQ];
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int q = min(tid + 256 * i, lim - 1);
-      const size_t o = (size_t)(row0 + q / gpr) * hmax + 8 * (q % gpr);
-      vh[i] = *reinterpret_cast<const uint4 *>(w.h_hi + o);
-      vl[i] = *reinterpret_cast<const uint4 *>(w.h_lo + o);
-    }
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-      const int q = tid + 256 * i;
-      if (q < lim) {
-        const int m = q / gpr, qq = q % gpr;
-        *reinterpret_cast<uint4 *>(shi + m * K + 8 * swz(m, qq)) = vh[i];
-        *reinterpret_cast<uint4 *>(slo + m * K + 8 * swz(m, qq)) = vl[i];
-      }
-    }
-  }
+  lds_dma_wait();
   __syncthreads();
   UnpackConsts kc;
   kc.init();
@@ -492,7 +500,9 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, b1, d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, b0, d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, b1, d, 0, 0, 0);
-        S::fold(acc[r], d, xs, aux_f32<FP16>(sr[r][u]), aux_f32<FP16>(br[r][u]));
+        const uint32_t sw = pair_aux ? (sr[r][u & ~1] >> (16 * (u & 1))) & 0xffffu : sr[r][u];
+        const uint32_t bw = pair_aux ? (br[r][u & ~1] >> (16 * (u & 1))) & 0xffffu : br[r][u];
+        S::fold(acc[r], d, xs, aux_f32<FP16>(sw), aux_f32<FP16>(bw));
       }
     }
   }
