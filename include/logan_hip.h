@@ -257,8 +257,9 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
  * (logan-qwen4/src/lib.rs:14907-14922). Launches of that path on one device
  * must not overlap. sync_errors returns its sticky error word for the
  * current device: 0 = healthy; bit 0 = a phase hand-off wait timed out (the
- * output of that call was not valid); bits 1-2 = arrival counters not at
- * rest between launches. */
+ * output of that call was not valid); bit 1 = a launch counter not on a
+ * launch boundary, bit 2 = launch counters out of step (both checked between
+ * launches). */
 void logan_hip_set_moe_fused(int on);
 uint32_t logan_hip_moe_sync_errors(void);
 

@@ -33,21 +33,27 @@
 // host can read the word with logan_hip_moe_sync_errors(); results of later
 // launches are then not guaranteed either).
 //
-// Hand-off without L2 maintenance: h pairs, counters and the epoch are
-// written and read only with device-scope (sc1) relaxed atomics / loads,
-// which are coherent across the XCDs' L2s. Each launch's tag is derived from
-// the epoch word that the last B block of the previous launch advanced, so
-// pairs left by earlier launches never pass the tag check. An agent-scope
+// Hand-off without L2 maintenance: h pairs and counters are written and
+// read only with device-scope (sc1) relaxed atomics / loads, which are
+// coherent across the XCDs' L2s. An h pair's tag names its launch, so pairs
+// left by earlier launches never pass the tag check. An agent-scope
 // release/acquire fence would instead write back / invalidate the whole L2
 // of each XCD per wave (buffer_wbl2 / buffer_inv), which measured tens of
 // microseconds per launch here.
 //
-// The counters and the epoch live in module-scope device memory (zero when
-// the code object loads). B blocks count their completion over kDoneCtrs
-// counters and then one top counter; the block that completes the count
-// puts every counter back to zero and advances the epoch, so each launch
-// starts from zero without a memset. Launches of this kernel on one device
-// must therefore not overlap (one stream, or serialised streams).
+// Launch numbers without a completion count: every block takes a ticket
+// from one of kTickets 64-bit counters (block b from counter b % kTickets);
+// the launch number is ticket >> kTicketShift. The block that takes a
+// counter's last ticket of the launch adds what is left to the next multiple
+// of 2^kTicketShift, and counters that no block of a small grid uses are
+// advanced by one launch as well, so every block of the next launch again
+// reads one launch number. Launches of this kernel on one device must
+// therefore not overlap (one stream, or serialised streams): the next launch
+// starts only after this one has ended, its realigning atomics included.
+// Arrival counters come in two sets used by alternate launches; each launch
+// zeroes the set the next one will use. All of this lives in module-scope
+// device memory (zero when the code object loads), so no launch needs a
+// memset and nothing is left to count once the outputs are written.
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 #include "route_dev.hpp"
@@ -58,22 +64,21 @@ constexpr int kFusedMaxSlots = 12;  // k + 1 (routed + shared)
 // Each slot's arrivals are spread over kSubCtrs counters (the i-th A block of
 // a slot arrives on counter i % kSubCtrs), each on its own 256-byte line:
 // same-address atomics serialise at the memory side (~40 ns each measured
-// here). B completion likewise goes over kDoneCtrs counters, then btop.
+// here). Launch tickets likewise go over kTickets counters.
 constexpr int kSubCtrs = 4;
 constexpr int kLine = 64;  // u32 per 256-byte line
-constexpr int kDoneCtrs = 16;
+constexpr int kTickets = 64;
+constexpr int kTicketShift = 20;  // tickets per launch and counter stay below 2^20
 struct FusedSync {
-  uint32_t ctr[kFusedMaxSlots][kSubCtrs][kLine];
-  uint32_t bctr[kDoneCtrs][kLine];
-  uint32_t btop[kLine];
-  uint32_t epoch[kLine];
+  unsigned long long tk[kTickets][kLine / 2];
+  uint32_t ctr[2][kFusedMaxSlots][kSubCtrs][kLine];
   uint32_t error[kLine];
 };
 __device__ FusedSync g_fused_sync;
 
 constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit data format
 constexpr int kCpolSc1 = 16;           // cache policy: device scope (sc1)
-// h pairs rotate over kSlices workspace slices (slice = epoch % kSlices), so
+// h pairs rotate over kSlices workspace slices (slice = launch % kSlices), so
 // a line that an XCD's L2 still holds from an earlier launch is many launches
 // old; B reads pairs through L2 first and re-reads with sc1 on a stale tag.
 constexpr int kSlices = 16;
@@ -141,10 +146,31 @@ __device__ __forceinline__ bool read_pairs(__amdgpu_buffer_rsrc_t rs, int off, i
   return ok;
 }
 
-// tag of this launch's h pairs: odd, so zeroed memory never passes
-__device__ __forceinline__ uint32_t launch_tag() {
-  return (ld_agent(&g_fused_sync.epoch[0]) << 1) | 1u;
+// This block's ticket (thread 0; the value is used later, so the atomic's
+// round trip overlaps the block's first loads).
+__device__ __forceinline__ unsigned long long take_ticket() {
+  return __hip_atomic_fetch_add(&g_fused_sync.tk[blockIdx.x % kTickets][0], 1ull, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Launch number from the ticket; the holder of a counter's last ticket of
+// this launch realigns the counter for the next launch, and counters no
+// block of a small grid uses are advanced by one launch too (counter
+// j >= gridDim.x by block j mod gridDim.x), so all counters stay in step.
+__device__ __forceinline__ uint32_t launch_number(unsigned long long t) {
+  const int j = blockIdx.x % kTickets;
+  const unsigned long long n = (gridDim.x - 1 - j) / kTickets + 1;  // blocks on counter j
+  if ((t & ((1ull << kTicketShift) - 1)) == n - 1)
+    __hip_atomic_fetch_add(&g_fused_sync.tk[j][0], (1ull << kTicketShift) - n, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  for (int u = blockIdx.x + gridDim.x; u < kTickets; u += gridDim.x)
+    __hip_atomic_fetch_add(&g_fused_sync.tk[u][0], 1ull << kTicketShift, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  return (uint32_t)(t >> kTicketShift);
+}
+
+// tag of a launch's h pairs: odd, so zeroed memory never passes
+__device__ __forceinline__ uint32_t launch_tag(uint32_t lid) { return (lid << 1) | 1u; }
 
 // expected arrivals on sub-counter q of a slot with n A waves
 __device__ __forceinline__ uint32_t sub_need(int n, int q) {
@@ -169,7 +195,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __shared__ __align__(16) uint32_t s_xp[64 * CPLA][16];  // A: x pairs per chunk
   __shared__ __align__(16) float s_xs[64 * CPLA][kWaves];  // A: partial sums of x
   __shared__ __align__(16) float s_xsp[64 * CPLA][kWaves]; // A: partial sums of x' (pairs)
-  __shared__ uint32_t s_left;  // A: waves of the block still running; B: waves done polling
+  __shared__ uint32_t s_left;  // A: waves of the block still running
+  __shared__ uint32_t s_lid;   // launch number
   __shared__ float s_gsig;
 
   const int lane = threadIdx.x & 63;
@@ -190,6 +217,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     const int jb = shared ? item - g.k * g.wpr : item % g.wpr;
     const int rows = shared ? a.sinter : a.inter;
 
+    unsigned long long tk = 0;
+    if (threadIdx.x == 0) tk = take_ticket();
     // every wave of an A block serves the same slot: wave 0 routes for all
     uint32_t key[KPL];
     if (!shared && wave == 0) route_keys<KPL>(logits, a.E, key);
@@ -241,8 +270,10 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
       if (lane == 0) s_sel[0] = mine;
     }
+    if (threadIdx.x == 0) s_lid = launch_number(tk);
     __syncthreads();
     const int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
+    const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
     // bank fields copied once (scalar) rather than re-read per use
     const DevMat gm = shared ? a.sgate.m : a.gate.m;
     const DevMat um = shared ? a.sup.m : a.up.m;
@@ -282,8 +313,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
         rsu[u][i] = usc[p];
         rbu[u][i] = ubi[p];
       }
-    // this launch's tag, loaded behind the weights (it is needed only at the end)
-    const uint32_t tag = launch_tag();
+    const uint32_t tag = launch_tag(lid);
     // keep every load above issued before any of their consumers
     __builtin_amdgcn_sched_barrier(0);
     float pg[UA], pu[UA];
@@ -331,7 +361,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       const float up = __int_as_float(__builtin_amdgcn_ds_bpermute((lane + 32) << 2, __float_as_int(t)));
       hval = silu(t) * up;
     }
-    const int slice = (int)((tag >> 1) % kSlices);
+    const int slice = (int)(lid % kSlices);
     uint64_t *hrow = reinterpret_cast<uint64_t *>(a.ws) + ((size_t)slice * g.slots + slot) * hmax;
     const int r = lane >> 4;
     if ((lane & 15) == 0 && r < UA && j0 + r < rows) {
@@ -342,7 +372,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     // behind the stores and without waiting for them (B checks the tags).
     if (lane == 0 && atomicSub(&s_left, 1u) == 1u) {
       const int first = shared ? g.k * g.wpr / kWaves : slot * (g.wpr / kWaves);
-      __hip_atomic_fetch_add(&g_fused_sync.ctr[slot][(blockIdx.x - first) % kSubCtrs][0], 1u,
+      __hip_atomic_fetch_add(&g_fused_sync.ctr[lid & 1][slot][(blockIdx.x - first) % kSubCtrs][0], 1u,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return;
@@ -357,8 +387,9 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   const bool has_shared = a.sdown.m.w != nullptr;
 
   // wave 0 routes for the block
+  unsigned long long tk = 0;
+  if (threadIdx.x == 0) tk = take_ticket();
   uint32_t key[KPL];
-  if (threadIdx.x == 0) s_left = 0;
   if (wave == 0) route_keys<KPL>(logits, a.E, key);
 
   // route-independent loads first: the shared slot's down rows
@@ -393,7 +424,16 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       if (a.w_out) a.w_out[lane] = wr;
     }
   }
+  if (threadIdx.x == 0) s_lid = launch_number(tk);
   __syncthreads();
+  const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
+  const uint32_t tag = launch_tag(lid);
+  // zero the arrival counters the next launch uses (the previous launch,
+  // their last user, has ended): counter j by block j mod nB
+  if (wave == 0) {
+    const int j = bb + g.nB_blocks * lane;
+    if (j < kFusedMaxSlots * kSubCtrs) st_agent(&g_fused_sync.ctr[(lid + 1) & 1][j / kSubCtrs][j % kSubCtrs][0], 0u);
+  }
 #pragma unroll
   for (int t = 0; t < kSlotsPerWave; ++t) {
     const int s = wave + t * kWaves;
@@ -425,7 +465,6 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
   }
-  const uint32_t tag = launch_tag();
   __builtin_amdgcn_sched_barrier(0);
   // shared-expert scalar gate sigmoid(se_g . x) (logan-qwen4/src/lib.rs:7602-7604)
   if (wave == kWaves - 1) {
@@ -461,7 +500,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     const bool mine = t < kSlotsPerWave && s < g.slots;
     const int nb = ((has_shared && s == g.k) ? g.wps : g.wpr) / kWaves;  // A blocks of slot s
     const uint32_t need = mine ? sub_need(nb, q) : 0u;
-    uint32_t *cp = &g_fused_sync.ctr[mine ? s : 0][q][0];
+    uint32_t *cp = &g_fused_sync.ctr[lid & 1][mine ? s : 0][q][0];
     bool done = !mine || ld_agent(cp) >= need;
     uint32_t spins = 0;
     while (!__all(done)) {
@@ -473,21 +512,9 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
   }
-  // Completion, counted once every wave of the block has seen its slots'
-  // arrivals (the counters are not read again; the epoch is already in every
-  // wave's tag): the last wave of the block to get here counts the block on
-  // bctr[bb % kDoneCtrs]. The returned count is looked at only after the
-  // combine, so the atomic's round trip overlaps the h reads and the math.
-  bool counted = false;
-  uint32_t done_prev = 0;
-  if (lane == 0 && atomicAdd(&s_left, 1u) == kWaves - 1) {
-    counted = true;
-    done_prev = __hip_atomic_fetch_add(&g_fused_sync.bctr[bb % kDoneCtrs][0], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-  }
   // lane covers h[VPL*lane .. VPL*lane + VPL) of each slot: first through
   // L2, then (stale or not yet landed) with device-scope loads
-  const int slice = (int)((tag >> 1) % kSlices);
+  const int slice = (int)(lid % kSlices);
   const __amdgpu_buffer_rsrc_t hrsrc = __builtin_amdgcn_make_buffer_rsrc(
       a.ws, (short)0, kSlices * g.slots * hmax * 8, kBufWord3);
   float hv[kSlotsPerWave][VPL];
@@ -586,30 +613,6 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
   }
 
-  // the block completing its bctr counts on btop; the block completing btop
-  // resets every counter (one store per lane) and advances the epoch
-  if (__builtin_amdgcn_readfirstlane(counted ? 1 : 0)) {
-    const uint32_t prev = __builtin_amdgcn_readfirstlane(done_prev);
-    const int nb = g.nB_blocks;
-    const int c = bb % kDoneCtrs;
-    const int nbc = nb < kDoneCtrs ? nb : kDoneCtrs;
-    const int needc = nb / kDoneCtrs + (c < nb % kDoneCtrs ? 1 : 0);
-    if (prev == (uint32_t)needc - 1) {
-      uint32_t top = 0;
-      if (lane == 0)
-        top = __hip_atomic_fetch_add(&g_fused_sync.btop[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__builtin_amdgcn_readfirstlane(top) == (uint32_t)nbc - 1) {
-        static_assert(kFusedMaxSlots * kSubCtrs <= 64 && kDoneCtrs <= 64, "one lane per counter");
-        if (lane < kFusedMaxSlots * kSubCtrs) st_agent(&g_fused_sync.ctr[lane / kSubCtrs][lane % kSubCtrs][0], 0u);
-        if (lane < kDoneCtrs) st_agent(&g_fused_sync.bctr[lane][0], 0u);
-        if (lane == 0) {
-          st_agent(&g_fused_sync.btop[0], 0u);
-          __hip_atomic_fetch_add(&g_fused_sync.epoch[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-  }
-
 }
 
 // ---------------------------------------------------------------- launch
@@ -682,11 +685,13 @@ uint32_t moe_fused_sync_errors() {
   if (hipMemcpyFromSymbol(&s, HIP_SYMBOL(g_fused_sync), sizeof(s), 0, hipMemcpyDeviceToHost) !=
       hipSuccess)
     return 0xffffffffu;
-  uint32_t busy = 0, bbusy = s.btop[0];
-  for (int c = 0; c < kFusedMaxSlots; ++c)
-    for (int q = 0; q < kSubCtrs; ++q) busy |= s.ctr[c][q][0];
-  for (int c = 0; c < kDoneCtrs; ++c) bbusy |= s.bctr[c][0];
-  return s.error[0] | (busy ? 2u : 0u) | (bbusy ? 4u : 0u);
+  // between launches every ticket counter sits on the same launch boundary
+  uint32_t off = 0, apart = 0;
+  for (int j = 0; j < kTickets; ++j) {
+    off |= (s.tk[j][0] & ((1ull << kTicketShift) - 1)) != 0;
+    apart |= (s.tk[j][0] >> kTicketShift) != (s.tk[0][0] >> kTicketShift);
+  }
+  return s.error[0] | (off ? 2u : 0u) | (apart ? 4u : 0u);
 }
 
 }  // namespace lh

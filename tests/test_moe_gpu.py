@@ -292,6 +292,49 @@ def test_moe_fused_agrees_with_multi_launch(gpu):
     assert _lib.lib().logan_hip_moe_sync_errors() == 0
 
 
+@pytest.mark.parametrize("fused_mode", [1], indirect=True)
+@pytest.mark.parametrize("E,k,D,inter,sinter,bits,gs,shared,fp16", [
+    (16, 4, 256, 128, None, 4, 32, False, False),   # 4 chunks per row, no shared expert
+    (32, 4, 512, 256, 384, 4, 64, True, False),     # shared inter wider than routed
+    (64, 8, 512, 384, 128, 6, 64, True, False),     # shared inter narrower than routed
+    (64, 8, 4096, 256, None, 4, 64, True, False),   # two x chunks per lane (D > 2048)
+    (64, 8, 4096, 256, None, 6, 64, True, False),
+    (64, 8, 4096, 256, None, 8, 64, True, True),
+    (64, 8, 4096, 256, None, 5, 64, True, False),   # 5-bit at D > 2048: multi-launch path
+    (64, 6, 1024, 1024, None, 4, 64, True, False),  # 32 chunks per row
+    (64, 6, 1024, 1024, 512, 8, 64, True, False),
+    (64, 6, 1024, 768, None, 5, 128, True, True),
+    (64, 6, 1024, 640, None, 6, 32, True, False),
+    (32, 11, 512, 512, None, 6, 64, True, True),    # 12 slots, the most one launch serves
+    (1024, 10, 2048, 512, None, 4, 64, True, False),
+])
+def test_moe_fused_shapes(gpu, fused_mode, E, k, D, inter, sinter, bits, gs, shared, fp16):
+    """Single-token block over the shapes the one-launch kernel serves (row
+    chunks 4..32, shared width above/below the routed one, D up to 4096, 5/6/8
+    bit, fp16 sidecars, group sizes 32..128, 1..12 slots) against the oracle."""
+    import torch
+
+    print(f"fused shape E={E} k={k} D={D} inter={inter} sinter={sinter} bits={bits} gs={gs}",
+          flush=True)
+    layer = Layer(torch, E, k, D, inter, bits, gs, shared=shared, seed=E + k + D + bits,
+                  sinter=sinter, fp16=fp16)
+    rng = np.random.default_rng(D + inter)
+    for rep in range(2):
+        xb = make_x(rng, 1, D)
+        lb = make_logits(rng, 1, E)
+        out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+        out16, idx2, _ = run_layer(torch, layer, xb, lb, torch.bfloat16)
+        out32 = out32.cpu().numpy()
+        np.testing.assert_array_equal(idx, idx2)
+        np.testing.assert_array_equal(out16.view(torch.int16).cpu().numpy().view(np.uint16),
+                                      bf16_bits(out32))
+        ref, ridx, rw = layer.ref(bf16_to_f32(xb[0]), bf16_to_f32(lb[0]))
+        np.testing.assert_array_equal(idx[0], ridx)
+        np.testing.assert_allclose(w[0], rw, rtol=1e-5)
+        err = normwise_rel(out32[0], ref)
+        assert err <= 5e-5, f"rep {rep}: {err:.3e}"
+
+
 @pytest.fixture
 def mfma_min_b(request):
     """Set the smallest batch that takes the MFMA path for one test, restore
