@@ -254,9 +254,8 @@ __global__ __launch_bounds__(256) void gemv_bf16_multi_kernel(GemvMultiParams mp
   gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT>(a, blockIdx.x - mp.block_start[i]);
 }
 
-template <int BITS, int LANES, int CPL, int MT, int SPLIT = 1>
+template <int BITS, int LANES, int CPL, int MT, int SPLIT, int U>
 static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiParams *mp = nullptr) {
-  constexpr int U = CPL == 1 ? 4 : (CPL == 2 ? 2 : 1);
   constexpr int rows_per_block = (256 / LANES / SPLIT) * U;
   if (mp) {
     mp->block_start[0] = 0;
@@ -273,15 +272,22 @@ static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiPa
   return hipGetLastError();
 }
 
+// Rows longer than 64 chunks are split across waves (SPLIT) rather than
+// given more chunks per lane: one chunk per lane and two rows per team keep
+// registers low, so more waves - and more loads - are in flight. Measured at
+// the config-2 / config-5 shapes (8-bit 14336x4096: 14.5 -> 13.0 us; 8-bit
+// 4096x14336: 18.8 -> 15.6 us; 4-bit 2048x4096: 4.5 -> 3.7 us). Rows of up
+// to 64 chunks keep four rows per team (two measured faster launched back to
+// back, slower inside a graph).
 template <int BITS, int MT>
 static hipError_t gemv_dispatch_shape(const GemvParams &p, hipStream_t st, GemvMultiParams *mp) {
   const int C = p.I >> 5;
-  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT>(p, st, mp);
-  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT>(p, st, mp);
-  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT>(p, st, mp);
-  if (C <= 128) return gemv_launch_t<BITS, 64, 2, MT>(p, st, mp);
-  if (C <= 256) return gemv_launch_t<BITS, 64, 4, MT>(p, st, mp);
-  if (C <= 512) return gemv_launch_t<BITS, 64, 4, MT, 2>(p, st, mp);
+  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT, 1, 4>(p, st, mp);
+  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT, 1, 4>(p, st, mp);
+  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT, 1, 4>(p, st, mp);
+  if (C <= 128) return gemv_launch_t<BITS, 64, 1, MT, 2, 2>(p, st, mp);
+  if (C <= 256) return gemv_launch_t<BITS, 64, 1, MT, 4, 2>(p, st, mp);
+  if (C <= 512) return gemv_launch_t<BITS, 64, 2, MT, 4, 2>(p, st, mp);
   return hipErrorInvalidValue;
 }
 
