@@ -15,19 +15,23 @@
 // Launch structure (all on one stream):
 //   1. moe_route_group_kernel   one block: route every token, shared-expert
 //                               gate, x of every token as bf16 pairs, group
-//                               the (token, rank) slots by expert: one record
-//                               per group (expert, first row, rows, first
-//                               tokens) and a grouped row per slot
-//   2. moe_gateup_kernel        per (group, 16 rows): gate and up rows loaded
-//                               once, applied to every token of the group,
-//                               SwiGLU fused -> h[grouped row][j] (f32)
-//   3. moe_down_kernel          per (group, 32 rows): down rows loaded once,
-//                               applied to h of every row of the group
-//                               -> y[grouped row][d] (f32)
+//                               the (token, rank) slots by expert and cut
+//                               each expert's rows into sub-groups of at most
+//                               kSubTok: one record per sub-group (expert,
+//                               first row, rows, tokens) and a grouped row
+//                               per slot
+//   2. moe_gateup_kernel        per (sub-group, 16 rows): gate and up rows
+//                               loaded once, applied to every token of the
+//                               sub-group, SwiGLU fused -> h[grouped row][j]
+//   3. moe_down_kernel          per (sub-group, 32 rows): down rows loaded
+//                               once, applied to h of every row of the
+//                               sub-group -> y[grouped row][d] (f32)
 //   4. moe_combine_kernel       out[t][d] = sum_r w_r y[row(t,r)][d] (rank
 //                               order) + gs_t * y[shared row t][d] -> bf16
-// A group's record carries what its blocks need first, so each block starts
-// its weight and activation loads after one dependent load.
+// A sub-group's record carries what its blocks need first, so each block
+// starts its weight and activation loads after one dependent load. The
+// shared expert's blocks (kSubTok tokens each) come first in launches 2 and
+// 3: at the end of the grid they ran alone for the last third of each launch.
 #include <cstdlib>
 
 #include "affine_dev.hpp"
@@ -80,11 +84,19 @@ hipError_t launch_route_topk(const void *logits, int logits_f32, int B, int E, i
 // Grouped order: the B*k routed (token, rank) slots sorted by expert (one
 // group per distinct expert), then the B shared-expert slots. h and y rows
 // are stored in grouped order, so a group's rows are contiguous.
-constexpr int kRecInts = 8;  // group record: expert, first grouped row, rows, tokens[0..3], 0
+constexpr int kRecInts = 8;  // sub-group record: expert, first grouped row, rows, tokens[0..3], 0
+// Each expert's tokens are cut into sub-groups of at most kSubTok, so that no
+// block of the gate/up and down launches carries many more tokens than the
+// others; the shared expert's sub-groups (all B tokens, in order) need no
+// record and go first in both launches.
+constexpr int kSubTok = 4;
+__host__ __device__ inline int max_subgroups(int B, int k, int E) {
+  const int nslots = B * k;
+  return (nslots < E ? nslots : E) + (nslots + kSubTok - 1) / kSubTok;
+}
 struct MoeWs {
-  int *n_groups;      // [1]  routed groups
-  int *rec;           // [G+1][kRecInts]; rec[G] is the shared expert's
-  int *tok;           // [B*k] token of each grouped routed row
+  int *n_groups;      // [1]  routed sub-groups
+  int *rec;           // [max_subgroups][kRecInts]
   int *gpos;          // [B*k] grouped row of slot t*k + r
   int32_t *topk_idx;  // [B*k]
   float *topk_w;      // [B*k]
@@ -100,7 +112,6 @@ static inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int E, int k) {
   MoeWs w{};
-  const size_t G = (size_t)(B * k < E ? B * k : E);
   const size_t slots = (size_t)B * k + B;
   const size_t hmax = (size_t)(inter > sinter ? inter : sinter);
   size_t off = 0;
@@ -111,8 +122,7 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
     return p;
   };
   w.n_groups = reinterpret_cast<int *>(take(sizeof(int)));
-  w.rec = reinterpret_cast<int *>(take(sizeof(int) * (G + 1) * kRecInts));
-  w.tok = reinterpret_cast<int *>(take(sizeof(int) * (size_t)B * k));
+  w.rec = reinterpret_cast<int *>(take(sizeof(int) * (size_t)max_subgroups(B, k, E) * kRecInts));
   w.gpos = reinterpret_cast<int *>(take(sizeof(int) * (size_t)B * k));
   w.topk_idx = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * (size_t)B * k));
   w.topk_w = reinterpret_cast<float *>(take(sizeof(float) * (size_t)B * k));
@@ -200,6 +210,7 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
   __shared__ int s_gid[kMaxE];
   __shared__ int s_fill[kMaxE];
   __shared__ int s_tok[kMaxB * kMaxK];
+  __shared__ int s_gex[kMaxB * kMaxK];
   __shared__ int s_wave_tot[kGroupThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = kGroupThreads / 64;
@@ -260,13 +271,14 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
   __syncthreads();
   for (int i = tid; i < nslots; i += kGroupThreads) atomicAdd(&s_cnt[s_idx[i]], 1);
   __syncthreads();
-  // exclusive scans over experts: entry start and group id (E <= 1024 = one per thread)
+  // exclusive scans over experts: first grouped row and first sub-group
+  // (E <= 1024 = one per thread)
   {
     const int e = tid;
     const int c = e < a.E ? s_cnt[e] : 0;
-    const int f = c > 0 ? 1 : 0;
-    // pack (count, flag) into one int: count < 2^20, flag sum < 2^11
-    int v = (c << 11) | f;
+    const int f = (c + kSubTok - 1) / kSubTok;
+    // pack (count, sub-groups) into one int: count sum <= 2048 < 2^15, sub-group sum < 2^16
+    int v = (c << 16) | f;
     int incl = v;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -279,12 +291,12 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
     for (int q = 0; q < wave; ++q) prefix += s_wave_tot[q];
     const int excl = prefix + incl - v;
     if (e < a.E) {
-      s_start[e] = excl >> 11;
-      s_gid[e] = excl & 2047;
+      s_start[e] = excl >> 16;
+      s_gid[e] = excl & 0xffff;
     }
     if (tid == kGroupThreads - 1) {
       const int tot = prefix + incl;
-      *w.n_groups = tot & 2047;
+      *w.n_groups = tot & 0xffff;
     }
   }
   // placement within a group in arrival order: every row's arithmetic is
@@ -295,26 +307,22 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
     const int e = s_idx[i];
     const int gp = s_start[e] + atomicAdd(&s_fill[e], 1);
     s_tok[gp] = i / a.k;
-    w.tok[gp] = i / a.k;
+    s_gex[gp] = e;
     w.gpos[i] = gp;
   }
   __syncthreads();
-  // one record per group (and the shared expert's at index G)
-  const int G = nslots < a.E ? nslots : a.E;
-  for (int e = tid; e < a.E; e += kGroupThreads) {
-    const int c = s_cnt[e];
-    if (c > 0) {
-      const int off = s_start[e];
-      int4 *r = reinterpret_cast<int4 *>(w.rec + (size_t)s_gid[e] * kRecInts);
-      r[0] = make_int4(e, off, c, s_tok[off]);
-      r[1] = make_int4(c > 1 ? s_tok[off + 1] : 0, c > 2 ? s_tok[off + 2] : 0,
-                       c > 3 ? s_tok[off + 3] : 0, 0);
+  // one record per sub-group: the kSubTok grouped rows from each multiple of
+  // kSubTok within an expert's rows
+  for (int gp = tid; gp < nslots; gp += kGroupThreads) {
+    const int e = s_gex[gp];
+    const int rel = gp - s_start[e];
+    if (rel % kSubTok == 0) {
+      const int c = min(s_cnt[e] - rel, kSubTok);
+      int4 *r = reinterpret_cast<int4 *>(w.rec + (size_t)(s_gid[e] + rel / kSubTok) * kRecInts);
+      r[0] = make_int4(e, gp, c, s_tok[gp]);
+      r[1] = make_int4(c > 1 ? s_tok[gp + 1] : 0, c > 2 ? s_tok[gp + 2] : 0,
+                       c > 3 ? s_tok[gp + 3] : 0, 0);
     }
-  }
-  if (tid == 0) {
-    int4 *r = reinterpret_cast<int4 *>(w.rec + (size_t)G * kRecInts);
-    r[0] = make_int4(0, nslots, a.B, 0);
-    r[1] = make_int4(1, 2, 3, 0);
   }
 }
 
@@ -333,16 +341,20 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
   const int C = a.D >> 5;
   UnpackConsts kc;
   kc.init();
-  const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
+  // the shared expert's sub-groups first, then the routed ones
+  const int nsh = a.sgate.m.w ? (a.B + kSubTok - 1) / kSubTok : 0;
   const int item = blockIdx.x;
-  const bool shared = item >= ipg * G;
-  const int g = shared ? G : item / ipg;
-  const int rb = shared ? item - ipg * G : item % ipg;
-  // one load round for the group: its record carries the first tokens
+  const bool shared = item < nsh * ipg_s;
+  const int g = shared ? item / ipg_s : (item - nsh * ipg_s) / ipg;
+  const int rb = shared ? item % ipg_s : (item - nsh * ipg_s) % ipg;
+  // one load round for a routed sub-group: its record carries its tokens
   const int ng = *w.n_groups;
-  const int4 rc0 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[0];
-  const int4 rc1 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[1];
-  if (shared ? (a.sgate.m.w == nullptr || rb >= ipg_s) : g >= ng) return;
+  const int4 rr0 = reinterpret_cast<const int4 *>(w.rec + (size_t)(shared ? 0 : g) * kRecInts)[0];
+  const int4 rr1 = reinterpret_cast<const int4 *>(w.rec + (size_t)(shared ? 0 : g) * kRecInts)[1];
+  if (!shared && g >= ng) return;
+  const int s0 = g * kSubTok;
+  const int4 rc0 = shared ? make_int4(0, a.B * a.k + s0, min(kSubTok, a.B - s0), s0) : rr0;
+  const int4 rc1 = shared ? make_int4(s0 + 1, s0 + 2, s0 + 3, 0) : rr1;
   const int ge = rc0.x;
   const int off = __builtin_amdgcn_readfirstlane(rc0.y);
   const int cnt = __builtin_amdgcn_readfirstlane(rc0.z);
@@ -423,12 +435,7 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
       for (int i = 0; i < CPL; ++i)
 #pragma unroll
         for (int q = 0; q < BITS; ++q) asm volatile("" : "+v"(wg[u][i][q]), "+v"(wu[u][i][q]));
-    if (i_t > 0) {
-      const int t = shared ? i_t
-                           : (i_t == 1 ? rc1.x
-                                       : i_t == 2 ? rc1.y : i_t == 3 ? rc1.z : w.tok[off + i_t]);
-      load_x(__builtin_amdgcn_readfirstlane(t));
-    }
+    if (i_t > 0) load_x(__builtin_amdgcn_readfirstlane(i_t == 1 ? rc1.x : i_t == 2 ? rc1.y : rc1.z));
     float pg[U], pu[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) pg[u] = pu[u] = 0.f;
@@ -468,14 +475,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   const int lane = threadIdx.x & 63;
   const int lb = threadIdx.x % LANES;
   const int rsub = threadIdx.x / LANES;
-  const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
+  // the shared expert's sub-groups first, then the routed ones
+  const int nsh = a.sdown.m.w ? (a.B + kSubTok - 1) / kSubTok : 0;
   const int item = blockIdx.x;
-  const bool shared = item >= G * ipg;
-  const int g = shared ? G : item / ipg;
-  const int rb = shared ? item - G * ipg : item % ipg;
+  const bool shared = item < nsh * ipg;
+  const int g = item / ipg - (shared ? 0 : nsh);
+  const int rb = item % ipg;
   const int ng = *w.n_groups;
-  const int4 rc0 = reinterpret_cast<const int4 *>(w.rec + (size_t)g * kRecInts)[0];
-  if (shared ? a.sdown.m.w == nullptr : g >= ng) return;
+  const int4 rr0 = reinterpret_cast<const int4 *>(w.rec + (size_t)(shared ? 0 : g) * kRecInts)[0];
+  if (!shared && g >= ng) return;
+  const int rows0 = a.B * a.k + g * kSubTok;
+  const int4 rc0 = shared ? make_int4(0, rows0, min(kSubTok, a.B - g * kSubTok), 0) : rr0;
   const int ge = rc0.x;
   const int off = __builtin_amdgcn_readfirstlane(rc0.y);
   const int cnt = __builtin_amdgcn_readfirstlane(rc0.z);
@@ -602,13 +612,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a, MoeWs w) {
 template <int BITS>
 static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
   const int Cd = a.D >> 5;
-  const int G = a.B * a.k < a.E ? a.B * a.k : a.E;
-  // gate/up: 16 rows per block, every possible group (blocks of groups that
-  // did not form leave at once)
+  const int msub = max_subgroups(a.B, a.k, a.E);
+  const int nsh = a.sgate.m.w ? (a.B + kSubTok - 1) / kSubTok : 0;
+  // gate/up: 16 rows per block, the shared expert's sub-groups and every
+  // possible routed sub-group (blocks of sub-groups that did not form leave
+  // at once)
   {
     const int ipg = (a.inter + 15) / 16;
     const int ipg_s = a.sgate.m.w ? (a.sinter + 15) / 16 : 0;
-    const int grid = G * ipg + ipg_s;
+    const int grid = nsh * ipg_s + msub * ipg;
     if (Cd <= 64)
       hipLaunchKernelGGL((moe_gateup_kernel<BITS, 1>), dim3(grid), dim3(256), 0, st, a, w, ipg, ipg_s);
     else if (Cd <= 128)
@@ -622,7 +634,7 @@ static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
     const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
     const int Ci = kmax >> 5;
     const int ipg = (a.D + kDownRows - 1) / kDownRows;
-    const int grid = (G + (a.sdown.m.w ? 1 : 0)) * ipg;
+    const int grid = (nsh + msub) * ipg;
     if (Ci <= 16) hipLaunchKernelGGL((moe_down_kernel<BITS, 16>), dim3(grid), dim3(256), 0, st, a, w, ipg);
     else if (Ci <= 32) hipLaunchKernelGGL((moe_down_kernel<BITS, 32>), dim3(grid), dim3(256), 0, st, a, w, ipg);
     else return -1;
