@@ -267,7 +267,9 @@ uint32_t logan_hip_moe_sync_errors(void);
  * path (4/5/6/8-bit codes with group sizes that are multiples of 64; each
  * expert's weights read once per 16 of its tokens); smaller batches and
  * other geometries take the per-token dot-product path in passes of up to
- * 64 tokens. Default 24, or LOGAN_HIP_MOE_MFMA_MIN_B from the environment.
+ * 64 tokens. b > 0 sets one threshold for every code width; b <= 0
+ * restores the defaults: 56 tokens for 4-bit codes, 24 for 5/6/8-bit
+ * (LOGAN_HIP_MOE_MFMA_MIN_B from the environment, when set, replaces them).
  * Both paths follow the same reference semantics (logan-qwen4/src/lib.rs
  * :8692-8711, :8759-8815); this control has no counterpart in the
  * reference (its batched path is host-side, lib.rs:9714-9721). */

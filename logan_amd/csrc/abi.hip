@@ -700,7 +700,7 @@ void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }
 
 uint32_t logan_hip_moe_sync_errors(void) { return lh::moe_fused_sync_errors(); }
 
-void logan_hip_set_moe_mfma_min_batch(int b) { lh::set_moe_mfma_min_batch(b < 1 ? 1 : b); }
+void logan_hip_set_moe_mfma_min_batch(int b) { lh::set_moe_mfma_min_batch(b); }
 
 const char *logan_hip_version(void) { return "logan-hip 0.1.0 (gfx950)"; }
 

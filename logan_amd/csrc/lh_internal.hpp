@@ -106,11 +106,16 @@ void set_moe_fused_enabled(int on);
 // applicable, -1 launch failure
 constexpr int kMaxBatch = 4096;         // tokens per moe_block call
 constexpr int kMaxBatchSlots = 65536;   // tokens * top_k
+// smallest batch on the MFMA path by code width (measured crossovers with the
+// per-token path, config-3 shapes: 4-bit between 48 and 64 tokens, 5/6-bit
+// below 24)
 constexpr int kMfmaMinBatchDefault = 24;
+constexpr int kMfmaMinBatch4Bit = 56;
 bool moe_mfma_supported(const MoeArgs &a);
 int launch_moe_mfma(const MoeArgs &a, hipStream_t st);
 size_t moe_mfma_workspace_bytes(int B, int D, int inter, int sinter, int E, int k);
-// smallest batch that takes the MFMA path (LOGAN_HIP_MOE_MFMA_MIN_B)
+// smallest batch that takes the MFMA path for every code width
+// (LOGAN_HIP_MOE_MFMA_MIN_B); b <= 0 restores the per-width defaults
 void set_moe_mfma_min_batch(int b);
 // 1 ok, 0 unsupported geometry (nothing launched), -1 launch failure
 int launch_moe_block(const MoeArgs &a, hipStream_t st);

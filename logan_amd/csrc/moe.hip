@@ -13,13 +13,13 @@
 // exp(l_r - l_0) / sum_{r<k} exp(l_j - l_0), which equals val_r / wsum.
 //
 // Launch structure (all on one stream):
-//   1. moe_route_group_kernel   one block: route every token, shared-expert
-//                               gate, x of every token as bf16 pairs, group
-//                               the (token, rank) slots by expert and cut
-//                               each expert's rows into sub-groups of at most
-//                               kSubTok: one record per sub-group (expert,
-//                               first row, rows, tokens) and a grouped row
-//                               per slot
+//   1. moe_route_tok_kernel     one block per token: top-k, shared-expert
+//                               gate, x as bf16 pairs
+//      moe_group_kernel         one block: group the (token, rank) slots by
+//                               expert and cut each expert's rows into
+//                               sub-groups of at most kSubTok: one record per
+//                               sub-group (expert, first row, rows, tokens)
+//                               and a grouped row per slot
 //   2. moe_gateup_kernel        per (sub-group, 16 rows): gate and up rows
 //                               loaded once, applied to every token of the
 //                               sub-group, SwiGLU fused -> h[grouped row][j]
@@ -145,17 +145,20 @@ size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k) {
   return m > mfma ? m : mfma;
 }
 
+// > 0: one threshold for every code width; 0: the per-width defaults;
+// -1: the environment not read yet
 static int g_mfma_min_b = -1;
 
-void set_moe_mfma_min_batch(int b) { g_mfma_min_b = b; }
+void set_moe_mfma_min_batch(int b) { g_mfma_min_b = b > 0 ? b : 0; }
 
-static int mfma_min_batch() {
+static int mfma_min_batch(int bits) {
   if (g_mfma_min_b < 0) {
     const char *v = getenv("LOGAN_HIP_MOE_MFMA_MIN_B");
-    g_mfma_min_b = v ? atoi(v) : kMfmaMinBatchDefault;
-    if (g_mfma_min_b < 1) g_mfma_min_b = 1;
+    const int e = v ? atoi(v) : 0;
+    g_mfma_min_b = e > 0 ? e : 0;
   }
-  return g_mfma_min_b;
+  if (g_mfma_min_b > 0) return g_mfma_min_b;
+  return bits == 4 ? kMfmaMinBatch4Bit : kMfmaMinBatchDefault;
 }
 
 static int g_fused_enabled = -1;
@@ -171,21 +174,22 @@ static bool fused_enabled() {
 }
 
 // ---------------------------------------------------------------------------
-// 1. route + shared gate + grouping (one block of 1024 threads, B <= 64)
+// 1. route + shared gate (one block per token), then grouping (one block)
 
-constexpr int kGroupThreads = 1024;
-
-// xp[t][c] = make_xchunk_bf16 of chunk c of token t (pairs, sum x, sum x')
+// x of token t as the gate/up kernels' operand: xp[t][c] = make_xchunk_bf16
+// of chunk c (pairs, sum x, sum x'), one chunk per lane and step
 template <int BITS>
-__device__ __forceinline__ void convert_x_pairs(const MoeArgs &a, const MoeWs &w, int tid, int nthr) {
+__device__ __forceinline__ void convert_x_token(const MoeArgs &a, const MoeWs &w, int t, int lane) {
   const int C = a.D >> 5;
-  for (int it = tid; it < a.B * C; it += nthr) {
-    const int t = it / C, c = it % C;
+  for (int c = lane; c < C; c += 64) {
     const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D + 32 * c);
+    uint4 xq[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xq[v] = src[v];
     uint32_t xb[32];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const uint4 q = src[v];
+      const uint4 q = xq[v];
       xb[8 * v + 0] = q.x & 0xffffu; xb[8 * v + 1] = q.x >> 16;
       xb[8 * v + 2] = q.y & 0xffffu; xb[8 * v + 3] = q.y >> 16;
       xb[8 * v + 4] = q.z & 0xffffu; xb[8 * v + 5] = q.z >> 16;
@@ -193,17 +197,75 @@ __device__ __forceinline__ void convert_x_pairs(const MoeArgs &a, const MoeWs &w
     }
     XChunk xc;
     make_xchunk_bf16<BITS>(xc, xb);
-    uint4 *dst = reinterpret_cast<uint4 *>(w.xp + (size_t)it * 16);
+    const size_t it = (size_t)t * C + c;
+    uint4 *dst = reinterpret_cast<uint4 *>(w.xp + it * 16);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
       dst[v] = make_uint4(xc.p[4 * v], xc.p[4 * v + 1], xc.p[4 * v + 2], xc.p[4 * v + 3]);
-    w.xps[(size_t)it * 2] = xc.xs;
-    w.xps[(size_t)it * 2 + 1] = xc.xsp;
+    w.xps[it * 2] = xc.xs;
+    w.xps[it * 2 + 1] = xc.xsp;
   }
 }
 
-template <int KPL, bool F32>
-__global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs a, MoeWs w) {
+// One block of two waves per token t = blockIdx.x: wave 0 selects the top-k
+// (route_dev.hpp: wave_topk_lanes), wave 1 computes the shared-expert gate
+// sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604) and writes x_t in
+// the operand form. The tokens' selections run on as many CUs as there are
+// tokens (one CU holding all of them spent 0.8 us of VALU per token).
+template <int KPL, bool F32, int BITS>
+__global__ __launch_bounds__(128) void moe_route_tok_kernel(MoeArgs a, MoeWs w) {
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 64) {
+    int id;
+    float wt;
+    wave_topk_lanes<KPL, F32>(a.logits, (size_t)t * a.E, a.E, a.k, id, wt);
+    if (lane < a.k) {
+      w.topk_idx[t * a.k + lane] = id;
+      w.topk_w[t * a.k + lane] = wt;
+      if (a.idx_out) a.idx_out[t * a.k + lane] = id;
+      if (a.w_out) a.w_out[t * a.k + lane] = wt;
+    }
+    return;
+  }
+  if (a.sgate.m.w) {
+    float g = 1.0f;
+    if (a.se_gate_vec) {
+      // 16-byte loads, all in flight (8 bf16 per lane per step)
+      const int n8 = a.D >> 3;
+      g = 0.f;
+      for (int c0 = 0; c0 < n8; c0 += 256) {
+        uint4 gq[4], xq[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int c = min(c0 + v * 64 + lane, n8 - 1);
+          gq[v] = reinterpret_cast<const uint4 *>(a.se_gate_vec)[c];
+          xq[v] = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D)[c];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          if (c0 + v * 64 + lane < n8) {
+            g = dot2(gq[v].x, xq[v].x, g);
+            g = dot2(gq[v].y, xq[v].y, g);
+            g = dot2(gq[v].z, xq[v].z, g);
+            g = dot2(gq[v].w, xq[v].w, g);
+          }
+        }
+      }
+      g = team_sum<64>(g);
+      g = 1.0f / (1.0f + __expf(-g));
+    }
+    if (lane == 0) w.gs[t] = g;
+  }
+  convert_x_token<BITS>(a, w, t, lane);
+}
+
+constexpr int kGroupThreads = 1024;
+
+// One block: group the (token, rank) slots by expert and cut each expert's
+// rows into sub-groups of at most kSubTok: one record per sub-group and a
+// grouped row per slot.
+__global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(MoeArgs a, MoeWs w) {
   __shared__ int s_idx[kMaxB * kMaxK];
   __shared__ int s_cnt[kMaxE];
   __shared__ int s_start[kMaxE];
@@ -213,61 +275,9 @@ __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(MoeArgs 
   __shared__ int s_gex[kMaxB * kMaxK];
   __shared__ int s_wave_tot[kGroupThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nwaves = kGroupThreads / 64;
   const int nslots = a.B * a.k;
-
+  for (int i = tid; i < nslots; i += kGroupThreads) s_idx[i] = w.topk_idx[i];
   for (int e = tid; e < a.E; e += kGroupThreads) s_cnt[e] = 0;
-
-  for (int t = wave; t < a.B; t += nwaves) {
-    int id;
-    float wt;
-    wave_topk_lanes<KPL, F32>(a.logits, (size_t)t * a.E, a.E, a.k, id, wt);
-    if (lane < a.k) {
-      s_idx[t * a.k + lane] = id;
-      w.topk_idx[t * a.k + lane] = id;
-      w.topk_w[t * a.k + lane] = wt;
-      if (a.idx_out) a.idx_out[t * a.k + lane] = id;
-      if (a.w_out) a.w_out[t * a.k + lane] = wt;
-    }
-    // shared-expert scalar gate: sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604)
-    if (a.sgate.m.w) {
-      float g = 0.f;
-      if (a.se_gate_vec) {
-        // 16-byte loads, all in flight (chunk c = 8 bf16 per lane per step)
-        const int n8 = a.D >> 3;
-        for (int c0 = 0; c0 < n8; c0 += 256) {
-          uint4 gq[4], xq[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int c = min(c0 + v * 64 + lane, n8 - 1);
-            gq[v] = reinterpret_cast<const uint4 *>(a.se_gate_vec)[c];
-            xq[v] = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D)[c];
-          }
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            if (c0 + v * 64 + lane < n8) {
-              g = dot2(gq[v].x, xq[v].x, g);
-              g = dot2(gq[v].y, xq[v].y, g);
-              g = dot2(gq[v].z, xq[v].z, g);
-              g = dot2(gq[v].w, xq[v].w, g);
-            }
-          }
-        }
-        g = team_sum<64>(g);
-        g = 1.0f / (1.0f + __expf(-g));
-      } else {
-        g = 1.0f;
-      }
-      if (lane == 0) w.gs[t] = g;
-    }
-  }
-  // x of every token as the gate/up kernels' operand (one chunk per thread)
-  switch (a.gate.m.bits) {
-    case 4: convert_x_pairs<4>(a, w, tid, kGroupThreads); break;
-    case 5: convert_x_pairs<5>(a, w, tid, kGroupThreads); break;
-    case 6: convert_x_pairs<6>(a, w, tid, kGroupThreads); break;
-    default: convert_x_pairs<8>(a, w, tid, kGroupThreads); break;
-  }
   __syncthreads();
   for (int i = tid; i < nslots; i += kGroupThreads) atomicAdd(&s_cnt[s_idx[i]], 1);
   __syncthreads();
@@ -462,16 +472,20 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
 // ---------------------------------------------------------------------------
 // 3. down projection of h for every slot of a group
 
-constexpr int kDownRows = 32;  // output rows per down block
+// output rows per down block: 64 for 4-bit codes with one chunk per lane
+// (16 KB of codes per block; 64 rows took 28.6 us against 33.5 us at 32 rows
+// and 49.1 us at 16 for config 3, B = 16), 32 otherwise (the 5/6/8-bit code
+// extraction of 64 rows needs over 200 registers)
+__host__ __device__ constexpr int down_rows(int bits, int lanes) { return bits == 4 && lanes == 16 ? 64 : 32; }
 
-// One block: kDownRows output rows d of one expert group's down projection (a row
+// One block: down_rows output rows d of one expert group's down projection (a row
 // per LANES lanes, PASSES rows per lane), applied to h of every slot of the
 // group with f32 FMAs: y = scale * sum code*h + bias * sum h.
 template <int BITS, int LANES>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int ipg) {
   constexpr int kHq = LANES / 8;     // float4 of one h row per thread (K <= 32 * LANES)
   constexpr int RPP = 256 / LANES;  // rows per pass of the block
-  constexpr int PASSES = kDownRows / RPP;
+  constexpr int PASSES = down_rows(BITS, LANES) / RPP;
   const int lane = threadIdx.x & 63;
   const int lb = threadIdx.x % LANES;
   const int rsub = threadIdx.x / LANES;
@@ -498,7 +512,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   const uint8_t *wb = dm.w + (size_t)e * dws;
   const uint16_t *scb = dm.sc + (size_t)e * dps;
   const uint16_t *bib = dm.bi + (size_t)e * dps;
-  const int d0 = rb * kDownRows;
+  const int d0 = rb * down_rows(BITS, LANES);
   const int cl = min(lb, Ck - 1);
   const int gi = cl / (dm.gs >> 5);
 
@@ -629,15 +643,16 @@ static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
       return 0;
     if (hipGetLastError() != hipSuccess) return -1;
   }
-  // down: kDownRows rows per block
+  // down: down_rows(BITS, LANES) rows per block
   {
     const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
     const int Ci = kmax >> 5;
-    const int ipg = (a.D + kDownRows - 1) / kDownRows;
+    if (Ci > 32) return -1;
+    const int rows = Ci <= 16 ? down_rows(BITS, 16) : down_rows(BITS, 32);
+    const int ipg = (a.D + rows - 1) / rows;
     const int grid = (nsh + msub) * ipg;
     if (Ci <= 16) hipLaunchKernelGGL((moe_down_kernel<BITS, 16>), dim3(grid), dim3(256), 0, st, a, w, ipg);
-    else if (Ci <= 32) hipLaunchKernelGGL((moe_down_kernel<BITS, 32>), dim3(grid), dim3(256), 0, st, a, w, ipg);
-    else return -1;
+    else hipLaunchKernelGGL((moe_down_kernel<BITS, 32>), dim3(grid), dim3(256), 0, st, a, w, ipg);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   {
@@ -659,6 +674,28 @@ static bool bank_ok(const DevBank &b, int O, int I, int bits, int gs) {
   if (m.row_bytes != (long long)m.I * m.bits / 8) return false;
   if (b.w_stride % 16 != 0) return false;
   return true;
+}
+
+template <int BITS>
+static void launch_route_tok_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
+  const dim3 g(a.B), b(128);
+  if (a.logits_f32) {
+    if (a.E <= 512) hipLaunchKernelGGL((moe_route_tok_kernel<8, true, BITS>), g, b, 0, st, a, w);
+    else hipLaunchKernelGGL((moe_route_tok_kernel<16, true, BITS>), g, b, 0, st, a, w);
+  } else {
+    if (a.E <= 512) hipLaunchKernelGGL((moe_route_tok_kernel<8, false, BITS>), g, b, 0, st, a, w);
+    else hipLaunchKernelGGL((moe_route_tok_kernel<16, false, BITS>), g, b, 0, st, a, w);
+  }
+}
+
+static int launch_route_tok(const MoeArgs &a, const MoeWs &w, int bits, hipStream_t st) {
+  switch (bits) {
+    case 4: launch_route_tok_bits<4>(a, w, st); break;
+    case 5: launch_route_tok_bits<5>(a, w, st); break;
+    case 6: launch_route_tok_bits<6>(a, w, st); break;
+    default: launch_route_tok_bits<8>(a, w, st); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_moe_block(const MoeArgs &a, hipStream_t st) {
@@ -688,7 +725,7 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
     const int rc = launch_moe_fused_b1(aa, st);
     if (rc != 0) return rc;
   }
-  if (a.B >= mfma_min_batch()) {
+  if (a.B >= mfma_min_batch(bits)) {
     const int rc = launch_moe_mfma(aa, st);
     if (rc != 0) return rc;
   }
@@ -703,17 +740,8 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
     if (a.idx_out) c.idx_out = a.idx_out + (size_t)b0 * a.k;
     if (a.w_out) c.w_out = a.w_out + (size_t)b0 * a.k;
     MoeWs w = moe_ws_layout(a.ws, c.B, a.D, a.inter, sinter, a.E, a.k);
-    if (a.logits_f32) {
-      if (a.E <= 512)
-        hipLaunchKernelGGL((moe_route_group_kernel<8, true>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
-      else
-        hipLaunchKernelGGL((moe_route_group_kernel<16, true>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
-    } else {
-      if (a.E <= 512)
-        hipLaunchKernelGGL((moe_route_group_kernel<8, false>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
-      else
-        hipLaunchKernelGGL((moe_route_group_kernel<16, false>), dim3(1), dim3(kGroupThreads), 0, st, c, w);
-    }
+    if (launch_route_tok(c, w, bits, st) != 0) return -1;
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, st, c, w);
     if (hipGetLastError() != hipSuccess) return -1;
     int rc = 0;
     switch (bits) {

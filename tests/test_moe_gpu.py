@@ -344,7 +344,7 @@ def mfma_min_b(request):
     b = getattr(request, "param", 1)
     _lib.lib().logan_hip_set_moe_mfma_min_batch(b)
     yield b
-    _lib.lib().logan_hip_set_moe_mfma_min_batch(24)
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(0)
 
 
 def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
@@ -434,7 +434,7 @@ def test_moe_prefill_chunk_sampled(gpu):
     try:
         out_d, idx_d, _ = run_layer(torch, layer, xb, lb, torch.float32)
     finally:
-        _lib.lib().logan_hip_set_moe_mfma_min_batch(24)
+        _lib.lib().logan_hip_set_moe_mfma_min_batch(0)
     np.testing.assert_array_equal(idx, idx_d)
     out_d = out_d.cpu().numpy()
     for t in range(B):
