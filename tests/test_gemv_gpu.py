@@ -120,6 +120,46 @@ def test_gemv_is_deterministic(gpu):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("M,bits", [(4, 8), (17, 4)])
+def test_gemv_splitk_repeats_and_graph_replays(gpu, M, bits):
+    """The K-split product's last-arriving block sums the partials and sets
+    its row block's counter back to zero: back-to-back calls and replays of a
+    captured graph (eager calls in between) all give the same bits, and the
+    oracle's values."""
+    import torch
+    from logan_amd.device import affine_gemv
+
+    O, I, gs = 4096 + 37, 4096, 64
+    print(f"splitk repeats O={O} I={I} bits={bits} M={M}", flush=True)
+    rng = np.random.default_rng(11 + M)
+    w, sc, bi = make_affine(rng, O, I, bits, gs)
+    xb = make_x(rng, M, I)
+    m = dev_matrix(torch, w, sc, bi, O, I, bits, gs)
+    xd = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    ref0 = affine_gemv(m, xd, out_dtype=torch.float32)
+    for _ in range(4):
+        assert torch.equal(affine_gemv(m, xd, out_dtype=torch.float32), ref0)
+    xf = bf16_to_f32(xb)
+    y = ref0.cpu().numpy()
+    for r in range(M):
+        assert normwise_rel(y[r], oracle.affine_gemv(xf[r], w, sc, bi, O, I, bits, gs)) <= 2e-5
+    out = torch.empty_like(ref0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        out.copy_(affine_gemv(m, xd, out_dtype=torch.float32))
+    for _ in range(3):
+        out.zero_()
+        with torch.cuda.stream(stream):
+            gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref0)
+        assert torch.equal(affine_gemv(m, xd, out_dtype=torch.float32), ref0)
+        torch.cuda.synchronize()
+    del gr
+
+
 def test_gemv_linearity(gpu):
     """W(x1) + W(x2) == W(x1 + x2) up to rounding (size-independent check at
     the config-1 shape)."""
