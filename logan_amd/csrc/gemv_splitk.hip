@@ -8,22 +8,16 @@
 // in LDS (in the operand order of the code width) and feed all 8 waves, so
 // the activation traffic is 1/8 of a wave-private load; every wave issues
 // its x staging loads, its scale/bias words and then all eight of its 64-code
-// steps' weight loads before its first wait. Each block
-// writes its partial sums for its (token, row) pairs into a scratch slot and
-// counts itself in on its row block's arrival counter; the block that
-// arrives last adds the row block's K partials in K order (deterministic,
-// whichever block is last) into y and sets the counter back to zero. (A
-// second launch for the sums cost about 4.5 us per product.) Partials and
-// counters are written and read only with device-scope (sc1) relaxed atomics,
-// which are coherent across the XCDs' L2s; a block's partial stores have
-// completed (s_waitcnt vmcnt(0)) before it counts itself in. An agent-scope
-// release/acquire fence would instead write back / invalidate the whole L2
-// per block (802 us against 91 us for a config-2 layer at M = 4).
+// steps' weight loads before its first wait. Each block writes its partial
+// sums for its (token, row) pairs into a scratch slot, and a second kernel
+// adds the K partials in order (deterministic) into y. (The last-arriving
+// block of a row block adding them instead, behind device-scope atomics,
+// measured slower: 87.9 against 84.4 us for a config-2 layer at M = 8, since
+// one block then reads every partial of its rows in series.)
 //
-// Scratch: kSkSlots module-scope slots of kSkSlotFloats floats and
-// kSkMaxRowBlocks counters; the host picks slots round-robin, so launches
-// that overlap on one device do not share a slot unless more than kSkSlots
-// of them are in flight at once.
+// Scratch: kSkSlots module-scope slots of kSkSlotFloats floats; the host
+// picks slots round-robin, so launches that overlap on one device do not
+// share a slot unless more than kSkSlots of them are in flight at once.
 #include <atomic>
 
 #include "lh_internal.hpp"
@@ -36,13 +30,8 @@ constexpr int kSkSteps = kSkKc / 64;
 constexpr int kSkRows = 128;  // rows per block
 constexpr int kSkSlots = 4;
 constexpr size_t kSkSlotFloats = size_t(1) << 21;  // 8 MB per slot
-constexpr int kSkMaxRowBlocks = 8192;              // N <= 1,048,576
-// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt [3:0] and
-// [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15)
-constexpr int kWaitVm0 = 0x0F70;
 
 static __device__ __align__(256) float g_sk_part[kSkSlots * kSkSlotFloats];
-static __device__ unsigned g_sk_ctr[kSkSlots][kSkMaxRowBlocks];  // zero at rest
 
 struct SplitParams {
   const uint8_t *w;
@@ -51,8 +40,6 @@ struct SplitParams {
   const uint16_t *x;
   long long row_bytes;
   int N, K, ng, gsteps, x_stride, M, slot;
-  void *y;
-  int y_stride, y_bf16;
 };
 
 template <int BITS, int MT, bool FP16, bool AUX8>
@@ -148,55 +135,37 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
       S::fold(acc[t], d, xs, s, b);
     }
   }
-  const float *part0 = g_sk_part + (size_t)p.slot * kSkSlotFloats;
-  const int MN = p.M * p.N;  // <= kSkSlotFloats / KS
-  if (n < p.N) {
-    float *part = const_cast<float *>(part0) + (size_t)ks * MN;
+  if (n >= p.N) return;
+  float *part = g_sk_part + (size_t)p.slot * kSkSlotFloats + (size_t)ks * p.M * p.N;
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 16 * t + 4 * g + i;
-        if (m < p.M)
-          __hip_atomic_store(&part[(size_t)m * p.N + n], acc[t][i], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      }
-  }
-  // arrival: every thread's partial stores complete before thread 0 counts
-  // the block in
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned old = __hip_atomic_fetch_add(&g_sk_ctr[p.slot][blockIdx.x], 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    s_last = old == gridDim.y - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const int KS = gridDim.y;
-  const int n0 = blockIdx.x * kSkRows;
-  for (int i = tid; i < p.M * kSkRows; i += 512) {
-    const int m = i / kSkRows, nn = n0 + i % kSkRows;
-    if (nn >= p.N) continue;
-    const size_t o = (size_t)m * p.N + nn;
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * t + 4 * g + i;
+      if (m < p.M) part[(size_t)m * p.N + n] = acc[t][i];
+    }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, int M, int N, void *y,
+                                                            int y_stride, int y_bf16) {
+  const float *part = g_sk_part + (size_t)slot * kSkSlotFloats;
+  const int MN = M * N;  // <= kSkSlotFloats
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < MN; i += gridDim.x * 256) {
     // eight partials in flight at a time, added in K order
-    float sum = 0.f;
+    float s = 0.f;
     for (int k0 = 0; k0 < KS; k0 += 8) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = __hip_atomic_load(&part0[(size_t)min(k0 + j, KS - 1) * MN + o], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+      for (int j = 0; j < 8; ++j) v[j] = part[min(k0 + j, KS - 1) * MN + i];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sum += k0 + j < KS ? v[j] : 0.f;
+      for (int j = 0; j < 8; ++j) s += k0 + j < KS ? v[j] : 0.f;
     }
-    if (p.y_bf16)
-      reinterpret_cast<uint16_t *>(p.y)[(size_t)m * p.y_stride + nn] = (uint16_t)f32_to_bf16_rne(sum);
+    const int m = i / N, n = i - m * N;
+    if (y_bf16)
+      reinterpret_cast<uint16_t *>(y)[(size_t)m * y_stride + n] = (uint16_t)f32_to_bf16_rne(s);
     else
-      reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + nn] = sum;
+      reinterpret_cast<float *>(y)[(size_t)m * y_stride + n] = s;
   }
-  if (tid == 0) __hip_atomic_store(&g_sk_ctr[p.slot][blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 bool affine_splitk_supported(const DevMat &m, int M) {
@@ -207,7 +176,6 @@ bool affine_splitk_supported(const DevMat &m, int M) {
   const uintptr_t need = m.bits == 4 ? 7 : m.bits == 8 ? 15 : 3;
   if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
   const size_t KS = (size_t)m.I / kSkKc;
-  if ((m.O + kSkRows - 1) / kSkRows > kSkMaxRowBlocks) return false;
   return KS * (size_t)M * (size_t)m.O <= kSkSlotFloats;
 }
 
@@ -248,9 +216,6 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
   p.x_stride = x_stride;
   p.M = M;
   p.slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
-  p.y = y;
-  p.y_stride = y_stride;
-  p.y_bf16 = y_bf16;
   // 16-byte runs of eight u16 scale/bias words per 512 codes
   const bool aux8 = m.gs == 64 && (m.ng % 8) == 0 &&
                     ((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 15) == 0;
@@ -260,6 +225,13 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
     case 6: splitk_launch_bits<6>(p, m.fp16, aux8, st); break;
     default: splitk_launch_bits<8>(p, m.fp16, aux8, st); break;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t MN = (size_t)M * m.O;
+  size_t blocks = (MN + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.slot, m.I / kSkKc, M,
+                     m.O, y, y_stride, y_bf16);
   return hipGetLastError();
 }
 

@@ -117,6 +117,14 @@ __device__ __forceinline__ void lds_dma16(const void *src, uint16_t *lds_wave) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave, 16, 0, 0);
 }
 __device__ __forceinline__ void lds_dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait for the copies while the N vector-memory instructions issued after the
+// last of them may still be in flight (loads complete in issue order). N must
+// not exceed the number actually issued after the copies.
+template <int N>
+__device__ __forceinline__ void lds_dma_wait_behind() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 template <int BITS>
 struct MfmaStep {

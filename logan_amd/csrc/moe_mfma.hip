@@ -391,8 +391,9 @@ __global__ __launch_bounds__(WAVES * 64, MOE_GU_MINW) void moe_gateup_mfma_kerne
 }
 
 // ---------------------------------------------------------------------------
-// 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512: every
-//    weight and scale/bias load of the wave is issued before h is staged
+// 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512: h copied
+//    into LDS first, then every scale/bias and weight load of the wave, and
+//    each step waits only for its own weights
 
 template <int BITS, bool FP16>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
@@ -420,18 +421,12 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
   const bool pair_aux = __builtin_amdgcn_readfirstlane(gsteps == 1 && (dbk.m.ng & 1) == 0);
   SkRaw<BITS> wr[2][NS];
   uint32_t sr[2][NS], br[2][NS];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int d = min(rb * 128 + wave * 32 + 16 * r + r16, a.D - 1);
-    const uint8_t *wrow = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
-#pragma unroll
-    for (int u = 0; u < NS; ++u) S::load_raw(wr[r][u], wrow, min(u, steps - 1) * 64 + 16 * g);
-  }
   {
-    // stage h (hi, lo) of the tile's rows straight into LDS, in flight with
-    // the weight loads (physical granule P of row m holds logical granule
-    // P ^ (m & 15)); rows past the tile repeat its last row, which no operand
-    // of a stored output reads
+    // stage h (hi, lo) of the tile's rows straight into LDS, first: loads
+    // complete in issue order, so the steps' weights (issued last) may still
+    // be in flight when the copies are waited for (physical granule P of row
+    // m holds logical granule P ^ (m & 15)); rows past the tile repeat its
+    // last row, which no operand of a stored output reads
     constexpr int NQ = kMTok * kMDownK / 8 / 256;
     const int gpr = K >> 3;  // >= 16
     auto dma = [&](int base) {
@@ -474,7 +469,16 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
       }
     }
   }
-  lds_dma_wait();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int d = min(rb * 128 + wave * 32 + 16 * r + r16, a.D - 1);
+    const uint8_t *wrow = dbk.m.w + eo * dbk.w_stride + (size_t)d * dbk.m.row_bytes;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) S::load_raw(wr[r][u], wrow, min(u, steps - 1) * 64 + 16 * g);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // at least 2 * NS weight loads follow the copies
+  lds_dma_wait_behind<2 * NS>();
   __syncthreads();
   UnpackConsts kc;
   kc.init();
