@@ -387,26 +387,8 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
 
   uint32_t wg[U][CPL][BITS], wu[U][CPL][BITS];
   uint32_t rsg[U][CPL], rbg[U][CPL], rsu[U][CPL], rbu[U][CPL];
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-      load_chunk<BITS>(wg[u][i], gwb + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
-      load_chunk<BITS>(wu[u][i], uwb + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
-    }
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-      const size_t p = (size_t)j * gm.ng + (c >> gshift);
-      rsg[u][i] = gsc[p];
-      rbg[u][i] = gbi[p];
-      rsu[u][i] = usc[p];
-      rbu[u][i] = ubi[p];
-    }
-  // token 0's x pairs ride with the weights
+  // loads in the order they are needed (they complete in issue order): token
+  // 0's x pairs, the scale/bias words, then the rows' codes
   uint32_t xpn[CPL][16];
   float2 xsn[CPL];
   auto load_x = [&](int t) {
@@ -422,6 +404,25 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
     }
   };
   load_x(__builtin_amdgcn_readfirstlane(rc0.w));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+      const size_t p = (size_t)j * gm.ng + (c >> gshift);
+      rsg[u][i] = gsc[p];
+      rbg[u][i] = gbi[p];
+      rsu[u][i] = usc[p];
+      rbu[u][i] = ubi[p];
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+      load_chunk<BITS>(wg[u][i], gwb + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+      load_chunk<BITS>(wu[u][i], uwb + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
+    }
   __builtin_amdgcn_sched_barrier(0);
   // the packed rows stay in registers; each token unpacks them again (groups
   // hold one or two tokens in the common case)
@@ -438,13 +439,16 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
     }
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   for (int i_t = 0; i_t < cnt; ++i_t) {
-    // keep the unpack inside the loop (not hoisted into 128 live registers)
+    // keep the unpack inside the loop (not hoisted into 128 live registers);
+    // not before the first token, whose rows start as their own loads land
+    if (i_t > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < CPL; ++i)
+        for (int i = 0; i < CPL; ++i)
 #pragma unroll
-        for (int q = 0; q < BITS; ++q) asm volatile("" : "+v"(wg[u][i][q]), "+v"(wu[u][i][q]));
+          for (int q = 0; q < BITS; ++q) asm volatile("" : "+v"(wg[u][i][q]), "+v"(wu[u][i][q]));
+    }
     if (i_t > 0) load_x(__builtin_amdgcn_readfirstlane(i_t == 1 ? rc1.x : i_t == 2 ? rc1.y : rc1.z));
     float pg[U], pu[U];
 #pragma unroll
@@ -518,20 +522,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
 
   uint32_t wv[PASSES][BITS];
   uint32_t rs[PASSES], rbi[PASSES];
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int d = min(d0 + p * RPP + rsub, a.D - 1);
-    load_chunk<BITS>(wv[p], wb + (size_t)d * dm.row_bytes + (size_t)cl * (4 * BITS));
-  }
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int d = min(d0 + p * RPP + rsub, a.D - 1);
-    rs[p] = scb[(size_t)d * dm.ng + gi];
-    rbi[p] = bib[(size_t)d * dm.ng + gi];
-  }
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
-  // the group's first h row (K floats, 2 per thread for K <= 512) rides with
-  // the weights
+  // loads in the order they are needed (they complete in issue order): the
+  // sub-group's first h row (K floats, 2 per thread for K <= 512), the
+  // scale/bias words, then the rows' codes
   auto load_h = [&](int row, float4 (&hq)[kHq]) {
 #pragma unroll
     for (int v = 0; v < kHq; ++v) {
@@ -542,6 +536,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   };
   float4 hq[kHq];
   load_h(off, hq);
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int d = min(d0 + p * RPP + rsub, a.D - 1);
+    rs[p] = scb[(size_t)d * dm.ng + gi];
+    rbi[p] = bib[(size_t)d * dm.ng + gi];
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int d = min(d0 + p * RPP + rsub, a.D - 1);
+    load_chunk<BITS>(wv[p], wb + (size_t)d * dm.row_bytes + (size_t)cl * (4 * BITS));
+  }
   __builtin_amdgcn_sched_barrier(0);
   float sc[PASSES], bi[PASSES];
 #pragma unroll

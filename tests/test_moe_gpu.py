@@ -153,9 +153,9 @@ def fused_mode(request):
 
 
 @pytest.mark.parametrize("fused_mode", [1, 0], indirect=True, ids=["fused", "multi"])
-@pytest.mark.parametrize("bits,B,zipf", [(4, 1, False), (4, 16, False), (5, 1, True),
-                                         (6, 1, True), (5, 32, True), (6, 32, True),
-                                         (8, 4, False), (8, 1, False)])
+@pytest.mark.parametrize("bits,B,zipf", [(4, 1, False), (4, 16, False), (4, 40, True),
+                                         (5, 1, True), (6, 1, True), (5, 32, True),
+                                         (6, 32, True), (8, 4, False), (8, 1, False)])
 def test_moe_block_matches_oracle(gpu, fused_mode, bits, B, zipf):
     """Configs 3 and 4: E=512, top-10, D=2048, inter=512, g64, shared expert."""
     import torch
