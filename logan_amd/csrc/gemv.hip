@@ -46,10 +46,11 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   __shared__ float s_part[SPLIT > 1 ? TEAMS * U * MT : 1];
 
   // Loads are branch-free (row and chunk clamped into the matrix, x rows
-  // clamped to M) and issued x first, then every weight chunk, then the raw
-  // scale/bias words, so they are all in flight together; the values of
-  // dead lanes are masked where they are used. In-order vmcnt lets the x
-  // conversion wait for the x loads alone.
+  // clamped to M) and issued in the order they are needed: x, the raw
+  // scale/bias words, then every weight chunk, all in flight together; the
+  // values of dead lanes are masked where they are used. Loads complete in
+  // issue order (vmcnt), so the x conversion and the scale/bias conversion
+  // wait for their own loads alone and row u's products for its chunks.
   int gidx[CPL];
   bool cval[CPL];
   int cc[CPL];
@@ -82,18 +83,18 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
     for (int u = 0; u < U; ++u) {
       const int row = min(r0 + u, a.O - 1);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j)
-        load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = min(r0 + u, a.O - 1);
-#pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const size_t pi = (size_t)row * a.ng + gidx[j];
         scr[u][j] = a.sc[pi];
         bir[u][j] = a.bi[pi];
       }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = min(r0 + u, a.O - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
     }
     // keep every load above issued before any of their consumers
     __builtin_amdgcn_sched_barrier(0);
