@@ -291,17 +291,10 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     const int gsh = __builtin_ctz(gm.gs >> 5);  // group sizes are 32 * 2^n
 
     // branch-free loads (clamped row / chunk; dead lanes get zero scale and
-    // bias where they are used)
+    // bias where they are used), the scale/bias words before the codes: loads
+    // complete in issue order, so row u's products wait only for its chunks
     uint32_t wg[UA][CPLA][BITS], wu[UA][CPLA][BITS];
     uint32_t rsg[UA][CPLA], rbg[UA][CPLA], rsu[UA][CPLA], rbu[UA][CPLA];
-#pragma unroll
-    for (int u = 0; u < UA; ++u)
-#pragma unroll
-      for (int i = 0; i < CPLA; ++i) {
-        const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-        load_chunk<BITS>(wg[u][i], gw + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
-        load_chunk<BITS>(wu[u][i], uw + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
-      }
 #pragma unroll
     for (int u = 0; u < UA; ++u)
 #pragma unroll
@@ -312,6 +305,14 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
         rbg[u][i] = gbi[p];
         rsu[u][i] = usc[p];
         rbu[u][i] = ubi[p];
+      }
+#pragma unroll
+    for (int u = 0; u < UA; ++u)
+#pragma unroll
+      for (int i = 0; i < CPLA; ++i) {
+        const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
+        load_chunk<BITS>(wg[u][i], gw + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS>(wu[u][i], uw + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
       }
     const uint32_t tag = launch_tag(lid);
     // keep every load above issued before any of their consumers
