@@ -297,8 +297,9 @@ def bench_config2(torch, device, synth, args):
             for L in layers:
                 device.affine_gemv(L["qkv"], x, out=qkv)
                 device.affine_gemv(L["o"], att, out=o)
-                device.affine_gemv(L["gate"], o, out=gt)
-                device.affine_gemv(L["up"], o, out=up)
+                # gate+up: the config's 4096 -> 2 x 14336 projection, one
+                # product of the two matrices that share x
+                device.affine_gemv_multi([L["gate"], L["up"]], o, outs=[gt, up])
                 device.silu_mul(gt, up)
                 device.affine_gemv(L["down"], gt, out=y)
 

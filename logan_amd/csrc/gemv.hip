@@ -369,8 +369,9 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
 }
 
 // Matrices sharing x (same I, bits, group size, aux type): one launch per
-// token pair through the dot2 kernel; three or more tokens run the MFMA path
-// matrix by matrix.
+// token pair through the dot2 kernel; 3..32 tokens one K-split launch and one
+// reduce for all of them where the K-split form applies, otherwise the MFMA
+// path matrix by matrix.
 hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
                                   int x_stride, int M, int y_bf16, hipStream_t st) {
   if (n <= 0 || n > kMultiMax || M <= 0) return hipErrorInvalidValue;
@@ -380,6 +381,9 @@ hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, cons
       return hipErrorInvalidValue;
   }
   if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  // 3..32 tokens: one K-split launch and one reduce for all the products
+  if (M >= 3 && M <= 32 && n > 1 && affine_splitk_multi_supported(ms, n, M))
+    return launch_affine_splitk_multi(ms, n, x, x_stride, M, ys, y_bf16, st);
   if (M >= 3 && affine_skinny_supported(ms[0])) {
     for (int i = 0; i < n; ++i) {
       hipError_t e = launch_gemv_bf16(ms[i], x, x_stride, M, ys[i], ms[i].O, y_bf16, st);

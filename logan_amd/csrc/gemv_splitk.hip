@@ -40,10 +40,28 @@ struct SplitParams {
   const uint16_t *x;
   long long row_bytes;
   int N, K, ng, gsteps, x_stride, M, slot;
+  size_t part_off;  // this product's partials within the slot
+};
+
+// Products that share x (same K, code width, group size and sidecar type),
+// one grid: block b belongs to product i for start[i] <= b < start[i + 1].
+constexpr int kSkMultiMax = 8;
+struct SplitMulti {
+  SplitParams m[kSkMultiMax];
+  int start[kSkMultiMax + 1];
+  int n;
+};
+struct ReduceMulti {
+  void *y[kSkMultiMax];
+  size_t part_off[kSkMultiMax];
+  int N[kSkMultiMax];
+  int y_stride[kSkMultiMax];
+  int start[kSkMultiMax + 1];  // prefix sums of M * N
+  int n, KS, M, slot, y_bf16;
 };
 
 template <int BITS, int MT, bool FP16, bool AUX8>
-__global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
+__device__ __forceinline__ void splitk_block(const SplitParams &p, int rb) {
   __shared__ __align__(16) uint16_t sx[16 * MT * kSkKc];
   using S = MfmaStep<BITS>;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -51,7 +69,7 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
   const int r16 = lane & 15, g = lane >> 4;
   const int ks = blockIdx.y;
   const int k0 = ks * kSkKc;
-  const int n = blockIdx.x * kSkRows + wave * 16 + r16;
+  const int n = rb * kSkRows + wave * 16 + r16;
   const int row = min(n, p.N - 1);
   const uint8_t *wrow = p.w + (size_t)row * p.row_bytes;
   const uint16_t *srow = p.sc + (size_t)row * p.ng;
@@ -136,7 +154,7 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
     }
   }
   if (n >= p.N) return;
-  float *part = g_sk_part + (size_t)p.slot * kSkSlotFloats + (size_t)ks * p.M * p.N;
+  float *part = g_sk_part + (size_t)p.slot * kSkSlotFloats + p.part_off + (size_t)ks * p.M * p.N;
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -144,6 +162,18 @@ __global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
       const int m = 16 * t + 4 * g + i;
       if (m < p.M) part[(size_t)m * p.N + n] = acc[t][i];
     }
+}
+
+template <int BITS, int MT, bool FP16, bool AUX8>
+__global__ __launch_bounds__(512) void skinny_splitk_kernel(SplitParams p) {
+  splitk_block<BITS, MT, FP16, AUX8>(p, blockIdx.x);
+}
+
+template <int BITS, int MT, bool FP16, bool AUX8>
+__global__ __launch_bounds__(512) void skinny_splitk_multi_kernel(SplitMulti mp) {
+  int i = 0;
+  while (i + 1 < mp.n && (int)blockIdx.x >= mp.start[i + 1]) ++i;
+  splitk_block<BITS, MT, FP16, AUX8>(mp.m[i], blockIdx.x - mp.start[i]);
 }
 
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, int M, int N, void *y,
@@ -165,6 +195,33 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, in
       reinterpret_cast<uint16_t *>(y)[(size_t)m * y_stride + n] = (uint16_t)f32_to_bf16_rne(s);
     else
       reinterpret_cast<float *>(y)[(size_t)m * y_stride + n] = s;
+  }
+}
+
+// The reduce of several products in one grid (each element added in K order,
+// as in splitk_reduce_kernel).
+__global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r) {
+  const float *part = g_sk_part + (size_t)r.slot * kSkSlotFloats;
+  const int total = r.start[r.n];
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    int j = 0;
+    while (j + 1 < r.n && i >= r.start[j + 1]) ++j;
+    const int li = i - r.start[j];
+    const int MN = r.M * r.N[j];
+    const float *pj = part + r.part_off[j];
+    float s = 0.f;
+    for (int k0 = 0; k0 < r.KS; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = pj[(size_t)min(k0 + q, r.KS - 1) * MN + li];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s += k0 + q < r.KS ? v[q] : 0.f;
+    }
+    const int m = li / r.N[j], nn = li - m * r.N[j];
+    if (r.y_bf16)
+      reinterpret_cast<uint16_t *>(r.y[j])[(size_t)m * r.y_stride[j] + nn] = (uint16_t)f32_to_bf16_rne(s);
+    else
+      reinterpret_cast<float *>(r.y[j])[(size_t)m * r.y_stride[j] + nn] = s;
   }
 }
 
@@ -216,6 +273,7 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
   p.x_stride = x_stride;
   p.M = M;
   p.slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
+  p.part_off = 0;
   // 16-byte runs of eight u16 scale/bias words per 512 codes
   const bool aux8 = m.gs == 64 && (m.ng % 8) == 0 &&
                     ((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 15) == 0;
@@ -232,6 +290,95 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.slot, m.I / kSkKc, M,
                      m.O, y, y_stride, y_bf16);
+  return hipGetLastError();
+}
+
+template <int BITS, int MT>
+static void splitk_multi_launch_t(const SplitMulti &mp, int KS, bool fp16, bool aux8, hipStream_t st) {
+  const dim3 grid(mp.start[mp.n], KS);
+  if (fp16) {
+    if (aux8) hipLaunchKernelGGL((skinny_splitk_multi_kernel<BITS, MT, true, true>), grid, dim3(512), 0, st, mp);
+    else hipLaunchKernelGGL((skinny_splitk_multi_kernel<BITS, MT, true, false>), grid, dim3(512), 0, st, mp);
+  } else {
+    if (aux8) hipLaunchKernelGGL((skinny_splitk_multi_kernel<BITS, MT, false, true>), grid, dim3(512), 0, st, mp);
+    else hipLaunchKernelGGL((skinny_splitk_multi_kernel<BITS, MT, false, false>), grid, dim3(512), 0, st, mp);
+  }
+}
+
+template <int BITS>
+static void splitk_multi_launch_bits(const SplitMulti &mp, int KS, int M, bool fp16, bool aux8,
+                                     hipStream_t st) {
+  if (M <= 16) splitk_multi_launch_t<BITS, 1>(mp, KS, fp16, aux8, st);
+  else splitk_multi_launch_t<BITS, 2>(mp, KS, fp16, aux8, st);
+}
+
+bool affine_splitk_multi_supported(const DevMat *ms, int n, int M) {
+  if (n < 1 || n > kSkMultiMax) return false;
+  size_t floats = 0;
+  for (int i = 0; i < n; ++i) {
+    const DevMat &m = ms[i];
+    if (!affine_splitk_supported(m, M)) return false;
+    if (m.I != ms[0].I || m.bits != ms[0].bits || m.gs != ms[0].gs || m.fp16 != ms[0].fp16) return false;
+    floats += (size_t)(m.I / kSkKc) * M * m.O;
+  }
+  return floats <= kSkSlotFloats;
+}
+
+// ys[i][M][O_i] = x . W_i^T for products that share x: one K-split launch and
+// one reduce launch for all of them (gate/up, q/k/v) instead of two launches
+// per product.
+hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
+                                      void *const *ys, int y_bf16, hipStream_t st) {
+  if (!affine_splitk_multi_supported(ms, n, M)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  SplitMulti mp{};
+  ReduceMulti r{};
+  const int KS = ms[0].I / kSkKc;
+  const int slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
+  bool aux8 = true;
+  size_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    const DevMat &m = ms[i];
+    aux8 = aux8 && m.gs == 64 && (m.ng % 8) == 0 &&
+           ((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 15) == 0;
+    SplitParams &p = mp.m[i];
+    p.w = m.w;
+    p.sc = m.sc;
+    p.bi = m.bi;
+    p.x = x;
+    p.row_bytes = m.row_bytes;
+    p.N = m.O;
+    p.K = m.I;
+    p.ng = m.ng;
+    p.gsteps = m.gs / 64;
+    p.x_stride = x_stride;
+    p.M = M;
+    p.slot = slot;
+    p.part_off = off;
+    r.y[i] = ys[i];
+    r.part_off[i] = off;
+    r.N[i] = m.O;
+    r.y_stride[i] = m.O;
+    off += (size_t)KS * M * m.O;
+    mp.start[i + 1] = mp.start[i] + (m.O + kSkRows - 1) / kSkRows;
+    r.start[i + 1] = r.start[i] + M * m.O;
+  }
+  mp.n = r.n = n;
+  r.KS = KS;
+  r.M = M;
+  r.slot = slot;
+  r.y_bf16 = y_bf16;
+  switch (ms[0].bits) {
+    case 4: splitk_multi_launch_bits<4>(mp, KS, M, ms[0].fp16, aux8, st); break;
+    case 5: splitk_multi_launch_bits<5>(mp, KS, M, ms[0].fp16, aux8, st); break;
+    case 6: splitk_multi_launch_bits<6>(mp, KS, M, ms[0].fp16, aux8, st); break;
+    default: splitk_multi_launch_bits<8>(mp, KS, M, ms[0].fp16, aux8, st); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  size_t blocks = ((size_t)r.start[n] + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, st, r);
   return hipGetLastError();
 }
 

@@ -38,6 +38,9 @@ hipError_t launch_affine_skinny(const DevMat &m, const uint16_t *x, int x_stride
                                 int y_stride, int y_bf16, hipStream_t st);
 // K split across blocks (gemv_splitk.hip): I % 512 == 0, groups of 64k,
 // 3 <= M <= 32; partial sums in module-scope scratch slots
+bool affine_splitk_multi_supported(const DevMat *ms, int n, int M);
+hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
+                                      void *const *ys, int y_bf16, hipStream_t st);
 bool affine_splitk_supported(const DevMat &m, int M);
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);

@@ -416,25 +416,28 @@ def test_host_shared_expert(gpu):
         dsc.tensor.free()
 
 
-@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 8, 17])
 @pytest.mark.parametrize("shapes", [[(8192, 2048), (512, 2048), (512, 2048)],
                                     [(12288, 2048), (64, 2048)],
                                     [(77, 1024), (300, 1024), (64, 1024), (1000, 1024), (5, 1024),
                                      (128, 1024), (256, 1024), (33, 1024)]],
                          ids=["qkv", "qkvz_ba", "eight"])
-def test_gemv_multi_equals_single_launches(gpu, shapes, M):
-    """Matrices sharing x in one launch: every output bit-identical to its own
+def test_gemv_multi_equals_single_launches(gpu, shapes, M, bits):
+    """Matrices sharing x in one launch (3..32 tokens: one K-split launch and
+    one reduce for all of them): every output bit-identical to its own
     affine_gemv launch, the first against the oracle."""
     import torch
     from logan_amd.device import affine_gemv, affine_gemv_multi
 
-    rng = np.random.default_rng(len(shapes) * 10 + M)
+    print(f"multi shapes={len(shapes)} M={M} bits={bits}", flush=True)
+    rng = np.random.default_rng(len(shapes) * 10 + M + bits)
     I = shapes[0][1]
     host, mats = [], []
     for O, _ in shapes:
-        w, sc, bi = make_affine(rng, O, I, 4, 64)
+        w, sc, bi = make_affine(rng, O, I, bits, 64)
         host.append((w, sc, bi))
-        mats.append(dev_matrix(torch, w, sc, bi, O, I, 4, 64))
+        mats.append(dev_matrix(torch, w, sc, bi, O, I, bits, 64))
     xb = make_x(rng, M, I)
     xd = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
     outs = affine_gemv_multi(mats, xd, out_dtype=torch.float32)
@@ -444,8 +447,9 @@ def test_gemv_multi_equals_single_launches(gpu, shapes, M):
     for m, o in zip(mats, outs16):
         assert torch.equal(o, affine_gemv(m, xd, out_dtype=torch.bfloat16))
     w, sc, bi = host[0]
-    ref = oracle.affine_gemv(bf16_to_f32(xb[0]), w, sc, bi, shapes[0][0], I, 4, 64)
-    assert normwise_rel(outs[0].cpu().numpy()[0], ref) <= 2e-5
+    for r in (0, M - 1):
+        ref = oracle.affine_gemv(bf16_to_f32(xb[r]), w, sc, bi, shapes[0][0], I, bits, 64)
+        assert normwise_rel(outs[0].cpu().numpy()[r], ref) <= 2e-5
 
 
 def test_gemv_multi_rejects_mixed_geometry(gpu):
