@@ -167,8 +167,11 @@ int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_s
  * command buffer (coli_metal_matmul_multi,
  * logan-metal/metal/backend_metal.mm:2290-2493, up to 16 descriptors each
  * with its own x); here the shared x is read once per block and the
- * matrices' row blocks form one grid. Every matrix has the same I, bits,
- * group_size and aux type. 1 ok, 0 unsupported, -1 launch failure. */
+ * matrices' row blocks form one grid (for 3..32 rows of x where the K-split
+ * form applies: one K-split grid and one partial-sum reduction for all the
+ * matrices, through the same scratch slots as logan_hip_affine_gemv). Every
+ * matrix has the same I, bits, group_size and aux type. 1 ok, 0 unsupported,
+ * -1 launch failure. */
 int logan_hip_affine_gemv_multi(const LoganHipAffine *ws, int count, const void *x, int M,
                                 int x_stride, void *const *ys, int y_dtype, void *stream);
 
