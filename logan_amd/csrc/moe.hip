@@ -7,10 +7,12 @@
 //   out = sum_r (y_r * weight_r) in rank order + sy * sigmoid(se_g.x).
 //
 // Selection is done on the logits with the key (logit desc, index asc).
-// softmax is strictly increasing in the logit wherever exp(l - max) does not
-// underflow, so equal logits <=> equal probabilities and the order matches
-// the reference's selection on probabilities. Weights are
-// exp(l_r - l_0) / sum_{r<k} exp(l_j - l_0), which equals val_r / wsum.
+// softmax is non-decreasing in the logit, so this order is the reference's
+// selection on probabilities unless two different logits round to the same
+// probability; route_dev.hpp checks for that and then recomputes the
+// reference's probabilities (route_exact). Weights are
+// exp(l_r - l_0) / sum_{r<k} exp(l_j - l_0), which equals val_r / wsum up to
+// rounding (exactly the reference's val_r / wsum on the recomputed path).
 //
 // Launch structure (all on one stream):
 //   1. moe_route_tok_kernel     one block per token: top-k, shared-expert

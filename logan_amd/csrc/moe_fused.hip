@@ -23,7 +23,9 @@
 //
 // Every wave computes the route itself from the bf16 logits (top-k with the
 // key (logit desc, index asc): per-lane sorted keys, k rounds of a DPP wave
-// max), so no block waits for another before streaming weights.
+// max, and the reference's probability arithmetic instead where a tie in
+// probability could reorder it), so no block waits for another before
+// streaming weights.
 //
 // Progress: A blocks never wait on another block. Workgroups are dispatched in
 // ID order, and every A block precedes every B block, so a B block can only be
@@ -268,6 +270,22 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       uint32_t mine = sel[0];
 #pragma unroll
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
+      // a probability tie the logit order cannot see (route_dev.hpp): this
+      // slot's rank then comes from the reference's own arithmetic
+      const float m = sel_logit(sel[0]), ls = sel_logit(mine);
+      if (!bf16_rank_tie_free(m, ls)) {
+        bool cand = false, pair = false;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i)
+          cand = cand || (key[i] != 0u && tie_other(unord16(key[i] >> 16), ls, m));
+#pragma unroll
+        for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
+          pair = pair || (r < slot && tie_pair(sel_logit(sel[r]), sel_logit(sel[r + 1]), m));
+        if (__any(cand) || pair || tie_global(m, ls)) {
+          const RouteLane rl = route_exact<KPL, false>(logits, 0, a.E, a.k);
+          mine = 0xffffu - (uint32_t)__builtin_amdgcn_readlane(rl.idx, slot);
+        }
+      }
       if (lane == 0) s_sel[0] = mine;
     }
     if (threadIdx.x == 0) s_lid = launch_number(tk);
@@ -414,11 +432,34 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     uint32_t mine = 0;
 #pragma unroll
     for (int r = 0; r < kFusedMaxSlots; ++r) mine = lane == r ? sel0[r] : mine;
+    const float m = sel_logit(sel0[0]);
+    float llast = m;
+#pragma unroll
+    for (int r = 0; r < kFusedMaxSlots; ++r) llast = r == g.k - 1 ? sel_logit(sel0[r]) : llast;
+    bool exact = false;
+    if (!bf16_ranks_tie_free(m, llast)) {
+      bool cand = false, pair = false;
+#pragma unroll
+      for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
+        pair = pair || (r + 1 < g.k && tie_pair(sel_logit(sel0[r]), sel_logit(sel0[r + 1]), m));
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        cand = cand || (key[i] != 0u && tie_other(unord16(key[i] >> 16), llast, m));
+      exact = __any(cand) || pair || tie_global(m, llast);
+    }
+    float wr;
+    if (exact) {
+      // a probability tie the logit order cannot see (route_dev.hpp)
+      const RouteLane rl = route_exact<KPL, false>(logits, 0, a.E, g.k);
+      mine = lane < g.k ? 0xffffu - (uint32_t)rl.idx : 0u;
+      wr = rl.w;
+    } else {
+      // combine weights, one rank per lane (logan-qwen4/src/lib.rs:8694):
+      // w_r = exp(l_r - l_0) / sum_{r<k} exp(l_r - l_0)
+      const float ev = lane < g.k ? __expf(sel_logit(mine) - m) : 0.f;
+      wr = ev / wave_sum_f32(ev);
+    }
     if (lane < kFusedMaxSlots) s_sel[lane] = mine;
-    // combine weights, one rank per lane (logan-qwen4/src/lib.rs:8694):
-    // w_r = exp(l_r - l_0) / sum_{r<k} exp(l_r - l_0)
-    const float ev = lane < g.k ? __expf(sel_logit(mine) - sel_logit(sel0[0])) : 0.f;
-    const float wr = ev / wave_sum_f32(ev);
     if (lane < kFusedMaxSlots) s_w[lane] = wr;
     if (bb == 0 && lane < g.k) {
       if (a.idx_out) a.idx_out[lane] = sel_expert(mine);

@@ -4,6 +4,16 @@
 // larger value first, equal values -> lower expert index) is a selection on
 // unique keys (ordered value, inverted index): each lane keeps its keys
 // sorted, and each round takes the wave maximum of the lanes' best keys.
+//
+// The reference selects on softmax probabilities, p_i = fl(exp(fl(l_i - m))
+// / s) (lib.rs:4558-4574), which are only non-decreasing in the logit: two
+// different logits can share a probability (an exp argument rounded to the
+// same value, an exp that underflows, two exps one ulp apart that divide to
+// the same quotient), and the reference then takes the lower index. The
+// fast selection runs on the logits and checks afterwards whether any pair
+// that matters could tie that way; when one could, the wave recomputes the
+// reference's probabilities (same max, exp, sequential sum, division) and
+// selects on them (route_exact).
 #pragma once
 #include <cstdint>
 
@@ -187,17 +197,138 @@ __device__ __forceinline__ void sort_desc_u64(uint64_t (&v)[N]) {
       }
 }
 
+// ---- probability ties the logit order cannot see ---------------------------
+//
+// With a faithful exp (< 1 ulp), |fl(l_a - m) - fl(l_b - m)| > kTieGap makes
+// the two exps differ by several ulps, so their quotients by the same sum
+// differ too: only logits whose exp arguments are within kTieGap, exps in
+// the underflow range, or non-finite values can tie in probability while
+// differing in logit. A tie run (equal probabilities) is contiguous in
+// logit order and every member is within kTieGap of every other, so for the
+// ranks [0, R] it suffices to check consecutive selected ranks and the
+// unselected logits against rank R's.
+constexpr float kTieGap = 0x1p-19f;
+constexpr float kTieFloor = -80.0f;  // exp(-80) ~ 1.8e-35: still normal
+
+// rank pair (a above b in logit order) that may share a probability
+__device__ __forceinline__ bool tie_pair(float la, float lb, float m) {
+  return la != lb && (la - m) - (lb - m) <= kTieGap;
+}
+// an unselected logit lu that may share rank R's probability (or is NaN)
+__device__ __forceinline__ bool tie_other(float lu, float lr, float m) {
+  return (lu != lu) || (lu != lr && fabsf((lu - m) - (lr - m)) <= kTieGap);
+}
+// the reference's max (lib.rs:4560-4565: fold from -1e30, NaN ignored) may
+// differ from rank 0's logit, or rank R's exp may underflow
+__device__ __forceinline__ bool tie_global(float m, float lr) {
+  return !(fabsf(m) <= 3.0e38f) || m < -1e30f || (lr - m) < kTieFloor;
+}
+
+// bf16 logits: two different bf16 values of magnitude >= 2^-9 are at least
+// 2^-17 apart, and with |max| < 64 their exp arguments fl(l - m) are exact
+// (at most 23 significant bits), so such a logit shares its probability with
+// no different logit unless its exp underflows. These uniform tests let the
+// bf16 paths skip the per-lane checks above in all but rare cases:
+// rank r alone (logit lr) ...
+__device__ __forceinline__ bool bf16_rank_tie_free(float m, float lr) {
+  return fabsf(m) < 64.f && fabsf(lr) >= 0x1p-9f && (lr - m) >= kTieFloor;
+}
+// ... or every rank down to the one with logit llast (all logits in
+// [llast, m], none of them in (-2^-9, 2^-9))
+__device__ __forceinline__ bool bf16_ranks_tie_free(float m, float llast) {
+  return fabsf(m) < 64.f && (llast >= 0x1p-9f || m <= -0x1p-9f) && (llast - m) >= kTieFloor;
+}
+
+struct RouteLane {
+  int idx;  // rank (lane) < k: expert; else -1
+  float w;  // rank (lane) < k: val_r / wsum; else 0
+};
+
+// The reference's routing of one token, recomputed by one wave
+// (logan-qwen4/src/lib.rs:4558-4574 softmax_row, :8031-8043 selection and
+// wsum, :8694 weight): m = max(-1e30, l) ignoring NaN; e_i = exp(fl(l_i - m))
+// rounded to f32 from a double-precision exp; s = e_0 + e_1 + ... in index
+// order (f32, sequential); p_i = e_i / s; top-k on (p desc, index asc);
+// wsum = sum of the k selected p in rank order; w_r = p_r / wsum. A NaN sum
+// leaves every comparison false, so the reference keeps ranks 0..k-1 as
+// experts 0..k-1 with NaN weights; so does this. Taken only when the
+// logit-keyed selection could differ (see the checks above), so it is
+// written for clarity, not speed.
+template <int KPL, bool F32>
+__device__ __noinline__ RouteLane route_exact(const void *logits, size_t row_off, int E, int k) {
+  const int lane = threadIdx.x & 63;
+  float l[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int e = i * 64 + lane;
+    const int ee = e < E ? e : 0;
+    if constexpr (F32)
+      l[i] = reinterpret_cast<const float *>(logits)[row_off + ee];
+    else
+      l[i] = bf16_to_f32(reinterpret_cast<const uint16_t *>(logits)[row_off + ee]);
+  }
+  float mm = -1e30f;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i)
+    if (i * 64 + lane < E && l[i] > mm) mm = l[i];
+  const float m = unord32f(wave_max_u32(ord32f(mm)));
+  float ev[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const float d = __fsub_rn(l[i], m);
+    ev[i] = i * 64 + lane < E ? (float)exp((double)d) : 0.f;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i)
+    for (int j = 0; j < 64 && i * 64 + j < E; ++j)
+      s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[i]), j)));
+  RouteLane out;
+  if (!(s == s)) {
+    out.idx = lane < k ? lane : -1;
+    out.w = lane < k ? __int_as_float(0x7fc00000) : 0.f;
+    return out;
+  }
+  uint64_t key[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int e = i * 64 + lane;
+    const float p = __fdiv_rn(ev[i], s);  // >= +0: its bits order as the value
+    key[i] = e < E ? (((uint64_t)__float_as_uint(p) << 32) | (0xffffffffu - (uint32_t)e)) : 0ull;
+  }
+  sort_desc_u64<KPL>(key);
+  uint64_t kmine = 0;
+  for (int r = 0; r < k; ++r) {
+    const uint64_t mx = wave_max_u64(key[0]);
+    kmine = lane == r ? mx : kmine;
+    const bool mine = key[0] == mx;
+#pragma unroll
+    for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
+    key[KPL - 1] = mine ? 0ull : key[KPL - 1];
+  }
+  const float val = __uint_as_float((uint32_t)(kmine >> 32));
+  float wsum = 0.f;
+  for (int r = 0; r < k; ++r)
+    wsum = __fadd_rn(wsum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), r)));
+  out.idx = lane < k ? (int)(0xffffffffu - (uint32_t)kmine) : -1;
+  out.w = lane < k ? __fdiv_rn(val, wsum) : 0.f;
+  return out;
+}
+
 // One wave: top-k of E logits (bf16 or f32) of one token. On return lane r
 // (r < k) holds rank r's expert in *idx and its weight
 // w_r = exp(l_r - l_0) / sum_{j<k} exp(l_j - l_0) (= val_r / wsum of
 // logan-qwen4/src/lib.rs:8043, :8694) in *w; other lanes get idx -1, w 0.
-// KPL = keys per lane (E <= 64 * KPL).
+// When a probability tie could reorder the selection, the result is
+// route_exact's instead. KPL = keys per lane (E <= 64 * KPL).
 template <int KPL, bool F32>
 __device__ __forceinline__ void wave_topk_lanes(const void *logits, size_t row_off, int E, int k,
                                                 int &idx, float &w) {
   const int lane = threadIdx.x & 63;
   float lmine = 0.f;
   uint32_t emine = 0xffffffffu;
+  bool cand = false;  // a logit of this lane may share a probability with another
+  float m = 0.f, llast = 0.f;
   if constexpr (!F32) {
     uint32_t key[KPL];
     const uint16_t *lg = reinterpret_cast<const uint16_t *>(logits) + row_off;
@@ -215,15 +346,30 @@ __device__ __forceinline__ void wave_topk_lanes(const void *logits, size_t row_o
     uint32_t kmine = 0;
 #pragma unroll 1
     for (int r = 0; r < k; ++r) {
-      const uint32_t m = wave_max_u32(key[0]);
-      kmine = lane == r ? m : kmine;
-      const bool mine = key[0] == m;
+      const uint32_t mx = wave_max_u32(key[0]);
+      kmine = lane == r ? mx : kmine;
+      const bool mine = key[0] == mx;
 #pragma unroll
       for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
       key[KPL - 1] = mine ? 0u : key[KPL - 1];
     }
     lmine = unord16(kmine >> 16);
     emine = 0xffffu - (kmine & 0xffffu);
+    m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmine), 0));
+    llast = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmine), k - 1));
+    if (!bf16_ranks_tie_free(m, llast)) {  // rare: the full checks
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        cand = cand || (key[i] != 0u && tie_other(unord16(key[i] >> 16), llast, m));
+      const float lnext = __shfl(lmine, (lane + 1) & 63, 64);
+      cand = cand || (lane + 1 < k && tie_pair(lmine, lnext, m));
+      if (__any(cand) || tie_global(m, llast)) {
+        const RouteLane rl = route_exact<KPL, F32>(logits, row_off, E, k);
+        idx = rl.idx;
+        w = rl.w;
+        return;
+      }
+    }
   } else {
     uint64_t key[KPL];
     const float *lg = reinterpret_cast<const float *>(logits) + row_off;
@@ -237,18 +383,31 @@ __device__ __forceinline__ void wave_topk_lanes(const void *logits, size_t row_o
     uint64_t kmine = 0;
 #pragma unroll 1
     for (int r = 0; r < k; ++r) {
-      const uint64_t m = wave_max_u64(key[0]);
-      kmine = lane == r ? m : kmine;
-      const bool mine = key[0] == m;
+      const uint64_t mx = wave_max_u64(key[0]);
+      kmine = lane == r ? mx : kmine;
+      const bool mine = key[0] == mx;
 #pragma unroll
       for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
       key[KPL - 1] = mine ? 0ull : key[KPL - 1];
     }
     lmine = unord32f((uint32_t)(kmine >> 32));
     emine = 0xffffffffu - (uint32_t)kmine;
+    m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmine), 0));
+    llast = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmine), k - 1));
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      cand = cand || (key[i] != 0ull && tie_other(unord32f((uint32_t)(key[i] >> 32)), llast, m));
+    // consecutive selected ranks (lane r: ranks r, r + 1)
+    const float lnext = __shfl(lmine, (lane + 1) & 63, 64);
+    cand = cand || (lane + 1 < k && tie_pair(lmine, lnext, m));
+    if (__any(cand) || tie_global(m, llast)) {
+      const RouteLane rl = route_exact<KPL, F32>(logits, row_off, E, k);
+      idx = rl.idx;
+      w = rl.w;
+      return;
+    }
   }
-  const float l0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lmine), 0));
-  const float ev = lane < k ? __expf(lmine - l0) : 0.f;
+  const float ev = lane < k ? __expf(lmine - m) : 0.f;
   const float ws = wave_sum_f32(ev);
   idx = lane < k ? (int)emine : -1;
   w = lane < k ? ev / ws : 0.f;

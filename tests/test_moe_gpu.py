@@ -152,16 +152,18 @@ def fused_mode(request):
     assert _lib.lib().logan_hip_moe_sync_errors() == 0
 
 
-@pytest.mark.parametrize("fused_mode", [1, 0], indirect=True, ids=["fused", "multi"])
-@pytest.mark.parametrize("bits,B,zipf", [(4, 1, False), (4, 16, False), (4, 40, True),
-                                         (5, 1, True), (6, 1, True), (5, 32, True),
-                                         (6, 32, True), (8, 4, False), (8, 1, False)])
+MOE_CASES = [(4, 1, False), (4, 16, False), (4, 40, True), (5, 1, True), (6, 1, True),
+             (5, 32, True), (6, 32, True), (8, 4, False), (8, 1, False)]
+
+
+# B > 1 always takes the multi-launch path, so only B = 1 runs both ways
+@pytest.mark.parametrize("fused_mode,bits,B,zipf",
+                         [(1, *c) for c in MOE_CASES] + [(0, *c) for c in MOE_CASES if c[1] == 1],
+                         indirect=["fused_mode"])
 def test_moe_block_matches_oracle(gpu, fused_mode, bits, B, zipf):
     """Configs 3 and 4: E=512, top-10, D=2048, inter=512, g64, shared expert."""
     import torch
 
-    if fused_mode == 0 and B > 1:
-        pytest.skip("B > 1 always takes the multi-launch path")
     print(f"moe bits={bits} B={B} zipf={zipf} fused={fused_mode}", flush=True)
     layer = Layer(torch, 512, 10, 2048, 512, bits, 64, seed=bits * 10 + B)
     rng = np.random.default_rng(1000 + B)

@@ -115,6 +115,72 @@ def test_spark_affine8_reference_closed_form():
     np.testing.assert_array_equal(y, np.full(O, c["expected"], np.float32))
 
 
+def _spark_case(rng, O, I):
+    """Integer codes, integer x and power-of-two scales/biases that differ per
+    (row, group): every product and partial sum is exact in f32, so the
+    expected accumulator is exact and only the final bf16 rounding is left."""
+    ng = I // 64
+    codes = rng.integers(0, 256, (O, I)).astype(np.uint8)
+    x = rng.integers(-3, 4, I).astype(np.float32)
+    sc = np.float32([0.25, 0.5, 1.0, 2.0])[rng.integers(0, 4, (O, ng))]
+    bi = np.float32([-32.0, -8.0, 4.0, 24.0])[rng.integers(0, 4, (O, ng))]
+    return codes, x, sc, bi
+
+
+def _spark_expected(codes, x, sc, bi, bias=True, row_params=True):
+    O, I = codes.shape
+    acc = np.zeros(O, np.float64)
+    for r in range(O):
+        pr = r if row_params else 0
+        for g in range(I // 64):
+            s = slice(64 * g, 64 * g + 64)
+            acc[r] += sc[pr, g] * float(codes[r, s].astype(np.float64) @ x[s])
+            if bias:
+                acc[r] += bi[pr, g] * float(x[s].sum())
+    return acc
+
+
+def test_spark_affine8_closed_form_bias_and_rounding():
+    """logan-spark/src/lib.rs:346-367: acc = sum_g sc[r,g] * dot_g + bi[r,g] *
+    xsum[g], then bf16 RNE. With exact accumulators the oracle must equal
+    torch's bf16 rounding of the exact value; the case is built so that a
+    dropped bias term, row-0 parameters for every row, or no rounding all
+    give different outputs."""
+    rng = np.random.default_rng(41)
+    O, I = 16, 256
+    codes, x, sc, bi = _spark_case(rng, O, I)
+    aux = np.concatenate([bf16_bits(sc.ravel()), bf16_bits(bi.ravel())])
+    y = oracle.spark_affine8_gemv(x, codes.ravel(), aux, O, I)
+    exact = _spark_expected(codes, x, sc, bi)
+    assert np.all(np.abs(exact) < 2.0 ** 24)  # exact in f32
+    want = _bf16_round_torch(exact.astype(np.float32))
+    np.testing.assert_array_equal(y, want)
+    # the case separates the plausible mistakes
+    assert np.sum(want != exact.astype(np.float32)) >= O // 2  # rounding visible
+    assert np.sum(_bf16_round_torch(_spark_expected(codes, x, sc, bi, bias=False)
+                                    .astype(np.float32)) != want) >= O - 1
+    assert np.sum(_bf16_round_torch(_spark_expected(codes, x, sc, bi, row_params=False)
+                                    .astype(np.float32)) != want) >= O - 2
+
+
+def test_spark_affine8_random_against_float64():
+    """Random codes, bf16 N(0,1) x and make_affine's bf16 scale/bias: the
+    oracle is within 1 bf16 ulp of RNE(float64 dequant-then-dot), and equal
+    to it for nearly every row (f32 accumulation only moves outputs that sit
+    next to a rounding boundary)."""
+    rng = np.random.default_rng(42)
+    O, I = 256, 4096
+    w, sc, bi = make_affine(rng, O, I, 8, 64)
+    x = bf16_to_f32(make_x(rng, 1, I))[0]
+    aux = np.concatenate([sc, bi])
+    y = oracle.spark_affine8_gemv(x, w.ravel(), aux, O, I)
+    ref64 = dequant_f64(w, sc, bi, O, I, 8, 64) @ x.astype(np.float64)
+    want = _bf16_round_torch(ref64.astype(np.float32))
+    ulp = np.abs(want) * 2.0 ** -7
+    assert np.all(np.abs(y - want) <= ulp * 1.0001)
+    assert np.mean(y == want) >= 0.95
+
+
 @pytest.mark.parametrize("bits,gs", [(4, 64), (5, 128), (6, 64), (8, 128)])
 def test_gemv_reference_generator_against_float64(bits, gs):
     """The generator of logan-metal/src/lib.rs:1310-1378 (codes
