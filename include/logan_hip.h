@@ -13,8 +13,9 @@
  *     and their [scales][biases] sidecar are host byte arrays uploaded to HBM
  *     once on first use and cached behind an opaque tensor handle that the
  *     caller keeps and frees (backend_metal.h:59-66, :180).
- *     Every `logan_hip_*` symbol of this layer is also exported under its
- *     `coli_metal_*` name, so logan-metal's unmodified Rust FFI block links.
+ *     The library also exports logan-metal's own C names for every function
+ *     its Rust FFI blocks declare (include/logan_metal_ffi.h): those of this
+ *     layer forward here, the rest are advisory or decline.
  *
  *  2. Device-native entry points (`logan_hip_affine_*`, `logan_hip_route_topk`,
  *     `logan_hip_moe_block*`): every pointer is device memory already resident
@@ -33,8 +34,9 @@
  * Dequantised weight: code*scale + bias (logan-qwen4/src/lib.rs:3703-3727).
  *
  * Threading: every entry point of layer 1 serialises on one process-wide
- * mutex (as backend_metal.mm:1678); route begin/finish is single-in-flight per
- * process (a second begin waits for the first one's work to retire).
+ * mutex (as backend_metal.mm:1678). Each pending route-island handle owns its
+ * device buffers until finish/discard, so other calls (the shared expert,
+ * GEMVs, further begins) may run between a begin and its finish.
  */
 #ifndef LOGAN_HIP_H
 #define LOGAN_HIP_H
@@ -125,6 +127,17 @@ void logan_hip_moe_route_drop_model(uint64_t model_id);
 int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
                             const float *x, float *out, int D, int Iinter);
 void logan_hip_shared_expert_drop_model(uint64_t model_id);
+
+/* Host-pointer element-wise ops on the GPU (stage in HBM, run, copy back,
+ * wait): in-place RMSNorm of nrows rows of n floats,
+ * x = x * (1 / sqrt(mean(x^2) + eps)) * w (replaces coli_metal_rmsnorm,
+ * backend_metal.h:24, backend_metal.mm:2147-2166 with kernel a_rmsnorm
+ * :705-714); y += a (coli_metal_add, backend_metal.mm:2168-2185); the SwiGLU
+ * g = silu(g) * u (coli_metal_silu_mul, :2187-2204). 1 ok, 0 declined,
+ * -1 failure. */
+int logan_hip_host_rmsnorm(float *x, const float *w, int n, int nrows, float eps);
+int logan_hip_host_add(float *y, const float *a, int n);
+int logan_hip_host_silu_mul(float *g, const float *u, int n);
 
 /* Replace coli_metal_tensor_free / coli_metal_tensor_bytes (backend_metal.h:180-181). */
 void logan_hip_tensor_free(LoganHipTensor *tensor);

@@ -96,6 +96,9 @@ SIGNATURES = {
     "logan_hip_moe_route_drop_model": (None, [_U64]),
     "logan_hip_shared_expert": (_I, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _P, _I, _I]),
     "logan_hip_shared_expert_drop_model": (None, [_U64]),
+    "logan_hip_host_rmsnorm": (_I, [_P, _P, _I, _I, C.c_float]),
+    "logan_hip_host_add": (_I, [_P, _P, _I]),
+    "logan_hip_host_silu_mul": (_I, [_P, _P, _I]),
     "logan_hip_tensor_free": (None, [_P]),
     "logan_hip_tensor_bytes": (_SZ, [_P]),
     "logan_hip_affine_gemv": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),

@@ -53,13 +53,48 @@ struct DevBuf {
     n = 0;
   }
 };
-DevBuf g_xbuf, g_ybuf, g_gubuf, g_ws;
+DevBuf g_xbuf, g_ybuf, g_ws;
+
+// Device buffers of one route-island submission: x [D], gate/up outputs
+// [2 K M], expert outputs [K D]. Each pending handle owns one set from the
+// pool until finish/discard, so calls made between begin and finish (the
+// shared expert, other GEMVs, another begin) never touch it.
+struct RouteBufs {
+  DevBuf x, gu, out;
+};
+std::vector<RouteBufs *> g_route_pool;  // idle sets
+
+RouteBufs *route_bufs_take(size_t xb, size_t gub, size_t outb) {
+  RouteBufs *b = nullptr;
+  if (!g_route_pool.empty()) {
+    b = g_route_pool.back();
+    g_route_pool.pop_back();
+  } else {
+    b = new (std::nothrow) RouteBufs();
+    if (!b) return nullptr;
+  }
+  if (!b->x.ensure(xb) || !b->gu.ensure(gub) || !b->out.ensure(outb)) {
+    g_route_pool.push_back(b);
+    return nullptr;
+  }
+  return b;
+}
 
 struct RoutePending {
   hipEvent_t ev = nullptr;
+  RouteBufs *bufs = nullptr;
   int K = 0, D = 0;
 };
-RoutePending *g_route_inflight = nullptr;  // at most one (single in-flight)
+
+// back to the pool once the submission's work has retired
+void route_release_locked(RoutePending *p) {
+  if (p->ev) {
+    hipEventSynchronize(p->ev);
+    hipEventDestroy(p->ev);
+  }
+  if (p->bufs) g_route_pool.push_back(p->bufs);
+  delete p;
+}
 
 using clk = std::chrono::steady_clock;
 inline uint64_t now_ns() {
@@ -219,14 +254,6 @@ void prof_kernel_time() {
     g_prof[3] += (uint64_t)(ms * 1e6);
 }
 
-void retire_route_locked() {
-  if (g_route_inflight) {
-    hipEventSynchronize(g_route_inflight->ev);
-    // the pending handle stays owned by the caller; only buffers are released
-    g_route_inflight = nullptr;
-  }
-}
-
 lh::DevMat devmat(const LoganHipAffine &a) {
   lh::DevMat m{};
   m.w = reinterpret_cast<const uint8_t *>(a.weights);
@@ -277,12 +304,17 @@ int logan_hip_available(void) {
 void logan_hip_shutdown(void) {
   std::lock_guard<std::mutex> lk(g_mtx);
   if (!g_ok) return;
-  retire_route_locked();
   hipStreamSynchronize(g_stream);
   g_xbuf.release();
   g_ybuf.release();
-  g_gubuf.release();
   g_ws.release();
+  for (RouteBufs *b : g_route_pool) {
+    b->x.release();
+    b->gu.release();
+    b->out.release();
+    delete b;
+  }
+  g_route_pool.clear();
 }
 
 void logan_hip_stats(size_t *tensor_count, size_t *tensor_bytes) {
@@ -363,7 +395,6 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
                                   descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
     if (!ts[i]) return 0;
   }
-  retire_route_locked();
   // staging: shared x, then private x's; outputs concatenated
   size_t xn = shared_I > 0 ? (size_t)S * shared_I : 0, yn = 0;
   std::vector<size_t> xoff(count, 0), yoff(count, 0);
@@ -437,21 +468,19 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
                                   descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
     if (!ts[i]) return nullptr;
   }
-  retire_route_locked();
-  if (!g_xbuf.ensure((size_t)D * 4 + 16) || !g_gubuf.ensure((size_t)2 * K * M * 4 + 16) ||
-      !g_ybuf.ensure((size_t)K * D * 4 + 16))
-    return nullptr;
   RoutePending *p = new (std::nothrow) RoutePending();
   if (!p) return nullptr;
-  if (hipEventCreateWithFlags(&p->ev, hipEventDisableTiming) != hipSuccess) {
-    delete p;
+  p->bufs = route_bufs_take((size_t)D * 4 + 16, (size_t)2 * K * M * 4 + 16, (size_t)K * D * 4 + 16);
+  if (!p->bufs || hipEventCreateWithFlags(&p->ev, hipEventDisableTiming) != hipSuccess) {
+    p->ev = nullptr;
+    route_release_locked(p);
     return nullptr;
   }
   p->K = K;
   p->D = D;
-  float *dx = reinterpret_cast<float *>(g_xbuf.p);
-  float *gu = reinterpret_cast<float *>(g_gubuf.p);
-  float *out = reinterpret_cast<float *>(g_ybuf.p);
+  float *dx = reinterpret_cast<float *>(p->bufs->x.p);
+  float *gu = reinterpret_cast<float *>(p->bufs->gu.p);
+  float *out = reinterpret_cast<float *>(p->bufs->out.p);
   // gate -> gu[i*M], up -> gu[K*M + i*M]; down(silu(gate)*up) -> out[i*D]
   std::vector<lh::GenDesc> s1, s2;
   for (int i = 0; i < K; ++i) {
@@ -475,7 +504,6 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
     p->K = -1;
     return p;
   }
-  g_route_inflight = p;
   return p;
 }
 
@@ -494,13 +522,11 @@ int logan_hip_moe_route_finish(void *pending, float *out, int count) {
     rc = -1;
   } else {
     const int K = std::min(count, p->K);
-    if (hipMemcpy(out, g_ybuf.p, (size_t)K * p->D * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpy(out, p->bufs->out.p, (size_t)K * p->D * 4, hipMemcpyDeviceToHost) != hipSuccess)
       rc = -1;
   }
   prof_add(2, now_ns() - t0);
-  if (g_route_inflight == p) g_route_inflight = nullptr;
-  hipEventDestroy(p->ev);
-  delete p;
+  route_release_locked(p);
   return rc;
 }
 
@@ -508,19 +534,21 @@ void logan_hip_moe_route_discard(void *pending) {
   if (!pending) return;
   RoutePending *p = reinterpret_cast<RoutePending *>(pending);
   std::lock_guard<std::mutex> lk(g_mtx);
-  hipEventSynchronize(p->ev);
-  if (g_route_inflight == p) g_route_inflight = nullptr;
-  hipEventDestroy(p->ev);
-  delete p;
+  route_release_locked(p);
 }
 
 void logan_hip_moe_route_drop_model(uint64_t model_id) {
   (void)model_id;
   std::lock_guard<std::mutex> lk(g_mtx);
   if (!g_ok) return;
-  retire_route_locked();
-  hipStreamSynchronize(g_stream);
-  g_gubuf.release();
+  // idle buffer sets only; those of pending handles return on finish/discard
+  for (RouteBufs *b : g_route_pool) {
+    b->x.release();
+    b->gu.release();
+    b->out.release();
+    delete b;
+  }
+  g_route_pool.clear();
 }
 
 int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
@@ -538,10 +566,7 @@ void logan_hip_shared_expert_drop_model(uint64_t model_id) { logan_hip_moe_route
 void logan_hip_tensor_free(LoganHipTensor *t) {
   if (!t) return;
   std::lock_guard<std::mutex> lk(g_mtx);
-  if (g_ok) {
-    retire_route_locked();
-    hipStreamSynchronize(g_stream);
-  }
+  if (g_ok) hipStreamSynchronize(g_stream);  // queued work may still read the tensor
   if (t->w) hipFree(t->w);
   if (t->sc) hipFree(t->sc);
   if (g_tensor_count) g_tensor_count--;
@@ -550,6 +575,61 @@ void logan_hip_tensor_free(LoganHipTensor *t) {
 }
 
 size_t logan_hip_tensor_bytes(const LoganHipTensor *t) { return t ? t->wbytes + t->abytes : 0; }
+
+// Host-pointer element-wise ops (backend_metal.mm:2147-2204): stage the
+// operands in HBM, run the kernel, copy the result back, wait.
+namespace {
+int host_ew(float *dst, size_t n_dst, const float *src, size_t n_src,
+            hipError_t (*run)(float *, const float *, hipStream_t, const void *), const void *arg) {
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return 0;
+  if (!g_xbuf.ensure(n_dst * 4 + 16) || !g_ybuf.ensure(n_src * 4 + 16)) return 0;
+  float *dd = reinterpret_cast<float *>(g_xbuf.p);
+  float *ds = reinterpret_cast<float *>(g_ybuf.p);
+  hipError_t e = hipMemcpyAsync(dd, dst, n_dst * 4, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(ds, src, n_src * 4, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = run(dd, ds, g_stream, arg);
+  if (e == hipSuccess) e = hipMemcpyAsync(dst, dd, n_dst * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? 1 : -1;
+}
+struct RmsArg {
+  int n, nrows;
+  float eps;
+};
+}  // namespace
+
+int logan_hip_host_rmsnorm(float *x, const float *w, int n, int nrows, float eps) {
+  if (!x || !w || n <= 0 || nrows <= 0) return 0;
+  const RmsArg arg{n, nrows, eps};
+  return host_ew(x, (size_t)n * nrows, w, (size_t)n,
+                 [](float *d, const float *s, hipStream_t st, const void *a) {
+                   const RmsArg &r = *reinterpret_cast<const RmsArg *>(a);
+                   return lh::launch_rmsnorm(d, s, r.n, r.nrows, r.eps, st);
+                 },
+                 &arg);
+}
+
+int logan_hip_host_add(float *y, const float *a, int n) {
+  if (!y || !a || n <= 0) return 0;
+  const long long nn = n;
+  return host_ew(y, (size_t)n, a, (size_t)n,
+                 [](float *d, const float *s, hipStream_t st, const void *a) {
+                   return lh::launch_add(d, s, *reinterpret_cast<const long long *>(a), st);
+                 },
+                 &nn);
+}
+
+int logan_hip_host_silu_mul(float *g, const float *u, int n) {
+  if (!g || !u || n <= 0) return 0;
+  const long long nn = n;
+  return host_ew(g, (size_t)n, u, (size_t)n,
+                 [](float *d, const float *s, hipStream_t st, const void *a) {
+                   return lh::launch_silu_mul(d, s, *reinterpret_cast<const long long *>(a), false,
+                                              st);
+                 },
+                 &nn);
+}
 
 // ---------------------------------------------------------------------------
 
@@ -703,43 +783,5 @@ uint32_t logan_hip_moe_sync_errors(void) { return lh::moe_fused_sync_errors(); }
 void logan_hip_set_moe_mfma_min_batch(int b) { lh::set_moe_mfma_min_batch(b); }
 
 const char *logan_hip_version(void) { return "logan-hip 0.1.0 (gfx950)"; }
-
-// ---------------------------------------------------------------------------
-// logan-metal symbol names (backend_metal.h) for the implemented subset, so
-// logan-metal's Rust FFI block links against this library unchanged.
-
-int coli_metal_init(void) { return logan_hip_init(); }
-int coli_metal_available(void) { return logan_hip_available(); }
-void coli_metal_shutdown(void) { logan_hip_shutdown(); }
-void coli_metal_stats(size_t *c, size_t *b) { logan_hip_stats(c, b); }
-int coli_metal_mem_info(size_t *u, size_t *t) { return logan_hip_mem_info(u, t); }
-void coli_metal_profile_set_on(int on) { logan_hip_profile_set_on(on); }
-void coli_metal_profile_reset(void) { logan_hip_profile_reset(); }
-void coli_metal_profile_get(uint64_t *a, uint64_t *b, uint64_t *c, uint64_t *d) {
-  logan_hip_profile_get(a, b, c, d);
-}
-int coli_metal_matmul(LoganHipTensor **t, float *y, const float *x, const void *w,
-                      const float *scales, int fmt, int S, int I, int O, int gs) {
-  return logan_hip_matmul(t, y, x, w, scales, fmt, S, I, O, gs);
-}
-int coli_metal_matmul_multi(const float *x, int S, LoganHipMatmulDesc *d, int count) {
-  return logan_hip_matmul_multi(x, S, d, count);
-}
-void *coli_metal_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc *d, int count,
-                                 const float *x, int D, int M) {
-  return logan_hip_moe_route_begin(model_id, layer, d, count, x, D, M);
-}
-int coli_metal_moe_route_finish(void *p, float *out, int count) {
-  return logan_hip_moe_route_finish(p, out, count);
-}
-void coli_metal_moe_route_discard(void *p) { logan_hip_moe_route_discard(p); }
-void coli_metal_moe_route_drop_model(uint64_t m) { logan_hip_moe_route_drop_model(m); }
-int coli_metal_shared_mxfp4(uint64_t model_id, int layer, LoganHipMatmulDesc *d, int count,
-                            const float *x, float *out, int D, int Iinter) {
-  return logan_hip_shared_expert(model_id, layer, d, count, x, out, D, Iinter);
-}
-void coli_metal_shared_mxfp4_drop_model(uint64_t m) { logan_hip_shared_expert_drop_model(m); }
-void coli_metal_tensor_free(LoganHipTensor *t) { logan_hip_tensor_free(t); }
-size_t coli_metal_tensor_bytes(const LoganHipTensor *t) { return logan_hip_tensor_bytes(t); }
 
 }  // extern "C"

@@ -67,4 +67,46 @@ hipError_t launch_silu_mul(void *g, const void *u, long long n, bool bf16, hipSt
   return hipGetLastError();
 }
 
+// In-place RMSNorm of each row of x [nrows][n]:
+//   x[r][i] = x[r][i] * (1 / sqrt(sum_i x[r][i]^2 / n + eps)) * w[i]
+// (logan-metal/metal/backend_metal.mm:705-714 a_rmsnorm, reached through
+// coli_metal_rmsnorm :2147-2166). One 256-thread block per row; the sum of
+// squares is a wave DPP/shuffle reduction plus one LDS step.
+__global__ __launch_bounds__(kEwThreads) void rmsnorm_f32_kernel(float *x, const float *w, int n,
+                                                                 float eps) {
+  float *xr = x + (size_t)blockIdx.x * n;
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += kEwThreads) s = fmaf(xr[i], xr[i], s);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  __shared__ float red[kEwThreads / 64];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kEwThreads / 64; ++i) tot += red[i];
+  const float r = 1.0f / sqrtf(tot / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += kEwThreads) xr[i] = xr[i] * r * w[i];
+}
+
+// y[i] += a[i] (backend_metal.mm:782-783 a_add, via coli_metal_add :2168-2185)
+__global__ __launch_bounds__(kEwThreads) void add_f32_kernel(float *y, const float *a, long long n) {
+  const long long i = (long long)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i < n) y[i] += a[i];
+}
+
+hipError_t launch_rmsnorm(float *x, const float *w, int n, int nrows, float eps, hipStream_t st) {
+  if (n <= 0 || nrows <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3((unsigned)nrows), dim3(kEwThreads), 0, st, x, w, n, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float *y, const float *a, long long n, hipStream_t st) {
+  if (n <= 0) return hipErrorInvalidValue;
+  const long long blocks = (n + kEwThreads - 1) / kEwThreads;
+  if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(add_f32_kernel, dim3((unsigned)blocks), dim3(kEwThreads), 0, st, y, a, n);
+  return hipGetLastError();
+}
+
 }  // namespace lh

@@ -45,6 +45,9 @@ bool affine_splitk_supported(const DevMat &m, int M);
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);
 hipError_t launch_silu_mul(void *g, const void *u, long long n, bool bf16, hipStream_t st);
+// in-place RMSNorm of nrows rows of n floats with weight w[n]; y += a
+hipError_t launch_rmsnorm(float *x, const float *w, int n, int nrows, float eps, hipStream_t st);
+hipError_t launch_add(float *y, const float *a, long long n, hipStream_t st);
 
 // ---- generic GEMV over up to 16 descriptors, f32 activations ----
 struct GenDesc {

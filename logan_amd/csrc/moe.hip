@@ -139,12 +139,17 @@ static MoeWs moe_ws_layout(void *base, int B, int D, int inter, int sinter, int 
 
 constexpr int kMaxB = 64;  // tokens per launch of the dot2 path (larger batches go in chunks)
 
+// The single-launch B = 1 path's tagged h pairs own the first bytes of the
+// workspace; the per-token and MFMA paths lay out their buffers after them,
+// so no other path ever writes where a tag is checked.
+static size_t fused_region_bytes(int inter, int sinter, int k) {
+  return al256(moe_fused_workspace_bytes(k + 1, inter, sinter));
+}
+
 size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k) {
   const size_t general = moe_ws_layout(nullptr, B < kMaxB ? B : kMaxB, D, inter, sinter, E, k).total;
-  const size_t fused = moe_fused_workspace_bytes(k + 1, inter, sinter);
   const size_t mfma = moe_mfma_workspace_bytes(B, D, inter, sinter, E, k);
-  size_t m = general > fused ? general : fused;
-  return m > mfma ? m : mfma;
+  return fused_region_bytes(inter, sinter, k) + (general > mfma ? general : mfma);
 }
 
 // > 0: one threshold for every code width; 0: the per-width defaults;
@@ -730,10 +735,15 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
   if (a.ws_bytes < moe_workspace_bytes(a.B, a.D, a.inter, sinter, a.E, a.k)) return 0;
   MoeArgs aa = a;
   aa.sinter = sinter;
+  const size_t fz = fused_region_bytes(a.inter, sinter, a.k);
   if (fused_enabled()) {
-    const int rc = launch_moe_fused_b1(aa, st);
+    MoeArgs af = aa;
+    af.ws_bytes = fz;
+    const int rc = launch_moe_fused_b1(af, st);
     if (rc != 0) return rc;
   }
+  aa.ws = reinterpret_cast<char *>(a.ws) + fz;
+  aa.ws_bytes = a.ws_bytes - fz;
   if (a.B >= mfma_min_batch(bits)) {
     const int rc = launch_moe_mfma(aa, st);
     if (rc != 0) return rc;
@@ -748,7 +758,7 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
     c.out = reinterpret_cast<char *>(a.out) + (size_t)b0 * a.D * (a.out_f32 ? 4 : 2);
     if (a.idx_out) c.idx_out = a.idx_out + (size_t)b0 * a.k;
     if (a.w_out) c.w_out = a.w_out + (size_t)b0 * a.k;
-    MoeWs w = moe_ws_layout(a.ws, c.B, a.D, a.inter, sinter, a.E, a.k);
+    MoeWs w = moe_ws_layout(aa.ws, c.B, a.D, a.inter, sinter, a.E, a.k);
     if (launch_route_tok(c, w, bits, st) != 0) return -1;
     hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, st, c, w);
     if (hipGetLastError() != hipSuccess) return -1;

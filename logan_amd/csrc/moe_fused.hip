@@ -50,12 +50,15 @@
 // of 2^kTicketShift, and counters that no block of a small grid uses are
 // advanced by one launch as well, so every block of the next launch again
 // reads one launch number. Launches of this kernel on one device must
-// therefore not overlap (one stream, or serialised streams): the next launch
-// starts only after this one has ended, its realigning atomics included.
+// therefore not overlap: the next launch starts only after this one has
+// ended, its realigning atomics included (the launcher orders launches that
+// come on different streams, see fused_launch).
 // Arrival counters come in two sets used by alternate launches; each launch
 // zeroes the set the next one will use. All of this lives in module-scope
 // device memory (zero when the code object loads), so no launch needs a
 // memset and nothing is left to count once the outputs are written.
+#include <mutex>
+
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 #include "route_dev.hpp"
@@ -171,8 +174,11 @@ __device__ __forceinline__ uint32_t launch_number(unsigned long long t) {
   return (uint32_t)(t >> kTicketShift);
 }
 
-// tag of a launch's h pairs: odd, so zeroed memory never passes
-__device__ __forceinline__ uint32_t launch_tag(uint32_t lid) { return (lid << 1) | 1u; }
+// tag of a launch's h pairs: odd, so zeroed memory never passes, and mixed
+// with a constant so that the small integers and ordinary floats a
+// workspace may hold from earlier use do not look like a recent launch's tag
+constexpr uint32_t kTagMix = 0x6A09E666u;  // even: the tag stays odd
+__device__ __forceinline__ uint32_t launch_tag(uint32_t lid) { return ((lid << 1) | 1u) ^ kTagMix; }
 
 // expected arrivals on sub-counter q of a slot with n A waves
 __device__ __forceinline__ uint32_t sub_need(int n, int q) {
@@ -664,11 +670,46 @@ size_t moe_fused_workspace_bytes(int slots, int inter, int sinter) {
   return (size_t)kSlices * slots * hmax * sizeof(uint64_t);  // (value, tag) pairs
 }
 
+// Launches of this kernel on one device share the module-scope ticket and
+// arrival counters, so they must not overlap. Launches on one stream are
+// ordered by the stream; when a launch comes on another stream than the
+// previous one, it first waits (hipStreamWaitEvent) for an event recorded
+// after that launch. Launches recorded into a graph are ordered by the
+// graph's stream; replays of such a graph must not overlap other launches
+// of this kernel on the device (nothing is recorded or waited for while a
+// stream captures).
+namespace {
+constexpr int kMaxDevices = 64;
+struct FusedOrder {
+  hipStream_t last = nullptr;
+  hipEvent_t ev = nullptr;
+  bool pending = false;  // ev marks the end of the last launch
+};
+std::mutex g_order_mtx;
+FusedOrder g_order[kMaxDevices];
+}  // namespace
+
 template <int BITS, int CPLA, int LANESB, int KPL>
 static int fused_launch(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) return 0;
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> lk(g_order_mtx);
+  FusedOrder &o = g_order[dev];
+  if (!capturing && o.pending && o.last != st && hipStreamWaitEvent(st, o.ev, 0) != hipSuccess)
+    return -1;
   auto kern = moe_fused_b1_kernel<BITS, CPLA, LANESB, KPL>;
   hipLaunchKernelGGL(kern, dim3(g.nA_blocks + g.nB_blocks), dim3(kWaves * 64), 0, st, a, g);
-  return hipGetLastError() == hipSuccess ? 1 : -1;
+  if (hipGetLastError() != hipSuccess) return -1;
+  o.last = st;
+  o.pending = false;
+  if (!capturing) {
+    if (!o.ev && hipEventCreateWithFlags(&o.ev, hipEventDisableTiming) != hipSuccess) return 1;
+    o.pending = hipEventRecord(o.ev, st) == hipSuccess;
+  }
+  return 1;
 }
 
 template <int BITS, int CPLA, int LANESB>

@@ -59,6 +59,10 @@ def lib() -> C.CDLL:
         h.lo_spark_affine8_gemv.argtypes = [P, P, P, P, SZ, SZ]
         h.lo_affine_qmm_bf16.restype = None
         h.lo_affine_qmm_bf16.argtypes = [P, P, P, P, P, SZ, SZ, SZ, I, SZ, I]
+        h.lo_rmsnorm.restype = None
+        h.lo_rmsnorm.argtypes = [P, P, SZ, SZ, C.c_float]
+        h.lo_add.restype = None
+        h.lo_add.argtypes = [P, P, SZ]
         h.lo_silu.restype = C.c_float
         h.lo_silu.argtypes = [C.c_float]
         h.lo_silu_mul.restype = None
@@ -145,6 +149,24 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     uu = np.ascontiguousarray(u, np.float32)
     assert out.size == uu.size
     lib().lo_silu_mul(_p(out), _p(uu), out.size)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Row-wise x * (1/sqrt(mean(x^2) + eps)) * w of x [nrows, n] (new array)."""
+    out = np.array(x, np.float32, copy=True, order="C")
+    ww = np.ascontiguousarray(w, np.float32)
+    n = ww.size
+    assert out.size % n == 0
+    lib().lo_rmsnorm(_p(out), _p(ww), n, out.size // n, eps)
+    return out
+
+
+def add(y: np.ndarray, a: np.ndarray) -> np.ndarray:
+    out = np.array(y, np.float32, copy=True, order="C")
+    aa = np.ascontiguousarray(a, np.float32)
+    assert out.size == aa.size
+    lib().lo_add(_p(out), _p(aa), out.size)
     return out
 
 

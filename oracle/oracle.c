@@ -256,6 +256,27 @@ void lo_spark_affine8_gemv(float *y, const float *x, const uint8_t *w,
   free(xsum);
 }
 
+/* In-place RMSNorm of nrows rows of n: the Metal kernel a_rmsnorm
+ * (logan-metal/metal/backend_metal.mm:705-714, x * rsqrt(mean(x^2) + eps) *
+ * w), with the sum of squares in double and the scale formed as
+ * logan-core/src/math.rs:207-216 forms it (that CPU routine multiplies by
+ * 1 + w; the Metal kernel that coli_metal_rmsnorm runs multiplies by w). */
+void lo_rmsnorm(float *x, const float *w, size_t n, size_t nrows, float eps) {
+  for (size_t r = 0; r < nrows; ++r) {
+    float *xr = x + r * n;
+    double ms = 0.0;
+    for (size_t i = 0; i < n; ++i) ms += (double)xr[i] * (double)xr[i];
+    float q = (float)ms / (float)n + eps;
+    float sc = 1.0f / sqrtf(q);
+    for (size_t i = 0; i < n; ++i) xr[i] = xr[i] * sc * w[i];
+  }
+}
+
+/* y[i] += a[i] (backend_metal.mm:782-783, a_add) */
+void lo_add(float *y, const float *a, size_t n) {
+  for (size_t i = 0; i < n; ++i) y[i] = y[i] + a[i];
+}
+
 /* logan-qwen4/src/lib.rs:4516-4518 */
 float lo_silu(float x) {
   float e = expf(-x);

@@ -66,6 +66,8 @@ void lo_affine_qmm_bf16(float *y, const float *x, const uint8_t *w,
                         int fp16);
 
 /* logan-qwen4/src/lib.rs:4516-4518. */
+void lo_rmsnorm(float *x, const float *w, size_t n, size_t nrows, float eps);
+void lo_add(float *y, const float *a, size_t n);
 float lo_silu(float x);
 void lo_silu_mul(float *g, const float *u, size_t n);
 /* logan-qwen4/src/lib.rs:4558-4574 (= logan-qwen/src/lib.rs:260-276). */

@@ -466,3 +466,56 @@ def test_gemv_multi_rejects_mixed_geometry(gpu):
             affine_gemv_multi(bad, x)
     with pytest.raises(Exception):
         affine_gemv_multi([a, b], x)
+
+
+def test_host_route_island_survives_calls_between_begin_and_finish(gpu):
+    """The reference's caller runs the shared expert (and may run other
+    GEMVs) between begin and finish (backend_metal.mm:3745-3747). Here:
+    begin A, shared expert, a dense matmul, begin B on other experts, finish
+    B, then finish A: every output against the oracle."""
+    from logan_amd import backend
+
+    rng = np.random.default_rng(123)
+    D, M, bits, gs = 2048, 512, 4, 64
+
+    def expert_descs(k):
+        descs, mats = [], []
+        for _ in range(k):
+            g = make_affine(rng, M, D, bits, gs)
+            u = make_affine(rng, M, D, bits, gs)
+            d = make_affine(rng, D, M, bits, gs)
+            mats.append((g, u, d))
+            for (w, sc, bi), (o, i) in ((g, (M, D)), (u, (M, D)), (d, (D, M))):
+                descs.append(backend.MlxAffineMatmulDesc(backend.Tensor(), np.zeros(0, np.float32),
+                                                         w, aux_bytes(sc, bi), bits, gs, False, i, o))
+        return descs, mats
+
+    xa = bf16_to_f32(make_x(rng, D))
+    xb = bf16_to_f32(make_x(rng, D))
+    da, ma = expert_descs(4)
+    db, mb = expert_descs(2)
+    ds, ms = expert_descs(1)
+    pa = backend.moe_route_begin(da, xa, D, M)
+    assert pa is not None
+    sh = np.zeros(D, np.float32)
+    assert backend.shared_expert(ds, xa, sh, D, M) is True
+    (wg, scg, big) = make_affine(rng, 1000, D, bits, gs)
+    y = np.zeros(1000, np.float32)
+    t = backend.Tensor()
+    assert backend.hip_matmul_mlx_affine(t, y, xa, wg, aux_bytes(scg, big), bits, gs, False, D, 1000)
+    pb = backend.moe_route_begin(db, xb, D, M)
+    assert pb is not None
+    outb = np.zeros(2 * D, np.float32)
+    assert backend.moe_route_finish(pb, outb) == 1
+    outa = np.zeros(4 * D, np.float32)
+    assert backend.moe_route_finish(pa, outa) == 1
+    for e, (g, u, d) in enumerate(ma):
+        assert normwise_rel(outa[e * D:(e + 1) * D], _expert_ref(xa, g, u, d, D, M, bits, gs)) < 1e-4
+    for e, (g, u, d) in enumerate(mb):
+        assert normwise_rel(outb[e * D:(e + 1) * D], _expert_ref(xb, g, u, d, D, M, bits, gs)) < 1e-4
+    g, u, d = ms[0]
+    assert normwise_rel(sh, _expert_ref(xa, g, u, d, D, M, bits, gs)) < 1e-4
+    assert normwise_rel(y, oracle.affine_gemv(xa, wg, scg, big, 1000, D, bits, gs)) < 1e-4
+    t.free()
+    for dsc in da + db + ds:
+        dsc.tensor.free()

@@ -456,3 +456,63 @@ def test_moe_large_batch_per_token_passes(gpu, mfma_min_b):
     lb = make_logits(rng, B, 512, zipf_s=1.1)
     out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
     _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(0, B, 3))
+
+
+def test_moe_fused_after_other_paths_on_one_workspace(gpu, fused_mode):
+    """The single-launch B=1 path's tagged h pairs must never be confused with
+    what else a workspace holds: the workspace starts filled with small odd
+    integers (what a stale tag of an early launch looks like), then takes a
+    per-token (B=16) and an MFMA (B=64) call, then B=1 calls; every result
+    against the oracle."""
+    import torch
+    from logan_amd import _lib
+    from logan_amd.device import moe_block
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=41)
+    rng = np.random.default_rng(42)
+    ws = torch.arange(1, 2 * (layer.dev.workspace_bytes(64) // 4) + 1, 2, dtype=torch.int32,
+                      device="cuda")[: layer.dev.workspace_bytes(64) // 4].contiguous()
+    ws8 = ws.view(torch.uint8)
+    for B in (16, 64, 1, 1, 1):
+        xb = make_x(rng, B, 2048)
+        lb = make_logits(rng, B, 512)
+        x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+        lg = to_dev(lb.view(np.int16), torch).view(torch.bfloat16)
+        out, idx, _ = moe_block(layer.dev, x, lg, workspace=ws8, return_routing=True,
+                                out_dtype=torch.float32)
+        out, idx = out.cpu().numpy(), idx.cpu().numpy()
+        xf, lf = bf16_to_f32(xb), bf16_to_f32(lb)
+        for t in range(B):
+            ref, ridx, _ = layer.ref(xf[t], lf[t])
+            np.testing.assert_array_equal(idx[t], ridx)
+            assert normwise_rel(out[t], ref) <= 5e-5, f"B={B} token {t}"
+    assert _lib.lib().logan_hip_moe_sync_errors() == 0
+
+
+def test_moe_fused_launches_on_two_streams(gpu, fused_mode):
+    """Single-launch B=1 calls alternating between two streams with no
+    synchronisation in between: the library orders them (the launches share
+    device-scope counters), every output against a single-stream run."""
+    import torch
+    from logan_amd import _lib
+    from logan_amd.device import moe_block
+
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=43)
+    rng = np.random.default_rng(44)
+    n = 12
+    xs = [to_dev(make_x(rng, 1, 2048).view(np.int16), torch).view(torch.bfloat16) for _ in range(n)]
+    ls = [to_dev(make_logits(rng, 1, 512).view(np.int16), torch).view(torch.bfloat16) for _ in range(n)]
+    want = [moe_block(layer.dev, xs[i], ls[i], out_dtype=torch.float32) for i in range(n)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    wss = [torch.empty(layer.dev.workspace_bytes(1), dtype=torch.uint8, device="cuda")
+           for _ in range(2)]
+    outs = [torch.empty((1, 2048), dtype=torch.float32, device="cuda") for _ in range(n)]
+    for i in range(n):
+        s = s1 if i % 2 == 0 else s2
+        with torch.cuda.stream(s):
+            moe_block(layer.dev, xs[i], ls[i], out=outs[i], workspace=wss[i % 2], stream=s)
+    torch.cuda.synchronize()
+    for i in range(n):
+        assert torch.equal(outs[i], want[i]), i
+    assert _lib.lib().logan_hip_moe_sync_errors() == 0

@@ -373,3 +373,31 @@ def test_silu_mul_closed_form():
                               np.array([5.0, 2.0, 1.0, 0.0], np.float32))
     assert special[0] == 0.0 and special[1] == 200.0
     assert special[2] == 0.0 and special[3] == 0.0
+
+
+def test_rmsnorm_closed_form_and_float64():
+    """Constant rows c with eps = 0 normalise to sign(c) * w exactly (c a power
+    of two: mean(x^2) = c^2 exact); random rows match a float64 statement of
+    x / sqrt(mean(x^2) + eps) * w. A missing 1/n, a dropped eps or weights
+    applied per row instead of per column fail one of these."""
+    w = np.arange(1, 9, dtype=np.float32) * np.float32(0.5)
+    x = np.stack([np.full(8, 4.0, np.float32), np.full(8, -0.25, np.float32)])
+    np.testing.assert_array_equal(oracle.rmsnorm(x, w, 0.0), np.stack([w, -w]))
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((5, 2048)).astype(np.float32) * 3
+    w = rng.standard_normal(2048).astype(np.float32)
+    eps = 1e-5
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + eps) * w
+    got = oracle.rmsnorm(x, w, eps)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    # eps matters where the rows are small
+    tiny = np.full((1, 2048), 1e-3, np.float32)
+    assert not np.allclose(oracle.rmsnorm(tiny, w, 1e-5), oracle.rmsnorm(tiny, w, 0.0))
+
+
+def test_add_is_elementwise_sum():
+    rng = np.random.default_rng(8)
+    y = rng.standard_normal(1000).astype(np.float32)
+    a = rng.standard_normal(1000).astype(np.float32)
+    np.testing.assert_array_equal(oracle.add(y, a), y + a)
