@@ -266,6 +266,20 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
                         int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
                         float *w_out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): logan_hip_moe_block without a workspace argument. Its
+ * workspace is a library-owned file-scope device array of
+ * LOGAN_HIP_MOE_STATIC_SCRATCH_BYTES on each device (held until the process
+ * ends); the call allocates nothing. Calls whose workspace would exceed it
+ * (B above a few hundred tokens at the config-3 shapes: 57 MB at B = 512)
+ * return 0 and print why. Every call on a device shares that device's array:
+ * calls whose executions overlap on one device (other streams) race. */
+#define LOGAN_HIP_MOE_STATIC_SCRATCH_BYTES (64u << 20)
+int logan_hip_moe_block_static(const LoganHipMoeBlock *blk, const void *x, const void *logits,
+                               int logits_dtype, int B, void *out, int out_dtype,
+                               int32_t *idx_out, float *w_out, void *stream);
+
 /* Controls of the routed-MoE block's single-launch B = 1 path (one kernel
  * with an in-kernel hand-off between the gate/up and down phases). It is on
  * by default (LOGAN_HIP_MOE_FUSED=0 in the environment turns it off);

@@ -103,6 +103,29 @@ inline uint64_t now_ns() {
       .count();
 }
 
+// Workspace of logan_hip_moe_block_static: a file-scope device array (each
+// device that runs the library holds its own copy until the process ends).
+// In host code `scratch` only names the variable; its device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kStaticScratchBytes = LOGAN_HIP_MOE_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mtx;
+void *g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch` (nullptr when it cannot be had).
+void *scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mtx);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
 bool init_locked() {
   if (g_tried) return g_ok;
   g_tried = true;
@@ -118,6 +141,7 @@ bool init_locked() {
     return false;
   }
   if (hipSetDevice(dev) != hipSuccess) return false;
+  if (!scratch_on_current_device()) return false;
   // default-priority stream
   if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) return false;
   if (hipEventCreate(&g_prof_ev0) != hipSuccess || hipEventCreate(&g_prof_ev1) != hipSuccess)
@@ -286,6 +310,7 @@ lh::DevBank devbank(const LoganHipAffineBank &b) {
 }
 
 int rc_from(hipError_t e) { return e == hipSuccess ? 1 : -1; }
+
 
 }  // namespace
 
@@ -774,6 +799,37 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
   a.ws = g_ws.p;
   a.ws_bytes = g_ws.n;
   return lh::launch_moe_block(a, st);
+}
+
+int logan_hip_moe_block_static(const LoganHipMoeBlock *blk, const void *x, const void *logits,
+                               int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
+                               float *w_out, void *stream) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || !x || !logits || !out || B <= 0) return 0;
+  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
+  if (out_dtype != LOGAN_HIP_F32 && out_dtype != LOGAN_HIP_BF16) return 0;
+  const size_t need =
+      lh::moe_workspace_bytes(B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
+  if (need > kStaticScratchBytes) {
+    std::fprintf(stderr,
+                 "[logan-hip] moe_block_static: B=%d needs a %zu-byte workspace; the static "
+                 "scratch holds %zu bytes (use logan_hip_moe_block with a workspace)\n",
+                 B, need, kStaticScratchBytes);
+    return 0;
+  }
+  void *ws = scratch_on_current_device();
+  if (!ws) return 0;
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.logits = logits;
+  a.logits_f32 = logits_dtype == LOGAN_HIP_F32;
+  a.B = B;
+  a.out = out;
+  a.out_f32 = out_dtype == LOGAN_HIP_F32;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  a.ws = ws;
+  a.ws_bytes = kStaticScratchBytes;
+  return lh::launch_moe_block(a, reinterpret_cast<hipStream_t>(stream));
 }
 
 void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }

@@ -267,3 +267,35 @@ def moe_block(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
     if return_routing:
         return out, idx, w
     return out
+
+
+def moe_block_static(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
+                     out: Optional[torch.Tensor] = None, return_routing: bool = False,
+                     out_dtype: torch.dtype = torch.bfloat16, stream=None):
+    """moe_block on the library's static device scratch (no workspace, no
+    allocation inside the call; logan_hip_moe_block_static)."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("logits must be bf16 or f32")
+    B, D = x.shape
+    if out is None:
+        out = torch.empty((B, D), dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("out must be bf16 or f32")
+    od = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    idx = w = None
+    if return_routing:
+        idx = torch.empty((B, layer.top_k), dtype=torch.int32, device=x.device)
+        w = torch.empty((B, layer.top_k), dtype=torch.float32, device=x.device)
+    blk = layer.c()
+    dt = L.LOGAN_HIP_BF16 if logits.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    rc = L.lib().logan_hip_moe_block_static(C.byref(blk), _dev(x, "x"), _dev(logits, "logits"), dt,
+                                            B, _dev(out, "out"), od,
+                                            idx.data_ptr() if idx is not None else None,
+                                            w.data_ptr() if w is not None else None,
+                                            _stream(stream))
+    _check(rc, "moe_block_static")
+    if return_routing:
+        return out, idx, w
+    return out
