@@ -77,11 +77,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--gemv-launches", type=int, default=2048)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4",
-                    help="secondary legs to run (comma list of gemv, dense8, moe3, stack5, moe4; "
-                         "'none' for none)")
+    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4,dropin",
+                    help="secondary legs to run (comma list of gemv, dense8, moe3, stack5, moe4, "
+                         "dropin; 'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
     ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
@@ -458,6 +458,117 @@ def bench_gemv(torch, device, synth, args):
     return dict(us_per_launch=us, gbps=gbps, launches=launches)
 
 
+def bench_dropin(torch, synth, args):
+    """The host-pointer drop-in layer, called the way logan-metal's engines
+    call it (host f32 activations and outputs, weights cached behind tensor
+    handles after the first call): config 1 through coli_metal_matmul, and a
+    config-3 B=1 layer through coli_metal_moe_route_begin -> the shared
+    expert (between begin and finish, as the reference's caller does) ->
+    finish, with the caller's own softmax top-10 and rank-ordered combine on
+    the host (logan-qwen4/src/lib.rs:7993-8043, :8692-8711). Each figure is
+    wall-clock per call (PCIe copies and synchronisation included) and device
+    time only (the library's profile counters: events around the kernels)."""
+    import ctypes as C
+
+    import numpy as np
+    from logan_amd import _lib as L
+    from logan_amd import backend
+
+    lib = L.lib()
+    lib.coli_metal_matmul.restype = C.c_int32
+    lib.coli_metal_matmul.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                      C.c_int32]
+    rng = np.random.default_rng(77)
+    res = {}
+    # ---- config 1
+    w, sc, bi = synth.make_affine(rng, GEMV_O, GEMV_I, BITS, GS)
+    aux = synth.aux_bytes(sc, bi)
+    x = synth.bf16_to_f32(synth.make_x(rng, GEMV_I))
+    y = np.zeros(GEMV_O, np.float32)
+    t = C.c_void_p()
+    assert lib.coli_metal_matmul(C.byref(t), y.ctypes.data, x.ctypes.data, w.ctypes.data,
+                                 aux.ctypes.data, 16, 1, GEMV_I, GEMV_O, GS) == 1
+    n = 400
+
+    def timed(fn, n):
+        lib.logan_hip_profile_reset()
+        lib.logan_hip_profile_set_on(1)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        wall = (time.perf_counter() - t0) / n * 1e6
+        lib.logan_hip_profile_set_on(0)
+        v = [C.c_uint64(0) for _ in range(4)]
+        lib.logan_hip_profile_get(*[C.byref(c) for c in v])
+        return wall, v[3].value / n / 1e3
+
+    wall, kern = timed(lambda: lib.coli_metal_matmul(C.byref(t), y.ctypes.data, x.ctypes.data,
+                                                     w.ctypes.data, aux.ctypes.data, 16, 1,
+                                                     GEMV_I, GEMV_O, GS), n)
+    lib.logan_hip_tensor_free(t)
+    res["gemv_config1"] = dict(us_per_call_wall=round(wall, 2), us_device=round(kern, 2),
+                               gbps_device=round(GEMV_BYTES / (kern * 1e-6) / 1e9, 1),
+                               calls=n, path="coli_metal_matmul (fmt 16)")
+    log(f"drop-in gemv: {wall:.1f} us/call wall, {kern:.2f} us device")
+    # ---- config-3 layer, B = 1
+    nexp = 64
+    g = synth.make_affine(rng, INTER, D, BITS, GS, E=nexp)
+    u = synth.make_affine(rng, INTER, D, BITS, GS, E=nexp)
+    dn = synth.make_affine(rng, D, INTER, BITS, GS, E=nexp)
+    sg, su, sd = (synth.make_affine(rng, INTER, D, BITS, GS), synth.make_affine(rng, INTER, D, BITS, GS),
+                  synth.make_affine(rng, D, INTER, BITS, GS))
+    se_g = synth.bf16_to_f32(synth.bf16_bits(rng.standard_normal(D).astype(np.float32) * 0.05))
+
+    def desc(t3, e, o, i):
+        ww, ss, bb = t3
+        if e is not None:
+            ww, ss, bb = ww[e], ss[e], bb[e]
+        return backend.MlxAffineMatmulDesc(backend.Tensor(), np.zeros(0, np.float32), ww,
+                                           synth.aux_bytes(ss, bb), BITS, GS, False, i, o)
+
+    experts = [[desc(g, e, INTER, D), desc(u, e, INTER, D), desc(dn, e, D, INTER)] for e in range(nexp)]
+    shared = [desc(sg, None, INTER, D), desc(su, None, INTER, D), desc(sd, None, D, INTER)]
+    xs = [synth.bf16_to_f32(synth.make_x(rng, D)) for _ in range(16)]
+    lgs = [synth.bf16_to_f32(synth.make_logits(rng, 1, nexp)[0]) for _ in range(16)]
+    out = np.zeros(D, np.float32)
+
+    def layer(i):
+        xv, lg = xs[i % 16], lgs[i % 16]
+        p = np.exp(lg - lg.max())
+        p /= p.sum()
+        idx = np.argsort(-p, kind="stable")[:TOPK]
+        wts = p[idx] / p[idx].sum()
+        pend = backend.moe_route_begin([d for e in idx for d in experts[e]], xv, D, INTER)
+        sy = np.zeros(D, np.float32)
+        assert backend.shared_expert(shared, xv, sy, D, INTER)
+        ys = np.zeros(TOPK * D, np.float32)
+        assert backend.moe_route_finish(pend, ys) == 1
+        acc = np.zeros(D, np.float32)
+        for r in range(TOPK):
+            acc += ys[r * D:(r + 1) * D] * wts[r]
+        gs_ = 1.0 / (1.0 + np.exp(-float(se_g @ xv)))
+        out[:] = acc + sy * np.float32(gs_)
+
+    for i in range(nexp):  # first use uploads every expert's handles
+        layer(i)
+    nl = 100
+    wall, kern = timed(lambda: layer(np.random.randint(16)), nl)
+    per_layer_bytes = (TOPK + 1) * PER_EXPERT
+    res["moe_b1_config3"] = dict(us_per_layer_wall=round(wall, 1), us_device=round(kern, 1),
+                                 gbps_device=round(per_layer_bytes / (kern * 1e-6) / 1e9, 1),
+                                 layers=nl, experts_resident=nexp,
+                                 path="coli_metal_moe_route_begin + coli_metal_shared_mxfp4 + "
+                                      "coli_metal_moe_route_finish, host routing and combine")
+    log(f"drop-in moe layer: {wall:.1f} us wall, {kern:.1f} us device")
+    for e in experts:
+        for d in e:
+            d.tensor.free()
+    for d in shared:
+        d.tensor.free()
+    return res
+
+
 def measured_traffic():
     """HBM bytes per fused-MoE launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a plain copy of known
@@ -468,11 +579,30 @@ def measured_traffic():
     return json.loads(f.read_text()).get("hbm_bytes_per_launch")
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, layer, seconds):
-    """The oracle (single thread) on tokens of layer 0 until `seconds` pass."""
+    """The reference's CPU path restated by the oracle (oracle/oracle.c), on
+    the host cores of this box, on bounded samples of the same workloads:
+    the config-3 MoE token (softmax top-10, 11 expert MLPs, rank-ordered
+    combine, shared expert) and the config-1 q4 GEMV, each with 1 thread
+    (what the reference runs: logan-qwen4/src/lib.rs:3752-3763, :8759) and
+    row-parallel over the host threads (its own row split, :3785-3807).
+    Each figure is the median of 5 runs; `seconds` bounds the whole leg."""
+    import os
+
     import numpy as np
 
     import oracle
+    from logan_amd import synth
 
     def host(b):
         return (b.weights.cpu().numpy(), b.scales.cpu().numpy().view(np.uint16),
@@ -483,23 +613,59 @@ def cpu_baseline(torch, layer, seconds):
                                                           layer.shared_down))
     se_g = layer.shared_gate_vec.float().cpu().numpy()
     rng = np.random.default_rng(0)
-    from logan_amd import synth
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = nproc
+    # the box's share for one GPU is 16 threads (the reference's default is
+    # n - 1 of the available threads, lib.rs:3660-3675)
+    par = max(1, min(16, avail - 1 if avail > 1 else 1))
+    xs = [synth.bf16_to_f32(synth.make_x(rng, D)) for _ in range(4)]
+    lgs = [synth.bf16_to_f32(synth.make_logits(rng, 1, E)[0]) for _ in range(4)]
+    gw, gsc, gbi = synth.make_affine(rng, GEMV_O, GEMV_I, BITS, GS)
+    gx = synth.bf16_to_f32(synth.make_x(rng, GEMV_I))
 
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        x = synth.bf16_to_f32(synth.make_x(rng, D))
-        lg = synth.bf16_to_f32(synth.make_logits(rng, 1, E)[0])
-        oracle.moe_token(x, lg, TOPK, D, INTER, BITS, GS, gate, up, down, shared, se_g, nthreads=1)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    us_tok = el / n * 1e6
-    return dict(value=LAYER_BYTES_B1 * n / el / 1e9, unit="GB/s", cores=1, kind="port",
-                us_per_token_layer=us_tok,
-                sample=f"{n} tokens of one config-3 MoE layer (B=1, 4-bit, E=512, top-10 + shared), "
-                       f"oracle lo_moe_token, 1 thread, {el:.1f} s")
+    def runs(fn, total_s):
+        """5 runs sharing about total_s: median seconds per call."""
+        t0 = time.perf_counter()
+        fn(0)
+        once = max(time.perf_counter() - t0, 1e-6)
+        n = max(1, int(total_s / 5 / once))
+        res = []
+        for r in range(5):
+            t0 = time.perf_counter()
+            for i in range(n):
+                fn(i)
+            res.append((time.perf_counter() - t0) / n)
+        return float(np.median(res)), n
+
+    budget = max(seconds, 5.0) / 2.0  # per thread count, over both workloads
+    out = {}
+    for name, th in (("1thread", 1), ("parallel", par)):
+        moe_s, moe_n = runs(lambda i: oracle.moe_token(xs[i % 4], lgs[i % 4], TOPK, D, INTER, BITS,
+                                                       GS, gate, up, down, shared, se_g,
+                                                       nthreads=th), budget * 0.8)
+        gemv_s, gemv_n = runs(lambda i: oracle.affine_gemv(gx, gw, gsc, gbi, GEMV_O, GEMV_I, BITS,
+                                                           GS, nthreads=th), budget * 0.2)
+        out[name] = dict(threads=th, moe_us_per_token_layer=round(moe_s * 1e6, 1),
+                         moe_gbps=round(LAYER_BYTES_B1 / moe_s / 1e9, 4), moe_calls_per_run=moe_n,
+                         gemv_us=round(gemv_s * 1e6, 1),
+                         gemv_gbps=round(GEMV_BYTES / gemv_s / 1e9, 4), gemv_calls_per_run=gemv_n)
+        log(f"cpu {name} ({th} threads): moe {moe_s * 1e6:.0f} us/token-layer, "
+            f"gemv {gemv_s * 1e6:.0f} us")
+    one = out["1thread"]
+    return dict(value=one["moe_gbps"], unit="GB/s", cores=1, kind="port",
+                us_per_token_layer=one["moe_us_per_token_layer"],
+                sample=(f"config-3 MoE token (B=1, 4-bit, E=512, top-10 + shared) through the "
+                        f"oracle's lo_moe_token, median of 5 runs of {one['moe_calls_per_run']} "
+                        f"tokens, 1 thread"),
+                row_parallel=out["parallel"], single_thread=one,
+                gemv_config1={"1thread_us": one["gemv_us"], "1thread_gbps": one["gemv_gbps"],
+                              "parallel_us": out["parallel"]["gemv_us"],
+                              "parallel_gbps": out["parallel"]["gemv_gbps"],
+                              "parallel_threads": par},
+                nproc=nproc, threads_available=avail, cpu_model=cpu_model(), stat="median of 5")
 
 
 def main():
@@ -555,6 +721,8 @@ def main():
             secondary["stack_config5"] = bench_config5(torch, device, synth, args, layers)
         if "moe4" in legs:
             secondary["moe_config4"] = bench_config4(torch, device, synth, args)
+        if "dropin" in legs:
+            secondary["dropin"] = bench_dropin(torch, synth, args)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")

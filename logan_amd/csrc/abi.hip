@@ -54,6 +54,7 @@ struct DevBuf {
   }
 };
 DevBuf g_xbuf, g_ybuf, g_ws;
+DevBuf g_hlbuf, g_y2buf;  // hi/lo activation pairs and pair products of matmul_multi
 
 // Device buffers of one route-island submission: x [D], gate/up outputs
 // [2 K M], expert outputs [K D]. Each pending handle owns one set from the
@@ -61,6 +62,11 @@ DevBuf g_xbuf, g_ybuf, g_ws;
 // shared expert, other GEMVs, another begin) never touch it.
 struct RouteBufs {
   DevBuf x, gu, out;
+  void release() {
+    x.release();
+    gu.release();
+    out.release();
+  }
 };
 std::vector<RouteBufs *> g_route_pool;  // idle sets
 
@@ -82,6 +88,7 @@ RouteBufs *route_bufs_take(size_t xb, size_t gub, size_t outb) {
 
 struct RoutePending {
   hipEvent_t ev = nullptr;
+  hipEvent_t pev0 = nullptr, pev1 = nullptr;  // around the kernels, when profiling
   RouteBufs *bufs = nullptr;
   int K = 0, D = 0;
 };
@@ -92,6 +99,8 @@ void route_release_locked(RoutePending *p) {
     hipEventSynchronize(p->ev);
     hipEventDestroy(p->ev);
   }
+  if (p->pev0) hipEventDestroy(p->pev0);
+  if (p->pev1) hipEventDestroy(p->pev1);
   if (p->bufs) g_route_pool.push_back(p->bufs);
   delete p;
 }
@@ -293,6 +302,78 @@ lh::DevMat devmat(const LoganHipAffine &a) {
   return m;
 }
 
+lh::DevMat tensor_mat(const LoganHipTensor *t) {
+  lh::DevMat m{};
+  m.w = t->w;
+  m.sc = t->sc;
+  m.bi = t->bi;
+  m.I = t->I;
+  m.O = t->O;
+  m.gs = t->gs;
+  m.bits = t->bits;
+  m.fp16 = t->fp16;
+  m.row_bytes = (long long)t->I * t->bits / 8;
+  m.ng = t->I / t->gs;
+  return m;
+}
+
+// staging offsets in elements, rounded so every sub-buffer is 256-byte aligned
+inline size_t al_elems(size_t n, size_t esize) {
+  const size_t per = 256 / esize;
+  return (n + per - 1) / per * per;
+}
+
+// Products that share one activation (hi/lo row pairs xhl, 2 S rows) on the
+// bf16 kernels, grouped into multi-matrix launches of like geometry.
+hipError_t launch_shared_x_groups(const std::vector<lh::DevMat> &ms, const std::vector<void *> &ys,
+                                  const uint16_t *xhl, int I, int M2, hipStream_t st) {
+  std::vector<char> done(ms.size(), 0);
+  for (size_t i = 0; i < ms.size(); ++i) {
+    if (done[i]) continue;
+    lh::DevMat gm[lh::kGemvMultiMax];
+    void *gy[lh::kGemvMultiMax];
+    int n = 0;
+    for (size_t j = i; j < ms.size() && n < lh::kGemvMultiMax; ++j) {
+      if (done[j] || ms[j].bits != ms[i].bits || ms[j].gs != ms[i].gs || ms[j].fp16 != ms[i].fp16)
+        continue;
+      gm[n] = ms[j];
+      gy[n] = ys[j];
+      ++n;
+      done[j] = 1;
+    }
+    hipError_t e = lh::launch_gemv_bf16_multi(gm, gy, n, xhl, I, M2, 0, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// One f32 activation row per product (xs[i]) on the dot2 kernel's f32 form,
+// grouped into multi-matrix launches of like geometry; outputs f32.
+hipError_t launch_f32x_groups(const std::vector<lh::DevMat> &ms, const std::vector<const float *> &xs,
+                              const std::vector<void *> &ys, hipStream_t st) {
+  std::vector<char> done(ms.size(), 0);
+  for (size_t i = 0; i < ms.size(); ++i) {
+    if (done[i]) continue;
+    lh::DevMat gm[lh::kGemvMultiMax];
+    const float *gx[lh::kGemvMultiMax];
+    void *gy[lh::kGemvMultiMax];
+    int n = 0;
+    for (size_t j = i; j < ms.size() && n < lh::kGemvMultiMax; ++j) {
+      if (done[j] || ms[j].I != ms[i].I || ms[j].bits != ms[i].bits || ms[j].gs != ms[i].gs ||
+          ms[j].fp16 != ms[i].fp16)
+        continue;
+      gm[n] = ms[j];
+      gx[n] = xs[j];
+      gy[n] = ys[j];
+      ++n;
+      done[j] = 1;
+    }
+    hipError_t e = lh::launch_gemv_f32x_multi(gm, nullptr, gx, gy, n, 0, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 bool affine_ok(const LoganHipAffine *a) {
   if (!a || !a->weights || !a->scales || !a->biases) return false;
   if (!(a->bits == 4 || a->bits == 5 || a->bits == 6 || a->bits == 8)) return false;
@@ -334,9 +415,7 @@ void logan_hip_shutdown(void) {
   g_ybuf.release();
   g_ws.release();
   for (RouteBufs *b : g_route_pool) {
-    b->x.release();
-    b->gu.release();
-    b->out.release();
+    b->release();
     delete b;
   }
   g_route_pool.clear();
@@ -420,26 +499,69 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
                                   descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
     if (!ts[i]) return 0;
   }
-  // staging: shared x, then private x's; outputs concatenated
-  size_t xn = shared_I > 0 ? (size_t)S * shared_I : 0, yn = 0;
-  std::vector<size_t> xoff(count, 0), yoff(count, 0);
+  // staging (f32): shared x, then private x's; outputs concatenated. Products
+  // whose geometry the bf16 kernels take run there: a one-row activation on
+  // the dot2 kernel's f32 form (the row split into bf16 hi + lo in
+  // registers, both halves' products added), several rows as bf16 (hi, lo)
+  // row pairs through the row-batched kernels with each output row re-joined
+  // as y = y_hi + y_lo. The rest take the exact per-element kernel.
+  std::vector<lh::DevMat> mat(count);
+  std::vector<char> fast(count);
+  bool shared_pairs = false;
+  for (int i = 0; i < count; ++i) {
+    mat[i] = tensor_mat(ts[i]);
+    fast[i] = lh::gemv_bf16_supported(mat[i]);
+    shared_pairs = shared_pairs || (fast[i] && !descs[i].x && S > 1);
+  }
+  size_t xn = shared_I > 0 ? al_elems((size_t)S * shared_I, 4) : 0, yn = 0;
+  size_t hln = shared_pairs ? al_elems((size_t)2 * S * shared_I, 2) : 0, y2n = 0;
+  std::vector<size_t> xoff(count, 0), yoff(count, 0), hloff(count, 0), y2off(count, 0);
   for (int i = 0; i < count; ++i) {
     const int s = descs[i].x ? descs[i].S : S;
     if (descs[i].x) {
       xoff[i] = xn;
-      xn += (size_t)s * descs[i].I;
+      xn += al_elems((size_t)s * descs[i].I, 4);
+      if (fast[i] && s > 1) {
+        hloff[i] = hln;
+        hln += al_elems((size_t)2 * s * descs[i].I, 2);
+      }
     }
     yoff[i] = yn;
-    yn += (size_t)s * descs[i].O;
+    yn += al_elems((size_t)s * descs[i].O, 4);
+    if (fast[i] && s > 1) {
+      y2off[i] = y2n;
+      y2n += al_elems((size_t)2 * s * descs[i].O, 4);
+    }
   }
   if (!g_xbuf.ensure(xn * 4 + 16) || !g_ybuf.ensure(yn * 4 + 16)) return 0;
+  if (hln && (!g_hlbuf.ensure(hln * 2 + 16) || !g_y2buf.ensure(y2n * 4 + 16))) return 0;
   float *dx = reinterpret_cast<float *>(g_xbuf.p);
   float *dy = reinterpret_cast<float *>(g_ybuf.p);
+  uint16_t *dhl = reinterpret_cast<uint16_t *>(g_hlbuf.p);
+  float *dy2 = reinterpret_cast<float *>(g_y2buf.p);
   std::vector<lh::GenDesc> ds;
+  lh::HiloBatch split{}, join{};
+  std::vector<lh::DevMat> shared_m, row_m;
+  std::vector<void *> shared_y, row_y;
+  std::vector<const float *> row_x;
+  if (shared_pairs) split.j[split.n++] = lh::HiloJob{dx, dhl, S, shared_I};
   for (int i = 0; i < count; ++i) {
     const int s = descs[i].x ? descs[i].S : S;
     const float *xs = descs[i].x ? dx + xoff[i] : dx;
-    ds.push_back(gen_desc(ts[i], xs, nullptr, dy + yoff[i], s, ts[i]->I, ts[i]->O, 0));
+    if (!fast[i]) {
+      ds.push_back(gen_desc(ts[i], xs, nullptr, dy + yoff[i], s, ts[i]->I, ts[i]->O, 0));
+    } else if (s == 1) {
+      row_m.push_back(mat[i]);
+      row_x.push_back(xs);
+      row_y.push_back(dy + yoff[i]);
+    } else {
+      if (descs[i].x) split.j[split.n++] = lh::HiloJob{xs, dhl + hloff[i], s, descs[i].I};
+      else {
+        shared_m.push_back(mat[i]);
+        shared_y.push_back(dy2 + y2off[i]);
+      }
+      join.j[join.n++] = lh::HiloJob{dy2 + y2off[i], dy + yoff[i], s, descs[i].O};
+    }
   }
   uint64_t t1 = now_ns();
   prof_add(0, t1 - t0);
@@ -452,7 +574,16 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
                          hipMemcpyHostToDevice, g_stream);
   if (e != hipSuccess) return -1;
   if (g_prof_on) hipEventRecord(g_prof_ev0, g_stream);
-  e = launch_descs(ds, g_stream);
+  if (!row_m.empty()) e = launch_f32x_groups(row_m, row_x, row_y, g_stream);
+  if (e == hipSuccess && split.n) e = lh::launch_hilo_split(split, g_stream);
+  if (e == hipSuccess && !shared_m.empty())
+    e = launch_shared_x_groups(shared_m, shared_y, dhl, shared_I, 2 * S, g_stream);
+  for (int i = 0; i < count && e == hipSuccess; ++i)
+    if (fast[i] && descs[i].x && descs[i].S > 1)
+      e = lh::launch_gemv_bf16(mat[i], dhl + hloff[i], descs[i].I, 2 * descs[i].S, dy2 + y2off[i],
+                               descs[i].O, 0, g_stream);
+  if (e == hipSuccess && !ds.empty()) e = launch_descs(ds, g_stream);
+  if (e == hipSuccess && join.n) e = lh::launch_hilo_join(join, g_stream);
   if (e != hipSuccess) return -1;
   if (g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
   uint64_t t2 = now_ns();
@@ -493,6 +624,20 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
                                   descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
     if (!ts[i]) return nullptr;
   }
+  // fast path: every matrix on the bf16 kernels, gate/up and downs each of
+  // one geometry (x and h as bf16 hi/lo row pairs, f32 products)
+  std::vector<lh::DevMat> mat((size_t)K * 3);
+  bool fast = true;
+  for (int i = 0; i < K * 3; ++i) {
+    mat[i] = tensor_mat(ts[i]);
+    fast = fast && lh::gemv_bf16_supported(mat[i]);
+  }
+  for (int i = 0; fast && i < K; ++i)
+    for (int r = 0; r < 3; ++r) {
+      const lh::DevMat &a = mat[i * 3 + r], &b = mat[r == 2 ? 2 : 0];
+      fast = fast && a.bits == b.bits && a.gs == b.gs && a.fp16 == b.fp16;
+    }
+  fast = fast && M % 4 == 0;  // 16-byte aligned per-expert h rows
   RoutePending *p = new (std::nothrow) RoutePending();
   if (!p) return nullptr;
   p->bufs = route_bufs_take((size_t)D * 4 + 16, (size_t)2 * K * M * 4 + 16, (size_t)K * D * 4 + 16);
@@ -506,25 +651,50 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
   float *dx = reinterpret_cast<float *>(p->bufs->x.p);
   float *gu = reinterpret_cast<float *>(p->bufs->gu.p);
   float *out = reinterpret_cast<float *>(p->bufs->out.p);
-  // gate -> gu[i*M], up -> gu[K*M + i*M]; down(silu(gate)*up) -> out[i*D]
-  std::vector<lh::GenDesc> s1, s2;
-  for (int i = 0; i < K; ++i) {
-    s1.push_back(gen_desc(ts[i * 3 + 0], dx, nullptr, gu + (size_t)i * M, 1, D, M, 0));
-    s1.push_back(gen_desc(ts[i * 3 + 1], dx, nullptr, gu + (size_t)K * M + (size_t)i * M, 1, D, M, 0));
-    s2.push_back(gen_desc(ts[i * 3 + 2], gu + (size_t)i * M, gu + (size_t)K * M + (size_t)i * M,
-                          out + (size_t)i * D, 1, M, D, 1));
-  }
   uint64_t t1 = now_ns();
-  prof_add(0, t1 - t0);
   hipError_t e = hipMemcpyAsync(dx, x, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
-  if (e == hipSuccess) e = launch_descs(s1, g_stream);
-  if (e == hipSuccess) e = launch_descs(s2, g_stream);
+  if (g_prof_on && hipEventCreate(&p->pev0) == hipSuccess && hipEventCreate(&p->pev1) == hipSuccess)
+    hipEventRecord(p->pev0, g_stream);
+  if (fast) {
+    // gate/up products (f32 x on the dot2 kernel's f32 form) -> gu [K][M]
+    // and gu [K][M] + K M; h = silu(g) * u in place; downs read h -> out[e]
+    std::vector<lh::DevMat> gum, dm;
+    std::vector<const float *> gux, dxs;
+    std::vector<void *> guy, dys;
+    for (int i = 0; i < K; ++i) {
+      gum.push_back(mat[i * 3 + 0]);
+      gux.push_back(dx);
+      guy.push_back(gu + (size_t)i * M);
+      gum.push_back(mat[i * 3 + 1]);
+      gux.push_back(dx);
+      guy.push_back(gu + (size_t)K * M + (size_t)i * M);
+      dm.push_back(mat[i * 3 + 2]);
+      dxs.push_back(gu + (size_t)i * M);
+      dys.push_back(out + (size_t)i * D);
+    }
+    prof_add(0, t1 - t0);
+    if (e == hipSuccess) e = launch_f32x_groups(gum, gux, guy, g_stream);
+    if (e == hipSuccess) e = lh::launch_silu_mul(gu, gu + (size_t)K * M, (long long)K * M, false, g_stream);
+    if (e == hipSuccess) e = launch_f32x_groups(dm, dxs, dys, g_stream);
+  } else {
+    // gate -> gu[i*M], up -> gu[K*M + i*M]; down(silu(gate)*up) -> out[i*D]
+    std::vector<lh::GenDesc> s1, s2;
+    for (int i = 0; i < K; ++i) {
+      s1.push_back(gen_desc(ts[i * 3 + 0], dx, nullptr, gu + (size_t)i * M, 1, D, M, 0));
+      s1.push_back(gen_desc(ts[i * 3 + 1], dx, nullptr, gu + (size_t)K * M + (size_t)i * M, 1, D, M, 0));
+      s2.push_back(gen_desc(ts[i * 3 + 2], gu + (size_t)i * M, gu + (size_t)K * M + (size_t)i * M,
+                            out + (size_t)i * D, 1, M, D, 1));
+    }
+    prof_add(0, now_ns() - t0);
+    if (e == hipSuccess) e = launch_descs(s1, g_stream);
+    if (e == hipSuccess) e = launch_descs(s2, g_stream);
+  }
+  if (p->pev1) hipEventRecord(p->pev1, g_stream);
   if (e == hipSuccess) e = hipEventRecord(p->ev, g_stream);
   prof_add(1, now_ns() - t1);
   if (e != hipSuccess) {
-    // submitted work may be partially queued: drain it, report as a decline
-    // would hide a real failure, so the handle is still returned and finish
-    // reports -1.
+    // submitted work may be partially queued: drain it; a decline would hide
+    // a real failure, so the handle is still returned and finish reports -1
     hipStreamSynchronize(g_stream);
     p->K = -1;
     return p;
@@ -551,6 +721,9 @@ int logan_hip_moe_route_finish(void *pending, float *out, int count) {
       rc = -1;
   }
   prof_add(2, now_ns() - t0);
+  float ms = 0.f;
+  if (g_prof_on && p->pev1 && hipEventElapsedTime(&ms, p->pev0, p->pev1) == hipSuccess)
+    g_prof[3] += (uint64_t)(ms * 1e6);
   route_release_locked(p);
   return rc;
 }
@@ -568,9 +741,7 @@ void logan_hip_moe_route_drop_model(uint64_t model_id) {
   if (!g_ok) return;
   // idle buffer sets only; those of pending handles return on finish/discard
   for (RouteBufs *b : g_route_pool) {
-    b->x.release();
-    b->gu.release();
-    b->out.release();
+    b->release();
     delete b;
   }
   g_route_pool.clear();

@@ -155,31 +155,6 @@ __device__ __forceinline__ void xpair_bf16(const uint32_t (&xb)[32], int p, uint
   sp = xl + xh;
 }
 
-// f32 activations: x' = hi + lo (both bf16, RNE) so the pair dot keeps ~16
-// significant bits of x. xs is the sum of the true x (bias term); xsp is the
-// sum of hi + lo, i.e. of exactly what the products saw, so the offset
-// cancels without amplifying the split residual.
-template <int BITS>
-__device__ __forceinline__ void make_xchunk_f32(XChunk &hi, XChunk &lo,
-                                                const float (&xf)[32]) {
-  float s = 0.f, sp = 0.f;
-#pragma unroll
-  for (int p = 0; p < 16; ++p) {
-    const int kl = PairMap<BITS>::lo(p), kh = PairMap<BITS>::hi(p);
-    const float xl = xf[kl] * xscale(PairMap<BITS>::slo(p));
-    const float xh = xf[kh] * xscale(PairMap<BITS>::shi(p));
-    const uint32_t hl = f32_to_bf16_rne(xl), hh = f32_to_bf16_rne(xh);
-    const uint32_t ll = f32_to_bf16_rne(xl - bf16_to_f32(hl));
-    const uint32_t lh = f32_to_bf16_rne(xh - bf16_to_f32(hh));
-    hi.p[p] = hl | (hh << 16);
-    lo.p[p] = ll | (lh << 16);
-    s += xf[kl] + xf[kh];
-    sp += (bf16_to_f32(hl) + bf16_to_f32(ll)) + (bf16_to_f32(hh) + bf16_to_f32(lh));
-  }
-  hi.xs = lo.xs = s;
-  hi.xsp = lo.xsp = sp;
-}
-
 // Constants kept in registers so the unpack uses v_and_or_b32 (VOP3 on gfx9
 // takes no literal operands).
 struct UnpackConsts {

@@ -95,6 +95,47 @@ __global__ __launch_bounds__(kEwThreads) void add_f32_kernel(float *y, const flo
   if (i < n) y[i] += a[i];
 }
 
+// ---- f32 activations on the bf16 GEMV kernels (hi/lo row pairs) ----------
+
+__global__ __launch_bounds__(kEwThreads) void hilo_split_kernel(HiloBatch b) {
+  const HiloJob j = b.j[blockIdx.y];
+  const long long i = (long long)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= (long long)j.rows * j.n) return;
+  const long long r = i / j.n, c = i % j.n;
+  const float v = j.src[i];
+  const uint32_t hi = f32_to_bf16_rne(v);
+  uint16_t *d = reinterpret_cast<uint16_t *>(j.dst);
+  d[(2 * r) * j.n + c] = (uint16_t)hi;
+  d[(2 * r + 1) * j.n + c] = (uint16_t)f32_to_bf16_rne(v - bf16_to_f32(hi));  // v - hi is exact
+}
+
+__global__ __launch_bounds__(kEwThreads) void hilo_join_kernel(HiloBatch b) {
+  const HiloJob j = b.j[blockIdx.y];
+  const long long i = (long long)blockIdx.x * kEwThreads + threadIdx.x;
+  if (i >= (long long)j.rows * j.n) return;
+  const long long r = i / j.n, c = i % j.n;
+  reinterpret_cast<float *>(j.dst)[i] = j.src[(2 * r) * j.n + c] + j.src[(2 * r + 1) * j.n + c];
+}
+
+static hipError_t hilo_launch(bool split, const HiloBatch &b, hipStream_t st) {
+  if (b.n <= 0 || b.n > kHiloMaxJobs) return hipErrorInvalidValue;
+  long long most = 0;
+  for (int i = 0; i < b.n; ++i) {
+    if (b.j[i].rows <= 0 || b.j[i].n <= 0 || !b.j[i].src || !b.j[i].dst) return hipErrorInvalidValue;
+    most = max(most, (long long)b.j[i].rows * b.j[i].n);
+  }
+  const long long blocks = (most + kEwThreads - 1) / kEwThreads;
+  if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+  if (split)
+    hipLaunchKernelGGL(hilo_split_kernel, dim3((unsigned)blocks, b.n), dim3(kEwThreads), 0, st, b);
+  else
+    hipLaunchKernelGGL(hilo_join_kernel, dim3((unsigned)blocks, b.n), dim3(kEwThreads), 0, st, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_hilo_split(const HiloBatch &b, hipStream_t st) { return hilo_launch(true, b, st); }
+hipError_t launch_hilo_join(const HiloBatch &b, hipStream_t st) { return hilo_launch(false, b, st); }
+
 hipError_t launch_rmsnorm(float *x, const float *w, int n, int nrows, float eps, hipStream_t st) {
   if (n <= 0 || nrows <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3((unsigned)nrows), dim3(kEwThreads), 0, st, x, w, n, eps);

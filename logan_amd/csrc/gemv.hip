@@ -32,8 +32,14 @@ struct GemvParams {
 // SPLIT > 1: SPLIT teams share one row, each over a contiguous K segment of
 // LANES*CPL chunks; their partial sums meet in LDS and are added in segment
 // order.
-template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+// XF: the activation is one f32 row (a.x points at floats); its two operand
+// rows are hi = bf16(x) and lo = bf16(x - hi) (|x - hi - lo| <= 2^-18 |x|),
+// split in registers, and their partial sums are added before the team
+// reduction, so the kernel writes one f32 (or bf16) output row (MT == 2).
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF = false>
 __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
+  static_assert(!XF || MT == 2, "f32 activations use the two-row operand form");
+  constexpr int MO = XF ? 1 : MT;  // output rows
   constexpr int TEAMS = 256 / LANES;
   constexpr int ROWTEAMS = TEAMS / SPLIT;
   const int lane = threadIdx.x & (LANES - 1);
@@ -63,14 +69,25 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   }
 
   uint4 xr[MT][CPL][4];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const int mm = m < a.M ? m : a.M - 1;
+  if constexpr (XF) {
+    // 32 f32 per chunk: xr[0] and xr[1] hold its first and second half
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)mm * a.x_stride + 32 * cc[j]);
+      const uint4 *src =
+          reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(a.x) + 32 * cc[j]);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) xr[m][j][v] = src[v];
+      for (int v = 0; v < 8; ++v) xr[v >> 2][j][v & 3] = src[v];
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int mm = m < a.M ? m : a.M - 1;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.x + (size_t)mm * a.x_stride + 32 * cc[j]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xr[m][j][v] = src[v];
+      }
     }
   }
 
@@ -99,7 +116,26 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
     // keep every load above issued before any of their consumers
     __builtin_amdgcn_sched_barrier(0);
     XChunk xc[MT][CPL];
-    {
+    if constexpr (XF) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        uint32_t xh[32], xl[32];
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const uint4 t = xr[v >> 2][j][v & 3];
+          const uint32_t w4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float f = cval[j] ? __uint_as_float(w4[q]) : 0.f;
+            const uint32_t hi = f32_to_bf16_rne(f);
+            xh[4 * v + q] = hi;
+            xl[4 * v + q] = f32_to_bf16_rne(f - bf16_to_f32(hi));  // f - hi is exact
+          }
+        }
+        make_xchunk_bf16<BITS>(xc[0][j], xh);
+        make_xchunk_bf16<BITS>(xc[1][j], xl);
+      }
+    } else {
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
 #pragma unroll
@@ -145,14 +181,18 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
         }
       }
     }
-    if constexpr (LANES == 64 && SPLIT == 1 && U * MT >= 2) {
+    if constexpr (XF) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) part[u][0] += part[u][1];  // y = W.hi + W.lo
+    }
+    if constexpr (LANES == 64 && SPLIT == 1 && U * MO >= 2) {
       // four (row, token) sums per wave_reduce4; row r of lanes gets value r
-      constexpr int NV = U * MT;
+      constexpr int NV = U * MO;
       float vals[NV];
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) vals[u * MT + m] = part[u][m];
+        for (int m = 0; m < MO; ++m) vals[u * MO + m] = part[u][m];
       const int rr = lane >> 4;
 #pragma unroll
       for (int g0 = 0; g0 < NV; g0 += 4) {
@@ -160,9 +200,9 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
                                      g0 + 2 < NV ? vals[g0 + 2] : 0.f,
                                      g0 + 3 < NV ? vals[g0 + 3] : 0.f);
         const int idx = g0 + rr;
-        const int u = idx / MT, m = idx % MT;
+        const int u = idx / MO, m = idx % MO;
         const int row = r0 + u;
-        if ((lane & 15) == 0 && idx < NV && row < a.O && m < a.M) {
+        if ((lane & 15) == 0 && idx < NV && row < a.O && (XF || m < a.M)) {
           if (a.y_bf16)
             reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
                 (uint16_t)f32_to_bf16_rne(t);
@@ -171,24 +211,24 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
         }
       }
     } else {
-      float tot[U][MT];
+      float tot[U][MO];
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) tot[u][m] = team_sum<LANES>(part[u][m]);
+        for (int m = 0; m < MO; ++m) tot[u][m] = team_sum<LANES>(part[u][m]);
       if constexpr (SPLIT > 1) {
         if (lane == 0) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int m = 0; m < MT; ++m) s_part[(team * U + u) * MT + m] = tot[u][m];
+            for (int m = 0; m < MO; ++m) s_part[(team * U + u) * MT + m] = tot[u][m];
         }
         __syncthreads();
         if (seg == 0 && lane == 0) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
+            for (int m = 0; m < MO; ++m) {
               float v = tot[u][m];
 #pragma unroll
               for (int s = 1; s < SPLIT; ++s) v += s_part[((team + s) * U + u) * MT + m];
@@ -201,9 +241,9 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
       for (int u = 0; u < U; ++u) {
         const int row = r0 + u;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
+        for (int m = 0; m < MO; ++m) {
           const float v = tot[u][m];
-          if (seg == 0 && lane == 0 && row < a.O && m < a.M) {
+          if (seg == 0 && lane == 0 && row < a.O && (XF || m < a.M)) {
             if (a.y_bf16)
               reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
                   (uint16_t)f32_to_bf16_rne(v);
@@ -216,9 +256,9 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   }
 }
 
-template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF>
 __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
-  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT>(a, blockIdx.x);
+  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT, XF>(a, blockIdx.x);
 }
 
 // Up to kMultiMax matrices sharing one activation in one launch: block b
@@ -228,6 +268,7 @@ struct GemvMultiDesc {
   const uint8_t *w;
   const uint16_t *sc;
   const uint16_t *bi;
+  const uint16_t *x;  // this matrix's activation rows, or nullptr: the shared x
   void *y;
   long long row_bytes;
   int O, ng;
@@ -239,7 +280,7 @@ struct GemvMultiParams {
   int n;
 };
 
-template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF>
 __global__ __launch_bounds__(256) void gemv_bf16_multi_kernel(GemvMultiParams mp) {
   int i = 0;
   while (i + 1 < mp.n && (int)blockIdx.x >= mp.block_start[i + 1]) ++i;
@@ -248,28 +289,29 @@ __global__ __launch_bounds__(256) void gemv_bf16_multi_kernel(GemvMultiParams mp
   a.sc = mp.d[i].sc;
   a.bi = mp.d[i].bi;
   a.y = mp.d[i].y;
+  if (mp.d[i].x) a.x = mp.d[i].x;
   a.row_bytes = mp.d[i].row_bytes;
   a.O = mp.d[i].O;
   a.ng = mp.d[i].ng;
   a.y_stride = mp.d[i].O;
-  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT>(a, blockIdx.x - mp.block_start[i]);
+  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT, XF>(a, blockIdx.x - mp.block_start[i]);
 }
 
-template <int BITS, int LANES, int CPL, int MT, int SPLIT, int U>
-static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiParams *mp = nullptr) {
+template <int BITS, int LANES, int CPL, int MT, int SPLIT, int U, bool XF>
+static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiParams *mp) {
   constexpr int rows_per_block = (256 / LANES / SPLIT) * U;
   if (mp) {
     mp->block_start[0] = 0;
     for (int i = 0; i < mp->n; ++i)
       mp->block_start[i + 1] = mp->block_start[i] + (mp->d[i].O + rows_per_block - 1) / rows_per_block;
     for (int i = mp->n + 1; i <= kMultiMax; ++i) mp->block_start[i] = mp->block_start[mp->n];
-    hipLaunchKernelGGL((gemv_bf16_multi_kernel<BITS, LANES, CPL, U, MT, SPLIT>),
+    hipLaunchKernelGGL((gemv_bf16_multi_kernel<BITS, LANES, CPL, U, MT, SPLIT, XF>),
                        dim3(mp->block_start[mp->n]), dim3(256), 0, st, *mp);
     return hipGetLastError();
   }
   const int blocks = (p.O + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((gemv_bf16_kernel<BITS, LANES, CPL, U, MT, SPLIT>), dim3(blocks), dim3(256), 0,
-                     st, p);
+  hipLaunchKernelGGL((gemv_bf16_kernel<BITS, LANES, CPL, U, MT, SPLIT, XF>), dim3(blocks), dim3(256),
+                     0, st, p);
   return hipGetLastError();
 }
 
@@ -280,26 +322,26 @@ static hipError_t gemv_launch_t(const GemvParams &p, hipStream_t st, GemvMultiPa
 // 4096x14336: 18.8 -> 15.6 us; 4-bit 2048x4096: 4.5 -> 3.7 us). Rows of up
 // to 64 chunks keep four rows per team (two measured faster launched back to
 // back, slower inside a graph).
-template <int BITS, int MT>
+template <int BITS, int MT, bool XF>
 static hipError_t gemv_dispatch_shape(const GemvParams &p, hipStream_t st, GemvMultiParams *mp) {
   const int C = p.I >> 5;
-  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT, 1, 4>(p, st, mp);
-  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT, 1, 4>(p, st, mp);
-  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT, 1, 4>(p, st, mp);
-  if (C <= 128) return gemv_launch_t<BITS, 64, 1, MT, 2, 2>(p, st, mp);
-  if (C <= 256) return gemv_launch_t<BITS, 64, 1, MT, 4, 2>(p, st, mp);
-  if (C <= 512) return gemv_launch_t<BITS, 64, 2, MT, 4, 2>(p, st, mp);
+  if (C <= 16) return gemv_launch_t<BITS, 16, 1, MT, 1, 4, XF>(p, st, mp);
+  if (C <= 32) return gemv_launch_t<BITS, 32, 1, MT, 1, 4, XF>(p, st, mp);
+  if (C <= 64) return gemv_launch_t<BITS, 64, 1, MT, 1, 4, XF>(p, st, mp);
+  if (C <= 128) return gemv_launch_t<BITS, 64, 1, MT, 2, 2, XF>(p, st, mp);
+  if (C <= 256) return gemv_launch_t<BITS, 64, 1, MT, 4, 2, XF>(p, st, mp);
+  if (C <= 512) return gemv_launch_t<BITS, 64, 2, MT, 4, 2, XF>(p, st, mp);
   return hipErrorInvalidValue;
 }
 
-template <int MT>
+template <int MT, bool XF = false>
 static hipError_t gemv_dispatch_bits(const GemvParams &p, int bits, hipStream_t st,
                                      GemvMultiParams *mp = nullptr) {
   switch (bits) {
-    case 4: return gemv_dispatch_shape<4, MT>(p, st, mp);
-    case 5: return gemv_dispatch_shape<5, MT>(p, st, mp);
-    case 6: return gemv_dispatch_shape<6, MT>(p, st, mp);
-    case 8: return gemv_dispatch_shape<8, MT>(p, st, mp);
+    case 4: return gemv_dispatch_shape<4, MT, XF>(p, st, mp);
+    case 5: return gemv_dispatch_shape<5, MT, XF>(p, st, mp);
+    case 6: return gemv_dispatch_shape<6, MT, XF>(p, st, mp);
+    case 8: return gemv_dispatch_shape<8, MT, XF>(p, st, mp);
   }
   return hipErrorInvalidValue;
 }
@@ -342,7 +384,8 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
       p.M = mt;
       p.y = y_bf16 ? (void *)(reinterpret_cast<uint16_t *>(y) + (size_t)m0 * y_stride)
                    : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
-      hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st) : gemv_dispatch_bits<1>(p, m.bits, st);
+      hipError_t e = mt == 2 ? gemv_dispatch_bits<2>(p, m.bits, st, nullptr)
+                             : gemv_dispatch_bits<1>(p, m.bits, st, nullptr);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -372,21 +415,26 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
 // token pair through the dot2 kernel; 3..32 tokens one K-split launch and one
 // reduce for all of them where the K-split form applies, otherwise the MFMA
 // path matrix by matrix.
-hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
-                                  int x_stride, int M, int y_bf16, hipStream_t st) {
+// xs (optional): per-matrix activations, each [M][x_stride], instead of the
+// shared x.
+static hipError_t gemv_bf16_multi_impl(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
+                                       const uint16_t *const *xs, int x_stride, int M, int y_bf16,
+                                       hipStream_t st) {
   if (n <= 0 || n > kMultiMax || M <= 0) return hipErrorInvalidValue;
   for (int i = 0; i < n; ++i) {
     if (!gemv_bf16_supported(ms[i]) || ms[i].I != ms[0].I || ms[i].bits != ms[0].bits ||
         ms[i].gs != ms[0].gs || ms[i].fp16 != ms[0].fp16 || !ys[i])
       return hipErrorInvalidValue;
+    const uint16_t *xi = xs ? xs[i] : x;
+    if (!xi || (reinterpret_cast<uintptr_t>(xi) & 15) != 0) return hipErrorInvalidValue;
   }
-  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  if ((x_stride & 7) != 0) return hipErrorInvalidValue;
   // 3..32 tokens: one K-split launch and one reduce for all the products
-  if (M >= 3 && M <= 32 && n > 1 && affine_splitk_multi_supported(ms, n, M))
+  if (!xs && M >= 3 && M <= 32 && n > 1 && affine_splitk_multi_supported(ms, n, M))
     return launch_affine_splitk_multi(ms, n, x, x_stride, M, ys, y_bf16, st);
-  if (M >= 3 && affine_skinny_supported(ms[0])) {
+  if (M >= 3 && (xs || affine_skinny_supported(ms[0]))) {
     for (int i = 0; i < n; ++i) {
-      hipError_t e = launch_gemv_bf16(ms[i], x, x_stride, M, ys[i], ms[i].O, y_bf16, st);
+      hipError_t e = launch_gemv_bf16(ms[i], xs ? xs[i] : x, x_stride, M, ys[i], ms[i].O, y_bf16, st);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -405,6 +453,7 @@ hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, cons
     p.x = x + (size_t)m0 * x_stride;
     p.M = mt;
     for (int i = 0; i < n; ++i) {
+      mp.d[i].x = xs ? xs[i] + (size_t)m0 * x_stride : nullptr;
       mp.d[i].w = ms[i].w;
       mp.d[i].sc = ms[i].sc;
       mp.d[i].bi = ms[i].bi;
@@ -419,6 +468,66 @@ hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, cons
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
+                                  int x_stride, int M, int y_bf16, hipStream_t st) {
+  return gemv_bf16_multi_impl(ms, ys, n, x, nullptr, x_stride, M, y_bf16, st);
+}
+
+hipError_t launch_gemv_bf16_multi_x(const DevMat *ms, const uint16_t *const *xs, void *const *ys,
+                                    int n, int x_stride, int M, int y_bf16, hipStream_t st) {
+  if (!xs) return hipErrorInvalidValue;
+  return gemv_bf16_multi_impl(ms, ys, n, nullptr, xs, x_stride, M, y_bf16, st);
+}
+
+// One f32 activation row per matrix (xs[i], or the shared x when xs is
+// null), f32 or bf16 output rows: the XF form of the dot2 kernel, all
+// matrices (same I, bits, group size, aux type) in one launch.
+hipError_t launch_gemv_f32x_multi(const DevMat *ms, const float *x, const float *const *xs,
+                                  void *const *ys, int n, int y_bf16, hipStream_t st) {
+  if (n <= 0 || n > kMultiMax) return hipErrorInvalidValue;
+  for (int i = 0; i < n; ++i) {
+    if (!gemv_bf16_supported(ms[i]) || ms[i].I != ms[0].I || ms[i].bits != ms[0].bits ||
+        ms[i].gs != ms[0].gs || ms[i].fp16 != ms[0].fp16 || !ys[i])
+      return hipErrorInvalidValue;
+    const float *xi = xs ? xs[i] : x;
+    if (!xi || (reinterpret_cast<uintptr_t>(xi) & 15) != 0) return hipErrorInvalidValue;
+  }
+  GemvMultiParams mp{};
+  GemvParams &p = mp.common;
+  p.I = ms[0].I;
+  p.gsc = ms[0].gs / 32;
+  p.gsc_shift = (p.gsc & (p.gsc - 1)) == 0 ? __builtin_ctz(p.gsc) : -1;
+  p.fp16 = ms[0].fp16;
+  p.x = reinterpret_cast<const uint16_t *>(x);
+  p.x_stride = p.I;
+  p.M = 2;
+  p.y_bf16 = y_bf16;
+  mp.n = n;
+  for (int i = 0; i < n; ++i) {
+    mp.d[i].x = xs ? reinterpret_cast<const uint16_t *>(xs[i]) : nullptr;
+    mp.d[i].w = ms[i].w;
+    mp.d[i].sc = ms[i].sc;
+    mp.d[i].bi = ms[i].bi;
+    mp.d[i].row_bytes = ms[i].row_bytes;
+    mp.d[i].O = ms[i].O;
+    mp.d[i].ng = ms[i].ng;
+    mp.d[i].y = ys[i];
+  }
+  if (n == 1) {  // the single-matrix kernel
+    p.w = ms[0].w;
+    p.sc = ms[0].sc;
+    p.bi = ms[0].bi;
+    p.row_bytes = ms[0].row_bytes;
+    p.O = ms[0].O;
+    p.ng = ms[0].ng;
+    p.y = ys[0];
+    p.y_stride = ms[0].O;
+    if (xs) p.x = reinterpret_cast<const uint16_t *>(xs[0]);
+    return gemv_dispatch_bits<2, true>(p, ms[0].bits, st, nullptr);
+  }
+  return gemv_dispatch_bits<2, true>(p, ms[0].bits, st, &mp);
 }
 
 // ---------------------------------------------------------------------------

@@ -27,6 +27,34 @@ bool gemv_bf16_supported(const DevMat &m);
 // [M][O_i]
 hipError_t launch_gemv_bf16_multi(const DevMat *ms, void *const *ys, int n, const uint16_t *x,
                                   int x_stride, int M, int y_bf16, hipStream_t st);
+// same, each matrix with its own activation rows xs[i] [M][x_stride]
+hipError_t launch_gemv_bf16_multi_x(const DevMat *ms, const uint16_t *const *xs, void *const *ys,
+                                    int n, int x_stride, int M, int y_bf16, hipStream_t st);
+constexpr int kGemvMultiMax = 8;
+// one f32 activation row per matrix (xs[i], or the shared x when xs is
+// null) on the dot2 kernel, split in registers into bf16 (hi, lo) operands
+// (|x - hi - lo| <= 2^-18 |x|); ys[i] [O_i] f32 (y_bf16 0) or bf16
+hipError_t launch_gemv_f32x_multi(const DevMat *ms, const float *x, const float *const *xs,
+                                  void *const *ys, int n, int y_bf16, hipStream_t st);
+
+// ---- f32 activations on the bf16 kernels: each f32 row x becomes the bf16
+// row pair (hi, lo) = (bf16(x), bf16(x - hi)), the products run on 2 rows
+// per activation row with f32 outputs, and each output row is y = y_hi + y_lo
+// (|x - hi - lo| <= 2^-18 |x|)
+struct HiloJob {
+  const float *src;  // [rows][n] f32
+  void *dst;         // split: uint16_t [2 rows][n]; join: float [rows][n]
+  int rows, n;
+};
+constexpr int kHiloMaxJobs = 32;
+struct HiloBatch {
+  HiloJob j[kHiloMaxJobs];
+  int n;
+};
+// split: dst = bf16 (hi, lo) row pairs of src; join: dst = src[2r] + src[2r+1]
+hipError_t launch_hilo_split(const HiloBatch &b, hipStream_t st);
+hipError_t launch_hilo_join(const HiloBatch &b, hipStream_t st);
+
 
 // ---- prefill / large-batch product on MFMA: bf16-rounded dequantised
 // weights (the reference QMM semantics), x bf16 [M, I], y [M, O] ----

@@ -519,3 +519,56 @@ def test_host_route_island_survives_calls_between_begin_and_finish(gpu):
     t.free()
     for dsc in da + db + ds:
         dsc.tensor.free()
+
+
+def test_host_multi_fast_and_exact_paths(gpu):
+    """coli_metal_matmul_multi with f32 host activations: products the bf16
+    kernels take run there on (hi, lo) activation pairs, the rest (group
+    size 16 here) on the exact per-element kernel; shared and private
+    activations with several rows each. Every row against the oracle's f32
+    GEMV within 2e-5 normwise, the reference CUDA twin's bar
+    (logan-qwen4/src/lib.rs:17176): both paths sum in another order than the
+    oracle's sequential loop."""
+    import ctypes as C
+    from logan_amd import _lib as L
+    from logan_amd.backend import Tensor
+
+    rng = np.random.default_rng(314)
+    S = 4
+    specs = [  # (O, I, bits, gs, private rows or 0 for the shared x)
+        (300, 2048, 4, 64, 0), (96, 2048, 5, 16, 0), (130, 1024, 8, 64, 3), (77, 512, 6, 32, 2),
+        (4096, 2048, 4, 64, 0)]
+    xs = bf16_to_f32(make_x(rng, S, 2048)).reshape(S, 2048) + np.float32(1e-3) * \
+        rng.standard_normal((S, 2048)).astype(np.float32)  # not bf16-exact: lo halves matter
+    raw = (L.MatmulDesc * len(specs))()
+    keep, mats, ys, privs = [], [], [], []
+    for k, (O, I, bits, gs, rows) in enumerate(specs):
+        w, sc, bi = make_affine(rng, O, I, bits, gs)
+        aux = aux_bytes(sc, bi)
+        n = rows if rows else S
+        y = np.zeros((n, O), np.float32)
+        xp = None
+        if rows:
+            xp = (rng.standard_normal((rows, I)) * 0.7).astype(np.float32)
+            privs.append(xp)
+        raw[k].tensor = None
+        raw[k].y = y.ctypes.data
+        raw[k].weights = w.ctypes.data
+        raw[k].scales = aux.ctypes.data
+        raw[k].fmt = {4: 16, 5: 17, 6: 18, 8: 19}[bits]
+        raw[k].I, raw[k].O, raw[k].gs = I, O, gs
+        raw[k].x = xp.ctypes.data if rows else None
+        raw[k].S = rows
+        keep += [w, aux]
+        mats.append((w, sc, bi, O, I, bits, gs))
+        ys.append((y, xp))
+    xs_c = np.ascontiguousarray(xs[:, :2048])
+    assert L.lib().logan_hip_matmul_multi(xs_c.ctypes.data, S, raw, len(specs)) == 1
+    for k, ((w, sc, bi, O, I, bits, gs), (y, xp)) in enumerate(zip(mats, ys)):
+        xin = xp if xp is not None else xs_c[:, :I]
+        for r in range(xin.shape[0]):
+            ref = oracle.affine_gemv(np.ascontiguousarray(xin[r]), w, sc, bi, O, I, bits, gs)
+            err = normwise_rel(y[r], ref)
+            assert err <= 2e-5, f"desc {k} row {r}: {err:.2e}"
+    for k in range(len(specs)):
+        Tensor(raw[k].tensor or 0).free()
