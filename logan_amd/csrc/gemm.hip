@@ -13,6 +13,9 @@
 // and 8 consecutive k at offset 8 * (l / 32) of each 16-wide k slice; the
 // result's element i of lane l is row 8 * (i / 4) + 4 * (l / 32) + i % 4,
 // column l % 32.
+#include <algorithm>
+#include <atomic>
+
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 
@@ -52,8 +55,45 @@ __device__ __forceinline__ uint32_t code_of(const uint32_t (&w)[DeqGeom<BITS>::D
   return c & ((1u << BITS) - 1u);
 }
 
+// Split-K: the blocks of one tile that share a k range write f32 partial
+// sums part[z][m][n] into one of kQSlots module-scope slots (taken round-robin
+// per call, so calls whose executions overlap on one device stay correct
+// while at most kQSlots are in flight); qmm_reduce_kernel adds them in z
+// order and writes y. slot < 0: one k range, y written directly.
+constexpr int kQSlots = 2;
+constexpr size_t kQSlotFloats = size_t(1) << 23;  // 32 MB per slot
+static __device__ __align__(256) float g_qmm_part[kQSlots * kQSlotFloats];
+
+__device__ __forceinline__ void qmm_store(const GemmParams &p, int slot, int z, int m, int n,
+                                          float v) {
+  if (slot >= 0)
+    g_qmm_part[(size_t)slot * kQSlotFloats + ((size_t)z * p.M + m) * p.N + n] = v;
+  else if (p.y_bf16)
+    reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)v;
+  else
+    reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = v;
+}
+
+__global__ __launch_bounds__(256) void qmm_reduce_kernel(GemmParams p, int slot, int KS) {
+  const float *part = g_qmm_part + (size_t)slot * kQSlotFloats;
+  const size_t MN = (size_t)p.M * p.N;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+    float v[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) v[z] = z < KS ? part[z * MN + i] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int z = 1; z < 16; ++z) s += z < KS ? v[z] : 0.f;  // in k order
+    const int m = (int)(i / p.N), n = (int)(i % p.N);
+    if (p.y_bf16)
+      reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)s;
+    else
+      reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = s;
+  }
+}
+
 template <int BITS>
-__global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
+__global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p, int ksteps, int slot) {
   using G = DeqGeom<BITS>;
   __shared__ __align__(16) __bf16 sW[kTile * kLdsStride];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -122,13 +162,15 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
     }
     __syncthreads();
   };
-  issue(0, wv0, sr0, br0, xa0);
-  for (int k0 = 0; k0 < p.K; k0 += 2 * kTile) {
-    if (k0 + kTile < p.K) issue(k0 + kTile, wv1, sr1, br1, xa1);
+  const int z = blockIdx.z;
+  const int kb = z * ksteps * kTile, ke = min(p.K, kb + ksteps * kTile);
+  issue(kb, wv0, sr0, br0, xa0);
+  for (int k0 = kb; k0 < ke; k0 += 2 * kTile) {
+    if (k0 + kTile < ke) issue(k0 + kTile, wv1, sr1, br1, xa1);
     __builtin_amdgcn_sched_barrier(0);
     step(wv0, sr0, br0, xa0);
-    if (k0 + kTile < p.K) {
-      if (k0 + 2 * kTile < p.K) issue(k0 + 2 * kTile, wv0, sr0, br0, xa0);
+    if (k0 + kTile < ke) {
+      if (k0 + 2 * kTile < ke) issue(k0 + 2 * kTile, wv0, sr0, br0, xa0);
       __builtin_amdgcn_sched_barrier(0);
       step(wv1, sr1, br1, xa1);
     }
@@ -138,33 +180,35 @@ __global__ __launch_bounds__(256) void affine_qmm_kernel(GemmParams p) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int m = bm0 + wm * 32 + 8 * (i / 4) + 4 * half + (i % 4);
-    if (m < p.M && n < p.N) {
-      if (p.y_bf16)
-        reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)acc[i];
-      else
-        reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = acc[i];
-    }
+    if (m < p.M && n < p.N) qmm_store(p, slot, z, m, n, acc[i]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Large tiles: 128 x 128 output per 256-thread block (each wave 64 x 64 as
 // 2 x 2 MFMA tiles), so every weight is dequantised once per 128 tokens. Per
-// 64-k step the block writes the x tile and the dequantised W tile into LDS;
-// the next step's global loads are issued into registers before the current
-// step's MFMAs. Blocks are numbered so that the M tiles of one N tile share an
-// XCD (block id mod 8) and meet the weight tile in that XCD's L2.
+// 64-k step the block writes the x tile and the dequantised W tile into one
+// of two LDS stages while the MFMAs read the other; the next step's global
+// loads are issued into registers before the current step's MFMAs, one
+// barrier per step. (x read straight into MFMA operand registers instead of
+// through LDS measured 1.7x slower: each load instruction then touches 32
+// rows.) Blocks are numbered so that the M tiles of one N tile share an XCD
+// (block id mod 8) and meet the weight tile in that XCD's L2.
 constexpr int kQ2 = 128;     // tile rows (m) and columns (n)
 constexpr int kQ2Ld = 72;    // bf16 per LDS row: 64 + 8 pad
 #ifndef QMM_MIN_TILES
 #define QMM_MIN_TILES 192
 #endif
 constexpr int kQ2MinTiles = QMM_MIN_TILES;
+constexpr int kQTargetBlocks = 512;  // about two blocks per CU
+static std::atomic<unsigned> g_qmm_next{0};
 
 template <int BITS>
-__global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mtiles, int ntiles) {
-  __shared__ __align__(16) __bf16 sA[kQ2 * kQ2Ld];
-  __shared__ __align__(16) __bf16 sB[kQ2 * kQ2Ld];
+__global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mtiles, int ntiles,
+                                                            int ksteps, int slot) {
+  // two stages: step s reads stage s % 2 while stage (s + 1) % 2 is filled
+  __shared__ __align__(16) __bf16 sA[2][kQ2 * kQ2Ld];
+  __shared__ __align__(16) __bf16 sB[2][kQ2 * kQ2Ld];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -201,8 +245,8 @@ __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mt
     r.b = brow[gi];
     return r;
   };
-  auto commit = [&](const Loads &r) {
-    uint4 *da = reinterpret_cast<uint4 *>(sA + lr * kQ2Ld + 32 * lh);
+  auto commit = [&](const Loads &r, int st) {
+    uint4 *da = reinterpret_cast<uint4 *>(sA[st] + lr * kQ2Ld + 32 * lh);
     da[0] = r.x0;
     da[1] = r.x1;
     da[2] = r.x2;
@@ -225,7 +269,7 @@ __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mt
       v[1] = (__bf16)fmaf((float)c[1], s, b);
       pk[j / 2] = __builtin_bit_cast(uint32_t, v);
     }
-    uint4 *db = reinterpret_cast<uint4 *>(sB + lr * kQ2Ld + 32 * lh);
+    uint4 *db = reinterpret_cast<uint4 *>(sB[st] + lr * kQ2Ld + 32 * lh);
 #pragma unroll
     for (int v = 0; v < 4; ++v) db[v] = make_uint4(pk[4 * v], pk[4 * v + 1], pk[4 * v + 2], pk[4 * v + 3]);
   };
@@ -235,31 +279,42 @@ __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mt
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-  auto mfma_step = [&]() {
+  auto mfma_step = [&](int st) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       bf16x8 a[2], b[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8 *>(sA + (wm * 64 + 32 * i + l32) * kQ2Ld + 16 * ks + 8 * half);
+        a[i] = *reinterpret_cast<const bf16x8 *>(sA[st] + (wm * 64 + 32 * i + l32) * kQ2Ld + 16 * ks +
+                                                 8 * half);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8 *>(sB + (wn * 64 + 32 * j + l32) * kQ2Ld + 16 * ks + 8 * half);
+        b[j] = *reinterpret_cast<const bf16x8 *>(sB[st] + (wn * 64 + 32 * j + l32) * kQ2Ld + 16 * ks +
+                                                 8 * half);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   };
-  // one step of loads in flight (the last step reloads itself, so every
-  // issue is unconditional); a second stage measured slower
-  Loads cur = issue(0);
-  for (int k0 = 0; k0 < p.K; k0 += 64) {
-    __syncthreads();  // the previous step's operand reads are done
-    commit(cur);
+  // per step: the MFMAs read stage s % 2 while the next step's operands
+  // (loaded during the previous step) are dequantised into the other stage,
+  // then the loads of step s + 2 are issued; one barrier per step (stage
+  // (s + 1) % 2 was last read in step s - 1, before that step's barrier).
+  // (Loads issued three steps ahead measured no faster.)
+  const int z = blockIdx.y;
+  const int kb = z * ksteps * 64, nst = (min(p.K, kb + ksteps * 64) - kb) / 64;
+  Loads cur = issue(kb);
+  commit(cur, 0);
+  cur = issue(kb + 64 * min(1, nst - 1));
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    mfma_step(s & 1);
+    if (s + 1 < nst) {
+      commit(cur, (s + 1) & 1);
+      cur = issue(kb + 64 * min(s + 2, nst - 1));
+    }
     __syncthreads();
-    cur = issue(min(k0 + 64, p.K - 64));
-    mfma_step();
   }
   // element e of tile (i, j): row 32 i + 8 (e / 4) + 4 half + e % 4, column 32 j + l32
 #pragma unroll
@@ -270,12 +325,7 @@ __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mt
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = bm0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * half + (e % 4);
-        if (m < p.M && n < p.N) {
-          if (p.y_bf16)
-            reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)acc[i][j][e];
-          else
-            reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = acc[i][j][e];
-        }
+        if (m < p.M && n < p.N) qmm_store(p, slot, z, m, n, acc[i][j][e]);
       }
     }
 }
@@ -309,26 +359,42 @@ hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, i
   p.x_stride = x_stride;
   p.y_stride = y_stride;
   p.y_bf16 = y_bf16;
-  // large tiles when their grid alone keeps the chip busy; smaller grids
-  // take the 64 x 64 kernel (four times the blocks)
+  // Large tiles when their grid alone keeps the chip busy, else 64 x 64
+  // tiles (four times the blocks); grids still short of about two blocks per
+  // CU split K as well (at most 16 ways, partials within one slot).
+  const int ksteps_all = m.I / 64;
   const int mt = (M + kQ2 - 1) / kQ2, nt = (m.O + kQ2 - 1) / kQ2;
-  if (M > kTile && mt * nt >= kQ2MinTiles) {
-    const int blocks = ((nt + 7) / 8) * 8 * mt;
+  const bool big = M > kTile && m.O >= kQ2 && (mt * nt >= kQ2MinTiles || m.I >= 512);
+  const int tiles = big ? mt * nt : ((M + kTile - 1) / kTile) * ((m.O + kTile - 1) / kTile);
+  int split = 1;
+  while (split < 16 && tiles * split < kQTargetBlocks && 2 * split <= ksteps_all &&
+         (size_t)(2 * split) * M * m.O <= kQSlotFloats)
+    split *= 2;
+  const int ksteps = (ksteps_all + split - 1) / split;
+  split = (ksteps_all + ksteps - 1) / ksteps;
+  const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
+  if (big) {
+    const dim3 grid(((nt + 7) / 8) * 8 * mt, split);
     switch (m.bits) {
-      case 4: hipLaunchKernelGGL(affine_qmm128_kernel<4>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
-      case 5: hipLaunchKernelGGL(affine_qmm128_kernel<5>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
-      case 6: hipLaunchKernelGGL(affine_qmm128_kernel<6>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
-      case 8: hipLaunchKernelGGL(affine_qmm128_kernel<8>, dim3(blocks), dim3(256), 0, st, p, mt, nt); break;
+      case 4: hipLaunchKernelGGL(affine_qmm128_kernel<4>, grid, dim3(256), 0, st, p, mt, nt, ksteps, slot); break;
+      case 5: hipLaunchKernelGGL(affine_qmm128_kernel<5>, grid, dim3(256), 0, st, p, mt, nt, ksteps, slot); break;
+      case 6: hipLaunchKernelGGL(affine_qmm128_kernel<6>, grid, dim3(256), 0, st, p, mt, nt, ksteps, slot); break;
+      case 8: hipLaunchKernelGGL(affine_qmm128_kernel<8>, grid, dim3(256), 0, st, p, mt, nt, ksteps, slot); break;
     }
-    return hipGetLastError();
+  } else {
+    const dim3 grid((M + kTile - 1) / kTile, (m.O + kTile - 1) / kTile, split);
+    switch (m.bits) {
+      case 4: hipLaunchKernelGGL(affine_qmm_kernel<4>, grid, dim3(256), 0, st, p, ksteps, slot); break;
+      case 5: hipLaunchKernelGGL(affine_qmm_kernel<5>, grid, dim3(256), 0, st, p, ksteps, slot); break;
+      case 6: hipLaunchKernelGGL(affine_qmm_kernel<6>, grid, dim3(256), 0, st, p, ksteps, slot); break;
+      case 8: hipLaunchKernelGGL(affine_qmm_kernel<8>, grid, dim3(256), 0, st, p, ksteps, slot); break;
+    }
   }
-  const dim3 grid((M + kTile - 1) / kTile, (m.O + kTile - 1) / kTile);
-  switch (m.bits) {
-    case 4: hipLaunchKernelGGL(affine_qmm_kernel<4>, grid, dim3(256), 0, st, p); break;
-    case 5: hipLaunchKernelGGL(affine_qmm_kernel<5>, grid, dim3(256), 0, st, p); break;
-    case 6: hipLaunchKernelGGL(affine_qmm_kernel<6>, grid, dim3(256), 0, st, p); break;
-    case 8: hipLaunchKernelGGL(affine_qmm_kernel<8>, grid, dim3(256), 0, st, p); break;
-  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || split == 1) return e;
+  const size_t mn = (size_t)M * m.O;
+  const int rblocks = (int)std::min<size_t>((mn + 255) / 256, 4096);
+  hipLaunchKernelGGL(qmm_reduce_kernel, dim3(rblocks), dim3(256), 0, st, p, slot, split);
   return hipGetLastError();
 }
 

@@ -132,3 +132,35 @@ def test_qmm_leaves_outside_untouched(gpu):
     torch.cuda.synchronize()
     assert rc == 1
     assert torch.all(y[:, O:] == 7.0)
+
+
+@pytest.mark.parametrize("O,I", [(64, 2048), (512, 2048), (2048, 4096), (8192, 2048)],
+                         ids=["ba", "k_v", "o_out", "q"])
+def test_qmm_config5_prefill_projections(gpu, O, I):
+    """The config-5 projections at the prefill chunk M = 512: grids with few
+    tiles split K (ordered f32 partials and a reduction launch), large grids
+    take the double-buffered 128 x 128 kernel. Sampled output columns against
+    the oracle; two calls give identical bits."""
+    import torch
+    from logan_amd.device import affine_qmm
+
+    print(f"qmm config5 O={O} I={I}", flush=True)
+    rng = np.random.default_rng(O + I)
+    M, bits, gs = 512, 4, 64
+    w, sc, bi = make_affine(rng, O, I, bits, gs)
+    xb = make_x(rng, M, I).reshape(M, I)
+    m = dev_matrix(torch, w, sc, bi, O, I, bits, gs)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    y = affine_qmm(m, x, out_dtype=torch.float32)
+    y2 = affine_qmm(m, x, out_dtype=torch.float32)
+    assert torch.equal(y, y2)
+    yb = affine_qmm(m, x, out_dtype=torch.bfloat16)
+    assert torch.equal(yb, y.to(torch.bfloat16))
+    y = y.cpu().numpy()
+    cols = np.unique(np.concatenate([np.arange(0, O, max(1, O // 24)), [O - 1]]))
+    ng = I // gs
+    ws = w.reshape(O, -1)[cols]
+    scs = sc.reshape(O, ng)[cols].reshape(-1)
+    bis = bi.reshape(O, ng)[cols].reshape(-1)
+    ref = oracle.affine_qmm_bf16(bf16_to_f32(xb).reshape(M, I), ws, scs, bis, len(cols), I, bits, gs)
+    assert normwise_rel(y[:, cols], ref) <= 1e-5
