@@ -79,9 +79,9 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4,dropin",
+    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4,dropin,router",
                     help="secondary legs to run (comma list of gemv, dense8, moe3, stack5, moe4, "
-                         "dropin; 'none' for none)")
+                         "dropin, router; 'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
     ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
@@ -458,6 +458,67 @@ def bench_gemv(torch, device, synth, args):
     return dict(us_per_launch=us, gbps=gbps, launches=launches)
 
 
+def bench_router(torch, device, synth, args, layers):
+    """Config 3, B = 1, with the router on device (logan_hip_moe_block_routed):
+    per layer the 512 x 2048 router GEMV (8-bit g64, as MLX checkpoints keep
+    routers) writes f32 logits and the single-launch block routes on them
+    (logan-qwen4/src/lib.rs:7990-7991). Same graph-replay timing as the
+    headline; bytes add the router matrix and the f32 logits written and
+    read, and drop the bf16 logits the headline reads."""
+    L = args.layers
+    n = args.warmup + args.steps
+    routers = []
+    for l in range(L):
+        w, sc, bi = synth.torch_affine(E, D, 8, GS, seed=7_000_000 + l)
+        # scales |N(0,1)| * 4e-4: logits of x ~ N(0,1) come out near N(0,1),
+        # the scale of real router logits
+        sc = (sc.view(torch.bfloat16).float() * 0.04).to(torch.bfloat16).view(torch.int16)
+        bi = (sc.view(torch.bfloat16).float() * -128).to(torch.bfloat16).view(torch.int16)
+        routers.append(device.AffineMatrix(w, sc, bi, E, D, 8, GS))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(54321)
+    xs = torch.randn((n, L, 1, D), device="cuda", generator=g).to(torch.bfloat16)
+    out = torch.empty((L, 1, D), dtype=torch.bfloat16, device="cuda")
+    lg = torch.empty((L, 1, E), dtype=torch.float32, device="cuda")
+    ws = torch.empty(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+
+    def step(i):
+        for l in range(L):
+            device.moe_block_routed(layers[l], routers[l], xs[i, l], out=out[l], logits=lg[l],
+                                    workspace=ws)
+
+    step(0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graphs = []
+    for i in range(n):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=stream):
+            step(i)
+        graphs.append(gr)
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            graphs[i].replay()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for i in range(args.warmup, n):
+            graphs[i].replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / args.steps / L
+    router_bytes = E * D + 2 * 2 * E * (D // GS)
+    nbytes = LAYER_BYTES_B1 - E * 2 + router_bytes + 2 * E * 4
+    log(f"config 3 B=1 with the router on device: {us:.2f} us/layer")
+    del graphs
+    return dict(us_per_layer=round(us, 2), bytes_per_layer=nbytes,
+                gbps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                frac_of_peak=round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBPS, 4), layers=L,
+                launches_per_layer=2, router="512 x 2048, 8-bit g64, f32 logits")
+
+
 def bench_dropin(torch, synth, args):
     """The host-pointer drop-in layer, called the way logan-metal's engines
     call it (host f32 activations and outputs, weights cached behind tensor
@@ -721,6 +782,8 @@ def main():
             secondary["stack_config5"] = bench_config5(torch, device, synth, args, layers)
         if "moe4" in legs:
             secondary["moe_config4"] = bench_config4(torch, device, synth, args)
+        if "router" in legs:
+            secondary["moe3_router_on_device"] = bench_router(torch, device, synth, args, layers)
         if "dropin" in legs:
             secondary["dropin"] = bench_dropin(torch, synth, args)
     cpu = None

@@ -266,6 +266,19 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
                         int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
                         float *w_out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The routed-MoE block with the router on device: logits[B][E] = x . router^T
+ * with f32 accumulation and f32 results (logan-qwen4/src/lib.rs:7990-7991,
+ * `matmul(&mut logits, x, &layer.router)` before softmax_row), written to
+ * `logits` (device f32 [B][E], caller-provided), then logan_hip_moe_block on
+ * those f32 logits (routing bit-exact against the reference's selection on
+ * the same logits). router: E rows of D columns, any geometry
+ * logan_hip_affine_gemv takes (MLX checkpoints keep it at 8-bit g64). Other
+ * arguments as logan_hip_moe_block. 1 ok, 0 unsupported, -1 failure. */
+int logan_hip_moe_block_routed(const LoganHipMoeBlock *blk, const LoganHipAffine *router,
+                               const void *x, int B, float *logits, void *out, int out_dtype,
+                               int32_t *idx_out, float *w_out, void *workspace,
+                               size_t workspace_bytes, void *stream);
+
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): logan_hip_moe_block without a workspace argument. Its

@@ -110,6 +110,8 @@ SIGNATURES = {
     "logan_hip_route_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "logan_hip_moe_workspace_bytes": (_SZ, [C.POINTER(MoeBlock), _I]),
     "logan_hip_moe_block": (_I, [C.POINTER(MoeBlock), _P, _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _P]),
+    "logan_hip_moe_block_routed": (_I, [C.POINTER(MoeBlock), C.POINTER(Affine), _P, _I, _P, _P, _I, _P,
+                                        _P, _P, _SZ, _P]),
     "logan_hip_moe_block_static": (_I, [C.POINTER(MoeBlock), _P, _P, _I, _I, _P, _I, _P, _P, _P]),
     "logan_hip_set_moe_fused": (None, [_I]),
     "logan_hip_set_moe_mfma_min_batch": (None, [_I]),

@@ -972,6 +972,25 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
   return lh::launch_moe_block(a, st);
 }
 
+int logan_hip_moe_block_routed(const LoganHipMoeBlock *blk, const LoganHipAffine *router,
+                               const void *x, int B, float *logits, void *out, int out_dtype,
+                               int32_t *idx_out, float *w_out, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || !affine_ok(router) || !x || !logits || B <= 0) return 0;
+  if (router->O != a.E || router->I != a.D) return 0;
+  const lh::DevMat rm = devmat(*router);
+  if (!lh::gemv_bf16_supported(rm) || (reinterpret_cast<uintptr_t>(x) & 15) != 0 || (a.D & 7) != 0)
+    return 0;
+  if (B > lh::kMaxBatch) return 0;
+  // the router product, then the block on its f32 logits (stream order)
+  const hipError_t e = lh::launch_gemv_bf16(rm, reinterpret_cast<const uint16_t *>(x), a.D, B,
+                                            logits, a.E, 0, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return -1;
+  return logan_hip_moe_block(blk, x, logits, LOGAN_HIP_F32, B, out, out_dtype, idx_out, w_out,
+                             workspace, workspace_bytes, stream);
+}
+
 int logan_hip_moe_block_static(const LoganHipMoeBlock *blk, const void *x, const void *logits,
                                int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
                                float *w_out, void *stream) {

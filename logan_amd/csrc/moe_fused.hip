@@ -21,11 +21,11 @@
 //   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
 //
-// Every wave computes the route itself from the bf16 logits (top-k with the
-// key (logit desc, index asc): per-lane sorted keys, k rounds of a DPP wave
-// max, and the reference's probability arithmetic instead where a tie in
-// probability could reorder it), so no block waits for another before
-// streaming weights.
+// Every wave computes the route itself from the router logits, bf16 or f32
+// (top-k with the key (logit desc, index asc): per-lane sorted keys, k rounds
+// of a DPP wave max, and the reference's probability arithmetic instead where
+// a tie in probability could reorder it), so no block waits for another
+// before streaming weights.
 //
 // Progress: A blocks never wait on another block. Workgroups are dispatched in
 // ID order, and every A block precedes every B block, so a B block can only be
@@ -185,7 +185,8 @@ __device__ __forceinline__ uint32_t sub_need(int n, int q) {
   return (uint32_t)(n / kSubCtrs + (q < n % kSubCtrs ? 1 : 0));
 }
 
-template <int BITS, int CPLA, int LANESB, int KPL>
+template <int BITS, int CPLA, int LANESB, int KPL, bool LF>
+// LF: f32 router logits (64-bit selection keys), else bf16.
 // Two 8-wave blocks per CU (4 waves per SIMD, <= 128 VGPRs) so all A and B
 // blocks of a config-3 launch are resident at once; the D > 2048 variants
 // hold two x chunks per lane and would spill there.
@@ -211,7 +212,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   // wave-uniform for the compiler too, so per-slot bank selection and
   // addressing stay scalar
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint16_t *logits = reinterpret_cast<const uint16_t *>(a.logits);
+  using RK = WaveKeys<KPL, LF>;
+  using Key = typename RK::K;
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   const int C = a.D >> 5;
   UnpackConsts kc;
@@ -228,8 +230,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     unsigned long long tk = 0;
     if (threadIdx.x == 0) tk = take_ticket();
     // every wave of an A block serves the same slot: wave 0 routes for all
-    uint32_t key[KPL];
-    if (!shared && wave == 0) route_keys<KPL>(logits, a.E, key);
+    RK rk;
+    if (!shared && wave == 0) rk.load(a.logits, a.E);
     // x does not depend on the route: in flight together with the logits
     uint4 xq[CPLA][4];
 #pragma unroll
@@ -271,28 +273,29 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
     if (!shared && wave == 0) {
-      uint32_t sel[kFusedMaxSlots];
-      route_select<KPL>(key, a.E, slot + 1, sel);
-      uint32_t mine = sel[0];
+      Key sel[kFusedMaxSlots];
+      rk.select(a.E, slot + 1, sel);
+      Key mine = sel[0];
 #pragma unroll
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
+      int ex = RK::expert(mine);
       // a probability tie the logit order cannot see (route_dev.hpp): this
       // slot's rank then comes from the reference's own arithmetic
-      const float m = sel_logit(sel[0]), ls = sel_logit(mine);
-      if (!bf16_rank_tie_free(m, ls)) {
+      const float m = RK::logit(sel[0]), ls = RK::logit(mine);
+      if (LF || !bf16_rank_tie_free(m, ls)) {
         bool cand = false, pair = false;
 #pragma unroll
         for (int i = 0; i < KPL; ++i)
-          cand = cand || (key[i] != 0u && tie_other(unord16(key[i] >> 16), ls, m));
+          cand = cand || (rk.key[i] != Key(0) && tie_other(RK::logit(rk.key[i]), ls, m));
 #pragma unroll
         for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
-          pair = pair || (r < slot && tie_pair(sel_logit(sel[r]), sel_logit(sel[r + 1]), m));
+          pair = pair || (r < slot && tie_pair(RK::logit(sel[r]), RK::logit(sel[r + 1]), m));
         if (__any(cand) || pair || tie_global(m, ls)) {
-          const RouteLane rl = route_exact<KPL, false>(logits, 0, a.E, a.k);
-          mine = 0xffffu - (uint32_t)__builtin_amdgcn_readlane(rl.idx, slot);
+          const RouteLane rl = route_exact<KPL, LF>(a.logits, 0, a.E, a.k);
+          ex = __builtin_amdgcn_readlane(rl.idx, slot);
         }
       }
-      if (lane == 0) s_sel[0] = mine;
+      if (lane == 0) s_sel[0] = 0xffffu - (uint32_t)ex;
     }
     if (threadIdx.x == 0) s_lid = launch_number(tk);
     __syncthreads();
@@ -414,8 +417,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   // wave 0 routes for the block
   unsigned long long tk = 0;
   if (threadIdx.x == 0) tk = take_ticket();
-  uint32_t key[KPL];
-  if (wave == 0) route_keys<KPL>(logits, a.E, key);
+  RK rk;
+  if (wave == 0) rk.load(a.logits, a.E);
 
   // route-independent loads first: the shared slot's down rows
   uint32_t wv[kSlotsPerWave][PASSES][BITS];
@@ -433,42 +436,44 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
   }
   if (wave == 0) {
-    uint32_t sel0[kFusedMaxSlots];
-    route_select<KPL>(key, a.E, g.k, sel0);
-    uint32_t mine = 0;
+    Key sel0[kFusedMaxSlots];
+    rk.select(a.E, g.k, sel0);
+    Key mine = 0;
 #pragma unroll
     for (int r = 0; r < kFusedMaxSlots; ++r) mine = lane == r ? sel0[r] : mine;
-    const float m = sel_logit(sel0[0]);
+    const float m = RK::logit(sel0[0]);
     float llast = m;
 #pragma unroll
-    for (int r = 0; r < kFusedMaxSlots; ++r) llast = r == g.k - 1 ? sel_logit(sel0[r]) : llast;
+    for (int r = 0; r < kFusedMaxSlots; ++r) llast = r == g.k - 1 ? RK::logit(sel0[r]) : llast;
     bool exact = false;
-    if (!bf16_ranks_tie_free(m, llast)) {
+    if (LF || !bf16_ranks_tie_free(m, llast)) {
       bool cand = false, pair = false;
 #pragma unroll
       for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
-        pair = pair || (r + 1 < g.k && tie_pair(sel_logit(sel0[r]), sel_logit(sel0[r + 1]), m));
+        pair = pair || (r + 1 < g.k && tie_pair(RK::logit(sel0[r]), RK::logit(sel0[r + 1]), m));
 #pragma unroll
       for (int i = 0; i < KPL; ++i)
-        cand = cand || (key[i] != 0u && tie_other(unord16(key[i] >> 16), llast, m));
+        cand = cand || (rk.key[i] != Key(0) && tie_other(RK::logit(rk.key[i]), llast, m));
       exact = __any(cand) || pair || tie_global(m, llast);
     }
     float wr;
+    uint32_t enc;  // 0xffff - expert of rank `lane`, 0 past the route
     if (exact) {
       // a probability tie the logit order cannot see (route_dev.hpp)
-      const RouteLane rl = route_exact<KPL, false>(logits, 0, a.E, g.k);
-      mine = lane < g.k ? 0xffffu - (uint32_t)rl.idx : 0u;
+      const RouteLane rl = route_exact<KPL, LF>(a.logits, 0, a.E, g.k);
+      enc = lane < g.k ? 0xffffu - (uint32_t)rl.idx : 0u;
       wr = rl.w;
     } else {
       // combine weights, one rank per lane (logan-qwen4/src/lib.rs:8694):
       // w_r = exp(l_r - l_0) / sum_{r<k} exp(l_r - l_0)
-      const float ev = lane < g.k ? __expf(sel_logit(mine) - m) : 0.f;
+      const float ev = lane < g.k ? __expf(RK::logit(mine) - m) : 0.f;
       wr = ev / wave_sum_f32(ev);
+      enc = lane < g.k ? 0xffffu - (uint32_t)RK::expert(mine) : 0u;
     }
-    if (lane < kFusedMaxSlots) s_sel[lane] = mine;
+    if (lane < kFusedMaxSlots) s_sel[lane] = enc;
     if (lane < kFusedMaxSlots) s_w[lane] = wr;
     if (bb == 0 && lane < g.k) {
-      if (a.idx_out) a.idx_out[lane] = sel_expert(mine);
+      if (a.idx_out) a.idx_out[lane] = sel_expert(enc);
       if (a.w_out) a.w_out[lane] = wr;
     }
   }
@@ -689,7 +694,7 @@ std::mutex g_order_mtx;
 FusedOrder g_order[kMaxDevices];
 }  // namespace
 
-template <int BITS, int CPLA, int LANESB, int KPL>
+template <int BITS, int CPLA, int LANESB, int KPL, bool LF>
 static int fused_launch(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
@@ -700,7 +705,7 @@ static int fused_launch(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
   FusedOrder &o = g_order[dev];
   if (!capturing && o.pending && o.last != st && hipStreamWaitEvent(st, o.ev, 0) != hipSuccess)
     return -1;
-  auto kern = moe_fused_b1_kernel<BITS, CPLA, LANESB, KPL>;
+  auto kern = moe_fused_b1_kernel<BITS, CPLA, LANESB, KPL, LF>;
   hipLaunchKernelGGL(kern, dim3(g.nA_blocks + g.nB_blocks), dim3(kWaves * 64), 0, st, a, g);
   if (hipGetLastError() != hipSuccess) return -1;
   o.last = st;
@@ -714,8 +719,13 @@ static int fused_launch(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
 
 template <int BITS, int CPLA, int LANESB>
 static int fused_kpl(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
-  if (a.E <= 512) return fused_launch<BITS, CPLA, LANESB, 8>(a, g, st);
-  if (a.E <= 1024) return fused_launch<BITS, CPLA, LANESB, 16>(a, g, st);
+  if (a.logits_f32) {
+    if (a.E <= 512) return fused_launch<BITS, CPLA, LANESB, 8, true>(a, g, st);
+    if (a.E <= 1024) return fused_launch<BITS, CPLA, LANESB, 16, true>(a, g, st);
+    return 0;
+  }
+  if (a.E <= 512) return fused_launch<BITS, CPLA, LANESB, 8, false>(a, g, st);
+  if (a.E <= 1024) return fused_launch<BITS, CPLA, LANESB, 16, false>(a, g, st);
   return 0;
 }
 
@@ -731,7 +741,7 @@ static int fused_bits(const MoeArgs &a, const FusedGeom &g, hipStream_t st) {
 
 // 1 launched, 0 not applicable (caller uses the multi-launch path), -1 error
 int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st) {
-  if (a.B != 1 || a.logits_f32) return 0;
+  if (a.B != 1) return 0;
   const int slots = a.k + (a.sdown.m.w ? 1 : 0);
   if (slots > kFusedMaxSlots || a.E > 1024) return 0;
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;

@@ -16,6 +16,7 @@
 // selects on them (route_exact).
 #pragma once
 #include <cstdint>
+#include <type_traits>
 
 #include "affine_dev.hpp"
 
@@ -100,47 +101,7 @@ __device__ __forceinline__ void sort_desc(uint32_t (&v)[N]) {
       }
 }
 
-// Routing by one wave, in two steps so the caller can put other loads in
-// flight between them: route_keys issues the logit loads (lane l holds
-// experts l + 64 i); route_select sorts each lane's keys and runs `rounds`
-// rounds of a wave max. sel[r] = 32-bit key of rank r: high half = ordered
-// logit, low half = 0xffff - expert.
-template <int KPL>
-__device__ __forceinline__ void route_keys(const uint16_t *logits, int E, uint32_t (&key)[KPL]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int e = i * 64 + lane;
-    key[i] = logits[e < E ? e : 0];
-  }
-}
-
-template <int KPL, int NSEL>
-__device__ __forceinline__ void route_select(uint32_t (&key)[KPL], int E, int rounds,
-                                             uint32_t (&sel)[NSEL]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int e = i * 64 + lane;
-    key[i] = e < E ? ((ord16(key[i]) << 16) | (0xffffu - (uint32_t)e)) : 0u;
-  }
-  sort_desc<KPL>(key);
-#pragma unroll
-  for (int r = 0; r < NSEL; ++r) {
-    sel[r] = 0;
-    if (r < rounds) {
-      const uint32_t m = wave_max_u32(key[0]);
-      sel[r] = m;
-      const bool mine = key[0] == m;  // keys are unique
-#pragma unroll
-      for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
-      key[KPL - 1] = mine ? 0u : key[KPL - 1];
-    }
-  }
-}
-
 __device__ __forceinline__ int sel_expert(uint32_t key) { return (int)(0xffffu - (key & 0xffffu)); }
-__device__ __forceinline__ float sel_logit(uint32_t key) { return unord16(key >> 16); }
 
 
 // ---- f32 logits: 64-bit keys (ordered f32 << 32 | ~index) -----------------
@@ -238,6 +199,71 @@ __device__ __forceinline__ bool bf16_rank_tie_free(float m, float lr) {
 __device__ __forceinline__ bool bf16_ranks_tie_free(float m, float llast) {
   return fabsf(m) < 64.f && (llast >= 0x1p-9f || m <= -0x1p-9f) && (llast - m) >= kTieFloor;
 }
+
+// Logit keys of one wave, for routing split into a load step and a select
+// step (other loads can be issued between them). bf16 logits give 32-bit
+// keys (ordered bf16 << 16 | 0xffff - expert), f32 logits 64-bit keys
+// (ordered f32 << 32 | 0xffffffff - expert); lane l holds experts
+// l + 64 i. After select, key[] holds this lane's unselected keys (0 =
+// none) and sel[r] the key of rank r.
+template <int KPL, bool LF>
+struct WaveKeys {
+  using K = typename std::conditional<LF, uint64_t, uint32_t>::type;
+  K key[KPL];
+  __device__ __forceinline__ void load(const void *logits, int E) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int e = i * 64 + lane, ee = e < E ? e : 0;
+      if constexpr (LF)
+        key[i] = __float_as_uint(reinterpret_cast<const float *>(logits)[ee]);
+      else
+        key[i] = reinterpret_cast<const uint16_t *>(logits)[ee];
+    }
+  }
+  template <int NSEL>
+  __device__ __forceinline__ void select(int E, int rounds, K (&sel)[NSEL]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int e = i * 64 + lane;
+      if constexpr (LF)
+        key[i] = e < E ? (((uint64_t)ord32f(__uint_as_float((uint32_t)key[i])) << 32) |
+                          (0xffffffffu - (uint32_t)e))
+                       : 0ull;
+      else
+        key[i] = e < E ? ((ord16(key[i]) << 16) | (0xffffu - (uint32_t)e)) : 0u;
+    }
+    if constexpr (LF)
+      sort_desc_u64<KPL>(key);
+    else
+      sort_desc<KPL>(key);
+#pragma unroll
+    for (int r = 0; r < NSEL; ++r) {
+      sel[r] = 0;
+      if (r < rounds) {
+        K m;
+        if constexpr (LF)
+          m = wave_max_u64(key[0]);
+        else
+          m = wave_max_u32(key[0]);
+        sel[r] = m;
+        const bool mine = key[0] == m;  // keys are unique
+#pragma unroll
+        for (int i = 0; i < KPL - 1; ++i) key[i] = mine ? key[i + 1] : key[i];
+        key[KPL - 1] = mine ? K(0) : key[KPL - 1];
+      }
+    }
+  }
+  __device__ static __forceinline__ int expert(K k) {
+    if constexpr (LF) return (int)(0xffffffffu - (uint32_t)k);
+    else return (int)(0xffffu - (k & 0xffffu));
+  }
+  __device__ static __forceinline__ float logit(K k) {
+    if constexpr (LF) return unord32f((uint32_t)(k >> 32));
+    else return unord16(k >> 16);
+  }
+};
 
 struct RouteLane {
   int idx;  // rank (lane) < k: expert; else -1

@@ -269,6 +269,40 @@ def moe_block(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
     return out
 
 
+def moe_block_routed(layer: MoeLayer, router: AffineMatrix, x: torch.Tensor,
+                     out: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None, return_routing: bool = False,
+                     out_dtype: torch.dtype = torch.bfloat16, stream=None):
+    """moe_block with the router product on device (logan_hip_moe_block_routed):
+    logits = x . router^T in f32 (returned), then the block on them."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    B, D = x.shape
+    if out is None:
+        out = torch.empty((B, D), dtype=out_dtype, device=x.device)
+    if logits is None:
+        logits = torch.empty((B, router.O), dtype=torch.float32, device=x.device)
+    od = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    idx = w = None
+    if return_routing:
+        idx = torch.empty((B, layer.top_k), dtype=torch.int32, device=x.device)
+        w = torch.empty((B, layer.top_k), dtype=torch.float32, device=x.device)
+    blk = layer.c()
+    rt = router.c()
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = _dev(workspace, "workspace"), workspace.numel() * workspace.element_size()
+    rc = L.lib().logan_hip_moe_block_routed(C.byref(blk), C.byref(rt), _dev(x, "x"), B,
+                                            _dev(logits, "logits"), _dev(out, "out"), od,
+                                            idx.data_ptr() if idx is not None else None,
+                                            w.data_ptr() if w is not None else None, ws_ptr,
+                                            ws_bytes, _stream(stream))
+    _check(rc, "moe_block_routed")
+    if return_routing:
+        return out, logits, idx, w
+    return out, logits
+
+
 def moe_block_static(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
                      out: Optional[torch.Tensor] = None, return_routing: bool = False,
                      out_dtype: torch.dtype = torch.bfloat16, stream=None):

@@ -516,3 +516,40 @@ def test_moe_fused_launches_on_two_streams(gpu, fused_mode):
     for i in range(n):
         assert torch.equal(outs[i], want[i]), i
     assert _lib.lib().logan_hip_moe_sync_errors() == 0
+
+
+@pytest.mark.parametrize("fused_mode,B,rbits,spread",
+                         [(1, 1, 8, 0.04), (0, 1, 8, 0.04), (1, 16, 8, 0.04), (1, 64, 4, 0.6),
+                          (1, 1, 4, 0.6), (1, 1, 8, 8.0), (1, 16, 8, 8.0)],
+                         indirect=["fused_mode"])
+def test_moe_block_with_router_on_device(gpu, fused_mode, B, rbits, spread):
+    """The router product on device (logan-qwen4/src/lib.rs:7990-7991) feeding
+    the block's f32-logit routing: the device logits against the oracle's
+    GEMV; the selection on those very logits bit-exact against the oracle's
+    softmax + top-k; the output against the oracle's MoE token on them.
+    `spread` scales the router: logits near N(0, 1) (the fast selection) or
+    in the hundreds (exps below the top one underflow: the recomputed
+    reference selection)."""
+    import torch
+    from logan_amd.device import AffineMatrix, moe_block_routed
+
+    print(f"moe router B={B} router bits={rbits} spread={spread} fused={fused_mode}", flush=True)
+    layer = Layer(torch, 512, 10, 2048, 512, 4, 64, seed=61 + B)
+    rng = np.random.default_rng(62 + B)
+    rw, rsc, rbi = make_affine(rng, 512, 2048, rbits, 64)
+    rsc = bf16_bits(bf16_to_f32(rsc) * np.float32(spread))
+    rbi = bf16_bits(bf16_to_f32(rsc) * np.float32(-(2 ** (rbits - 1))))
+    router = AffineMatrix(to_dev(rw, torch), to_dev(rsc.view(np.int16), torch),
+                          to_dev(rbi.view(np.int16), torch), 512, 2048, rbits, 64)
+    xb = make_x(rng, B, 2048)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    out, logits, idx, w = moe_block_routed(layer.dev, router, x, return_routing=True,
+                                           out_dtype=torch.float32)
+    out, logits, idx = out.cpu().numpy(), logits.cpu().numpy(), idx.cpu().numpy()
+    xf = bf16_to_f32(xb)
+    for t in range(B):
+        lref = oracle.affine_gemv(xf[t], rw, rsc, rbi, 512, 2048, rbits, 64)
+        assert normwise_rel(logits[t], lref) <= 2e-5
+        ref, ridx, _ = layer.ref(xf[t], logits[t])
+        np.testing.assert_array_equal(idx[t], ridx)
+        assert normwise_rel(out[t], ref) <= 5e-5
