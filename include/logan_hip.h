@@ -217,6 +217,35 @@ int logan_hip_affine_gemv_f32(const LoganHipAffine *w, const float *x, int M, in
 int logan_hip_affine_dequant(const LoganHipAffine *w, int row0, int nrows, float *out,
                              void *stream);
 
+/* One MXFP4 matrix in device memory (logan-metal fmt 7; planes 2 / 3 are
+ * fmt 9 / 10, the residual expansions whose products add,
+ * backend_metal.mm:438-490, 1860-1863, 1888-1890): codes
+ * [planes][O][I/2] (element 2j in the low nibble of byte j, E2M1; 16-byte
+ * aligned), scales [planes][O][I/32] E8M0 bytes (scale = 2^(byte - 127)). I a
+ * multiple of 32. */
+typedef struct LoganHipMxfp4 {
+  const void *codes;
+  const void *scales;
+  int O;
+  int I;
+  int planes; /* 1, 2, 3 */
+} LoganHipMxfp4;
+
+/* ys[i][O_i] = W_i . xs[i] for up to 16 matrices, each with its own
+ * activation, in one launch (the fmt 7/9/10 GEMV of backend_metal.mm
+ * :438-490, as coli_metal_matmul_multi batches it, :2290-2493). xs 16-byte
+ * aligned, x_dtype LOGAN_HIP_F32 (split in registers into bf16 hi + lo,
+ * |x - hi - lo| <= 2^-18 |x|) or LOGAN_HIP_BF16; y f32 or bf16 (RNE); f32
+ * accumulation, each 32-column group's sum scaled once by its power of two.
+ * 1 ok, 0 unsupported, -1 launch failure. */
+int logan_hip_mxfp4_gemv(const LoganHipMxfp4 *ws, int count, const void *const *xs, int x_dtype,
+                         void *const *ys, int y_dtype, void *stream);
+
+/* out[nrows][I] = E2M1(code) * 2^(scale - 127) of plane 0, rows
+ * [row0, row0+nrows), f32, through the decode instruction the GEMV uses —
+ * for bit-exact checks of the decode. */
+int logan_hip_mxfp4_dequant(const LoganHipMxfp4 *w, int row0, int nrows, float *out, void *stream);
+
 /* Router: per token, softmax over E logits then top-k with lower-index ties
  * (logan-qwen4/src/lib.rs:7993-8043); idx[B][k] in rank order, w[B][k] =
  * val_r / sum_{r<k} val (:8694). logits_dtype LOGAN_HIP_F32/BF16; E <= 1024,

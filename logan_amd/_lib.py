@@ -46,6 +46,16 @@ class Affine(C.Structure):
     ]
 
 
+class Mxfp4(C.Structure):
+    _fields_ = [
+        ("codes", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("O", C.c_int),
+        ("I", C.c_int),
+        ("planes", C.c_int),
+    ]
+
+
 class AffineBank(C.Structure):
     _fields_ = [
         ("weights", C.c_void_p),
@@ -95,6 +105,8 @@ SIGNATURES = {
     "logan_hip_moe_route_discard": (None, [_P]),
     "logan_hip_moe_route_drop_model": (None, [_U64]),
     "logan_hip_shared_expert": (_I, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _P, _I, _I]),
+    # logan-metal's own name for the shared-expert entry (include/logan_metal_ffi.h)
+    "coli_metal_shared_mxfp4": (_I, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _P, _I, _I]),
     "logan_hip_shared_expert_drop_model": (None, [_U64]),
     "logan_hip_host_rmsnorm": (_I, [_P, _P, _I, _I, C.c_float]),
     "logan_hip_host_add": (_I, [_P, _P, _I]),
@@ -107,6 +119,9 @@ SIGNATURES = {
     "logan_hip_affine_qmm": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
     "logan_hip_silu_mul": (_I, [_P, _P, C.c_longlong, _I, _P]),
     "logan_hip_affine_dequant": (_I, [C.POINTER(Affine), _I, _I, _P, _P]),
+    "logan_hip_mxfp4_gemv": (_I, [C.POINTER(Mxfp4), _I, C.POINTER(C.c_void_p), _I,
+                                  C.POINTER(C.c_void_p), _I, _P]),
+    "logan_hip_mxfp4_dequant": (_I, [C.POINTER(Mxfp4), _I, _I, _P, _P]),
     "logan_hip_route_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "logan_hip_moe_workspace_bytes": (_SZ, [C.POINTER(MoeBlock), _I]),
     "logan_hip_moe_block": (_I, [C.POINTER(MoeBlock), _P, _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _P]),

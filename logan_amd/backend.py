@@ -9,7 +9,8 @@ replaced by `hip_` where the reference name carries the backend:
     metal_matmul_mlx_affine_multi           :977-1062  -> hip_matmul_mlx_affine_multi
     moe_route_begin / moe_route_finish      :3822-3883 -> moe_route_begin / moe_route_finish
     MoeRoutePending (Drop => discard)       :3803-3815 -> MoeRoutePending (close/__del__)
-    shared_mxfp4 (affine form)              :2583-2678 -> shared_expert
+    shared_mxfp4 (MetalWeightDesc :188-196) :2583-2678 -> shared_mxfp4
+    shared_mxfp4 (affine descriptors)                  -> shared_expert
     dense_profile_start / _stop             :772-789   -> dense_profile_start / _stop
 
 Host arrays are numpy (f32 activations/outputs, u8 packed weights and the
@@ -147,12 +148,57 @@ class MlxAffineMatmulDesc:
     x: Optional[np.ndarray] = None
 
 
-def _raw_descs(descs: Sequence[MlxAffineMatmulDesc], with_y: bool):
+@dataclass
+class MetalWeightDesc:
+    """logan-metal/src/lib.rs:188-196: one weight of any fmt the backend
+    serves (7 / 9 / 10 MXFP4 with one / two / three planes, 15..24 affine);
+    `scales` holds the E8M0 bytes (MXFP4) or the [scales][biases] sidecar."""
+
+    tensor: Tensor
+    weights: np.ndarray
+    scales: np.ndarray
+    fmt: int
+    group_size: int
+    i: int
+    o: int
+    y: Optional[np.ndarray] = None
+    x: Optional[np.ndarray] = None
+
+
+MXFP4_PLANES = {7: 1, 9: 2, 10: 3}
+
+
+def _weight_desc_fmt(d: MetalWeightDesc, w: np.ndarray, a: np.ndarray) -> Optional[int]:
+    """Byte-size checks by format, as lib.rs:2606-2640 makes them (MXFP4:
+    ceil(i/2) code bytes and ceil(i/32) scale bytes per row and plane)."""
+    if d.i <= 0 or d.o <= 0:
+        return None
+    planes = MXFP4_PLANES.get(d.fmt)
+    if planes is not None:
+        if w.size < planes * d.o * ((d.i + 1) // 2) or a.size < planes * d.o * ((d.i + 31) // 32):
+            return None
+        return d.fmt
+    bits = {15: 8, 16: 4, 17: 5, 18: 6, 19: 8, 20: 4, 21: 4, 22: 5, 23: 6, 24: 8}.get(d.fmt)
+    if bits is None:
+        return None
+    gs = 64 if d.fmt == 15 else d.group_size
+    if gs <= 0 or d.i % gs != 0:
+        return None
+    if w.size < d.o * ((d.i * bits + 7) // 8) or a.size < 2 * d.o * (d.i // gs) * 2:
+        return None
+    return d.fmt
+
+
+def _raw_descs(descs, with_y: bool):
     raw = (L.MatmulDesc * len(descs))()
     keep = []
     for k, d in enumerate(descs):
-        w, a = _bytes(d.weights), _bytes(d.aux)
-        fmt = _affine_geometry_ok(d.bits, d.group_size, d.aux_fp16, d.i, d.o, w, a)
+        if isinstance(d, MetalWeightDesc):
+            w, a = _bytes(d.weights), _bytes(d.scales)
+            fmt = _weight_desc_fmt(d, w, a)
+        else:
+            w, a = _bytes(d.weights), _bytes(d.aux)
+            fmt = _affine_geometry_ok(d.bits, d.group_size, d.aux_fp16, d.i, d.o, w, a)
         if fmt is None:
             return None, None
         if with_y:
@@ -176,7 +222,7 @@ def _raw_descs(descs: Sequence[MlxAffineMatmulDesc], with_y: bool):
         raw[k].fmt = fmt
         raw[k].I = d.i
         raw[k].O = d.o
-        raw[k].gs = d.group_size
+        raw[k].gs = 0 if fmt in MXFP4_PLANES else d.group_size
         keep += [w, a]
     return raw, keep
 
@@ -268,6 +314,31 @@ def shared_expert(descs: Sequence[MlxAffineMatmulDesc], x: np.ndarray, out: np.n
     rc = L.lib().logan_hip_shared_expert(0, 0, raw, 3, _ptr(x), _ptr(out), d, iinter)
     _write_back(descs, raw)
     if rc == 1:
+        return True
+    if rc == 0:
+        return None
+    return False
+
+
+def shared_mxfp4(descs: Sequence[MetalWeightDesc], x: np.ndarray, out: np.ndarray, d: int,
+                 iinter: int, model_id: int = 1, layer: int = 0) -> Optional[bool]:
+    """logan-metal/src/lib.rs:2583-2678: [gate, up, down] of fmt 7 (MXFP4)
+    or 21..24 (affine, fp16 sidecars); Ok(Some(())) -> True, Ok(None)
+    (decline) -> None, Err(()) -> False."""
+    if (not hip_available() or model_id == 0 or len(descs) != 3 or d <= 0 or iinter <= 0):
+        return None
+    x, out = _f32(x), _f32(out)
+    if x.size < d or out.size < d:
+        return None
+    for dsc, (ei, eo) in zip(descs, ((d, iinter), (d, iinter), (iinter, d))):
+        if dsc.i != ei or dsc.o != eo or not (dsc.fmt == 7 or 21 <= dsc.fmt <= 24):
+            return None
+    raw, keep = _raw_descs(descs, with_y=False)
+    if raw is None:
+        return None
+    rc = L.lib().coli_metal_shared_mxfp4(model_id, layer, raw, 3, _ptr(x), _ptr(out), d, iinter)
+    _write_back(descs, raw)
+    if rc > 0:
         return True
     if rc == 0:
         return None

@@ -16,6 +16,7 @@ struct LoganHipTensor {
   uint16_t *sc = nullptr;
   uint16_t *bi = nullptr;
   int fmt = 0, I = 0, O = 0, gs = 0, bits = 0, fp16 = 0;
+  int planes = 0;  // MXFP4 planes (fmt 7 / 9 / 10: 1 / 2 / 3); 0 for affine codes
   size_t wbytes = 0, abytes = 0;
 };
 
@@ -182,6 +183,14 @@ bool fmt_info(int fmt, int gs_in, int &bits, int &fp16, int &gs) {
   return gs > 0;
 }
 
+// MXFP4 fmt -> number of stacked planes (backend_metal.mm:1860-1863); 0 otherwise
+int mx_planes(int fmt) { return fmt == 7 ? 1 : fmt == 9 ? 2 : fmt == 10 ? 3 : 0; }
+
+bool fmt_known(int fmt, int gs_in) {
+  int bits, fp16, gs;
+  return mx_planes(fmt) > 0 || fmt_info(fmt, gs_in, bits, fp16, gs);
+}
+
 bool geom_ok(long long I, long long O, int bits, int gs) {
   if (I <= 0 || O <= 0 || gs <= 0) return false;
   if (I % gs != 0) return false;
@@ -191,14 +200,18 @@ bool geom_ok(long long I, long long O, int bits, int gs) {
 
 // Create (first use) or validate the device copy of one affine tensor.
 // Returns nullptr on decline.
+LoganHipTensor *resolve_mxfp4_locked(LoganHipTensor **slot, const void *weights,
+                                     const void *aux, int fmt, int I, int O);
+
 LoganHipTensor *resolve_tensor_locked(LoganHipTensor **slot, const void *weights,
                                       const void *aux, int fmt, int I, int O, int gs_in) {
+  if (mx_planes(fmt)) return resolve_mxfp4_locked(slot, weights, aux, fmt, I, O);
   int bits, fp16, gs;
   if (!fmt_info(fmt, gs_in, bits, fp16, gs)) return nullptr;
   if (!geom_ok(I, O, bits, gs)) return nullptr;
   LoganHipTensor *t = slot ? *slot : nullptr;
   if (t) {
-    if (t->I != I || t->O != O || t->bits != bits || t->fp16 != fp16 || t->gs != gs)
+    if (t->planes || t->I != I || t->O != O || t->bits != bits || t->fp16 != fp16 || t->gs != gs)
       return nullptr;
     return t;
   }
@@ -234,6 +247,77 @@ LoganHipTensor *resolve_tensor_locked(LoganHipTensor **slot, const void *weights
   g_tensor_bytes += t->wbytes + t->abytes;
   if (slot) *slot = t;
   return t;
+}
+
+// MXFP4 tensors (fmt 7 / 9 / 10): codes [planes][O][I/2] and E8M0 scale
+// bytes [planes][O][I/32], planes back to back as the reference lays them
+// out (backend_metal.mm:460-470). The kernels take I a multiple of 32; other
+// widths decline.
+LoganHipTensor *resolve_mxfp4_locked(LoganHipTensor **slot, const void *weights,
+                                     const void *aux, int fmt, int I, int O) {
+  const int planes = mx_planes(fmt);
+  if (planes == 0 || I <= 0 || O <= 0 || I % 32 != 0) return nullptr;
+  LoganHipTensor *t = slot ? *slot : nullptr;
+  if (t) return (t->planes == planes && t->I == I && t->O == O) ? t : nullptr;
+  if (!weights || !aux) return nullptr;
+  t = new LoganHipTensor();
+  t->fmt = fmt;
+  t->I = I;
+  t->O = O;
+  t->gs = 32;
+  t->bits = 4;
+  t->planes = planes;
+  t->wbytes = (size_t)planes * O * (I / 2);
+  t->abytes = (size_t)planes * O * (I / 32);
+  void *sc = nullptr;
+  if (hipMalloc(&t->w, t->wbytes) != hipSuccess) {
+    delete t;
+    return nullptr;
+  }
+  if (hipMalloc(&sc, t->abytes) != hipSuccess) {
+    hipFree(t->w);
+    delete t;
+    return nullptr;
+  }
+  t->sc = reinterpret_cast<uint16_t *>(sc);
+  if (hipMemcpy(t->w, weights, t->wbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(sc, aux, t->abytes, hipMemcpyHostToDevice) != hipSuccess) {
+    hipFree(t->w);
+    hipFree(sc);
+    delete t;
+    return nullptr;
+  }
+  g_tensor_count++;
+  g_tensor_bytes += t->wbytes + t->abytes;
+  if (slot) *slot = t;
+  return t;
+}
+
+lh::Mx4Desc mx_desc(const LoganHipTensor *t, const void *x, void *y) {
+  lh::Mx4Desc d{};
+  d.w = t->w;
+  d.sc = reinterpret_cast<const uint8_t *>(t->sc);
+  d.x = x;
+  d.y = y;
+  d.wplane = (long long)t->O * (t->I / 2);
+  d.splane = (long long)t->O * (t->I / 32);
+  d.O = t->O;
+  d.I = t->I;
+  d.planes = t->planes;
+  return d;
+}
+
+// MXFP4 products (f32 activations and outputs) in launches of up to 16.
+hipError_t launch_mx_descs(const std::vector<lh::Mx4Desc> &ds, hipStream_t st) {
+  for (size_t b0 = 0; b0 < ds.size(); b0 += lh::kMx4MaxDescs) {
+    lh::Mx4Batch b{};
+    b.n = (int)std::min(ds.size() - b0, (size_t)lh::kMx4MaxDescs);
+    for (int i = 0; i < b.n; ++i) b.d[i] = ds[b0 + i];
+    b.y_bf16 = 0;
+    hipError_t e = lh::launch_mxfp4_gemv(b, true, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 lh::GenDesc gen_desc(const LoganHipTensor *t, const float *x, const float *up, float *y, int S,
@@ -510,7 +594,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   bool shared_pairs = false;
   for (int i = 0; i < count; ++i) {
     mat[i] = tensor_mat(ts[i]);
-    fast[i] = lh::gemv_bf16_supported(mat[i]);
+    fast[i] = !ts[i]->planes && lh::gemv_bf16_supported(mat[i]);
     shared_pairs = shared_pairs || (fast[i] && !descs[i].x && S > 1);
   }
   size_t xn = shared_I > 0 ? al_elems((size_t)S * shared_I, 4) : 0, yn = 0;
@@ -540,6 +624,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   uint16_t *dhl = reinterpret_cast<uint16_t *>(g_hlbuf.p);
   float *dy2 = reinterpret_cast<float *>(g_y2buf.p);
   std::vector<lh::GenDesc> ds;
+  std::vector<lh::Mx4Desc> mxs;  // MXFP4: one descriptor per activation row
   lh::HiloBatch split{}, join{};
   std::vector<lh::DevMat> shared_m, row_m;
   std::vector<void *> shared_y, row_y;
@@ -548,7 +633,10 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   for (int i = 0; i < count; ++i) {
     const int s = descs[i].x ? descs[i].S : S;
     const float *xs = descs[i].x ? dx + xoff[i] : dx;
-    if (!fast[i]) {
+    if (ts[i]->planes) {
+      for (int r = 0; r < s; ++r)
+        mxs.push_back(mx_desc(ts[i], xs + (size_t)r * ts[i]->I, dy + yoff[i] + (size_t)r * ts[i]->O));
+    } else if (!fast[i]) {
       ds.push_back(gen_desc(ts[i], xs, nullptr, dy + yoff[i], s, ts[i]->I, ts[i]->O, 0));
     } else if (s == 1) {
       row_m.push_back(mat[i]);
@@ -583,6 +671,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
       e = lh::launch_gemv_bf16(mat[i], dhl + hloff[i], descs[i].I, 2 * descs[i].S, dy2 + y2off[i],
                                descs[i].O, 0, g_stream);
   if (e == hipSuccess && !ds.empty()) e = launch_descs(ds, g_stream);
+  if (e == hipSuccess && !mxs.empty()) e = launch_mx_descs(mxs, g_stream);
   if (e == hipSuccess && join.n) e = lh::launch_hilo_join(join, g_stream);
   if (e != hipSuccess) return -1;
   if (g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
@@ -611,8 +700,7 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
   for (int i = 0; i < K; ++i)
     for (int r = 0; r < 3; ++r) {
       const LoganHipMatmulDesc &d = descs[i * 3 + r];
-      int bits, fp16, gs;
-      if (!fmt_info(d.fmt, d.gs, bits, fp16, gs)) return nullptr;
+      if (!fmt_known(d.fmt, d.gs)) return nullptr;
       if (d.I != expected_I[r] || d.O != expected_O[r]) return nullptr;
     }
   std::lock_guard<std::mutex> lk(g_mtx);
@@ -624,20 +712,18 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
                                   descs[i].fmt, descs[i].I, descs[i].O, descs[i].gs);
     if (!ts[i]) return nullptr;
   }
-  // fast path: every matrix on the bf16 kernels, gate/up and downs each of
-  // one geometry (x and h as bf16 hi/lo row pairs, f32 products)
+  // fast path: every matrix an MXFP4 one or one the bf16 kernels take (f32
+  // x split into bf16 hi/lo in registers, f32 products); h = silu(g) * u
+  // between the two stages. MXFP4 matrices need it (no fused-SwiGLU form).
   std::vector<lh::DevMat> mat((size_t)K * 3);
-  bool fast = true;
+  bool fast = true, any_mx = false;
   for (int i = 0; i < K * 3; ++i) {
     mat[i] = tensor_mat(ts[i]);
-    fast = fast && lh::gemv_bf16_supported(mat[i]);
+    any_mx = any_mx || ts[i]->planes;
+    fast = fast && (ts[i]->planes || lh::gemv_bf16_supported(mat[i]));
   }
-  for (int i = 0; fast && i < K; ++i)
-    for (int r = 0; r < 3; ++r) {
-      const lh::DevMat &a = mat[i * 3 + r], &b = mat[r == 2 ? 2 : 0];
-      fast = fast && a.bits == b.bits && a.gs == b.gs && a.fp16 == b.fp16;
-    }
   fast = fast && M % 4 == 0;  // 16-byte aligned per-expert h rows
+  if (any_mx && !fast) return nullptr;
   RoutePending *p = new (std::nothrow) RoutePending();
   if (!p) return nullptr;
   p->bufs = route_bufs_take((size_t)D * 4 + 16, (size_t)2 * K * M * 4 + 16, (size_t)K * D * 4 + 16);
@@ -661,21 +747,27 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
     std::vector<lh::DevMat> gum, dm;
     std::vector<const float *> gux, dxs;
     std::vector<void *> guy, dys;
+    std::vector<lh::Mx4Desc> gmx, dmx;
+    auto add = [&](int j, const float *xi, float *yi, bool down) {
+      if (ts[j]->planes) {
+        (down ? dmx : gmx).push_back(mx_desc(ts[j], xi, yi));
+        return;
+      }
+      (down ? dm : gum).push_back(mat[j]);
+      (down ? dxs : gux).push_back(xi);
+      (down ? dys : guy).push_back(yi);
+    };
     for (int i = 0; i < K; ++i) {
-      gum.push_back(mat[i * 3 + 0]);
-      gux.push_back(dx);
-      guy.push_back(gu + (size_t)i * M);
-      gum.push_back(mat[i * 3 + 1]);
-      gux.push_back(dx);
-      guy.push_back(gu + (size_t)K * M + (size_t)i * M);
-      dm.push_back(mat[i * 3 + 2]);
-      dxs.push_back(gu + (size_t)i * M);
-      dys.push_back(out + (size_t)i * D);
+      add(i * 3 + 0, dx, gu + (size_t)i * M, false);
+      add(i * 3 + 1, dx, gu + (size_t)K * M + (size_t)i * M, false);
+      add(i * 3 + 2, gu + (size_t)i * M, out + (size_t)i * D, true);
     }
     prof_add(0, t1 - t0);
-    if (e == hipSuccess) e = launch_f32x_groups(gum, gux, guy, g_stream);
+    if (e == hipSuccess && !gum.empty()) e = launch_f32x_groups(gum, gux, guy, g_stream);
+    if (e == hipSuccess && !gmx.empty()) e = launch_mx_descs(gmx, g_stream);
     if (e == hipSuccess) e = lh::launch_silu_mul(gu, gu + (size_t)K * M, (long long)K * M, false, g_stream);
-    if (e == hipSuccess) e = launch_f32x_groups(dm, dxs, dys, g_stream);
+    if (e == hipSuccess && !dm.empty()) e = launch_f32x_groups(dm, dxs, dys, g_stream);
+    if (e == hipSuccess && !dmx.empty()) e = launch_mx_descs(dmx, g_stream);
   } else {
     // gate -> gu[i*M], up -> gu[K*M + i*M]; down(silu(gate)*up) -> out[i*D]
     std::vector<lh::GenDesc> s1, s2;
@@ -1020,6 +1112,42 @@ int logan_hip_moe_block_static(const LoganHipMoeBlock *blk, const void *x, const
   a.ws = ws;
   a.ws_bytes = kStaticScratchBytes;
   return lh::launch_moe_block(a, reinterpret_cast<hipStream_t>(stream));
+}
+
+int logan_hip_mxfp4_gemv(const LoganHipMxfp4 *ws, int count, const void *const *xs, int x_dtype,
+                         void *const *ys, int y_dtype, void *stream) {
+  if (!ws || !xs || !ys || count <= 0 || count > lh::kMx4MaxDescs) return 0;
+  if ((x_dtype != LOGAN_HIP_F32 && x_dtype != LOGAN_HIP_BF16) ||
+      (y_dtype != LOGAN_HIP_F32 && y_dtype != LOGAN_HIP_BF16))
+    return 0;
+  lh::Mx4Batch b{};
+  b.n = count;
+  b.y_bf16 = y_dtype == LOGAN_HIP_BF16;
+  for (int i = 0; i < count; ++i) {
+    const LoganHipMxfp4 &m = ws[i];
+    if (!m.codes || !m.scales || m.planes < 1 || m.planes > 3) return 0;
+    if (!lh::mxfp4_supported(m.O, m.I, m.codes)) return 0;
+    if (!xs[i] || !ys[i] || (reinterpret_cast<uintptr_t>(xs[i]) & 15) != 0) return 0;
+    lh::Mx4Desc &d = b.d[i];
+    d.w = reinterpret_cast<const uint8_t *>(m.codes);
+    d.sc = reinterpret_cast<const uint8_t *>(m.scales);
+    d.x = xs[i];
+    d.y = ys[i];
+    d.wplane = (long long)m.O * (m.I / 2);
+    d.splane = (long long)m.O * (m.I / 32);
+    d.O = m.O;
+    d.I = m.I;
+    d.planes = m.planes;
+  }
+  return rc_from(lh::launch_mxfp4_gemv(b, x_dtype == LOGAN_HIP_F32, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int logan_hip_mxfp4_dequant(const LoganHipMxfp4 *w, int row0, int nrows, float *out, void *stream) {
+  if (!w || !w->codes || !w->scales || !out || !lh::mxfp4_supported(w->O, w->I, w->codes)) return 0;
+  if (row0 < 0 || nrows <= 0 || row0 + nrows > w->O) return 0;
+  return rc_from(lh::launch_mxfp4_dequant(reinterpret_cast<const uint8_t *>(w->codes),
+                                          reinterpret_cast<const uint8_t *>(w->scales), w->O, w->I,
+                                          row0, nrows, out, reinterpret_cast<hipStream_t>(stream)));
 }
 
 void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }

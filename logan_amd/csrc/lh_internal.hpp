@@ -97,6 +97,27 @@ struct GenBatch {
 constexpr int kGenRowsPerBlock = 4;
 hipError_t launch_gemv_generic(const GenBatch &b, hipStream_t st);
 
+// ---- MXFP4 (fmt 7; 2 / 3 residual planes = fmt 9 / 10) GEMV ----
+struct Mx4Desc {
+  const uint8_t *w;            // [planes][O][I/2], 16-byte aligned
+  const uint8_t *sc;           // [planes][O][I/32] E8M0 bytes
+  const void *x;               // [I] f32 or bf16, 16-byte aligned
+  void *y;                     // [O] f32 or bf16
+  long long wplane, splane;    // bytes between planes
+  int O, I, planes;
+};
+constexpr int kMx4MaxDescs = 16;
+struct Mx4Batch {
+  Mx4Desc d[kMx4MaxDescs];
+  int block_start[kMx4MaxDescs + 1];
+  int n;
+  int y_bf16;
+};
+bool mxfp4_supported(int O, int I, const void *w);
+hipError_t launch_mxfp4_gemv(Mx4Batch &b, bool x_f32, hipStream_t st);
+hipError_t launch_mxfp4_dequant(const uint8_t *w, const uint8_t *sc, int O, int I, int row0,
+                                int nrows, float *out, hipStream_t st);
+
 // ---- exact dequantisation of rows [row0, row0+nrows) to f32 ----
 hipError_t launch_dequant(const DevMat &m, int row0, int nrows, float *out, hipStream_t st);
 

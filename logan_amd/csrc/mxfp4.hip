@@ -1,0 +1,215 @@
+// MXFP4 (OCP microscaling FP4) GEMV for gfx950: logan-metal's fmt 7, and the
+// two- and three-plane residual forms fmt 9 / 10 (y = sum over planes of
+// W_p . x). Weights: per plane [O][I/2] bytes, element 2j in the low nibble
+// of byte j, an E2M1 code each (sign, two exponent bits, one mantissa bit);
+// scales: per plane [O][I/32] E8M0 bytes, scale = the f32 with bits
+// byte << 23 (logan-qwen4/src/lib.rs:2932-3038, matmul_mxfp4_bytes /
+// matmul_mxfp4_storage; logan-metal/metal/backend_metal.mm:438-459).
+//
+// One 32-column group is one 16-byte load of codes and one scale byte. The
+// codes are turned into exact bf16 pairs by v_cvt_scalef32_pk_bf16_fp4
+// (E2M1 values are exact in bf16; scale 1), dotted with x pairs by
+// v_dot2_f32_bf16, and the group's sum is scaled by its power of two (exact)
+// before it joins the row's f32 sum. f32 activations are split in registers
+// into bf16 hi + lo halves (|x - hi - lo| <= 2^-18 |x|) whose products are
+// summed. A team of LANES lanes owns U rows at a time; lane l takes the
+// groups l, l + LANES, ..., the next group's loads in flight while the
+// current one is used. Up to kMx4MaxDescs matrices (each with its own x and
+// y) share one launch.
+#include "affine_dev.hpp"
+#include "lh_internal.hpp"
+
+namespace lh {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kMx4U = 4;  // rows per team
+
+// the 32 codes of one 16-byte group as 16 bf16 pairs, element order
+__device__ __forceinline__ void mx4_pairs(const uint4 q, uint32_t (&pr)[16]) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    pr[4 * d + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 0));
+    pr[4 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 1));
+    pr[4 * d + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 2));
+    pr[4 * d + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], 1.0f, 3));
+  }
+}
+
+__device__ __forceinline__ float e8m0(uint32_t b) { return __uint_as_float(b << 23); }
+
+// one group's activation operands: bf16 pairs (and the lo halves for f32 x)
+template <bool XF>
+struct Mx4X {
+  uint32_t hi[16];
+  uint32_t lo[XF ? 16 : 1];
+};
+
+template <bool XF>
+__device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
+  if constexpr (XF) {
+    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + 32 * c);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const float4 f = src[v];
+      const float e[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int q = 0; q < 4; q += 2) {
+        const uint32_t h0 = f32_to_bf16_rne(e[q]), h1 = f32_to_bf16_rne(e[q + 1]);
+        const uint32_t l0 = f32_to_bf16_rne(e[q] - bf16_to_f32(h0));
+        const uint32_t l1 = f32_to_bf16_rne(e[q + 1] - bf16_to_f32(h1));
+        o.hi[2 * v + q / 2] = h0 | (h1 << 16);
+        o.lo[2 * v + q / 2] = l0 | (l1 << 16);
+      }
+    }
+  } else {
+    const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + 32 * c);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 t = src[v];
+      o.hi[4 * v] = t.x;
+      o.hi[4 * v + 1] = t.y;
+      o.hi[4 * v + 2] = t.z;
+      o.hi[4 * v + 3] = t.w;
+    }
+  }
+}
+
+template <int LANES, bool XF>
+__global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
+  int di = 0;
+  while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
+  const Mx4Desc d = b.d[di];
+  constexpr int TEAMS = 256 / LANES;
+  const int lane = threadIdx.x & (LANES - 1), team = threadIdx.x / LANES;
+  const int r0 = ((int)blockIdx.x - b.block_start[di]) * TEAMS * kMx4U + team * kMx4U;
+  const int C = d.I >> 5;
+  const long long rb = d.I >> 1;
+  float acc[kMx4U];
+#pragma unroll
+  for (int u = 0; u < kMx4U; ++u) acc[u] = 0.f;
+  float tot[kMx4U];
+#pragma unroll
+  for (int u = 0; u < kMx4U; ++u) tot[u] = 0.f;
+  for (int p = 0; p < d.planes; ++p) {
+    const uint8_t *wp = d.w + (size_t)p * d.wplane;
+    const uint8_t *sp = d.sc + (size_t)p * d.splane;
+    // groups of this lane, one ahead: codes and scale bytes of U rows, then x
+    auto load = [&](int c, uint4 (&q)[kMx4U], uint32_t (&s)[kMx4U]) {
+      const int cc = c < C ? c : C - 1;
+#pragma unroll
+      for (int u = 0; u < kMx4U; ++u) {
+        const int row = min(r0 + u, d.O - 1);
+        s[u] = sp[(size_t)row * C + cc];
+        q[u] = *reinterpret_cast<const uint4 *>(wp + (size_t)row * rb + 16 * (size_t)cc);
+      }
+    };
+    uint4 q0[kMx4U], q1[kMx4U];
+    uint32_t s0[kMx4U], s1[kMx4U];
+    Mx4X<XF> x0, x1;
+    int c = lane;
+    load(c, q0, s0);
+    mx4_load_x<XF>(d.x, c < C ? c : C - 1, x0);
+    auto use = [&](int cg, const uint4 (&q)[kMx4U], const uint32_t (&s)[kMx4U], const Mx4X<XF> &xv) {
+      if (cg >= C) return;
+#pragma unroll
+      for (int u = 0; u < kMx4U; ++u) {
+        uint32_t pr[16];
+        mx4_pairs(q[u], pr);
+        float g = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.hi[k], g);
+        if constexpr (XF) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.lo[k], g);
+        }
+        acc[u] = fmaf(g, e8m0(s[u]), acc[u]);  // g * 2^(s - 127) is exact
+      }
+    };
+    for (; c < C; c += 2 * LANES) {
+      load(c + LANES, q1, s1);
+      mx4_load_x<XF>(d.x, c + LANES < C ? c + LANES : C - 1, x1);
+      use(c, q0, s0, x0);
+      load(c + 2 * LANES, q0, s0);
+      mx4_load_x<XF>(d.x, c + 2 * LANES < C ? c + 2 * LANES : C - 1, x0);
+      use(c + LANES, q1, s1, x1);
+    }
+    // plane p's product joins the rows' totals (planes 2, 3 are residual
+    // corrections added in order, as the reference adds them)
+#pragma unroll
+    for (int u = 0; u < kMx4U; ++u) {
+      tot[u] += team_sum<LANES>(acc[u]);
+      acc[u] = 0.f;
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int u = 0; u < kMx4U; ++u) {
+      const int row = r0 + u;
+      if (row < d.O) {
+        if (b.y_bf16)
+          reinterpret_cast<uint16_t *>(d.y)[row] = (uint16_t)f32_to_bf16_rne(tot[u]);
+        else
+          reinterpret_cast<float *>(d.y)[row] = tot[u];
+      }
+    }
+  }
+}
+
+// out[r][c] = MX4[code] * scale for rows [row0, row0 + nrows) of plane 0,
+// through the same conversion instruction (then the exact scale multiply)
+__global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t *w, const uint8_t *sc, int I,
+                                                            int row0, int nrows, float *out) {
+  const long long n = (long long)nrows * (I >> 1);  // bytes = code pairs
+  for (long long t = (long long)blockIdx.x * 256 + threadIdx.x; t < n; t += (long long)gridDim.x * 256) {
+    const long long r = t / (I >> 1), j = t % (I >> 1);
+    const uint8_t byte = w[(size_t)(row0 + r) * (I >> 1) + j];
+    const float s = e8m0(sc[(size_t)(row0 + r) * (I >> 5) + (2 * j) / 32]);
+    const f32x2_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)byte, 1.0f, 0);
+    out[r * I + 2 * j] = v[0] * s;
+    out[r * I + 2 * j + 1] = v[1] * s;
+  }
+}
+
+bool mxfp4_supported(int O, int I, const void *w) {
+  return O > 0 && I > 0 && I % 32 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+}
+
+hipError_t launch_mxfp4_gemv(Mx4Batch &b, bool x_f32, hipStream_t st) {
+  if (b.n <= 0 || b.n > kMx4MaxDescs) return hipErrorInvalidValue;
+  int cmax = 0;
+  for (int i = 0; i < b.n; ++i) {
+    const Mx4Desc &d = b.d[i];
+    if (!mxfp4_supported(d.O, d.I, d.w) || !d.x || !d.y || d.planes < 1 || d.planes > 3)
+      return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(d.x) & 15) != 0) return hipErrorInvalidValue;
+    cmax = max(cmax, d.I >> 5);
+  }
+  const int lanes = cmax <= 16 ? 16 : 64;
+  const int rows_per_block = (256 / lanes) * kMx4U;
+  b.block_start[0] = 0;
+  for (int i = 0; i < b.n; ++i)
+    b.block_start[i + 1] = b.block_start[i] + (b.d[i].O + rows_per_block - 1) / rows_per_block;
+  const dim3 grid(b.block_start[b.n]);
+  if (lanes == 16) {
+    if (x_f32) hipLaunchKernelGGL((mxfp4_gemv_kernel<16, true>), grid, dim3(256), 0, st, b);
+    else hipLaunchKernelGGL((mxfp4_gemv_kernel<16, false>), grid, dim3(256), 0, st, b);
+  } else {
+    if (x_f32) hipLaunchKernelGGL((mxfp4_gemv_kernel<64, true>), grid, dim3(256), 0, st, b);
+    else hipLaunchKernelGGL((mxfp4_gemv_kernel<64, false>), grid, dim3(256), 0, st, b);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_mxfp4_dequant(const uint8_t *w, const uint8_t *sc, int O, int I, int row0,
+                                int nrows, float *out, hipStream_t st) {
+  if (!mxfp4_supported(O, I, w) || row0 < 0 || nrows <= 0 || row0 + nrows > O) return hipErrorInvalidValue;
+  const long long n = (long long)nrows * (I >> 1);
+  const int blocks = (int)std::min<long long>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3(blocks), dim3(256), 0, st, w, sc, I, row0, nrows, out);
+  return hipGetLastError();
+}
+
+}  // namespace lh

@@ -188,6 +188,59 @@ def affine_dequant(w: AffineMatrix, row0: int = 0, nrows: Optional[int] = None,
     return out
 
 
+@dataclass
+class Mxfp4Matrix:
+    """One MXFP4 matrix in HBM (logan-metal fmt 7; planes 2 / 3 = fmt 9 /
+    10): codes u8 [planes, O, I/2], E8M0 scale bytes u8 [planes, O, I/32]."""
+
+    codes: torch.Tensor
+    scales: torch.Tensor
+    O: int
+    I: int
+    planes: int = 1
+
+    def c(self) -> L.Mxfp4:
+        return L.Mxfp4(_dev(self.codes, "codes"), _dev(self.scales, "scales"), self.O, self.I,
+                       self.planes)
+
+
+def mxfp4_gemv(ws, xs, outs=None, out_dtype: torch.dtype = torch.float32, stream=None):
+    """[W_i . x_i] for up to 16 MXFP4 matrices, each with its own activation
+    (one row, f32 or bf16), in one launch (backend_metal.mm:438-490)."""
+    if not 1 <= len(ws) <= 16 or len(xs) != len(ws):
+        raise LoganHipError("between 1 and 16 matrices, one activation each")
+    dts = {x.dtype for x in xs}
+    if len(dts) != 1 or next(iter(dts)) not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("activations must all be bf16 or all f32")
+    for w, x in zip(ws, xs):
+        if x.numel() != w.I:
+            raise LoganHipError("activation length must equal I")
+    if outs is None:
+        outs = [torch.empty(w.O, dtype=out_dtype, device=xs[0].device) for w in ws]
+    ods = {o.dtype for o in outs}
+    if len(ods) != 1 or next(iter(ods)) not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("outputs must all be bf16 or all f32")
+    xd = L.LOGAN_HIP_BF16 if xs[0].dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    yd = L.LOGAN_HIP_BF16 if outs[0].dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    arr = (L.Mxfp4 * len(ws))(*[w.c() for w in ws])
+    xp = (C.c_void_p * len(ws))(*[_dev(x, "x") for x in xs])
+    yp = (C.c_void_p * len(ws))(*[_dev(o, "out") for o in outs])
+    rc = L.lib().logan_hip_mxfp4_gemv(arr, len(ws), xp, xd, yp, yd, _stream(stream))
+    _check(rc, "mxfp4_gemv")
+    return outs
+
+
+def mxfp4_dequant(w: Mxfp4Matrix, row0: int = 0, nrows: Optional[int] = None,
+                  stream=None) -> torch.Tensor:
+    """E2M1(code) * 2^(scale - 127) of plane 0 as f32, rows [row0, row0+nrows)."""
+    n = w.O - row0 if nrows is None else nrows
+    out = torch.empty((n, w.I), dtype=torch.float32, device=w.codes.device)
+    a = w.c()
+    rc = L.lib().logan_hip_mxfp4_dequant(C.byref(a), row0, n, _dev(out, "out"), _stream(stream))
+    _check(rc, "mxfp4_dequant")
+    return out
+
+
 def route_topk(logits: torch.Tensor, k: int, stream=None):
     """Per row: softmax top-k, lower-index ties; returns (idx int32 [B,k],
     weights f32 [B,k])."""

@@ -59,6 +59,10 @@ def lib() -> C.CDLL:
         h.lo_spark_affine8_gemv.argtypes = [P, P, P, P, SZ, SZ]
         h.lo_affine_qmm_bf16.restype = None
         h.lo_affine_qmm_bf16.argtypes = [P, P, P, P, P, SZ, SZ, SZ, I, SZ, I]
+        h.lo_mxfp4_value.restype = C.c_float
+        h.lo_mxfp4_value.argtypes = [C.c_uint8, C.c_uint8]
+        h.lo_mxfp4_gemv_stacked.restype = None
+        h.lo_mxfp4_gemv_stacked.argtypes = [P, P, P, P, SZ, SZ, I]
         h.lo_rmsnorm.restype = None
         h.lo_rmsnorm.argtypes = [P, P, SZ, SZ, C.c_float]
         h.lo_add.restype = None
@@ -150,6 +154,23 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     assert out.size == uu.size
     lib().lo_silu_mul(_p(out), _p(uu), out.size)
     return out
+
+
+def mxfp4_value(code: int, scale_byte: int) -> float:
+    return float(lib().lo_mxfp4_value(code, scale_byte))
+
+
+def mxfp4_gemv(x: np.ndarray, w, sc, O: int, I: int, stacks: int = 1) -> np.ndarray:
+    """y = W x for MXFP4 weights (fmt 7; stacks 2 / 3 = fmt 9 / 10):
+    w u8 [stacks][O][I/2], sc u8 [stacks][O][I/32]
+    (logan-qwen4/src/lib.rs:2932-3038)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint8)
+    sc = np.ascontiguousarray(sc, np.uint8)
+    assert w.size >= stacks * O * ((I + 1) // 2) and sc.size >= stacks * O * ((I + 31) // 32)
+    y = np.empty(O, np.float32)
+    lib().lo_mxfp4_gemv_stacked(_p(y), _p(x), _p(w), _p(sc), O, I, stacks)
+    return y
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -256,6 +256,50 @@ void lo_spark_affine8_gemv(float *y, const float *x, const uint8_t *w,
   free(xsum);
 }
 
+/* MXFP4 (OCP microscaling FP4, fmt 7): two E2M1 codes per byte, element 2j
+ * in the low nibble; one E8M0 scale byte per 32 columns, scale = the f32
+ * with bits byte << 23 (logan-qwen4/src/lib.rs:2932-2961, matmul_mxfp4_bytes;
+ * nibble order as :17676-17694). */
+static const float kMx4[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                               -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+float lo_mxfp4_value(uint8_t code, uint8_t scale_byte) {
+  return kMx4[code & 0xf] * f32_from_bits((uint32_t)scale_byte << 23);
+}
+
+/* y[r] = sum_col x[col] * MX4[code] * scale, in column order (lib.rs:2948-2961) */
+void lo_mxfp4_gemv(float *y, const float *x, const uint8_t *w, const uint8_t *sc, size_t o,
+                   size_t i) {
+  size_t rb = (i + 1) / 2, ng = (i + 31) / 32;
+  for (size_t row = 0; row < o; ++row) {
+    const uint8_t *wr = w + row * rb;
+    const uint8_t *sr = sc + row * ng;
+    float acc = 0.0f;
+    for (size_t col = 0; col < i; ++col) {
+      uint8_t packed = wr[col / 2];
+      uint8_t code = (col & 1) == 0 ? (packed & 0x0f) : (packed >> 4);
+      float scale = f32_from_bits((uint32_t)sr[col / 32] << 23);
+      acc = acc + (x[col] * kMx4[code]) * scale;
+    }
+    y[row] = acc;
+  }
+}
+
+/* fmt 7 / 9 / 10: one, two or three stacked MXFP4 planes, the later ones
+ * residual corrections added to the first plane's result in order
+ * (lib.rs:2985-3038, matmul_mxfp4_storage). */
+void lo_mxfp4_gemv_stacked(float *y, const float *x, const uint8_t *w, const uint8_t *sc,
+                           size_t o, size_t i, int stacks) {
+  size_t wb = o * ((i + 1) / 2), sb = o * ((i + 31) / 32);
+  lo_mxfp4_gemv(y, x, w, sc, o, i);
+  float *r = (float *)malloc(sizeof(float) * (o ? o : 1));
+  for (int s = 1; s < stacks; ++s) {
+    lo_mxfp4_gemv(r, x, w + (size_t)s * wb, sc + (size_t)s * sb, o, i);
+    for (size_t k = 0; k < o; ++k) y[k] = y[k] + r[k];
+  }
+  free(r);
+}
+
 /* In-place RMSNorm of nrows rows of n: the Metal kernel a_rmsnorm
  * (logan-metal/metal/backend_metal.mm:705-714, x * rsqrt(mean(x^2) + eps) *
  * w), with the sum of squares in double and the scale formed as

@@ -66,6 +66,11 @@ void lo_affine_qmm_bf16(float *y, const float *x, const uint8_t *w,
                         int fp16);
 
 /* logan-qwen4/src/lib.rs:4516-4518. */
+float lo_mxfp4_value(uint8_t code, uint8_t scale_byte);
+void lo_mxfp4_gemv(float *y, const float *x, const uint8_t *w, const uint8_t *sc, size_t o,
+                   size_t i);
+void lo_mxfp4_gemv_stacked(float *y, const float *x, const uint8_t *w, const uint8_t *sc,
+                           size_t o, size_t i, int stacks);
 void lo_rmsnorm(float *x, const float *w, size_t n, size_t nrows, float eps);
 void lo_add(float *y, const float *a, size_t n);
 float lo_silu(float x);

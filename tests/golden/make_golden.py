@@ -12,6 +12,12 @@ Sources (read as text; nothing from the reference is imported or run):
   * logan-qwen4/src/lib.rs:17056-17094  0x11 bytes (code 1), scale 1, bias 0, x = 1 -> y = 128
   * logan-qwen4/src/lib.rs:17015-17053  zero codes, scale 1, bias 1, x = 1 -> 128 (5-bit g128, 6-bit g64)
   * logan-spark/src/lib.rs:1327-1351    affine-8 code 2, scale 1, bias 0, I = 64 -> 128 (bf16 out)
+  * logan-qwen4/src/lib.rs:17676-17694  MXFP4 canonical nibble order: bytes
+      0x10 0x32 .. 0xfe with scale byte 127 hold 0, 0.5, 1, 1.5, 2, 3, 4, 6,
+      -0, -0.5, .., -6 (element 2i in the low nibble).
+  * logan-qwen4/src/lib.rs:17604-17651  MXFP4 projections: constant bytes
+      0x22 / 0x44 / 0xaa / 0xcc (codes 2, 4, 10, 12: 1, 2, -1, -2), scale byte
+      127 (1.0), I = 64, x = ((i % 7) - 3) / 8 -> value * sum(x).
   * logan-qwen4/src/lib.rs:17277-17348  stacked experts: expert 0 all-zero codes -> 0;
       expert 1 words 0x11111111 (code 1), scale 1, bias 0, x = 1, D = M = 64 ->
       64 * silu(64) * 64 per element (rel 1e-6).
@@ -80,8 +86,18 @@ def main() -> None:
            "scale": 1.0, "bias": 0.0, "x": 1.0,
            "expected_expert0": 0.0, "expected_expert1": 64.0 * (silu64 * 64.0),
            "rel_tol": 1e-6}
+    mx_order = {"source": "logan-qwen4/src/lib.rs:17676-17694",
+                "bytes": [0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE], "scale_byte": 127,
+                "expected": [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                             -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]}
+    xs = [((i % 7) - 3.0) / 8.0 for i in range(64)]
+    mx_proj = [{"source": "logan-qwen4/src/lib.rs:17604-17651", "O": o, "I": 64, "byte": b,
+                "scale_byte": 127, "x": xs, "expected": v * sum(xs)}
+               for o, b, v in ((64, 0x22, 1.0), (32, 0x44, 2.0), (32, 0xAA, -1.0),
+                               (16, 0xCC, -2.0))]
     OUT.write_text(json.dumps({"decode": cases, "gemv": gemv, "spark_affine8": spark,
-                               "expert": moe}, indent=1) + "\n")
+                               "expert": moe, "mxfp4_order": mx_order,
+                               "mxfp4_gemv": mx_proj}, indent=1) + "\n")
     print(f"wrote {OUT}")
 
 

@@ -401,3 +401,72 @@ def test_add_is_elementwise_sum():
     y = rng.standard_normal(1000).astype(np.float32)
     a = rng.standard_normal(1000).astype(np.float32)
     np.testing.assert_array_equal(oracle.add(y, a), y + a)
+
+
+def test_mxfp4_canonical_nibble_order_kat():
+    """logan-qwen4/src/lib.rs:17676-17694: bytes 0x10 0x32 .. 0xfe at scale
+    byte 127 hold 0, 0.5, .., 6, -0, .., -6, element 2j in the low nibble."""
+    c = GOLDEN["mxfp4_order"]
+    got = []
+    for b in c["bytes"]:
+        got += [oracle.mxfp4_value(b & 0xF, c["scale_byte"]), oracle.mxfp4_value(b >> 4, c["scale_byte"])]
+    np.testing.assert_array_equal(np.float32(got).view(np.uint32),
+                                  np.float32(c["expected"]).view(np.uint32))
+    # the same bytes through the GEMV with one-hot x pick each element
+    O, I = 1, 16
+    w = np.array(c["bytes"], np.uint8)
+    for col in range(I):
+        x = np.zeros(I, np.float32)
+        x[col] = 1.0
+        y = oracle.mxfp4_gemv(x, w, np.array([c["scale_byte"]], np.uint8), O, I)
+        assert y[0] == c["expected"][col]
+
+
+@pytest.mark.parametrize("case", GOLDEN["mxfp4_gemv"], ids=lambda c: hex(c["byte"]))
+def test_mxfp4_reference_projection_closed_forms(case):
+    """logan-qwen4/src/lib.rs:17604-17651: constant code bytes, scale 1."""
+    O, I = case["O"], case["I"]
+    y = oracle.mxfp4_gemv(np.float32(case["x"]), np.full(O * I // 2, case["byte"], np.uint8),
+                          np.full(O * I // 32, case["scale_byte"], np.uint8), O, I)
+    np.testing.assert_array_equal(y, np.full(O, case["expected"], np.float32))
+
+
+def test_mxfp4_decode_exhaustive_against_float64():
+    """Every code under a range of scale bytes: sign * E2M1 magnitude *
+    2^(byte - 127), with the E2M1 magnitudes rebuilt from the format (exponent
+    bits e, mantissa bit m: m/2 for e = 0, else 2^(e-1) (1 + m/2))."""
+    for code in range(16):
+        e, m, neg = (code >> 1) & 3, code & 1, code & 8
+        mag = m * 0.5 if e == 0 else 2.0 ** (e - 1) * (1 + m / 2)
+        for sb in (1, 64, 100, 126, 127, 128, 130, 200, 254):
+            want = (-mag if neg else mag) * 2.0 ** (sb - 127)
+            got = oracle.mxfp4_value(code, sb)
+            with np.errstate(over="ignore"):  # 6 * 2^127 is inf in f32, as in the reference
+                assert got == np.float32(want) and np.signbit(got) == bool(neg), (code, sb)
+
+
+@pytest.mark.parametrize("stacks", [1, 2, 3])
+def test_mxfp4_gemv_random_against_float64(stacks):
+    """Random bytes and scale bytes near 127, stacked planes (fmt 7/9/10):
+    the oracle against a float64 decode-then-dot of the summed planes; a
+    swapped nibble order or a dropped residual plane fails it."""
+    rng = np.random.default_rng(70 + stacks)
+    O, I = 40, 512
+    w = rng.integers(0, 256, (stacks, O, I // 2)).astype(np.uint8)
+    sc = rng.integers(120, 131, (stacks, O, I // 32)).astype(np.uint8)
+    x = rng.standard_normal(I).astype(np.float32)
+
+    def dec(wp, sp, swap=False):
+        lo, hi = (wp >> 4, wp & 0xF) if swap else (wp & 0xF, wp >> 4)
+        codes = np.stack([lo, hi], axis=-1).reshape(O, I)
+        tab = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6])
+        return tab[codes] * np.repeat(2.0 ** (sp.astype(np.float64) - 127), 32, axis=1)
+
+    ref = sum(dec(w[s], sc[s]) for s in range(stacks)) @ x.astype(np.float64)
+    y = oracle.mxfp4_gemv(x, w, sc, O, I, stacks)
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    swapped = sum(dec(w[s], sc[s], True) for s in range(stacks)) @ x.astype(np.float64)
+    assert np.abs(swapped - ref).max() > 1e-2 * np.abs(ref).max()
+    if stacks > 1:
+        first = dec(w[0], sc[0]) @ x.astype(np.float64)
+        assert np.abs(first - ref).max() > 1e-2 * np.abs(ref).max()
