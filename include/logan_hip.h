@@ -111,22 +111,38 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
  * One submission: K gate + K up GEMVs, SwiGLU h = silu(g)*u, K down GEMVs.
  * begin returns an opaque pending handle (NULL = pre-submit decline);
  * finish waits and writes the K expert outputs (count*D floats, expert-major);
- * the caller does its own rank-ordered weighted reduction. Unlike the
- * reference, fmt 16..19 (bf16 sidecars) are accepted as well as 21..24; fmt 7
- * (MXFP4) declines. */
+ * the caller does its own rank-ordered weighted reduction. fmt 7 (MXFP4) and
+ * 21..24 as the reference, and 16..19 (bf16 sidecars) as well, mixed per
+ * matrix. */
 void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
                                 const float *x, int D, int M);
 int logan_hip_moe_route_finish(void *pending, float *out, int count);
 void logan_hip_moe_route_discard(void *pending);
 void logan_hip_moe_route_drop_model(uint64_t model_id);
 
-/* Replaces coli_metal_shared_mxfp4 (backend_metal.h:146-149) for affine
- * weights: descs = [gate, up, down] (count == 3), out[D] =
+/* Replaces coli_metal_shared_mxfp4 (backend_metal.h:146-149): descs =
+ * [gate, up, down] (count == 3) of fmt 7 (MXFP4) or affine, out[D] =
  * down(silu(gate.x) * (up.x)). The scalar shared-expert gate stays with the
- * caller (logan-qwen4/src/lib.rs:7602-7604). fmt 7 declines. */
+ * caller (logan-qwen4/src/lib.rs:7602-7604). */
 int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
                             const float *x, float *out, int D, int Iinter);
 void logan_hip_shared_expert_drop_model(uint64_t model_id);
+
+/* Replaces coli_metal_llama_layer / coli_metal_llama_drop_model
+ * (backend_metal.h:102-115, backend_metal.mm:2495-2791): one dense
+ * Llama/MiniCPM5 decode layer on x[D] in place. descs are exactly
+ * [q, k, v, o, gate, up, down] of fmt 5 (raw bf16) or 15 (affine-8 g64, each
+ * weight rounded to bf16 as the reference's QMV does); RMSNorm, RoPE,
+ * attention over the layer's GPU-held f32 K/V cache, residuals and SwiGLU
+ * run on the device, and the position's K and V rows (after RoPE) come back
+ * in k_out / v_out [kv_heads * head_dim]. Calls for one (model_id, layer)
+ * must come in position order (pos = tokens so far, else 0); drop_model
+ * frees the caches. head_dim even and <= 256. 1 ok, 0 declined, -1 failure. */
+int logan_hip_host_llama_layer(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                               float *x, float *k_out, float *v_out, const float *in_norm,
+                               const float *post_norm, int D, int inter, int heads, int kv_heads,
+                               int head_dim, int pos, float theta, float eps);
+void logan_hip_host_llama_drop_model(uint64_t model_id);
 
 /* Host-pointer element-wise ops on the GPU (stage in HBM, run, copy back,
  * wait): in-place RMSNorm of nrows rows of n floats,
@@ -245,6 +261,43 @@ int logan_hip_mxfp4_gemv(const LoganHipMxfp4 *ws, int count, const void *const *
  * [row0, row0+nrows), f32, through the decode instruction the GEMV uses —
  * for bit-exact checks of the decode. */
 int logan_hip_mxfp4_dequant(const LoganHipMxfp4 *w, int row0, int nrows, float *out, void *stream);
+
+/* One matrix of the dense decode layer in device memory: fmt 5 = raw bf16
+ * weights [O][I] (I a multiple of 16); fmt 15 = MLX affine-8 codes u8 [O][I]
+ * with bf16 scales and biases [O][I/64] each (I a multiple of 64), every
+ * weight taken as RNE_bf16(code * scale + bias). 16-byte aligned. */
+typedef struct LoganHipDense {
+  const void *weights;
+  const void *scales;
+  const void *biases;
+  int O;
+  int I;
+  int fmt;
+} LoganHipDense;
+
+/* A dense Llama layer in device memory: its seven matrices, f32 norm
+ * weights [D], and the caller's f32 K/V cache [cache_tokens][kv_heads *
+ * head_dim] (K rows stored after RoPE). */
+typedef struct LoganHipLlamaLayer {
+  LoganHipDense q, k, v, o, gate, up, down;
+  const float *in_norm;
+  const float *post_norm;
+  float *k_cache;
+  float *v_cache;
+  int cache_tokens;
+  int D, inter, heads, kv_heads, head_dim;
+  float theta, eps;
+} LoganHipLlamaLayer;
+
+/* Workspace bytes of logan_hip_llama_layer at position pos (0 if the layer
+ * is unsupported). */
+size_t logan_hip_llama_workspace_bytes(const LoganHipLlamaLayer *L, int pos);
+
+/* The decode layer of logan_hip_host_llama_layer on device buffers: x[D] f32
+ * in place, K[pos] and V[pos] written to the caches (pos < cache_tokens),
+ * attention over positions 0..pos. 1 ok, 0 unsupported, -1 launch failure. */
+int logan_hip_llama_layer(const LoganHipLlamaLayer *L, float *x, int pos, void *ws, size_t ws_bytes,
+                          void *stream);
 
 /* Router: per token, softmax over E logits then top-k with lower-index ties
  * (logan-qwen4/src/lib.rs:7993-8043); idx[B][k] in rank order, w[B][k] =

@@ -13,7 +13,7 @@
  *    reference's 1 / 0 / -1 return convention;
  *  - advisory: host-memory registration, which this library does not need;
  *  - declining: operations outside the quantized-decode hot path (ANE and
- *    IOSurface bridges, GDN/HC/attention/Spark layers, MetalIO streaming,
+ *    IOSurface bridges, GDN/HC/MLA/Spark layers, MetalIO streaming,
  *    Apple8 tiles, BNNS), returning what the reference's non-macOS build
  *    returns to its callers (logan-metal/src/lib.rs:4322-5069: nothing is
  *    done, the caller keeps its CPU path).
@@ -67,6 +67,14 @@ int32_t coli_metal_shared_mxfp4(uint64_t model_id, int32_t layer, ColiMetalMatmu
                                 int32_t iinter);
 /* lib.rs:453 -> logan_hip_shared_expert_drop_model */
 void coli_metal_shared_mxfp4_drop_model(uint64_t model_id);
+/* lib.rs:285 -> logan_hip_host_llama_layer */
+int32_t coli_metal_llama_layer(uint64_t model_id, int32_t layer, ColiMetalMatmulDesc *descs,
+                               int32_t count, float *x, float *k_out, float *v_out,
+                               const float *input_norm, const float *post_norm, int32_t d,
+                               int32_t inter, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                               int32_t pos, float theta, float eps);
+/* lib.rs:304 -> logan_hip_host_llama_drop_model */
+void coli_metal_llama_drop_model(uint64_t model_id);
 /* lib.rs:454 -> logan_hip_host_rmsnorm */
 int32_t coli_metal_rmsnorm(float *x, const float *w, int32_t n, int32_t nrows, float eps);
 /* lib.rs:455 -> logan_hip_host_add */
@@ -146,14 +154,6 @@ void *logan_metal_gdn_conv_silu_begin(void *handle);
 int32_t logan_metal_gdn_conv_silu_finish(void *handle, double *gpu_ms);
 /* lib.rs:251: no-op */
 void logan_metal_gdn_conv_silu_free(void *handle);
-/* lib.rs:285: 0 */
-int32_t coli_metal_llama_layer(uint64_t model_id, int32_t layer, ColiMetalMatmulDesc *descs,
-                               int32_t count, float *x, float *k_out, float *v_out,
-                               const float *input_norm, const float *post_norm, int32_t d,
-                               int32_t inter, int32_t heads, int32_t kv_heads, int32_t head_dim,
-                               int32_t pos, float theta, float eps);
-/* lib.rs:304: no-op */
-void coli_metal_llama_drop_model(uint64_t model_id);
 /* lib.rs:305: 0 */
 int32_t coli_metal_gdn_mxfp4(uint64_t model_id, int32_t layer, ColiMetalMatmulDesc *descs,
                              int32_t count, const float *x, float *out, const float *a_log,

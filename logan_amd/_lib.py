@@ -56,6 +56,34 @@ class Mxfp4(C.Structure):
     ]
 
 
+class Dense(C.Structure):
+    _fields_ = [
+        ("weights", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("O", C.c_int),
+        ("I", C.c_int),
+        ("fmt", C.c_int),
+    ]
+
+
+class LlamaLayer(C.Structure):
+    _fields_ = [(n, Dense) for n in ("q", "k", "v", "o", "gate", "up", "down")] + [
+        ("in_norm", C.c_void_p),
+        ("post_norm", C.c_void_p),
+        ("k_cache", C.c_void_p),
+        ("v_cache", C.c_void_p),
+        ("cache_tokens", C.c_int),
+        ("D", C.c_int),
+        ("inter", C.c_int),
+        ("heads", C.c_int),
+        ("kv_heads", C.c_int),
+        ("head_dim", C.c_int),
+        ("theta", C.c_float),
+        ("eps", C.c_float),
+    ]
+
+
 class AffineBank(C.Structure):
     _fields_ = [
         ("weights", C.c_void_p),
@@ -122,6 +150,11 @@ SIGNATURES = {
     "logan_hip_mxfp4_gemv": (_I, [C.POINTER(Mxfp4), _I, C.POINTER(C.c_void_p), _I,
                                   C.POINTER(C.c_void_p), _I, _P]),
     "logan_hip_mxfp4_dequant": (_I, [C.POINTER(Mxfp4), _I, _I, _P, _P]),
+    "logan_hip_llama_workspace_bytes": (_SZ, [C.POINTER(LlamaLayer), _I]),
+    "logan_hip_llama_layer": (_I, [C.POINTER(LlamaLayer), _P, _I, _P, _SZ, _P]),
+    "logan_hip_host_llama_layer": (_I, [_U64, _I, C.POINTER(MatmulDesc), _I, _P, _P, _P, _P, _P,
+                                        _I, _I, _I, _I, _I, _I, C.c_float, C.c_float]),
+    "logan_hip_host_llama_drop_model": (None, [_U64]),
     "logan_hip_route_topk": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "logan_hip_moe_workspace_bytes": (_SZ, [C.POINTER(MoeBlock), _I]),
     "logan_hip_moe_block": (_I, [C.POINTER(MoeBlock), _P, _P, _I, _I, _P, _I, _P, _P, _P, _SZ, _P]),

@@ -12,6 +12,7 @@ replaced by `hip_` where the reference name carries the backend:
     shared_mxfp4 (MetalWeightDesc :188-196) :2583-2678 -> shared_mxfp4
     shared_mxfp4 (affine descriptors)                  -> shared_expert
     dense_profile_start / _stop             :772-789   -> dense_profile_start / _stop
+    llama_layer / llama_drop_model          :1559-1681 -> llama_layer / llama_drop_model
 
 Host arrays are numpy (f32 activations/outputs, u8 packed weights and the
 [scales][biases] u16 sidecar as bytes). Validation declines (returns False /
@@ -343,6 +344,76 @@ def shared_mxfp4(descs: Sequence[MetalWeightDesc], x: np.ndarray, out: np.ndarra
     if rc == 0:
         return None
     return False
+
+
+@dataclass
+class MetalMatmulDesc:
+    """logan-metal/src/lib.rs:160-168 (the llama layer's descriptors:
+    fmt 5 raw bf16 weights, fmt 15 affine-8 g64 with its sidecar)."""
+
+    tensor: Tensor
+    y: np.ndarray
+    weights: np.ndarray
+    scales: np.ndarray
+    fmt: int
+    i: int
+    o: int
+
+
+def llama_layer(model_id: int, layer: int, descs: Sequence[MetalMatmulDesc], x: np.ndarray,
+                k_out: np.ndarray, v_out: np.ndarray, input_norm: np.ndarray,
+                post_norm: np.ndarray, d: int, inter: int, heads: int, kv_heads: int,
+                head_dim: int, pos: int, theta: float, eps: float) -> int:
+    """logan-metal/src/lib.rs:1559-1675: 1 ok, 0 declined (x untouched),
+    -1 failure after submission. x [d] is updated in place; k_out / v_out
+    receive the position's K (after RoPE) and V rows."""
+    if (not hip_available() or model_id == 0 or len(descs) != 7 or d <= 0 or inter <= 0
+            or heads <= 0 or kv_heads <= 0 or head_dim <= 0 or heads % kv_heads != 0 or pos < 0):
+        return 0
+    x, k_out, v_out = _f32(x), _f32(k_out), _f32(v_out)
+    input_norm, post_norm = _f32(input_norm), _f32(post_norm)
+    kv = kv_heads * head_dim
+    if (x.size < d or k_out.size < kv or v_out.size < kv or input_norm.size < d
+            or post_norm.size < d):
+        return 0
+    q = heads * head_dim
+    expected = [(d, q), (d, kv), (d, kv), (q, d), (d, inter), (d, inter), (inter, d)]
+    raw = (L.MatmulDesc * 7)()
+    keep = []
+    dummy = np.ones(1, np.float32)
+    for k, (dsc, (ei, eo)) in enumerate(zip(descs, expected)):
+        w = _bytes(dsc.weights)
+        if dsc.fmt == 5:
+            need_w, need_s, a = ei * eo * 2, 0, dummy.view(np.uint8)
+        elif dsc.fmt == 15:
+            a = _bytes(dsc.scales)
+            need_w, need_s = ei * eo, 2 * eo * ((ei + 63) // 64) * 2
+        else:
+            return 0
+        if dsc.i != ei or dsc.o != eo or w.size < need_w or a.size < need_s:
+            return 0
+        raw[k].tensor = dsc.tensor.handle or None
+        raw[k].y = None
+        raw[k].weights = _ptr(w)
+        raw[k].scales = _ptr(a)
+        raw[k].fmt = dsc.fmt
+        raw[k].I = ei
+        raw[k].O = eo
+        raw[k].gs = 64 if dsc.fmt == 15 else 0
+        raw[k].x = None
+        raw[k].S = 1
+        keep += [w, a]
+    rc = L.lib().logan_hip_host_llama_layer(model_id, layer, raw, 7, _ptr(x), _ptr(k_out),
+                                            _ptr(v_out), _ptr(input_norm), _ptr(post_norm), d,
+                                            inter, heads, kv_heads, head_dim, pos, theta, eps)
+    _write_back(descs, raw)
+    return int(rc)
+
+
+def llama_drop_model(model_id: int) -> None:
+    """logan-metal/src/lib.rs:1677-1681."""
+    if model_id and hip_available():
+        L.lib().logan_hip_host_llama_drop_model(model_id)
 
 
 def dense_profile_start() -> None:

@@ -203,15 +203,19 @@ bool geom_ok(long long I, long long O, int bits, int gs) {
 LoganHipTensor *resolve_mxfp4_locked(LoganHipTensor **slot, const void *weights,
                                      const void *aux, int fmt, int I, int O);
 
+LoganHipTensor *resolve_bf16_locked(LoganHipTensor **slot, const void *weights, int I, int O);
+
 LoganHipTensor *resolve_tensor_locked(LoganHipTensor **slot, const void *weights,
                                       const void *aux, int fmt, int I, int O, int gs_in) {
   if (mx_planes(fmt)) return resolve_mxfp4_locked(slot, weights, aux, fmt, I, O);
+  if (fmt == 5) return resolve_bf16_locked(slot, weights, I, O);
   int bits, fp16, gs;
   if (!fmt_info(fmt, gs_in, bits, fp16, gs)) return nullptr;
   if (!geom_ok(I, O, bits, gs)) return nullptr;
   LoganHipTensor *t = slot ? *slot : nullptr;
   if (t) {
-    if (t->planes || t->I != I || t->O != O || t->bits != bits || t->fp16 != fp16 || t->gs != gs)
+    if (t->planes || t->fmt == 5 || t->I != I || t->O != O || t->bits != bits || t->fp16 != fp16 ||
+        t->gs != gs)
       return nullptr;
     return t;
   }
@@ -291,6 +295,57 @@ LoganHipTensor *resolve_mxfp4_locked(LoganHipTensor **slot, const void *weights,
   g_tensor_bytes += t->wbytes + t->abytes;
   if (slot) *slot = t;
   return t;
+}
+
+// Raw bf16 weights (fmt 5, [O][I], backend_metal.mm:1865): served by the
+// dense kernel, which takes I a multiple of 16; other widths decline.
+LoganHipTensor *resolve_bf16_locked(LoganHipTensor **slot, const void *weights, int I, int O) {
+  if (I <= 0 || O <= 0 || I % 16 != 0) return nullptr;
+  LoganHipTensor *t = slot ? *slot : nullptr;
+  if (t) return (t->fmt == 5 && t->I == I && t->O == O) ? t : nullptr;
+  if (!weights) return nullptr;
+  t = new LoganHipTensor();
+  t->fmt = 5;
+  t->I = I;
+  t->O = O;
+  t->bits = 16;
+  t->wbytes = (size_t)O * I * 2;
+  if (hipMalloc(&t->w, t->wbytes) != hipSuccess) {
+    delete t;
+    return nullptr;
+  }
+  if (hipMemcpy(t->w, weights, t->wbytes, hipMemcpyHostToDevice) != hipSuccess) {
+    hipFree(t->w);
+    delete t;
+    return nullptr;
+  }
+  g_tensor_count++;
+  g_tensor_bytes += t->wbytes;
+  if (slot) *slot = t;
+  return t;
+}
+
+lh::DenseMat dense_mat(const LoganHipTensor *t) {
+  lh::DenseMat m{};
+  m.w = t->w;
+  m.sc = t->fmt == 15 ? t->sc : nullptr;
+  m.bi = t->fmt == 15 ? t->bi : nullptr;
+  m.fmt = t->fmt;
+  m.O = t->O;
+  m.I = t->I;
+  return m;
+}
+
+// Dense (fmt 5) products, x as bf16 hi/lo halves, in launches of up to 8.
+hipError_t launch_dense5(const std::vector<lh::DenseDesc> &ds, hipStream_t st) {
+  for (size_t b0 = 0; b0 < ds.size(); b0 += lh::kDenseMaxDescs) {
+    lh::DenseBatch b{};
+    b.n = (int)std::min(ds.size() - b0, (size_t)lh::kDenseMaxDescs);
+    for (int i = 0; i < b.n; ++i) b.d[i] = ds[b0 + i];
+    hipError_t e = lh::launch_dense_gemv(b, 5, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 lh::Mx4Desc mx_desc(const LoganHipTensor *t, const void *x, void *y) {
@@ -397,7 +452,7 @@ lh::DevMat tensor_mat(const LoganHipTensor *t) {
   m.bits = t->bits;
   m.fp16 = t->fp16;
   m.row_bytes = (long long)t->I * t->bits / 8;
-  m.ng = t->I / t->gs;
+  m.ng = t->gs > 0 ? t->I / t->gs : 0;  // raw bf16 tensors have no groups
   return m;
 }
 
@@ -590,12 +645,13 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   // row pairs through the row-batched kernels with each output row re-joined
   // as y = y_hi + y_lo. The rest take the exact per-element kernel.
   std::vector<lh::DevMat> mat(count);
-  std::vector<char> fast(count);
+  std::vector<char> fast(count), dense5(count);
   bool shared_pairs = false;
   for (int i = 0; i < count; ++i) {
     mat[i] = tensor_mat(ts[i]);
-    fast[i] = !ts[i]->planes && lh::gemv_bf16_supported(mat[i]);
-    shared_pairs = shared_pairs || (fast[i] && !descs[i].x && S > 1);
+    dense5[i] = ts[i]->fmt == 5;
+    fast[i] = !ts[i]->planes && !dense5[i] && lh::gemv_bf16_supported(mat[i]);
+    shared_pairs = shared_pairs || (!descs[i].x && ((fast[i] && S > 1) || dense5[i]));
   }
   size_t xn = shared_I > 0 ? al_elems((size_t)S * shared_I, 4) : 0, yn = 0;
   size_t hln = shared_pairs ? al_elems((size_t)2 * S * shared_I, 2) : 0, y2n = 0;
@@ -605,7 +661,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
     if (descs[i].x) {
       xoff[i] = xn;
       xn += al_elems((size_t)s * descs[i].I, 4);
-      if (fast[i] && s > 1) {
+      if ((fast[i] && s > 1) || dense5[i]) {
         hloff[i] = hln;
         hln += al_elems((size_t)2 * s * descs[i].I, 2);
       }
@@ -625,6 +681,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   float *dy2 = reinterpret_cast<float *>(g_y2buf.p);
   std::vector<lh::GenDesc> ds;
   std::vector<lh::Mx4Desc> mxs;  // MXFP4: one descriptor per activation row
+  std::vector<lh::DenseDesc> d5s;  // raw bf16: one descriptor per activation row
   lh::HiloBatch split{}, join{};
   std::vector<lh::DevMat> shared_m, row_m;
   std::vector<void *> shared_y, row_y;
@@ -636,6 +693,18 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
     if (ts[i]->planes) {
       for (int r = 0; r < s; ++r)
         mxs.push_back(mx_desc(ts[i], xs + (size_t)r * ts[i]->I, dy + yoff[i] + (size_t)r * ts[i]->O));
+    } else if (dense5[i]) {
+      const uint16_t *hl = descs[i].x ? dhl + hloff[i] : dhl;
+      if (descs[i].x) split.j[split.n++] = lh::HiloJob{xs, dhl + hloff[i], s, descs[i].I};
+      for (int r = 0; r < s; ++r) {
+        lh::DenseDesc dd{};
+        dd.w = ts[i]->w;
+        dd.xhl = hl + (size_t)2 * r * ts[i]->I;
+        dd.y = dy + yoff[i] + (size_t)r * ts[i]->O;
+        dd.O = ts[i]->O;
+        dd.I = ts[i]->I;
+        d5s.push_back(dd);
+      }
     } else if (!fast[i]) {
       ds.push_back(gen_desc(ts[i], xs, nullptr, dy + yoff[i], s, ts[i]->I, ts[i]->O, 0));
     } else if (s == 1) {
@@ -672,6 +741,7 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
                                descs[i].O, 0, g_stream);
   if (e == hipSuccess && !ds.empty()) e = launch_descs(ds, g_stream);
   if (e == hipSuccess && !mxs.empty()) e = launch_mx_descs(mxs, g_stream);
+  if (e == hipSuccess && !d5s.empty()) e = launch_dense5(d5s, g_stream);
   if (e == hipSuccess && join.n) e = lh::launch_hilo_join(join, g_stream);
   if (e != hipSuccess) return -1;
   if (g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
@@ -850,6 +920,166 @@ int logan_hip_shared_expert(uint64_t model_id, int layer, LoganHipMatmulDesc *de
 }
 
 void logan_hip_shared_expert_drop_model(uint64_t model_id) { logan_hip_moe_route_drop_model(model_id); }
+
+// ---- dense Llama decode layer, host pointers (backend_metal.mm:2495-2791) ----
+//
+// One context per (model, layer): the norm weights' device copies, the
+// layer's K/V cache (f32, grown in steps of 256 tokens), staging for x and
+// the workspace. A call must come at the position the context has reached
+// (pos == tokens so far), as the reference requires (:2643).
+namespace {
+struct LlamaCtx {
+  uint64_t model_id = 0;
+  int layer = -1;
+  lh::LlamaDims dims{};
+  const float *host_in_norm = nullptr, *host_post_norm = nullptr;
+  float *in_norm = nullptr, *post_norm = nullptr, *kc = nullptr, *vc = nullptr;
+  int tokens = 0, cap = 0;
+  DevBuf x, ws;
+  void release() {
+    hipFree(in_norm);
+    hipFree(post_norm);
+    hipFree(kc);
+    hipFree(vc);
+    in_norm = post_norm = kc = vc = nullptr;
+    x.release();
+    ws.release();
+  }
+};
+std::vector<LlamaCtx *> g_llama;
+
+bool llama_same(const lh::LlamaDims &a, const lh::LlamaDims &b) {
+  return a.D == b.D && a.inter == b.inter && a.H == b.H && a.KH == b.KH && a.hd == b.hd &&
+         a.theta == b.theta && a.eps == b.eps;
+}
+
+bool llama_grow_locked(LlamaCtx *c, int need) {
+  if (need <= c->cap) return true;
+  const int cap = (need + 255) / 256 * 256;
+  const size_t kv = (size_t)c->dims.KH * c->dims.hd;
+  float *nk = nullptr, *nv = nullptr;
+  if (hipMalloc(&nk, (size_t)cap * kv * 4) != hipSuccess) return false;
+  if (hipMalloc(&nv, (size_t)cap * kv * 4) != hipSuccess) {
+    hipFree(nk);
+    return false;
+  }
+  if (c->tokens > 0 &&
+      (hipMemcpyAsync(nk, c->kc, (size_t)c->tokens * kv * 4, hipMemcpyDeviceToDevice, g_stream) != hipSuccess ||
+       hipMemcpyAsync(nv, c->vc, (size_t)c->tokens * kv * 4, hipMemcpyDeviceToDevice, g_stream) != hipSuccess ||
+       hipStreamSynchronize(g_stream) != hipSuccess)) {
+    hipFree(nk);
+    hipFree(nv);
+    return false;
+  }
+  hipFree(c->kc);
+  hipFree(c->vc);
+  c->kc = nk;
+  c->vc = nv;
+  c->cap = cap;
+  return true;
+}
+
+LlamaCtx *llama_ctx_locked(uint64_t model_id, int layer, const float *in_norm, const float *post_norm,
+                           const lh::LlamaDims &dims) {
+  for (LlamaCtx *c : g_llama) {
+    if (c->model_id != model_id || c->layer != layer) continue;
+    if (c->host_in_norm != in_norm || c->host_post_norm != post_norm || !llama_same(c->dims, dims))
+      return nullptr;
+    return c;
+  }
+  if (!model_id || layer < 0) return nullptr;
+  LlamaCtx *c = new (std::nothrow) LlamaCtx();
+  if (!c) return nullptr;
+  c->model_id = model_id;
+  c->layer = layer;
+  c->dims = dims;
+  c->host_in_norm = in_norm;
+  c->host_post_norm = post_norm;
+  const size_t nb = (size_t)dims.D * 4;
+  if (hipMalloc(&c->in_norm, nb) != hipSuccess || hipMalloc(&c->post_norm, nb) != hipSuccess ||
+      hipMemcpy(c->in_norm, in_norm, nb, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(c->post_norm, post_norm, nb, hipMemcpyHostToDevice) != hipSuccess ||
+      !c->x.ensure(nb) || !llama_grow_locked(c, 1)) {
+    c->release();
+    delete c;
+    return nullptr;
+  }
+  g_llama.push_back(c);
+  return c;
+}
+}  // namespace
+
+int logan_hip_host_llama_layer(uint64_t model_id, int layer, LoganHipMatmulDesc *descs, int count,
+                               float *x, float *k_out, float *v_out, const float *in_norm,
+                               const float *post_norm, int D, int inter, int H, int KH, int hd,
+                               int pos, float theta, float eps) {
+  if (!descs || count != 7 || !x || !k_out || !v_out || !in_norm || !post_norm || pos < 0) return 0;
+  const lh::LlamaDims dims{D, inter, H, KH, hd, theta, eps};
+  const int qdim = H * hd, kvdim = KH * hd;
+  const int ei[7] = {D, D, D, qdim, D, D, inter};
+  const int eo[7] = {qdim, kvdim, kvdim, D, inter, inter, D};
+  for (int i = 0; i < 7; ++i)
+    if ((descs[i].fmt != 5 && descs[i].fmt != 15) || descs[i].I != ei[i] || descs[i].O != eo[i])
+      return 0;
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return 0;
+  const uint64_t t0 = now_ns();
+  LoganHipTensor *ts[7];
+  lh::DenseMat mats[7];
+  for (int i = 0; i < 7; ++i) {
+    ts[i] = resolve_tensor_locked(&descs[i].tensor, descs[i].weights, descs[i].scales, descs[i].fmt,
+                                  descs[i].I, descs[i].O, descs[i].fmt == 15 ? 64 : 0);
+    if (!ts[i]) return 0;
+    mats[i] = dense_mat(ts[i]);
+  }
+  if (!lh::llama_supported(dims, mats)) return 0;
+  LlamaCtx *c = llama_ctx_locked(model_id, layer, in_norm, post_norm, dims);
+  if (!c || c->tokens != pos || !llama_grow_locked(c, pos + 1)) return 0;
+  if (!c->ws.ensure(lh::llama_workspace_bytes(dims, pos + 1))) return 0;
+  float *dx = reinterpret_cast<float *>(c->x.p);
+  const uint64_t t1 = now_ns();
+  prof_add(0, t1 - t0);
+  hipError_t e = hipMemcpyAsync(dx, x, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess && g_prof_on) hipEventRecord(g_prof_ev0, g_stream);
+  if (e == hipSuccess)
+    e = lh::launch_llama_layer(mats, c->in_norm, c->post_norm, dims, dx, c->kc, c->vc, pos, c->ws.p,
+                               g_stream);
+  if (e == hipSuccess && g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
+  const uint64_t t2 = now_ns();
+  prof_add(1, t2 - t1);
+  if (e == hipSuccess) e = hipMemcpyAsync(x, dx, (size_t)D * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(k_out, c->kc + (size_t)pos * kvdim, (size_t)kvdim * 4, hipMemcpyDeviceToHost,
+                       g_stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(v_out, c->vc + (size_t)pos * kvdim, (size_t)kvdim * 4, hipMemcpyDeviceToHost,
+                       g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  prof_add(2, now_ns() - t2);
+  if (e != hipSuccess) {
+    hipStreamSynchronize(g_stream);
+    return -1;
+  }
+  prof_kernel_time();
+  c->tokens = pos + 1;
+  return 1;
+}
+
+void logan_hip_host_llama_drop_model(uint64_t model_id) {
+  if (!model_id) return;
+  std::lock_guard<std::mutex> lk(g_mtx);
+  if (!g_ok) return;
+  hipStreamSynchronize(g_stream);
+  for (auto it = g_llama.begin(); it != g_llama.end();) {
+    if ((*it)->model_id == model_id) {
+      (*it)->release();
+      delete *it;
+      it = g_llama.erase(it);
+    } else {
+      ++it;
+    }
+  }
+}
 
 void logan_hip_tensor_free(LoganHipTensor *t) {
   if (!t) return;
@@ -1148,6 +1378,45 @@ int logan_hip_mxfp4_dequant(const LoganHipMxfp4 *w, int row0, int nrows, float *
   return rc_from(lh::launch_mxfp4_dequant(reinterpret_cast<const uint8_t *>(w->codes),
                                           reinterpret_cast<const uint8_t *>(w->scales), w->O, w->I,
                                           row0, nrows, out, reinterpret_cast<hipStream_t>(stream)));
+}
+
+static bool dense_from(const LoganHipDense &a, lh::DenseMat &m) {
+  if (!a.weights || (a.fmt != 5 && a.fmt != 15)) return false;
+  if (a.fmt == 15 && (!a.scales || !a.biases)) return false;
+  m.w = a.weights;
+  m.sc = a.fmt == 15 ? reinterpret_cast<const uint16_t *>(a.scales) : nullptr;
+  m.bi = a.fmt == 15 ? reinterpret_cast<const uint16_t *>(a.biases) : nullptr;
+  m.fmt = a.fmt;
+  m.O = a.O;
+  m.I = a.I;
+  return true;
+}
+
+static bool llama_from(const LoganHipLlamaLayer *L, lh::DenseMat mats[7], lh::LlamaDims &dims) {
+  if (!L) return false;
+  const LoganHipDense *ds[7] = {&L->q, &L->k, &L->v, &L->o, &L->gate, &L->up, &L->down};
+  for (int i = 0; i < 7; ++i)
+    if (!dense_from(*ds[i], mats[i])) return false;
+  dims = lh::LlamaDims{L->D, L->inter, L->heads, L->kv_heads, L->head_dim, L->theta, L->eps};
+  return lh::llama_supported(dims, mats);
+}
+
+size_t logan_hip_llama_workspace_bytes(const LoganHipLlamaLayer *L, int pos) {
+  lh::DenseMat mats[7];
+  lh::LlamaDims dims;
+  if (pos < 0 || !llama_from(L, mats, dims)) return 0;
+  return lh::llama_workspace_bytes(dims, pos + 1);
+}
+
+int logan_hip_llama_layer(const LoganHipLlamaLayer *L, float *x, int pos, void *ws, size_t ws_bytes,
+                          void *stream) {
+  lh::DenseMat mats[7];
+  lh::LlamaDims dims;
+  if (!x || !ws || pos < 0 || !llama_from(L, mats, dims)) return 0;
+  if (!L->in_norm || !L->post_norm || !L->k_cache || !L->v_cache || pos >= L->cache_tokens) return 0;
+  if (ws_bytes < lh::llama_workspace_bytes(dims, pos + 1)) return 0;
+  return rc_from(lh::launch_llama_layer(mats, L->in_norm, L->post_norm, dims, x, L->k_cache,
+                                        L->v_cache, pos, ws, reinterpret_cast<hipStream_t>(stream)));
 }
 
 void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }

@@ -40,6 +40,15 @@ int32_t coli_metal_shared_mxfp4(uint64_t model_id, int32_t layer, ColiMetalMatmu
 void coli_metal_shared_mxfp4_drop_model(uint64_t model_id) {
   logan_hip_shared_expert_drop_model(model_id);
 }
+int32_t coli_metal_llama_layer(uint64_t model_id, int32_t layer, ColiMetalMatmulDesc *descs,
+                               int32_t count, float *x, float *k_out, float *v_out,
+                               const float *input_norm, const float *post_norm, int32_t d,
+                               int32_t inter, int32_t heads, int32_t kv_heads, int32_t head_dim,
+                               int32_t pos, float theta, float eps) {
+  return logan_hip_host_llama_layer(model_id, layer, descs, count, x, k_out, v_out, input_norm,
+                                    post_norm, d, inter, heads, kv_heads, head_dim, pos, theta, eps);
+}
+void coli_metal_llama_drop_model(uint64_t model_id) { logan_hip_host_llama_drop_model(model_id); }
 int32_t coli_metal_rmsnorm(float *x, const float *w, int32_t n, int32_t nrows, float eps) {
   return logan_hip_host_rmsnorm(x, w, n, nrows, eps);
 }
@@ -107,10 +116,6 @@ int32_t logan_metal_gdn_conv_silu_run(void *) { return 0; }
 void *logan_metal_gdn_conv_silu_begin(void *) { return nullptr; }
 int32_t logan_metal_gdn_conv_silu_finish(void *, double *) { return 0; }
 void logan_metal_gdn_conv_silu_free(void *) {}
-int32_t coli_metal_llama_layer(uint64_t, int32_t, ColiMetalMatmulDesc *, int32_t, float *, float *,
-                               float *, const float *, const float *, int32_t, int32_t, int32_t,
-                               int32_t, int32_t, int32_t, float, float) { return 0; }
-void coli_metal_llama_drop_model(uint64_t) {}
 int32_t coli_metal_gdn_mxfp4(uint64_t, int32_t, ColiMetalMatmulDesc *, int32_t, const float *,
                              float *, const float *, const float *, const float *, const float *,
                              float *, float *, int32_t, int32_t, int32_t, int32_t, int32_t, int32_t,

@@ -118,6 +118,41 @@ hipError_t launch_mxfp4_gemv(Mx4Batch &b, bool x_f32, hipStream_t st);
 hipError_t launch_mxfp4_dequant(const uint8_t *w, const uint8_t *sc, int O, int I, int row0,
                                 int nrows, float *out, hipStream_t st);
 
+// ---- dense bf16-valued GEMV (fmt 5 raw bf16, fmt 15 affine-8 g64 with
+// every weight rounded to bf16) and the Llama decode layer ----
+struct DenseDesc {
+  const void *w;                  // fmt 5: bf16 [O][I]; fmt 15: u8 [O][I]; 16-byte aligned
+  const uint16_t *sc, *bi;        // fmt 15: bf16 [O][I/64] each
+  const uint16_t *xhl;            // [2][I]: bf16 hi then lo halves of the f32 activation
+  float *y;                       // [O]
+  const float *res;               // y = res + W x when set (may alias y)
+  int O, I;
+};
+constexpr int kDenseMaxDescs = 8;
+struct DenseBatch {
+  DenseDesc d[kDenseMaxDescs];
+  int block_start[kDenseMaxDescs + 1];
+  int n;
+};
+bool dense_supported(int fmt, int O, int I, const void *w);
+hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st);
+
+struct DenseMat {
+  const void *w;
+  const uint16_t *sc, *bi;
+  int fmt, O, I;
+};
+struct LlamaDims {
+  int D, inter, H, KH, hd;
+  float theta, eps;
+};
+// mats: q, k, v, o, gate, up, down
+bool llama_supported(const LlamaDims &m, const DenseMat mats[7]);
+size_t llama_workspace_bytes(const LlamaDims &m, int T);
+hipError_t launch_llama_layer(const DenseMat mats[7], const float *in_norm, const float *post_norm,
+                              const LlamaDims &m, float *x, float *kc, float *vc, int pos,
+                              void *ws, hipStream_t st);
+
 // ---- exact dequantisation of rows [row0, row0+nrows) to f32 ----
 hipError_t launch_dequant(const DevMat &m, int row0, int nrows, float *out, hipStream_t st);
 

@@ -241,6 +241,69 @@ def mxfp4_dequant(w: Mxfp4Matrix, row0: int = 0, nrows: Optional[int] = None,
     return out
 
 
+@dataclass
+class DenseMatrix:
+    """One matrix of the dense decode layer in HBM: fmt 5 weights bf16
+    [O, I]; fmt 15 affine-8 codes u8 [O, I] with bf16 scales / biases
+    [O, I/64]."""
+
+    weights: torch.Tensor
+    O: int
+    I: int
+    fmt: int
+    scales: Optional[torch.Tensor] = None
+    biases: Optional[torch.Tensor] = None
+
+    def c(self) -> L.Dense:
+        sc = _dev(self.scales, "scales") if self.scales is not None else None
+        bi = _dev(self.biases, "biases") if self.biases is not None else None
+        return L.Dense(_dev(self.weights, "weights"), sc, bi, self.O, self.I, self.fmt)
+
+
+@dataclass
+class LlamaLayer:
+    """A dense Llama layer in HBM with its f32 K/V cache
+    [cache_tokens, kv_heads * head_dim] (logan-metal/metal/backend_metal.mm
+    :2495-2791)."""
+
+    mats: list  # q, k, v, o, gate, up, down (DenseMatrix)
+    in_norm: torch.Tensor
+    post_norm: torch.Tensor
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    D: int
+    inter: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    theta: float
+    eps: float
+
+    def c(self) -> L.LlamaLayer:
+        m = [x.c() for x in self.mats]
+        return L.LlamaLayer(*m, _dev(self.in_norm, "in_norm"), _dev(self.post_norm, "post_norm"),
+                            _dev(self.k_cache, "k_cache"), _dev(self.v_cache, "v_cache"),
+                            self.k_cache.shape[0], self.D, self.inter, self.heads, self.kv_heads,
+                            self.head_dim, self.theta, self.eps)
+
+
+def llama_layer(layer: LlamaLayer, x: torch.Tensor, pos: int, workspace=None, stream=None):
+    """x [D] f32 in place: one decode layer at position pos; K/V rows land in
+    the layer's caches at row pos."""
+    if x.dtype != torch.float32 or x.numel() != layer.D:
+        raise LoganHipError("x must be f32 [D]")
+    c = layer.c()
+    need = int(L.lib().logan_hip_llama_workspace_bytes(C.byref(c), pos))
+    if need == 0:
+        raise LoganHipError("llama_layer: unsupported layer")
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    rc = L.lib().logan_hip_llama_layer(C.byref(c), _dev(x, "x"), pos, _dev(workspace, "workspace"),
+                                       workspace.numel(), _stream(stream))
+    _check(rc, "llama_layer")
+    return x
+
+
 def route_topk(logits: torch.Tensor, k: int, stream=None):
     """Per row: softmax top-k, lower-index ties; returns (idx int32 [B,k],
     weights f32 [B,k])."""

@@ -63,6 +63,11 @@ def lib() -> C.CDLL:
         h.lo_mxfp4_value.argtypes = [C.c_uint8, C.c_uint8]
         h.lo_mxfp4_gemv_stacked.restype = None
         h.lo_mxfp4_gemv_stacked.argtypes = [P, P, P, P, SZ, SZ, I]
+        h.lo_dense_gemv.restype = None
+        h.lo_dense_gemv.argtypes = [P, P, P, P, P, I, SZ, SZ]
+        h.lo_llama_layer.restype = I
+        h.lo_llama_layer.argtypes = [P, P, P, I, P, P, P, P, P, P, I, I, I, I, I, C.c_float,
+                                     C.c_float]
         h.lo_rmsnorm.restype = None
         h.lo_rmsnorm.argtypes = [P, P, SZ, SZ, C.c_float]
         h.lo_add.restype = None
@@ -171,6 +176,47 @@ def mxfp4_gemv(x: np.ndarray, w, sc, O: int, I: int, stacks: int = 1) -> np.ndar
     y = np.empty(O, np.float32)
     lib().lo_mxfp4_gemv_stacked(_p(y), _p(x), _p(w), _p(sc), O, I, stacks)
     return y
+
+
+def dense_gemv(x: np.ndarray, w, O: int, I: int, fmt: int, sc=None, bi=None) -> np.ndarray:
+    """y = W x for bf16-valued weights: fmt 5 w = bf16 bits u16 [O, I]; fmt 15
+    w = affine-8 codes u8 [O, I] with bf16 scale/bias bits [O, I/64]
+    (logan-llama/src/model.rs:1025-1033, weights.rs:441-516)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w)
+    y = np.empty(O, np.float32)
+    scp = np.ascontiguousarray(sc, np.uint16) if fmt == 15 else None
+    bip = np.ascontiguousarray(bi, np.uint16) if fmt == 15 else None
+    lib().lo_dense_gemv(_p(y), _p(x), _p(w), _p(scp) if scp is not None else None,
+                        _p(bip) if bip is not None else None, fmt, O, I)
+    return y
+
+
+def llama_layer(x, kc, vc, pos: int, mats, in_norm, post_norm, D, inter, H, KH, hd, theta, eps):
+    """One decode layer (logan-llama/src/model.rs:786-905). x [D] f32 (a new
+    array is returned); kc / vc [>= pos+1, KH*hd] f32 are updated in place at
+    row pos. mats: 7 tuples (fmt, w, sc, bi) for q, k, v, o, gate, up, down."""
+    out = np.array(x, np.float32, copy=True)
+    assert kc.dtype == np.float32 and vc.dtype == np.float32
+    assert kc.flags.c_contiguous and vc.flags.c_contiguous
+    keep = []
+    W, S, B, F = (C.c_void_p * 7)(), (C.c_void_p * 7)(), (C.c_void_p * 7)(), (C.c_int * 7)()
+    for i, (fmt, w, sc, bi) in enumerate(mats):
+        w = np.ascontiguousarray(w)
+        keep.append(w)
+        W[i] = w.ctypes.data
+        F[i] = fmt
+        if fmt == 15:
+            sc = np.ascontiguousarray(sc, np.uint16)
+            bi = np.ascontiguousarray(bi, np.uint16)
+            keep += [sc, bi]
+            S[i], B[i] = sc.ctypes.data, bi.ctypes.data
+    inn = np.ascontiguousarray(in_norm, np.float32)
+    pon = np.ascontiguousarray(post_norm, np.float32)
+    rc = lib().lo_llama_layer(_p(out), _p(kc), _p(vc), pos, W, S, B, F, _p(inn), _p(pon), D, inter,
+                              H, KH, hd, theta, eps)
+    assert rc == 1
+    return out
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:

@@ -466,3 +466,117 @@ void lo_moe_token_mt(float *out, const float *x, const float *logits, size_t E,
   moe_token_impl(out, x, logits, E, k, D, gate, up, down, se_gate, se_up,
                  se_down, se_g, idx_out, w_out, threads);
 }
+
+/* ---- dense Llama decode layer (logan-llama/src/model.rs:786-905) ---------- */
+
+/* One bf16-valued weight: fmt 5 holds the bf16 bits (weights dequantised and
+ * rounded at load, logan-llama/src/weights.rs:441-516, :548-552); fmt 15
+ * forms RNE_bf16(code * scale + bias) from an affine-8 code and its group's
+ * bf16 scale/bias (the same value; spark_qmv_affine8_fast,
+ * logan-metal/metal/backend_metal.mm:1143-1193). */
+static float dense_weight(const void *w, const uint16_t *sc, const uint16_t *bi, int fmt,
+                          size_t I, size_t row, size_t col) {
+  if (fmt == 5) return lo_bf16_to_f32(((const uint16_t *)w)[row * I + col]);
+  const size_t g = row * (I / 64) + col / 64;
+  const float code = (float)((const uint8_t *)w)[row * I + col];
+  const float v = code * lo_bf16_to_f32(sc[g]) + lo_bf16_to_f32(bi[g]);
+  return lo_bf16_to_f32(lo_f32_to_bf16(v));
+}
+
+/* linear_cpu_into (model.rs:1025-1033): y[r] = sum_j w[r][j] * x[j], f32 in
+ * column order */
+void lo_dense_gemv(float *y, const float *x, const void *w, const uint16_t *sc,
+                   const uint16_t *bi, int fmt, size_t O, size_t I) {
+  for (size_t r = 0; r < O; ++r) {
+    float acc = 0.0f;
+    for (size_t j = 0; j < I; ++j) acc = acc + dense_weight(w, sc, bi, fmt, I, r, j) * x[j];
+    y[r] = acc;
+  }
+}
+
+/* rms_norm_into (model.rs:1067-1073): f32 sum of squares in order */
+static void llama_rms(const float *x, const float *w, float eps, size_t n, float *out) {
+  float s = 0.0f;
+  for (size_t i = 0; i < n; ++i) s = s + x[i] * x[i];
+  const float mean = s / (float)n;
+  const float inv = 1.0f / sqrtf(mean + eps);
+  for (size_t i = 0; i < n; ++i) out[i] = x[i] * inv * w[i];
+}
+
+/* rope (model.rs:1087-1100) with the angles of :790-796 */
+static void llama_rope(float *x, int heads, int hd, int pos, float theta) {
+  const int half = hd / 2;
+  for (int h = 0; h < heads; ++h)
+    for (int i = 0; i < half; ++i) {
+      const float ang = (float)pos / powf(theta, (float)(2 * i) / (float)hd);
+      const float co = cosf(ang), si = sinf(ang);
+      const float a = x[h * hd + i], b = x[h * hd + half + i];
+      x[h * hd + i] = a * co - b * si;
+      x[h * hd + half + i] = a * si + b * co;
+    }
+}
+
+/* One decode layer at position pos for one token (model.rs:810-905 with
+ * rows = 1): kc / vc [pos + 1][kv_heads * hd] hold positions 0..pos-1 on
+ * entry; row pos is written (K after RoPE). x[D] is updated in place. mats
+ * are q, k, v, o, gate, up, down. Returns 0 on bad arguments. */
+int lo_llama_layer(float *x, float *kc, float *vc, int pos, const void *const *w,
+                   const uint16_t *const *sc, const uint16_t *const *bi, const int *fmt,
+                   const float *in_norm, const float *post_norm, int D, int inter, int H, int KH,
+                   int hd, float theta, float eps) {
+  if (D <= 0 || inter <= 0 || H <= 0 || KH <= 0 || H % KH != 0 || hd <= 0 || hd % 2 != 0 ||
+      pos < 0)
+    return 0;
+  const int qdim = H * hd, kvdim = KH * hd, T = pos + 1;
+  float *norm = malloc(sizeof(float) * D), *q = malloc(sizeof(float) * qdim);
+  float *att = calloc((size_t)qdim, sizeof(float)), *proj = malloc(sizeof(float) * D);
+  float *g = malloc(sizeof(float) * inter), *u = malloc(sizeof(float) * inter);
+  float *scores = malloc(sizeof(float) * T);
+  float *krow = kc + (size_t)pos * kvdim, *vrow = vc + (size_t)pos * kvdim;
+  llama_rms(x, in_norm, eps, D, norm);
+  lo_dense_gemv(q, norm, w[0], sc[0], bi[0], fmt[0], qdim, D);
+  lo_dense_gemv(krow, norm, w[1], sc[1], bi[1], fmt[1], kvdim, D);
+  lo_dense_gemv(vrow, norm, w[2], sc[2], bi[2], fmt[2], kvdim, D);
+  llama_rope(q, H, hd, pos, theta);
+  llama_rope(krow, KH, hd, pos, theta);
+  /* model.rs:838-869 */
+  for (int h = 0; h < H; ++h) {
+    const int grp = h / (H / KH);
+    const float *qh = q + h * hd;
+    for (int t = 0; t < T; ++t) {
+      const float *k = kc + (size_t)t * kvdim + grp * hd;
+      float s = 0.0f;
+      for (int z = 0; z < hd; ++z) s = s + qh[z] * k[z];
+      scores[t] = s / sqrtf((float)hd);
+    }
+    /* softmax, model.rs:1075-1086 */
+    float m = -INFINITY, tot = 0.0f;
+    for (int t = 0; t < T; ++t) m = fmaxf(m, scores[t]);
+    for (int t = 0; t < T; ++t) {
+      scores[t] = expf(scores[t] - m);
+      tot = tot + scores[t];
+    }
+    if (tot != 0.0f)
+      for (int t = 0; t < T; ++t) scores[t] = scores[t] / tot;
+    for (int t = 0; t < T; ++t) {
+      const float *v = vc + (size_t)t * kvdim + grp * hd;
+      for (int z = 0; z < hd; ++z) att[h * hd + z] = att[h * hd + z] + scores[t] * v[z];
+    }
+  }
+  lo_dense_gemv(proj, att, w[3], sc[3], bi[3], fmt[3], D, qdim);
+  for (int z = 0; z < D; ++z) x[z] = x[z] + proj[z];
+  llama_rms(x, post_norm, eps, D, norm);
+  lo_dense_gemv(g, norm, w[4], sc[4], bi[4], fmt[4], inter, D);
+  lo_dense_gemv(u, norm, w[5], sc[5], bi[5], fmt[5], inter, D);
+  for (int i = 0; i < inter; ++i) g[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+  lo_dense_gemv(proj, g, w[6], sc[6], bi[6], fmt[6], D, inter);
+  for (int z = 0; z < D; ++z) x[z] = x[z] + proj[z];
+  free(norm);
+  free(q);
+  free(att);
+  free(proj);
+  free(g);
+  free(u);
+  free(scores);
+  return 1;
+}

@@ -71,6 +71,15 @@ void lo_mxfp4_gemv(float *y, const float *x, const uint8_t *w, const uint8_t *sc
                    size_t i);
 void lo_mxfp4_gemv_stacked(float *y, const float *x, const uint8_t *w, const uint8_t *sc,
                            size_t o, size_t i, int stacks);
+/* logan-llama/src/model.rs:1025-1033 over bf16-valued weights (fmt 5 raw
+ * bf16, fmt 15 affine-8 g64 rounded to bf16). */
+void lo_dense_gemv(float *y, const float *x, const void *w, const uint16_t *sc,
+                   const uint16_t *bi, int fmt, size_t O, size_t I);
+/* logan-llama/src/model.rs:786-905, one token at position pos. */
+int lo_llama_layer(float *x, float *kc, float *vc, int pos, const void *const *w,
+                   const uint16_t *const *sc, const uint16_t *const *bi, const int *fmt,
+                   const float *in_norm, const float *post_norm, int D, int inter, int H, int KH,
+                   int hd, float theta, float eps);
 void lo_rmsnorm(float *x, const float *w, size_t n, size_t nrows, float eps);
 void lo_add(float *y, const float *a, size_t n);
 float lo_silu(float x);

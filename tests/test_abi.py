@@ -71,6 +71,8 @@ def test_struct_layouts_match_ctypes(tmp_path):
         "LoganHipMatmulDesc": (L.MatmulDesc, [f[0] for f in L.MatmulDesc._fields_]),
         "LoganHipAffine": (L.Affine, [f[0] for f in L.Affine._fields_]),
         "LoganHipMxfp4": (L.Mxfp4, [f[0] for f in L.Mxfp4._fields_]),
+        "LoganHipDense": (L.Dense, [f[0] for f in L.Dense._fields_]),
+        "LoganHipLlamaLayer": (L.LlamaLayer, [f[0] for f in L.LlamaLayer._fields_]),
         "LoganHipAffineBank": (L.AffineBank, [f[0] for f in L.AffineBank._fields_]),
         "LoganHipMoeBlock": (L.MoeBlock, [f[0] for f in L.MoeBlock._fields_]),
     }

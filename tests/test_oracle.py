@@ -470,3 +470,159 @@ def test_mxfp4_gemv_random_against_float64(stacks):
     if stacks > 1:
         first = dec(w[0], sc[0]) @ x.astype(np.float64)
         assert np.abs(first - ref).max() > 1e-2 * np.abs(ref).max()
+
+
+# ---- dense Llama decode layer ---------------------------------------------
+
+
+def _bf16v(v):
+    return bf16_to_f32(bf16_bits(np.array([v], np.float32)))[0]
+
+
+def _tiny_llama():
+    """The reference's own test model (logan-llama/tests/oracle_parity.rs
+    :1-100): D 4, inter 8, 2 heads over 1 kv head of dim 2, constant bf16
+    weights, unit norms, embedding row t = (4t .. 4t+3) / 20."""
+    D, inter, H, KH, hd = 4, 8, 2, 1, 2
+    shapes = [(H * hd, D), (KH * hd, D), (KH * hd, D), (D, H * hd), (inter, D), (inter, D),
+              (D, inter)]
+    consts = [0.1, 0.1, 0.1, 0.1, 0.02, 0.03, 0.02]
+    mats = [(5, np.full(s, bf16_bits(np.float32(c)), np.uint16), None, None)
+            for s, c in zip(shapes, consts)]
+    return D, inter, H, KH, hd, mats, consts
+
+
+def test_llama_tiny_model_closed_form():
+    """Two decode steps of the reference's tiny model against a float64
+    closed form: every projection of a constant-weight matrix is c * sum(in),
+    RoPE at pos 0 is the identity and at pos 1 rotates (a, a) by 1 rad, one
+    kv head serves both heads, and att is the softmax mix of the cached v."""
+    D, inter, H, KH, hd, mats, consts = _tiny_llama()
+    eps, theta = 1e-5, 10000.0
+    cq, ck, cv, co, cg, cu, cd = (float(_bf16v(c)) for c in consts)
+    kc = np.zeros((2, KH * hd), np.float32)
+    vc = np.zeros((2, KH * hd), np.float32)
+    ones = np.ones(D, np.float32)
+
+    def rms(v):
+        return v / np.sqrt(np.mean(v * v) + eps)
+
+    def mlp(x1):
+        pn = rms(x1)
+        g, u = cg * pn.sum(), cu * pn.sum()
+        h = g / (1 + np.exp(-g)) * u
+        return x1 + cd * inter * h
+
+    ks, vs, qs = [], [], []
+    for pos, tok in enumerate((1, 2)):
+        x = np.arange(4 * tok, 4 * tok + 4, dtype=np.float64) / 20
+        xf = np.float32(x)
+        got = oracle.llama_layer(xf, kc, vc, pos, mats, ones, ones, D, inter, H, KH, hd, theta, eps)
+        s = rms(x).sum()
+        q0, k0, v0 = cq * s, ck * s, cv * s
+        c, si = np.cos(pos), np.sin(pos)  # angle pos / theta^0 for the single pair
+        q = np.array([q0 * c - q0 * si, q0 * si + q0 * c])
+        k = np.array([k0 * c - k0 * si, k0 * si + k0 * c])
+        ks.append(k)
+        vs.append(np.array([v0, v0]))
+        sc = np.array([q @ kk / np.sqrt(hd) for kk in ks])
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        att = sum(pp * vv for pp, vv in zip(p, vs))  # [hd], same for both heads
+        x1 = x + co * 2 * att.sum()  # o row: c * sum over both heads' att
+        want = mlp(x1)
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-7)
+        np.testing.assert_allclose(kc[pos], k, rtol=2e-6, atol=1e-7)
+        np.testing.assert_allclose(vc[pos], [v0, v0], rtol=2e-6, atol=1e-7)
+
+
+def _np_llama_f64(x, kc, vc, pos, Ws, in_norm, post_norm, H, KH, hd, theta, eps):
+    """float64 decode layer in the Hugging Face formulation (rotate_half RoPE
+    with inv_freq = theta^(-2i/hd); repeat_kv grouping), written from the
+    model's definition: the independent check of the oracle."""
+    x = x.astype(np.float64)
+
+    def rms(v, w):
+        return v / np.sqrt(np.mean(v * v) + eps) * w
+
+    def rope(v, n):
+        v = v.reshape(n, hd)
+        inv = theta ** (-np.arange(0, hd, 2) / hd)
+        ang = np.concatenate([pos * inv, pos * inv])
+        rot = np.concatenate([-v[:, hd // 2:], v[:, :hd // 2]], axis=1)
+        return (v * np.cos(ang) + rot * np.sin(ang)).reshape(-1)
+
+    Wq, Wk, Wv, Wo, Wg, Wu, Wd = Ws
+    xn = rms(x, in_norm)
+    q, k, v = rope(Wq @ xn, H), rope(Wk @ xn, KH), Wv @ xn
+    K = np.vstack([kc[:pos].astype(np.float64), k[None]]).reshape(pos + 1, KH, hd)
+    V = np.vstack([vc[:pos].astype(np.float64), v[None]]).reshape(pos + 1, KH, hd)
+    K, V = np.repeat(K, H // KH, axis=1), np.repeat(V, H // KH, axis=1)
+    qh = q.reshape(H, hd)
+    s = np.einsum("hd,thd->ht", qh, K) / np.sqrt(hd)
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    att = np.einsum("ht,thd->hd", p, V).reshape(-1)
+    x1 = x + Wo @ att
+    pn = rms(x1, post_norm)
+    g, u = Wg @ pn, Wu @ pn
+    return x1 + Wd @ (g / (1 + np.exp(-g)) * u), k, v
+
+
+@pytest.mark.parametrize("fmt", [5, 15])
+def test_llama_layer_against_float64_model(fmt):
+    """Six positions of a random layer (4 heads over 2 kv heads of dim 16)
+    against the float64 Hugging Face formulation. A half-split RoPE taken as
+    interleaved pairs, h % KH grouping, a missing 1/sqrt(hd) or a dropped
+    residual each fail it."""
+    rng = np.random.default_rng(11 + fmt)
+    D, inter, H, KH, hd, theta, eps = 64, 128, 4, 2, 16, 10000.0, 1e-6
+    shapes = [(H * hd, D), (KH * hd, D), (KH * hd, D), (D, H * hd), (inter, D), (inter, D),
+              (D, inter)]
+    mats, Ws = [], []
+    for O, I in shapes:
+        if fmt == 5:
+            w = bf16_bits((rng.standard_normal((O, I)) * 0.15).astype(np.float32))
+            mats.append((5, w, None, None))
+            Ws.append(bf16_to_f32(w).astype(np.float64))
+        else:
+            codes = rng.integers(0, 256, (O, I)).astype(np.uint8)
+            sc = bf16_bits((np.abs(rng.standard_normal((O, I // 64))) * 0.002 + 1e-4).astype(np.float32))
+            bi = bf16_bits((-128 * bf16_to_f32(sc)).astype(np.float32))
+            mats.append((15, codes, sc, bi))
+            deq = codes * np.repeat(bf16_to_f32(sc), 64, axis=1) + np.repeat(bf16_to_f32(bi), 64, axis=1)
+            Ws.append(bf16_to_f32(bf16_bits(deq.astype(np.float32))).astype(np.float64))
+    in_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    post_norm = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    T = 6
+    kc = np.zeros((T, KH * hd), np.float32)
+    vc = np.zeros((T, KH * hd), np.float32)
+    for pos in range(T):
+        x = rng.standard_normal(D).astype(np.float32)
+        got = oracle.llama_layer(x, kc, vc, pos, mats, in_norm, post_norm, D, inter, H, KH, hd,
+                                 theta, eps)
+        want, k, v = _np_llama_f64(x, kc, vc, pos, Ws, in_norm.astype(np.float64),
+                                   post_norm.astype(np.float64), H, KH, hd, theta, eps)
+        assert np.abs(got - want).max() <= 2e-5 * np.abs(want).max(), pos
+        np.testing.assert_allclose(kc[pos], k, rtol=0, atol=2e-5 * np.abs(k).max())
+        np.testing.assert_allclose(vc[pos], v, rtol=0, atol=2e-5 * np.abs(v).max())
+
+
+def test_dense_gemv_fmt15_equals_fmt5_of_loader_weights():
+    """fmt 15 forms each weight as RNE_bf16(code * scale + bias), which is the
+    bf16 matrix logan-llama's loader stores (weights.rs:441-516): the two
+    products agree bit for bit."""
+    rng = np.random.default_rng(3)
+    O, I = 24, 256
+    codes = rng.integers(0, 256, (O, I)).astype(np.uint8)
+    sc = bf16_bits((np.abs(rng.standard_normal((O, I // 64))) * 0.01).astype(np.float32))
+    bi = bf16_bits((rng.standard_normal((O, I // 64)) * 0.5).astype(np.float32))
+    deq = codes.astype(np.float32) * np.repeat(bf16_to_f32(sc), 64, axis=1) + \
+        np.repeat(bf16_to_f32(bi), 64, axis=1)
+    w5 = bf16_bits(deq.astype(np.float32))
+    x = rng.standard_normal(I).astype(np.float32)
+    a = oracle.dense_gemv(x, codes, O, I, 15, sc, bi)
+    b = oracle.dense_gemv(x, w5, O, I, 5)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref = bf16_to_f32(w5).astype(np.float64) @ x.astype(np.float64)
+    assert np.abs(a - ref).max() <= 1e-5 * np.abs(ref).max()
