@@ -25,7 +25,10 @@ one a HIP graph of the product entry points timed with HIP events):
   * config 1: q4 GEMV 4096x2048 over 64 rotated weight copies;
   * config 2: dense 8-bit g64 decode layer (QKV 4096->6144, O 4096->4096,
     gate/up 4096->14336, SwiGLU, down 14336->4096) at M = 1, 4, 8 over 4
-    rotated layers (927 MB);
+    rotated layers (927 MB); and the whole Llama decode layer (norms, RoPE,
+    attention over 256 cached tokens, residuals) at M = 1 for affine-8 and
+    bf16 weights;
+  * MXFP4 (fmt 7): the config-1-shaped GEMV and a 16-matrix batch;
   * config 3 at B = 16 (and 32) over the 48 resident layers, distinct
     experts U counted from the routes;
   * config 4: 5-bit and 6-bit layers with Zipf(1.1) router logits at B = 1
@@ -79,9 +82,9 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="gemv,dense8,moe3,stack5,moe4,dropin,router",
-                    help="secondary legs to run (comma list of gemv, dense8, moe3, stack5, moe4, "
-                         "dropin, router; 'none' for none)")
+    ap.add_argument("--legs", default="gemv,dense8,llama,moe3,stack5,moe4,dropin,router,mxfp4",
+                    help="secondary legs to run (comma list of gemv, dense8, llama, moe3, stack5, "
+                         "moe4, dropin, router, mxfp4; 'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
     ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
@@ -311,6 +314,117 @@ def bench_config2(torch, device, synth, args):
                             frac_of_peak=round(gbps / PEAK_GBPS, 4))
     res["layers_rotated"] = nl
     del layers
+    torch.cuda.empty_cache()
+    return res
+
+
+DENSE_HEADS, DENSE_KV_HEADS, DENSE_HD, DENSE_CTX = 32, 8, 128, 256
+
+
+def bench_llama(torch, device, synth, args):
+    """Config 2 as the reference runs it at decode: the whole dense Llama layer
+    (coli_metal_llama_layer's device form, logan_hip_llama_layer) with
+    RMSNorms, RoPE, attention over a 256-token f32 K/V cache, residuals and
+    SwiGLU, for affine-8 g64 weights (fmt 15) and for the loader's bf16
+    weights (fmt 5), over 4 rotated layers each."""
+    nl, pos = 4, DENSE_CTX - 1
+    qd, kvd = DENSE_HEADS * DENSE_HD, DENSE_KV_HEADS * DENSE_HD
+    shapes = ((qd, DENSE_H), (kvd, DENSE_H), (kvd, DENSE_H), (DENSE_H, qd), (DENSE_F, DENSE_H),
+              (DENSE_F, DENSE_H), (DENSE_H, DENSE_F))
+    res = {"context_tokens": DENSE_CTX, "layers_rotated": nl}
+    for fmt in (15, 5):
+        layers = []
+        wbytes = 0
+        for l in range(nl):
+            mats = []
+            for j, (O, I) in enumerate(shapes):
+                if fmt == 15:
+                    w, sc, bi = synth.torch_affine(O, I, 8, GS, seed=700_000 + 10 * l + j)
+                    mats.append(device.DenseMatrix(w, O, I, 15, sc, bi))
+                    wbytes += O * I + 4 * O * (I // GS)
+                else:
+                    g = torch.Generator(device="cuda")
+                    g.manual_seed(710_000 + 10 * l + j)
+                    w = (torch.randn((O, I), device="cuda", generator=g) / (I ** 0.5)).to(torch.bfloat16)
+                    mats.append(device.DenseMatrix(w.view(torch.int16), O, I, 5))
+                    wbytes += O * I * 2
+            g = torch.Generator(device="cuda")
+            g.manual_seed(720_000 + l)
+            kc = torch.randn((DENSE_CTX, kvd), device="cuda", generator=g)
+            vc = torch.randn((DENSE_CTX, kvd), device="cuda", generator=g)
+            ones = torch.ones(DENSE_H, device="cuda")
+            layers.append(device.LlamaLayer(mats, ones, ones, kc, vc, DENSE_H, DENSE_F, DENSE_HEADS,
+                                            DENSE_KV_HEADS, DENSE_HD, 500000.0, 1e-5))
+        x = torch.randn(DENSE_H, device="cuda")
+        ws = torch.empty(device.llama_workspace_bytes(layers[0], pos), dtype=torch.uint8,
+                         device="cuda")
+
+        def step():
+            for L in layers:
+                device.llama_layer(L, x, pos, workspace=ws)
+
+        us = graph_us(torch, step, args.reps) / nl
+        nbytes = wbytes // nl + 2 * DENSE_CTX * kvd * 4 + 2 * DENSE_H * 4
+        gbps = nbytes / (us * 1e-6) / 1e9
+        name = "affine8_fmt15" if fmt == 15 else "bf16_fmt5"
+        log(f"llama layer {name}: {us:.2f} us/layer, {gbps:.0f} GB/s")
+        res[name] = dict(us_per_layer=round(us, 2), bytes_per_layer=nbytes, gbps=round(gbps, 1),
+                         frac_of_peak=round(gbps / PEAK_GBPS, 4))
+        del layers
+        torch.cuda.empty_cache()
+    return res
+
+
+def bench_mxfp4(torch, device, args):
+    """MXFP4 (fmt 7) GEMV at the config-1 shape (4096 x 2048) over 64 rotated
+    copies, and 16 expert-shaped matrices (512 x 2048) with their own x in
+    one launch over 16 rotated sets."""
+    O, I, copies = GEMV_O, GEMV_I, 64
+    mats = []
+    for c in range(copies):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(800_000 + c)
+        codes = torch.randint(0, 256, (O, I // 2), dtype=torch.uint8, device="cuda", generator=g)
+        sc = torch.randint(118, 136, (O, I // 32), dtype=torch.uint8, device="cuda", generator=g)
+        mats.append(device.Mxfp4Matrix(codes, sc, O, I))
+    x = torch.randn(I, device="cuda").to(torch.bfloat16)
+    y = torch.empty(O, dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        for m in mats:
+            device.mxfp4_gemv([m], [x], outs=[y])
+
+    us = graph_us(torch, step, args.reps) / copies
+    nbytes = O * I // 2 + O * I // 32 + I * 2 + O * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    log(f"mxfp4 gemv 4096x2048: {us:.2f} us/launch, {gbps:.0f} GB/s")
+    res = {"gemv_4096x2048": dict(us_per_launch=round(us, 3), bytes_per_launch=nbytes,
+                                  gbps=round(gbps, 1), frac_of_peak=round(gbps / PEAK_GBPS, 4),
+                                  rotation="64 copies (285 MB)")}
+    sets = []
+    for s_ in range(16):
+        ms = []
+        for e in range(16):
+            g = torch.Generator(device="cuda")
+            g.manual_seed(810_000 + 16 * s_ + e)
+            codes = torch.randint(0, 256, (INTER, D // 2), dtype=torch.uint8, device="cuda", generator=g)
+            sc = torch.randint(118, 136, (INTER, D // 32), dtype=torch.uint8, device="cuda", generator=g)
+            ms.append(device.Mxfp4Matrix(codes, sc, INTER, D))
+        sets.append(ms)
+    xs = [torch.randn(D, device="cuda") for _ in range(16)]
+    ys = [torch.empty(INTER, device="cuda") for _ in range(16)]
+
+    def step16():
+        for ms in sets:
+            device.mxfp4_gemv(ms, xs, outs=ys)
+
+    us16 = graph_us(torch, step16, args.reps) / len(sets)
+    nb16 = 16 * (INTER * D // 2 + INTER * D // 32 + D * 4 + INTER * 4)
+    g16 = nb16 / (us16 * 1e-6) / 1e9
+    log(f"mxfp4 16 x 512x2048 (f32 x): {us16:.2f} us/launch, {g16:.0f} GB/s")
+    res["batch16_512x2048_f32x"] = dict(us_per_launch=round(us16, 3), bytes_per_launch=nb16,
+                                        gbps=round(g16, 1), frac_of_peak=round(g16 / PEAK_GBPS, 4))
+    del mats, sets
     torch.cuda.empty_cache()
     return res
 
@@ -769,6 +883,8 @@ def main():
                 "rotation": "64 weight copies (302 MB) > 256 MB MALL"}
         if "dense8" in legs:
             secondary["dense8_config2"] = bench_config2(torch, device, synth, args)
+        if "llama" in legs:
+            secondary["llama_layer_config2"] = bench_llama(torch, device, synth, args)
         if "moe3" in legs:
             c3 = {}
             for B in (16, 32):
@@ -786,6 +902,8 @@ def main():
             secondary["moe3_router_on_device"] = bench_router(torch, device, synth, args, layers)
         if "dropin" in legs:
             secondary["dropin"] = bench_dropin(torch, synth, args)
+        if "mxfp4" in legs:
+            secondary["mxfp4"] = bench_mxfp4(torch, device, args)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")

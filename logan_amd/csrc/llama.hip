@@ -32,7 +32,7 @@ namespace lh {
 namespace {
 
 constexpr int kLT = 256;  // threads per block
-constexpr int kDU = 4;    // rows per wave in the dense GEMV
+constexpr int kDU = 4;    // rows per block in the dense GEMV
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -76,15 +76,17 @@ __device__ float block_max(float v, float *red) {
 
 // ---- dense GEMV: y[r] = (res ? res[r] : 0) + sum_j w[r][j] x[j] ----------
 //
-// One wave owns kDU rows; lane l takes the 16-column chunks l, l + 64, ...,
-// the next chunk's loads in flight while the current one is used.
+// A block owns kDU rows; its 4 waves split the 16-column chunks of those
+// rows (wave w, lane l: chunks 64 w + l, + 256, ...), the next chunk's loads
+// in flight while the current one is used; the 4 wave partials of a row are
+// added in wave order.
 template <int FMT>
 __global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
   int di = 0;
   while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
   const DenseDesc d = b.d[di];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = ((int)blockIdx.x - b.block_start[di]) * (kLT / 64) * kDU + wave * kDU;
+  const int r0 = ((int)blockIdx.x - b.block_start[di]) * kDU;
   const int C = d.I >> 4;
   const uint16_t *xh = d.xhl, *xl = d.xhl + d.I;
   constexpr int WD = FMT == 5 ? 8 : 4;  // dwords of one row's 16-column chunk
@@ -153,22 +155,27 @@ __global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
     }
   };
   Chunk k0, k1;
-  int c = lane;
+  int c = wave * 64 + lane;
   load(c, k0);
-  for (; c < C; c += 128) {
-    load(c + 64, k1);
+  for (; c < C; c += 512) {
+    load(c + 256, k1);
     use(c, k0);
-    load(c + 128, k0);
-    use(c + 64, k1);
+    load(c + 512, k0);
+    use(c + 256, k1);
   }
+  __shared__ float red[kLT / 64][kDU];
 #pragma unroll
-  for (int u = 0; u < kDU; ++u) acc[u] = team_sum<64>(acc[u]);
-  if (lane == 0) {
+  for (int u = 0; u < kDU; ++u) {
+    const float t = team_sum<64>(acc[u]);
+    if (lane == 0) red[wave][u] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < kDU) {
+    const int row = r0 + threadIdx.x;
+    float t = red[0][threadIdx.x];
 #pragma unroll
-    for (int u = 0; u < kDU; ++u) {
-      const int row = r0 + u;
-      if (row < d.O) d.y[row] = d.res ? d.res[row] + acc[u] : acc[u];
-    }
+    for (int w = 1; w < kLT / 64; ++w) t += red[w][threadIdx.x];
+    if (row < d.O) d.y[row] = d.res ? d.res[row] + t : t;
   }
 }
 
@@ -181,7 +188,7 @@ bool dense_supported(int fmt, int O, int I, const void *w) {
 
 hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
   if (b.n <= 0 || b.n > kDenseMaxDescs) return hipErrorInvalidValue;
-  constexpr int rows_per_block = (kLT / 64) * kDU;
+  constexpr int rows_per_block = kDU;
   b.block_start[0] = 0;
   for (int i = 0; i < b.n; ++i) {
     const DenseDesc &d = b.d[i];
@@ -200,15 +207,33 @@ hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
 
 // out = hi/lo halves of x * (1 / sqrt(sum x^2 / n + eps)) * w (a_rmsnorm,
 // backend_metal.mm:705-714; rms_norm_into, logan-llama/src/model.rs
-// :1067-1073). One block.
+// :1067-1073). One block; n a multiple of 4; loads unrolled so each thread's
+// are in flight together.
 __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const float *w, int n,
                                                          float eps, uint16_t *out) {
   __shared__ float red[kLT / 64];
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  const int n4 = n >> 2;
   float s = 0.f;
-  for (int i = threadIdx.x; i < n; i += kLT) s = fmaf(x[i], x[i], s);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < n4; i += kLT) {
+    const float4 v = x4[i];
+    s = fmaf(v.x, v.x, s);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+  }
   const float tot = block_sum(s, red);
   const float r = 1.0f / sqrtf(tot / (float)n + eps);
-  for (int i = threadIdx.x; i < n; i += kLT) put_hl(out, n, i, x[i] * r * w[i]);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < n4; i += kLT) {
+    const float4 v = x4[i], g = w4[i];
+    put_hl(out, n, 4 * i, v.x * r * g.x);
+    put_hl(out, n, 4 * i + 1, v.y * r * g.y);
+    put_hl(out, n, 4 * i + 2, v.z * r * g.z);
+    put_hl(out, n, 4 * i + 3, v.w * r * g.w);
+  }
 }
 
 // RoPE on the q and k heads of qkv [q | k | v] (pairs j, j + hd/2, angle
@@ -243,57 +268,101 @@ __global__ __launch_bounds__(kLT) void rope_store_kernel(float *qkv, float *kc, 
   }
 }
 
-// Attention of one head per block over T = pos + 1 cached positions
-// (logan-llama/src/model.rs:838-869; llama_attn_score / spark_softmax /
-// llama_attn_ctx, backend_metal.mm:1290-1302, :1370-1408): scores to
-// score[h][t], softmax in place (max, exp, sum, divide), then
-// att[h][d] = sum_t p_t V[t][kh][d], written as hi/lo halves.
-__global__ __launch_bounds__(kLT) void attn_kernel(const float *qkv, const float *kc,
-                                                   const float *vc, float *score, uint16_t *att,
-                                                   int H, int KH, int hd, int T) {
+// Attention over T = pos + 1 cached positions (logan-llama/src/model.rs
+// :838-869; llama_attn_score / spark_softmax / llama_attn_ctx,
+// backend_metal.mm:1290-1302, :1370-1408): s_t = q.K[t] / sqrt(hd),
+// p = softmax(s), att = sum_t p_t V[t], split over T in slices of kAttnTS
+// positions. Block (h, slice) forms its slice's scores, their max m, the
+// sum l of exp(s - m) and o = sum exp(s_t - m) V[t]; a second kernel joins
+// the slices in order, rescaling each by exp(m_slice - m_max), and writes
+// att = o / l as hi/lo halves.
+constexpr int kAttnQ = 16;   // q values per lane: head_dim <= 256
+constexpr int kAttnTS = 64;  // positions per slice
+
+__global__ __launch_bounds__(kLT) void attn_slice_kernel(const float *qkv, const float *kc,
+                                                         const float *vc, float *part, int H,
+                                                         int KH, int hd, int T) {
   __shared__ float red[kLT / 64];
-  __shared__ float part[kLT];
-  const int h = blockIdx.x, kh = h / (H / KH);
-  const int kvdim = KH * hd, qdim = H * hd;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float es[kAttnTS];
+  __shared__ float ps[kLT];
+  const int h = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
+  const int kh = h / (H / KH), kvdim = KH * hd;
+  const int t0 = sl * kAttnTS, nt = min(kAttnTS, T - t0);
+  const int sub = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const float *q = qkv + h * hd;
-  float *s = score + (size_t)h * T;
   const float rs = sqrtf((float)hd);
+  float qr[kAttnQ];
+#pragma unroll
+  for (int i = 0; i < kAttnQ; ++i) qr[i] = sub + 16 * i < hd ? q[sub + 16 * i] : 0.f;
+  const float *kb = kc + kh * hd + sub;
+  // scores: 16 groups of 16 lanes, 4 positions per group, loads together
+  float a[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = t0 + min(16 * j + grp, nt - 1);
+    const float *k = kb + (size_t)t * kvdim;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kAttnQ; ++i)
+      if (sub + 16 * i < hd) acc = fmaf(qr[i], k[16 * i], acc);
+    a[j] = acc;
+  }
   float mx = -INFINITY;
-  for (int t = wave; t < T; t += kLT / 64) {
-    const float *k = kc + (size_t)t * kvdim + kh * hd;
-    float a = 0.f;
-    for (int dd = lane; dd < hd; dd += 64) a = fmaf(q[dd], k[dd], a);
-    a = team_sum<64>(a);
-    const float sc = __fdiv_rn(a, rs);
-    if (lane == 0) s[t] = sc;
-    mx = fmaxf(mx, sc);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float sc = __fdiv_rn(team_sum<16>(a[j]), rs);
+    a[j] = sc;
+    if (16 * j + grp < nt) mx = fmaxf(mx, sc);
   }
-  mx = block_max(mx, red);  // also orders the score stores before the reads below
-  float sum = 0.f;
-  for (int t = threadIdx.x; t < T; t += kLT) {
-    const float e = __expf(s[t] - mx);
-    s[t] = e;
-    sum += e;
+  mx = block_max(mx, red);
+  float l = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tl = 16 * j + grp;
+    const float e = tl < nt ? __expf(a[j] - mx) : 0.f;
+    if (sub == 0) es[tl] = e;
+    if (sub == 0) l += e;
   }
-  sum = block_sum(sum, red);
-  for (int t = threadIdx.x; t < T; t += kLT) s[t] = __fdiv_rn(s[t], sum);
-  __syncthreads();
-  // P interleaved position partitions of hd threads each
+  l = block_sum(l, red);  // its barriers publish es[]
+  // o[d] = sum_t e_t V[t][d]: P partitions of hd threads, positions p, p + P, ...
   const int P = kLT / hd;
   const int d = threadIdx.x % hd, p = threadIdx.x / hd;
-  float a = 0.f;
+  float o = 0.f;
   if (p < P) {
-    const float *vcol = vc + kh * hd + d;
-    for (int t = p; t < T; t += P) a = fmaf(s[t], vcol[(size_t)t * kvdim], a);
+    const float *vcol = vc + (size_t)t0 * kvdim + kh * hd + d;
+#pragma unroll 8
+    for (int t = p; t < nt; t += P) o = fmaf(es[t], vcol[(size_t)t * kvdim], o);
   }
-  part[threadIdx.x] = a;
+  ps[threadIdx.x] = o;
   __syncthreads();
+  float *pr = part + ((size_t)h * S + sl) * (hd + 2);
   if (threadIdx.x < hd) {
-    float o = 0.f;
-    for (int pp = 0; pp < P; ++pp) o += part[pp * hd + threadIdx.x];
-    put_hl(att, qdim, h * hd + threadIdx.x, o);
+    float v = 0.f;
+    for (int pp = 0; pp < P; ++pp) v += ps[pp * hd + threadIdx.x];
+    pr[2 + threadIdx.x] = v;
   }
+  if (threadIdx.x == 0) {
+    pr[0] = mx;
+    pr[1] = l;
+  }
+}
+
+__global__ __launch_bounds__(kLT) void attn_join_kernel(const float *part, uint16_t *att, int H,
+                                                        int hd, int S) {
+  const int i = blockIdx.x * kLT + threadIdx.x;
+  if (i >= H * hd) return;
+  const int h = i / hd, d = i % hd;
+  const float *pr = part + (size_t)h * S * (hd + 2);
+  float m = -INFINITY;
+  for (int sl = 0; sl < S; ++sl) m = fmaxf(m, pr[(size_t)sl * (hd + 2)]);
+  float l = 0.f, o = 0.f;
+  for (int sl = 0; sl < S; ++sl) {
+    const float *q = pr + (size_t)sl * (hd + 2);
+    const float f = __expf(q[0] - m);
+    l = fmaf(q[1], f, l);
+    o = fmaf(q[2 + d], f, o);
+  }
+  put_hl(att, H * hd, i, __fdiv_rn(o, l));
 }
 
 // h = silu(g) * u (logan-llama/src/model.rs:888-890; moe_silu,
@@ -311,7 +380,7 @@ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct LlamaWs {
   uint16_t *xhl, *atthl, *pnhl, *hhl;
-  float *qkv, *score, *mg, *mu;
+  float *qkv, *part, *mg, *mu;
 };
 
 size_t llama_ws_layout(const LlamaDims &m, int T, uint8_t *base, LlamaWs *w) {
@@ -323,13 +392,14 @@ size_t llama_ws_layout(const LlamaDims &m, int T, uint8_t *base, LlamaWs *w) {
     return p;
   };
   uint8_t *xhl = take((size_t)2 * m.D * 2), *qkv = take((size_t)(qdim + 2 * kvdim) * 4);
-  uint8_t *score = take((size_t)m.H * T * 4), *att = take((size_t)2 * qdim * 2);
+  const int S = (T + kAttnTS - 1) / kAttnTS;
+  uint8_t *prt = take((size_t)m.H * S * (m.hd + 2) * 4), *att = take((size_t)2 * qdim * 2);
   uint8_t *pn = take((size_t)2 * m.D * 2), *mg = take((size_t)m.inter * 4);
   uint8_t *mu = take((size_t)m.inter * 4), *hh = take((size_t)2 * m.inter * 2);
   if (w) {
     w->xhl = reinterpret_cast<uint16_t *>(xhl);
     w->qkv = reinterpret_cast<float *>(qkv);
-    w->score = reinterpret_cast<float *>(score);
+    w->part = reinterpret_cast<float *>(prt);
     w->atthl = reinterpret_cast<uint16_t *>(att);
     w->pnhl = reinterpret_cast<uint16_t *>(pn);
     w->mg = reinterpret_cast<float *>(mg);
@@ -370,7 +440,9 @@ size_t llama_workspace_bytes(const LlamaDims &m, int T) { return llama_ws_layout
 
 bool llama_supported(const LlamaDims &m, const DenseMat mats[7]) {
   if (m.D <= 0 || m.inter <= 0 || m.H <= 0 || m.KH <= 0 || m.H % m.KH != 0) return false;
-  if (m.hd <= 0 || m.hd % 2 != 0 || m.hd > kLT || !(m.theta > 0.f) || !(m.eps > 0.f)) return false;
+  if (m.hd <= 0 || m.hd % 2 != 0 || m.hd > 16 * kAttnQ || !(m.theta > 0.f) || !(m.eps > 0.f))
+    return false;
+  if (m.D % 16 != 0) return false;  // the norms' float4 loads; the GEMVs need it too
   const int qdim = m.H * m.hd, kvdim = m.KH * m.hd;
   const int ei[7] = {m.D, m.D, m.D, qdim, m.D, m.D, m.inter};
   const int eo[7] = {qdim, kvdim, kvdim, m.D, m.inter, m.inter, m.D};
@@ -399,8 +471,11 @@ hipError_t launch_llama_layer(const DenseMat mats[7], const float *in_norm, cons
   const int rs_tasks = (m.H + m.KH) * (m.hd / 2) + kvdim;
   hipLaunchKernelGGL(rope_store_kernel, dim3((rs_tasks + kLT - 1) / kLT), dim3(kLT), 0, st, w.qkv,
                      kc, vc, m.H, m.KH, m.hd, pos, m.theta);
-  hipLaunchKernelGGL(attn_kernel, dim3(m.H), dim3(kLT), 0, st, w.qkv, kc, vc, w.score, w.atthl,
+  const int S = (T + kAttnTS - 1) / kAttnTS;
+  hipLaunchKernelGGL(attn_slice_kernel, dim3(m.H, S), dim3(kLT), 0, st, w.qkv, kc, vc, w.part,
                      m.H, m.KH, m.hd, T);
+  hipLaunchKernelGGL(attn_join_kernel, dim3((m.H * m.hd + kLT - 1) / kLT), dim3(kLT), 0, st,
+                     w.part, w.atthl, m.H, m.hd, S);
   const DenseDesc od = ddesc(mats[3], w.atthl, x, x);
   e = launch_dense_set(mats + 3, &od, 1, st);
   if (e != hipSuccess) return e;

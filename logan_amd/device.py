@@ -287,6 +287,11 @@ class LlamaLayer:
                             self.head_dim, self.theta, self.eps)
 
 
+def llama_workspace_bytes(layer: LlamaLayer, pos: int) -> int:
+    c = layer.c()
+    return int(L.lib().logan_hip_llama_workspace_bytes(C.byref(c), pos))
+
+
 def llama_layer(layer: LlamaLayer, x: torch.Tensor, pos: int, workspace=None, stream=None):
     """x [D] f32 in place: one decode layer at position pos; K/V rows land in
     the layer's caches at row pos."""
