@@ -39,7 +39,9 @@ one a HIP graph of the product entry points timed with HIP events):
     and B = 32, and a prefill chunk of M = 512 (projections on the MFMA
     product, MoE block in chunks of 64 tokens). The attention / recurrence
     math between the projections is outside the path: its inputs are
-    synthetic activations of the right shape.
+    synthetic activations of the right shape;
+  * loader: one config-3 layer's switch_mlp banks (906 MB) from a
+    safetensors file into HBM, whole banks and one expert at a time.
 """
 from __future__ import annotations
 
@@ -82,9 +84,10 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="gemv,dense8,llama,moe3,stack5,moe4,dropin,router,mxfp4",
+    ap.add_argument("--legs",
+                    default="gemv,dense8,llama,moe3,stack5,moe4,dropin,router,mxfp4,loader",
                     help="secondary legs to run (comma list of gemv, dense8, llama, moe3, stack5, "
-                         "moe4, dropin, router, mxfp4; 'none' for none)")
+                         "moe4, dropin, router, mxfp4, loader; 'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
     ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
@@ -427,6 +430,90 @@ def bench_mxfp4(torch, device, args):
     del mats, sets
     torch.cuda.empty_cache()
     return res
+
+
+def bench_loader(torch, args):
+    """Checkpoint -> HBM: one config-3 layer's stacked switch_mlp banks
+    (gate/up/down, 512 experts, 4-bit g64, 906 MB) written as a safetensors
+    file, then made resident by logan_hip_load_mlx_quantized_experts (three
+    whole-bank transfers), and the reference's per-expert form (one call per
+    (expert, role), 10 experts of a route). The file was just written, so the
+    page cache holds it: this is the host-memory -> HBM rate, set beside a
+    plain pinned host -> device copy of the same size."""
+    import tempfile
+
+    import numpy as np
+
+    from safetensors.numpy import save_file
+
+    from logan_amd import checkpoint
+
+    rng = np.random.default_rng(77)
+    tensors = {}
+    for role, O, I in (("gate_proj", INTER, D), ("up_proj", INTER, D), ("down_proj", D, INTER)):
+        words = I * BITS // 32
+        tensors[f"model.layers.0.mlp.switch_mlp.{role}.weight"] = rng.integers(
+            0, 2**32, (E, O, words), dtype=np.uint32)
+        for part in ("scales", "biases"):
+            # fp16 sidecars (the F16 form load_mlx_quantized_* accepts)
+            tensors[f"model.layers.0.mlp.switch_mlp.{role}.{part}"] = rng.integers(
+                0, 2**16, (E, O, I // GS), dtype=np.uint16).view(np.float16)
+    total = sum(a.nbytes for a in tensors.values())
+    tmpdir = os.environ.get("TMPDIR", "/tmp")
+    fd, path = tempfile.mkstemp(suffix=".safetensors", dir=tmpdir)
+    os.close(fd)
+    try:
+        save_file(tensors, path)
+        del tensors
+        roles = (("gate_proj", INTER, D), ("up_proj", INTER, D), ("down_proj", D, INTER))
+        with checkpoint.StFile.open(path) as st:
+            times = []
+            for rep in range(4):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                banks = [checkpoint.load_mlx_quantized_bank(st, f"model.layers.0.mlp.switch_mlp."
+                                                            f"{r}.weight", E, O, I)
+                         for r, O, I in roles]
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                del banks
+            bank_s = sorted(times[1:])[1]  # median of the 3 after the first
+            ex = rng.choice(E, TOPK, replace=False)
+            ts = []
+            for rep in range(4):
+                t0 = time.perf_counter()
+                held = [checkpoint.load_mlx_quantized_expert_wt(
+                    st, f"model.layers.0.mlp.switch_mlp.{r}.weight", int(e), E, O, I)
+                    for e in ex for r, O, I in roles]
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+                del held
+            ex_s = sorted(ts[1:])[1]
+    finally:
+        os.unlink(path)
+    n = 256 << 20
+    h = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    dbuf = torch.empty(n, dtype=torch.uint8, device="cuda")
+    cts = []
+    for _ in range(4):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dbuf.copy_(h, non_blocking=True)
+        torch.cuda.synchronize()
+        cts.append(time.perf_counter() - t0)
+    copy_gbps = n / sorted(cts[1:])[1] / 1e9
+    gbps = total / bank_s / 1e9
+    log(f"loader: 3 banks {total / 1e6:.0f} MB in {bank_s * 1e3:.1f} ms = {gbps:.1f} GB/s "
+        f"(pinned copy {copy_gbps:.1f} GB/s); 30 one-expert loads {ex_s * 1e3:.2f} ms")
+    del h, dbuf
+    torch.cuda.empty_cache()
+    return dict(bytes=total, banks_ms=round(bank_s * 1e3, 2), gbps=round(gbps, 2),
+                pinned_h2d_copy_gbps=round(copy_gbps, 2),
+                frac_of_pinned_copy=round(gbps / copy_gbps, 3),
+                one_expert_loads=dict(calls=3 * TOPK, ms=round(ex_s * 1e3, 3),
+                                      bytes=TOPK * PER_EXPERT,
+                                      gbps=round(TOPK * PER_EXPERT / ex_s / 1e9, 2)),
+                source="page cache (file just written); median of 3 after one warm-up")
 
 
 # Qwen3-Next-80B-A3B projections per layer (hidden 2048; 16 q heads x 256 with
@@ -904,6 +991,8 @@ def main():
             secondary["dropin"] = bench_dropin(torch, synth, args)
         if "mxfp4" in legs:
             secondary["mxfp4"] = bench_mxfp4(torch, device, args)
+        if "loader" in legs:
+            secondary["loader"] = bench_loader(torch, args)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")

@@ -400,6 +400,91 @@ uint32_t logan_hip_moe_sync_errors(void);
  * reference (its batched path is host-side, lib.rs:9714-9721). */
 void logan_hip_set_moe_mfma_min_batch(int b);
 
+/* ------------------------------------------------------------------------ */
+/* Layer 3: MLX quantized weights from a safetensors checkpoint into HBM     */
+/* ------------------------------------------------------------------------ */
+
+/* Message of the last call of this layer that returned 0, -1 or NULL on the
+ * calling thread (the reference's Err(String) text for a rejected tensor). */
+const char *logan_hip_last_error(void);
+
+typedef struct LoganHipStFile LoganHipStFile;
+
+/* StFile::open (logan-qwen4/src/lib.rs:508-531): one .safetensors file,
+ * header checked as parse_shard does (:326-421: header inside the file,
+ * known dtype, data_offsets inside the file, span == elements x width).
+ * NULL on error. */
+LoganHipStFile *logan_hip_st_open(const char *path);
+/* StFile::open_dir (lib.rs:537-595): every shard named by
+ * model.safetensors.index.json (sorted, deduplicated), or model.safetensors;
+ * names under model.language_model. / language_model.model. /
+ * language_model.lm_head. also answer to the engine's model. / lm_head.
+ * spelling (register, :460-503). NULL on error. */
+LoganHipStFile *logan_hip_st_open_dir(const char *dir);
+void logan_hip_st_close(LoganHipStFile *st);
+/* shard_count (lib.rs:598-600) */
+int logan_hip_st_shard_count(const LoganHipStFile *st);
+/* shape_of (lib.rs:946-948) plus dtype and payload bytes: 1 found, 0 absent.
+ * shape receives up to max_dims dims, *ndim the tensor's rank. */
+int logan_hip_st_tensor(const LoganHipStFile *st, const char *name, char *dtype, size_t dtype_cap,
+                        uint64_t *shape, int max_dims, int *ndim, uint64_t *nbytes);
+/* dtype_counts (lib.rs:671-680): distinct payloads of one dtype. */
+int logan_hip_st_dtype_count(const LoganHipStFile *st, const char *dtype);
+/* payload_range (lib.rs:726-760) into host memory: 1 ok, 0 rejected, -1 read
+ * failure. */
+int logan_hip_st_read(const LoganHipStFile *st, const char *name, uint64_t within, uint64_t len,
+                      void *dst);
+
+enum { LOGAN_HIP_WT_AFFINE = 1, LOGAN_HIP_WT_MXFP4 = 2 };
+
+/* A quantized weight (WtBytes::MlxAffine / WtBytes::Mxfp4,
+ * logan-qwen4/src/lib.rs:1560-1580) resident in HBM: the file's bytes
+ * unchanged, E experts stacked (E = 1 for a dense matrix). Affine: weights
+ * [E][O][I*bits/8], scales and biases u16 [E][O][I/group_size] (bf16, or
+ * fp16 when aux_fp16). MXFP4: weights [E][O][I/2], scales E8M0 bytes
+ * [E][O][ceil(I/32)], biases NULL. One device allocation, 256-byte aligned
+ * parts, released by logan_hip_quant_free. */
+typedef struct LoganHipQuantWt {
+  int kind; /* LOGAN_HIP_WT_AFFINE or LOGAN_HIP_WT_MXFP4 */
+  int E;
+  int O;
+  int I;
+  int bits;
+  int group_size;
+  int aux_fp16;
+  const void *weights;
+  const void *scales;
+  const void *biases;
+  uint64_t weight_bytes, scale_bytes, bias_bytes;
+  void *owner;
+} LoganHipQuantWt;
+
+/* load_mlx_quantized_wt (logan-qwen4/src/lib.rs:11818-11937) into HBM:
+ * `name` is the U32 [O, words] packed weight ending in .weight; bits =
+ * words*32/I must be 4, 5, 6 or 8; a BF16/F16 `.scales` [O, groups] with an
+ * identical `.biases` makes it affine (group_size = I/groups), a U8 `.scales`
+ * [O, ceil(I/32)] with 4-bit codes makes it MXFP4. 1 ok; 0 rejected (the
+ * reference's conditions and message, logan_hip_last_error), nothing
+ * allocated; -1 read or device failure. Blocking; calls serialise. */
+int logan_hip_load_mlx_quantized(const LoganHipStFile *st, const char *name, int O, int I,
+                                 LoganHipQuantWt *out);
+/* load_mlx_quantized_expert_wt (lib.rs:11939-12078) for the `count`
+ * consecutive experts e0 .. e0+count-1 of a stacked switch_mlp bank U32
+ * [experts, O, words] (count = 1 is the reference's one-expert read;
+ * count = experts makes the whole bank resident in one transfer). Same
+ * return convention. */
+int logan_hip_load_mlx_quantized_experts(const LoganHipStFile *st, const char *name, int e0,
+                                         int count, int experts, int O, int I,
+                                         LoganHipQuantWt *out);
+/* The same checks without reading or allocating anything: fills kind,
+ * geometry and the byte counts (pointers NULL). 1 accepted, 0 rejected. */
+int logan_hip_plan_mlx_quantized(const LoganHipStFile *st, const char *name, int O, int I,
+                                 LoganHipQuantWt *out);
+int logan_hip_plan_mlx_quantized_experts(const LoganHipStFile *st, const char *name, int e0,
+                                         int count, int experts, int O, int I,
+                                         LoganHipQuantWt *out);
+void logan_hip_quant_free(LoganHipQuantWt *w);
+
 /* Library version string. */
 const char *logan_hip_version(void);
 

@@ -14,6 +14,8 @@ LIB_PATH = PKG / "liblogan_hip.so"
 
 LOGAN_HIP_F32 = 0
 LOGAN_HIP_BF16 = 1
+LOGAN_HIP_WT_AFFINE = 1
+LOGAN_HIP_WT_MXFP4 = 2
 
 
 class MatmulDesc(C.Structure):
@@ -111,6 +113,25 @@ class MoeBlock(C.Structure):
     ]
 
 
+class QuantWt(C.Structure):
+    _fields_ = [
+        ("kind", C.c_int),
+        ("E", C.c_int),
+        ("O", C.c_int),
+        ("I", C.c_int),
+        ("bits", C.c_int),
+        ("group_size", C.c_int),
+        ("aux_fp16", C.c_int),
+        ("weights", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("biases", C.c_void_p),
+        ("weight_bytes", C.c_uint64),
+        ("scale_bytes", C.c_uint64),
+        ("bias_bytes", C.c_uint64),
+        ("owner", C.c_void_p),
+    ]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _SZ = C.c_size_t
@@ -165,6 +186,22 @@ SIGNATURES = {
     "logan_hip_set_moe_mfma_min_batch": (None, [_I]),
     "logan_hip_moe_sync_errors": (C.c_uint32, []),
     "logan_hip_version": (C.c_char_p, []),
+    "logan_hip_last_error": (C.c_char_p, []),
+    "logan_hip_st_open": (_P, [C.c_char_p]),
+    "logan_hip_st_open_dir": (_P, [C.c_char_p]),
+    "logan_hip_st_close": (None, [_P]),
+    "logan_hip_st_shard_count": (_I, [_P]),
+    "logan_hip_st_tensor": (_I, [_P, C.c_char_p, C.c_char_p, _SZ, C.POINTER(_U64), _I,
+                                 C.POINTER(_I), C.POINTER(_U64)]),
+    "logan_hip_st_dtype_count": (_I, [_P, C.c_char_p]),
+    "logan_hip_st_read": (_I, [_P, C.c_char_p, _U64, _U64, _P]),
+    "logan_hip_load_mlx_quantized": (_I, [_P, C.c_char_p, _I, _I, C.POINTER(QuantWt)]),
+    "logan_hip_load_mlx_quantized_experts": (_I, [_P, C.c_char_p, _I, _I, _I, _I, _I,
+                                                  C.POINTER(QuantWt)]),
+    "logan_hip_plan_mlx_quantized": (_I, [_P, C.c_char_p, _I, _I, C.POINTER(QuantWt)]),
+    "logan_hip_plan_mlx_quantized_experts": (_I, [_P, C.c_char_p, _I, _I, _I, _I, _I,
+                                                  C.POINTER(QuantWt)]),
+    "logan_hip_quant_free": (None, [C.POINTER(QuantWt)]),
 }
 
 _lib = None

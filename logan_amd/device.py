@@ -32,6 +32,16 @@ def _stream(stream) -> Optional[int]:
     return s.cuda_stream or None
 
 
+def _where(w) -> torch.device:
+    """The device holding a matrix: its tensors' device, or the `device` of a
+    matrix loaded from a checkpoint (logan_amd.checkpoint)."""
+    d = getattr(w, "device", None)
+    if d is not None:
+        return d
+    t = getattr(w, "weights", None)
+    return t.device if isinstance(t, torch.Tensor) else w.codes.device
+
+
 def _dev(t: torch.Tensor, name: str) -> int:
     if not t.is_cuda:
         raise LoganHipError(f"{name} must be a device tensor")
@@ -181,7 +191,7 @@ def affine_dequant(w: AffineMatrix, row0: int = 0, nrows: Optional[int] = None,
                    stream=None) -> torch.Tensor:
     """code*scale+bias as f32 for rows [row0, row0+nrows)."""
     n = w.O - row0 if nrows is None else nrows
-    out = torch.empty((n, w.I), dtype=torch.float32, device=w.weights.device)
+    out = torch.empty((n, w.I), dtype=torch.float32, device=_where(w))
     a = w.c()
     rc = L.lib().logan_hip_affine_dequant(C.byref(a), row0, n, _dev(out, "out"), _stream(stream))
     _check(rc, "affine_dequant")
@@ -234,7 +244,7 @@ def mxfp4_dequant(w: Mxfp4Matrix, row0: int = 0, nrows: Optional[int] = None,
                   stream=None) -> torch.Tensor:
     """E2M1(code) * 2^(scale - 127) of plane 0 as f32, rows [row0, row0+nrows)."""
     n = w.O - row0 if nrows is None else nrows
-    out = torch.empty((n, w.I), dtype=torch.float32, device=w.codes.device)
+    out = torch.empty((n, w.I), dtype=torch.float32, device=_where(w))
     a = w.c()
     rc = L.lib().logan_hip_mxfp4_dequant(C.byref(a), row0, n, _dev(out, "out"), _stream(stream))
     _check(rc, "mxfp4_dequant")
