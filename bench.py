@@ -591,8 +591,13 @@ def bench_config5(torch, device, synth, args, moe_layers):
     def proj_step():
         for l in range(nl):
             shapes = FULL_ATTN if l % FULL_EVERY == FULL_EVERY - 1 else LIN_ATTN
+            # the projections of the hidden state share one product launch
+            # (q/k/v, qkvz/ba), the output projection reads the attention output
+            grp = [(m, outs[name]) for (name, O, I), m in zip(shapes, proj[l]) if I == D]
+            device.affine_qmm_multi([m for m, _ in grp], x, outs=[o for _, o in grp])
             for (name, O, I), m in zip(shapes, proj[l]):
-                device.affine_qmm(m, x if I == D else att, out=outs[name])
+                if I != D:
+                    device.affine_qmm(m, att, out=outs[name])
 
     us_p = graph_us(torch, proj_step, args.reps)
     tflops = pflop_per_tok * M / (us_p * 1e-6) / 1e12

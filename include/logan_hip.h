@@ -214,6 +214,16 @@ int logan_hip_affine_gemv_multi(const LoganHipAffine *ws, int count, const void 
 int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                          int y_stride, int y_dtype, void *stream);
 
+/* Up to 8 matrices that read the same x (q/k/v, qkvz/ba of a prefill
+ * chunk) as one product: ys[i][M][O_i] = x . bf16(W_i)^T, each as
+ * logan_hip_affine_qmm. With M >= 256 and power-of-two group sizes their
+ * column tiles form one grid (the reference encodes its batch of products
+ * into one command buffer, backend_metal.mm:2290-2493); otherwise one launch
+ * per matrix. Every matrix has the same I, bits, group_size and aux type. 1
+ * ok, 0 unsupported, -1 launch failure. */
+int logan_hip_affine_qmm_multi(const LoganHipAffine *ws, int count, const void *x, int M,
+                               int x_stride, void *const *ys, int y_dtype, void *stream);
+
 /* SwiGLU between a dense gate/up pair and the down projection, in place:
  * g[i] = silu(g[i]) * u[i], silu(v) = v / (1 + exp(-v)), f32 arithmetic
  * (replaces coli_metal_silu_mul, logan-metal/metal/backend_metal.mm

@@ -1194,6 +1194,25 @@ int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_st
                                        reinterpret_cast<hipStream_t>(stream)));
 }
 
+int logan_hip_affine_qmm_multi(const LoganHipAffine *ws, int count, const void *x, int M,
+                               int x_stride, void *const *ys, int y_dtype, void *stream) {
+  if (!ws || !ys || !x || count <= 0 || count > 8 || M <= 0) return 0;
+  if (y_dtype != LOGAN_HIP_F32 && y_dtype != LOGAN_HIP_BF16) return 0;
+  lh::DevMat ms[8];
+  for (int i = 0; i < count; ++i) {
+    if (!affine_ok(&ws[i]) || !ys[i] || x_stride < ws[i].I) return 0;
+    ms[i] = devmat(ws[i]);
+    if (!lh::affine_qmm_supported(ms[i])) return 0;
+    if (ms[i].I != ms[0].I || ms[i].bits != ms[0].bits || ms[i].gs != ms[0].gs ||
+        ms[i].fp16 != ms[0].fp16)
+      return 0;
+  }
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return 0;
+  return rc_from(lh::launch_affine_qmm_multi(ms, count, reinterpret_cast<const uint16_t *>(x),
+                                             x_stride, M, ys, y_dtype == LOGAN_HIP_BF16,
+                                             reinterpret_cast<hipStream_t>(stream)));
+}
+
 int logan_hip_silu_mul(void *g, const void *u, long long n, int dtype, void *stream) {
   if (!g || !u || n <= 0) return 0;
   if (dtype != LOGAN_HIP_F32 && dtype != LOGAN_HIP_BF16) return 0;

@@ -18,6 +18,7 @@
 
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
+#include "mfma_dev.hpp"
 
 namespace lh {
 
@@ -330,6 +331,369 @@ __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mt
     }
 }
 
+// ---------------------------------------------------------------------------
+// 256 x 128 tiles for M >= 256, over up to kQMultiMax matrices that read the
+// same x (q/k/v, qkvz/ba) in one grid. 512 threads, waves 4 (m) x 2 (n), each
+// 64 x 64 as 2 x 2 v_mfma_f32_32x32x16_bf16 tiles, so every dequantised weight
+// serves 256 tokens (half the VALU per MFMA of the 128-row tiles).
+//   * step s's x rows and the codes / scale / bias of its weights are loaded
+//     into one of two register sets two steps ahead, then written to LDS
+//     stage s & 1 (the weights dequantised to bf16) one step ahead, and
+//     multiplied after the barrier that follows: one barrier per step, and
+//     the loads of the next two steps stay in flight across it;
+//   * LDS rows are 144 bytes (64 bf16 + 16 bytes of padding), so the 16
+//     lanes an operand read serves per clock (rows r .. r + 15 at one k
+//     offset) start on 16 different 4-bank groups of the 64 banks.
+constexpr int kQ3M = 256, kQ3N = 128;
+constexpr int kQ3Ld = 72;  // u16 per LDS row: 64 + 8 of padding
+constexpr int kQMultiMax = 8;
+
+struct QmmMat {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  void *y;
+  long long row_bytes;
+  int N, ng, y_stride, col0;  // col0: first column of this matrix in split partial rows
+};
+struct QmmMulti {
+  QmmMat m[kQMultiMax];
+  int tile_start[kQMultiMax + 1];  // first 128-column tile of matrix i
+  const uint16_t *x;
+  int n, M, K, gs, fp16, x_stride, y_bf16, part_N;
+  int vec;  // bit 0: y rows take 16-byte stores; bit 1: partial rows do
+};
+
+template <int BITS>
+struct Q3Raw {
+  uint32_t w[BITS == 4 ? 2 : BITS == 8 ? 4 : 3];
+  uint32_t s, b;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t q3_rsrc(const void *p, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                           (int)(bytes > 0x7fffffffLL ? 0x7fffffffLL : bytes),
+                                           0x00020000);
+}
+
+// 16 codes [k, k + 16) of a row (k a multiple of 16) and their group's scale
+// and bias: exactly three buffer loads
+template <int BITS>
+__device__ __forceinline__ void q3_load(Q3Raw<BITS> &r, __amdgpu_buffer_rsrc_t wr,
+                                        __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t br,
+                                        int rowoff, int poff, int k) {
+  if constexpr (BITS == 4) {
+    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, rowoff + (k >> 1), 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else if constexpr (BITS == 8) {
+    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, rowoff + k, 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+    r.w[3] = v.w;
+  } else {
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    const u32x3 v = __builtin_bit_cast(
+        u32x3, __builtin_amdgcn_raw_buffer_load_b96(wr, rowoff + 4 * ((k * BITS) >> 5), 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+    r.w[2] = v.z;
+  }
+  r.s = __builtin_amdgcn_raw_buffer_load_b16(sr, poff, 0, 0);
+  r.b = __builtin_amdgcn_raw_buffer_load_b16(br, poff, 0, 0);
+}
+
+// bf16(code * s + b) of the 16 codes, packed in pairs (code order); sh is the
+// bit where the first 5-bit code starts (0 or 16)
+template <int BITS>
+__device__ __forceinline__ void q3_dequant(const Q3Raw<BITS> &r, int sh, bool fp16, uint32_t (&pk)[8]) {
+  const float s = aux_to_f32_sel(r.s, fp16), b = aux_to_f32_sel(r.b, fp16);
+  float f[16];
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const uint32_t lo = r.w[d] & 0x0F0F0F0Fu, hi = (r.w[d] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[8 * d + 2 * i] = (float)((lo >> (8 * i)) & 255u);
+        f[8 * d + 2 * i + 1] = (float)((hi >> (8 * i)) & 255u);
+      }
+    }
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[4 * d + i] = (float)((r.w[d] >> (8 * i)) & 255u);
+  } else {
+    const uint32_t win[3] = {__builtin_amdgcn_alignbit(r.w[1], r.w[0], sh),
+                             __builtin_amdgcn_alignbit(r.w[2], r.w[1], sh), r.w[2] >> sh};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int bit = j * BITS, i = bit >> 5, o = bit & 31;
+      uint32_t v = win[i] >> o;
+      if (o + BITS > 32) v |= win[i + 1] << (32 - o);
+      f[j] = (float)(v & ((1u << BITS) - 1u));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    bf16x2 v;
+    v[0] = (__bf16)fmaf(f[2 * j], s, b);
+    v[1] = (__bf16)fmaf(f[2 * j + 1], s, b);
+    pk[j] = __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void q3_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__global__ __launch_bounds__(256) void qmm_reduce_multi_kernel(QmmMulti p, int slot, int KS) {
+  const float *part = g_qmm_part + (size_t)slot * kQSlotFloats;
+  const size_t MN = (size_t)p.M * p.part_N;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+    float v[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) v[z] = z < KS ? part[z * MN + i] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int z = 1; z < 16; ++z) s += z < KS ? v[z] : 0.f;  // in k order
+    const int m = (int)(i / p.part_N), c = (int)(i % p.part_N);
+    int mi = 0;
+#pragma unroll
+    for (int t = 1; t < kQMultiMax; ++t) mi = t < p.n && c >= p.m[t].col0 ? t : mi;
+    const QmmMat &q = p.m[mi];
+    const int n = c - q.col0;
+    if (p.y_bf16)
+      reinterpret_cast<__bf16 *>(q.y)[(size_t)m * q.y_stride + n] = (__bf16)s;
+    else
+      reinterpret_cast<float *>(q.y)[(size_t)m * q.y_stride + n] = s;
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(512) void affine_qmm256_kernel(QmmMulti p, int mtiles, int ntiles,
+                                                            int ksteps, int slot) {
+  __shared__ __align__(16) uint16_t sX[2][kQ3M * kQ3Ld];
+  __shared__ __align__(16) uint16_t sW[2][kQ3N * kQ3Ld];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+  // XCD-grouped tile order: the M tiles of one N tile share an XCD's L2
+  const int L = blockIdx.x;
+  const int grp = L / (8 * mtiles), rem = L % (8 * mtiles);
+  const int nt = grp * 8 + rem % 8, mt = rem / 8;
+  if (nt >= ntiles) return;
+  int mi = 0;
+#pragma unroll
+  for (int t = 1; t < kQMultiMax; ++t) mi = t < p.n && nt >= p.tile_start[t] ? t : mi;
+  mi = __builtin_amdgcn_readfirstlane(mi);
+  const QmmMat &mat = p.m[mi];
+  const int bm0 = mt * kQ3M, bn0 = (nt - p.tile_start[mi]) * kQ3N;
+  const int N = mat.N;
+
+  // dequantising role: row wr of the W tile, codes [16 q, 16 q + 16) of each step
+  const int wr = tid >> 2, q = tid & 3;
+  const int nrow = min(bn0 + wr, N - 1);
+  const __amdgpu_buffer_rsrc_t wrs = q3_rsrc(mat.w, (long long)N * mat.row_bytes);
+  const __amdgpu_buffer_rsrc_t srs = q3_rsrc(mat.sc, (long long)N * mat.ng * 2);
+  const __amdgpu_buffer_rsrc_t brs = q3_rsrc(mat.bi, (long long)N * mat.ng * 2);
+  const int rowoff = (int)((long long)nrow * mat.row_bytes);
+  const int prow = nrow * mat.ng;
+  const int gsh = __builtin_ctz(p.gs);  // group sizes are powers of two here
+  const int sh5 = (BITS == 5 && (q & 1)) ? 16 : 0;  // 5-bit run start inside its first dword
+  const int wdst = wr * kQ3Ld;
+
+  // x staging role: 16-byte granules g = 512 i + tid (i < 4) of the 256 x 8
+  // tile
+  const uint16_t *xsrc[4];
+  int xdst[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int g = 512 * i + tid;
+    const int r = g >> 3, lg = g & 7;
+    xsrc[i] = p.x + (size_t)min(bm0 + r, p.M - 1) * p.x_stride + 8 * lg;
+    xdst[i] = r * kQ3Ld + 8 * lg;
+  }
+
+  const int z = blockIdx.y;
+  const int kb = z * ksteps * 64;
+  const int nst = (min(p.K, kb + ksteps * 64) - kb) >> 6;
+
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct Set {
+    u32x4 x[4];  // native vectors: a HIP uint4 array copy would stay in memory
+    Q3Raw<BITS> w;
+  };
+  auto load = [&](int s, Set &r) {
+    const int k0 = kb + 64 * s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.x[i] = *reinterpret_cast<const u32x4 *>(xsrc[i] + k0);
+    const int k = k0 + 16 * q;
+    q3_load<BITS>(r.w, wrs, srs, brs, rowoff, 2 * (prow + (k >> gsh)), k);
+  };
+  auto stage = [&](const Set &r, int st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(sX[st] + xdst[i]) = r.x[i];
+    uint32_t pk[8];
+    q3_dequant<BITS>(r.w, sh5, p.fp16 != 0, pk);
+    uint16_t *d = sW[st] + wdst;
+    *reinterpret_cast<uint4 *>(d + 16 * q) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    *reinterpret_cast<uint4 *>(d + 16 * q + 8) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  auto mfma = [&](int st) {
+    const uint16_t *xa = sX[st] + (wm * 64 + l32) * kQ3Ld;
+    const uint16_t *wb = sW[st] + (wn * 64 + l32) * kQ3Ld;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int g = 16 * ks + 8 * half;
+      bf16x8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xa + 32 * kQ3Ld * i + g);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const bf16x8 *>(wb + 32 * kQ3Ld * j + g);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
+  auto barrier = [&]() {
+    // nothing moves across a step boundary (the scheduler would otherwise
+    // hoist the next set's conversions and wait for loads meant to stay in
+    // flight); the LDS writes of this wave are done, then the barrier alone
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Step s's x and W pass through a register set loaded two steps earlier,
+  // are written (W dequantised) into LDS stage s & 1 one step ahead, and
+  // multiplied after the barrier that follows. Iteration s: barrier; the
+  // MFMAs of step s (they run in the matrix pipe while the same wave goes
+  // on); stage step s + 1 from its set into the other stage; load step s + 3
+  // into that set.
+  Set ra, rb;
+  load(0, ra);
+  if (nst > 1) load(1, rb);
+  stage(ra, 0);
+  if (nst > 2) load(2, ra);
+  int s = 0;
+  // steady state, two steps per trip so each register set is a fixed one
+  for (; s + 4 < nst; s += 2) {
+    barrier();
+    mfma(0);
+    stage(rb, 1);
+    load(s + 3, rb);
+    barrier();
+    mfma(1);
+    stage(ra, 0);
+    load(s + 4, ra);
+  }
+  // tail: the last (at most four) steps, s even here; written out so that
+  // each register set stays a fixed one
+  if (s < nst) {
+    barrier();
+    mfma(0);
+    if (s + 1 < nst) stage(rb, 1);
+    if (s + 3 < nst) load(s + 3, rb);
+  }
+  if (s + 1 < nst) {
+    barrier();
+    mfma(1);
+    if (s + 2 < nst) stage(ra, 0);
+    if (s + 4 < nst) load(s + 4, ra);
+  }
+  if (s + 2 < nst) {
+    barrier();
+    mfma(0);
+    if (s + 3 < nst) stage(rb, 1);
+  }
+  if (s + 3 < nst) {
+    barrier();
+    mfma(1);
+  }
+
+  // Output through LDS, 32 rows of the wave's tile at a time: the wave
+  // writes them as f32 rows of 72 floats (element e of MFMA tile (i, j) is
+  // row 8 (e / 4) + 4 half + e % 4, column 32 j + l32), then stores whole
+  // rows with 16-byte stores (8 bf16 or 4 f32 per lane); ragged or unaligned
+  // edges take element stores.
+  constexpr int kTs = 72;
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();  // every wave is done with the operand tiles
+  float *tb = reinterpret_cast<float *>(&sX[0][0]) + wave * (32 * kTs);
+  const bool split = slot >= 0;
+  float *part = split ? g_qmm_part + (size_t)slot * kQSlotFloats + (size_t)z * p.M * p.part_N + mat.col0
+                      : nullptr;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        tb[(8 * (e / 4) + 4 * half + (e % 4)) * kTs + 32 * j + l32] = acc[i][j][e];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    const int m0 = bm0 + wm * 64 + 32 * i, n0 = bn0 + wn * 64;
+    if (!split && p.y_bf16) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int r = 8 * it + (lane >> 3), c = 8 * (lane & 7);
+        const float4 u = *reinterpret_cast<const float4 *>(tb + r * kTs + c);
+        const float4 v = *reinterpret_cast<const float4 *>(tb + r * kTs + c + 4);
+        const int m = m0 + r, n = n0 + c;
+        if (m >= p.M) continue;
+        __bf16 *dst = reinterpret_cast<__bf16 *>(mat.y) + (size_t)m * mat.y_stride + n;
+        const float f[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        if ((p.vec & 1) && n + 8 <= N) {
+          bf16x8 o;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) o[t] = (__bf16)f[t];
+          *reinterpret_cast<bf16x8 *>(dst) = o;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (n + t < N) dst[t] = (__bf16)f[t];
+        }
+      }
+    } else {
+      const bool vec = split ? (p.vec & 2) != 0 : (p.vec & 1) != 0;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int r = 4 * it + (lane >> 4), c = 4 * (lane & 15);
+        const float4 u = *reinterpret_cast<const float4 *>(tb + r * kTs + c);
+        const int m = m0 + r, n = n0 + c;
+        if (m >= p.M) continue;
+        float *dst = split ? part + (size_t)m * p.part_N + n
+                           : reinterpret_cast<float *>(mat.y) + (size_t)m * mat.y_stride + n;
+        if (vec && n + 4 <= N) {
+          *reinterpret_cast<float4 *>(dst) = u;
+        } else {
+          const float f[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (n + t < N) dst[t] = f[t];
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 bool affine_qmm_supported(const DevMat &m) {
   if (!(m.bits == 4 || m.bits == 5 || m.bits == 6 || m.bits == 8)) return false;
   if (m.I <= 0 || m.I % kTile != 0 || m.O <= 0) return false;
@@ -339,9 +703,103 @@ bool affine_qmm_supported(const DevMat &m) {
   return true;
 }
 
+// 256 x 128 tiles: every matrix supported, the same K / bits / group size /
+// aux type, power-of-two group sizes (the kernel shifts), at least 256 rows
+// of x, and offsets of every matrix within 2 GiB (32-bit buffer offsets)
+static bool qmm256_ok(const DevMat *ms, int n, int M) {
+  if (M < kQ3M || n < 1 || n > kQMultiMax) return false;
+  for (int i = 0; i < n; ++i) {
+    const DevMat &m = ms[i];
+    if (!affine_qmm_supported(m)) return false;
+    if (m.I != ms[0].I || m.bits != ms[0].bits || m.gs != ms[0].gs || m.fp16 != ms[0].fp16) return false;
+    if ((m.gs & (m.gs - 1)) != 0 || (long long)m.O * m.row_bytes > 0x7fffffffLL) return false;
+    if ((reinterpret_cast<uintptr_t>(m.w) & 15) != 0) return false;
+  }
+  return true;
+}
+
+static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
+                                void *const *ys, const int *y_strides, int y_bf16, hipStream_t st) {
+  QmmMulti p;
+  p.x = x;
+  p.n = n;
+  p.M = M;
+  p.K = ms[0].I;
+  p.gs = ms[0].gs;
+  p.fp16 = ms[0].fp16;
+  p.x_stride = x_stride;
+  p.y_bf16 = y_bf16;
+  int tiles = 0, cols = 0;
+  for (int i = 0; i < kQMultiMax; ++i) {
+    if (i < n) {
+      p.m[i] = QmmMat{ms[i].w, ms[i].sc, ms[i].bi, ys[i], ms[i].row_bytes, ms[i].O, ms[i].ng,
+                      y_strides[i], cols};
+      p.tile_start[i] = tiles;
+      tiles += (ms[i].O + kQ3N - 1) / kQ3N;
+      cols += ms[i].O;
+    } else {
+      p.m[i] = p.m[0];
+      p.tile_start[i] = tiles;
+    }
+  }
+  p.tile_start[kQMultiMax] = tiles;
+  p.part_N = cols;
+  bool yv = true, pv = (cols & 3) == 0;
+  for (int i = 0; i < n; ++i) {
+    const int es = y_bf16 ? 2 : 4;
+    yv = yv && (reinterpret_cast<uintptr_t>(ys[i]) & 15) == 0 && ((long long)y_strides[i] * es) % 16 == 0;
+    pv = pv && (p.m[i].col0 & 3) == 0;
+  }
+  p.vec = (yv ? 1 : 0) | (pv ? 2 : 0);
+  const int mt = (M + kQ3M - 1) / kQ3M;
+  const int ksteps_all = p.K / 64;
+  // split K while the grid is short of one block per CU and each k range
+  // keeps at least 8 steps
+  int split = 1;
+  while (split < 16 && mt * tiles * split < 192 && ksteps_all / (2 * split) >= 8 &&
+         (size_t)(2 * split) * M * cols <= kQSlotFloats)
+    split *= 2;
+  const int ksteps = (ksteps_all + split - 1) / split;
+  split = (ksteps_all + ksteps - 1) / ksteps;
+  const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
+  const dim3 grid(((tiles + 7) / 8) * 8 * mt, split);
+  switch (ms[0].bits) {
+    case 4: hipLaunchKernelGGL(affine_qmm256_kernel<4>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+    case 5: hipLaunchKernelGGL(affine_qmm256_kernel<5>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+    case 6: hipLaunchKernelGGL(affine_qmm256_kernel<6>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+    case 8: hipLaunchKernelGGL(affine_qmm256_kernel<8>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || split == 1) return e;
+  const size_t mn = (size_t)M * cols;
+  const int rblocks = (int)std::min<size_t>((mn + 255) / 256, 4096);
+  hipLaunchKernelGGL(qmm_reduce_multi_kernel, dim3(rblocks), dim3(256), 0, st, p, slot, split);
+  return hipGetLastError();
+}
+
+hipError_t launch_affine_qmm_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
+                                   void *const *ys, int y_bf16, hipStream_t st) {
+  if (n < 1 || n > kQMultiMax || M <= 0) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  int strides[kQMultiMax];
+  for (int i = 0; i < n; ++i) strides[i] = ms[i].O;
+  if (qmm256_ok(ms, n, M)) return launch_qmm256(ms, n, x, x_stride, M, ys, strides, y_bf16, st);
+  for (int i = 0; i < n; ++i) {
+    const hipError_t e = launch_affine_qmm(ms[i], x, x_stride, M, ys[i], ms[i].O, y_bf16, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                              int y_stride, int y_bf16, hipStream_t st) {
   if (!affine_qmm_supported(m) || M <= 0) return hipErrorInvalidValue;
+  if (qmm256_ok(&m, 1, M) && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (x_stride & 7) == 0) {
+    void *ys[1] = {y};
+    const int strides[1] = {y_stride};
+    return launch_qmm256(&m, 1, x, x_stride, M, ys, strides, y_bf16, st);
+  }
   if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
   GemmParams p;
   p.w = m.w;

@@ -61,6 +61,11 @@ hipError_t launch_hilo_join(const HiloBatch &b, hipStream_t st);
 hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                              int y_stride, int y_bf16, hipStream_t st);
 bool affine_qmm_supported(const DevMat &m);
+// up to 8 matrices sharing x (same I, bits, group size, aux type) in one
+// grid where the 256-row tiles apply, else one launch per matrix; ys[i] is
+// [M][O_i]
+hipError_t launch_affine_qmm_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
+                                   void *const *ys, int y_bf16, hipStream_t st);
 bool affine_skinny_supported(const DevMat &m);
 hipError_t launch_affine_skinny(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);

@@ -158,6 +158,30 @@ def affine_qmm(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = N
     return out
 
 
+def affine_qmm_multi(ws, x: torch.Tensor, outs=None, out_dtype: torch.dtype = torch.bfloat16,
+                     stream=None):
+    """Prefill products of up to 8 matrices sharing x in one grid: returns
+    [x . bf16(W_i)^T] (the QMM numerics of affine_qmm)."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    if not 1 <= len(ws) <= 8:
+        raise LoganHipError("between 1 and 8 matrices")
+    x2 = x.reshape(-1, ws[0].I)
+    M = x2.shape[0]
+    if outs is None:
+        outs = [torch.empty((M, w.O), dtype=out_dtype, device=x.device) for w in ws]
+    dts = {o.dtype for o in outs}
+    if len(dts) != 1 or next(iter(dts)) not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("outputs must all be bf16 or all f32")
+    yd = L.LOGAN_HIP_BF16 if outs[0].dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    arr = (L.Affine * len(ws))(*[w.c() for w in ws])
+    ptrs = (C.c_void_p * len(ws))(*[_dev(o, "out") for o in outs])
+    rc = L.lib().logan_hip_affine_qmm_multi(arr, len(ws), _dev(x2, "x"), M, ws[0].I, ptrs, yd,
+                                            _stream(stream))
+    _check(rc, "affine_qmm_multi")
+    return outs
+
+
 def silu_mul(g: torch.Tensor, u: torch.Tensor, stream=None) -> torch.Tensor:
     """In place g = silu(g) * u (f32 or bf16 device tensors of equal size;
     logan-metal/metal/backend_metal.mm:2187-2203). Returns g."""

@@ -164,3 +164,50 @@ def test_qmm_config5_prefill_projections(gpu, O, I):
     bis = bi.reshape(O, ng)[cols].reshape(-1)
     ref = oracle.affine_qmm_bf16(bf16_to_f32(xb).reshape(M, I), ws, scs, bis, len(cols), I, bits, gs)
     assert normwise_rel(y[:, cols], ref) <= 1e-5
+
+
+MULTI_CASES = [
+    # (M, [O_i], I, bits, gs, fp16)
+    (512, [8192, 512, 512], 2048, 4, 64, False),   # config-5 q / k / v in one grid
+    (512, [12288, 64], 2048, 4, 64, False),        # config-5 qkvz / ba
+    (300, [100, 257, 64], 192, 5, 64, True),       # ragged tiles, 5-bit runs at bit 16
+    (256, [130, 72], 512, 6, 128, False),
+    (384, [200, 96, 40, 33], 256, 8, 32, False),
+    (270, [96, 64], 192, 4, 96, False),            # group size 96: one launch per matrix
+    (64, [128, 96], 256, 4, 64, False),            # M < 256: one launch per matrix
+]
+
+
+@pytest.mark.parametrize("M,Os,I,bits,gs,fp16", MULTI_CASES, ids=lambda v: str(v))
+def test_qmm_multi_matches_oracle(gpu, M, Os, I, bits, gs, fp16):
+    """Matrices that share x in one product launch (logan_hip_affine_qmm_multi):
+    every output against the oracle (sampled columns of the wide ones, every
+    column of each last tile), the bf16 outputs equal to RNE of the f32 ones,
+    and repeated calls identical."""
+    import torch
+    from logan_amd.device import affine_qmm_multi
+
+    print(f"qmm multi M={M} Os={Os} I={I} bits={bits} gs={gs}", flush=True)
+    rng = np.random.default_rng(M + sum(Os) + bits)
+    mats, devs = [], []
+    for O in Os:
+        w, sc, bi = make_affine(rng, O, I, bits, gs, fp16)
+        mats.append((w, sc, bi))
+        devs.append(dev_matrix(torch, w, sc, bi, O, I, bits, gs, fp16))
+    xb = make_x(rng, M, I).reshape(M, I)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    ys = affine_qmm_multi(devs, x, out_dtype=torch.float32)
+    ys2 = affine_qmm_multi(devs, x, out_dtype=torch.float32)
+    ybs = affine_qmm_multi(devs, x, out_dtype=torch.bfloat16)
+    xf = bf16_to_f32(xb).reshape(M, I)
+    ng = I // gs
+    for (w, sc, bi), O, y, y2, yb in zip(mats, Os, ys, ys2, ybs):
+        assert torch.equal(y, y2)
+        assert torch.equal(yb, y.to(torch.bfloat16))
+        cols = np.unique(np.concatenate([np.arange(0, O, max(1, O // 40)),
+                                         np.arange(max(0, O - 130), O)]))
+        ws = w.reshape(O, -1)[cols]
+        scs = sc.reshape(O, ng)[cols].reshape(-1)
+        bis = bi.reshape(O, ng)[cols].reshape(-1)
+        ref = oracle.affine_qmm_bf16(xf, ws, scs, bis, len(cols), I, bits, gs, fp16)
+        assert normwise_rel(y.cpu().numpy()[:, cols], ref) <= 1e-5, O
