@@ -24,7 +24,7 @@ Secondary legs (reported under "secondary", same synthetic scheme, every
 one a HIP graph of the product entry points timed with HIP events):
   * config 1: q4 GEMV 4096x2048 over 64 rotated weight copies;
   * config 2: dense 8-bit g64 decode layer (QKV 4096->6144, O 4096->4096,
-    gate/up 4096->14336, SwiGLU, down 14336->4096) at M = 1, 4, 8 over 4
+    gate/up 4096->14336 with its SwiGLU, down 14336->4096) at M = 1, 4, 8 over 4
     rotated layers (927 MB); and the whole Llama decode layer (norms, RoPE,
     attention over 256 cached tokens, residuals) at M = 1 for affine-8 and
     bf16 weights;
@@ -303,10 +303,9 @@ def bench_config2(torch, device, synth, args):
             for L in layers:
                 device.affine_gemv(L["qkv"], x, out=qkv)
                 device.affine_gemv(L["o"], att, out=o)
-                # gate+up: the config's 4096 -> 2 x 14336 projection, one
-                # product of the two matrices that share x
-                device.affine_gemv_multi([L["gate"], L["up"]], o, outs=[gt, up])
-                device.silu_mul(gt, up)
+                # gate+up: the config's 4096 -> 2 x 14336 projection and its
+                # SwiGLU as one product of the two matrices that share x
+                device.affine_gemv_swiglu(L["gate"], L["up"], o, out=gt)
                 device.affine_gemv(L["down"], gt, out=y)
 
         us = graph_us(torch, step, args.reps) / nl

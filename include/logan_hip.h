@@ -204,6 +204,19 @@ int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_s
 int logan_hip_affine_gemv_multi(const LoganHipAffine *ws, int count, const void *x, int M,
                                 int x_stride, void *const *ys, int y_dtype, void *stream);
 
+/* The dense MLP's gate/up pair and its SwiGLU as one product:
+ * h[M][h_stride] = silu(gate . x) * (up . x), silu(v) = v / (1 + exp(-v)),
+ * from the f32 accumulators (logan-qwen4/src/lib.rs:8803-8812; replaces the
+ * two GEMVs plus coli_metal_silu_mul of the reference's dense layer,
+ * logan-metal/metal/backend_metal.mm:2187-2203). gate and up share I, O,
+ * bits, group_size and aux type. Token pairs take the dot2 kernel with each
+ * team computing a gate row and its up row; 3..32 tokens the K-split pair,
+ * whose reduction forms h. h bf16 (RNE) or f32. 1 ok, 0 unsupported, -1
+ * launch failure. */
+int logan_hip_affine_gemv_swiglu(const LoganHipAffine *gate, const LoganHipAffine *up,
+                                 const void *x, int M, int x_stride, void *h, int h_stride,
+                                 int h_dtype, void *stream);
+
 /* Prefill / large-batch form of the same product on MFMA, with the
  * reference QMM's numerics (logan-metal/metal/backend_metal.mm:1480-1560,
  * spark_qmm_affine8_t16o8): every dequantised weight code*scale + bias is

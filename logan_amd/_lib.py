@@ -165,6 +165,8 @@ SIGNATURES = {
     "logan_hip_affine_gemv": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
     "logan_hip_affine_gemv_f32": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _P]),
     "logan_hip_affine_gemv_multi": (_I, [C.POINTER(Affine), _I, _P, _I, _I, C.POINTER(_P), _I, _P]),
+    "logan_hip_affine_gemv_swiglu": (_I, [C.POINTER(Affine), C.POINTER(Affine), _P, _I, _I, _P, _I,
+                                          _I, _P]),
     "logan_hip_affine_qmm": (_I, [C.POINTER(Affine), _P, _I, _I, _P, _I, _I, _P]),
     "logan_hip_affine_qmm_multi": (_I, [C.POINTER(Affine), _I, _P, _I, _I, C.POINTER(_P), _I, _P]),
     "logan_hip_silu_mul": (_I, [_P, _P, C.c_longlong, _I, _P]),

@@ -1194,6 +1194,21 @@ int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_st
                                        reinterpret_cast<hipStream_t>(stream)));
 }
 
+int logan_hip_affine_gemv_swiglu(const LoganHipAffine *gate, const LoganHipAffine *up,
+                                 const void *x, int M, int x_stride, void *h, int h_stride,
+                                 int h_dtype, void *stream) {
+  if (!affine_ok(gate) || !affine_ok(up) || !x || !h || M <= 0) return 0;
+  if (x_stride < gate->I || h_stride < gate->O) return 0;
+  if (h_dtype != LOGAN_HIP_F32 && h_dtype != LOGAN_HIP_BF16) return 0;
+  const lh::DevMat g = devmat(*gate), u = devmat(*up);
+  if (!lh::gemv_bf16_supported(g) || !lh::gemv_bf16_supported(u)) return 0;
+  if (g.I != u.I || g.O != u.O || g.bits != u.bits || g.gs != u.gs || g.fp16 != u.fp16) return 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return 0;
+  return rc_from(lh::launch_gemv_swiglu(g, u, reinterpret_cast<const uint16_t *>(x), x_stride, M, h,
+                                        h_stride, h_dtype == LOGAN_HIP_BF16,
+                                        reinterpret_cast<hipStream_t>(stream)));
+}
+
 int logan_hip_affine_qmm_multi(const LoganHipAffine *ws, int count, const void *x, int M,
                                int x_stride, void *const *ys, int y_dtype, void *stream) {
   if (!ws || !ys || !x || count <= 0 || count > 8 || M <= 0) return 0;

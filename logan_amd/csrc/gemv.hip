@@ -27,6 +27,10 @@ struct GemvParams {
   int I, O, ng, gsc;  // gsc = chunks per group
   int gsc_shift;      // log2(gsc) when gsc is a power of two, else -1
   int fp16, x_stride, M, y_stride, y_bf16;
+  // SW (SwiGLU) form: the up matrix, same geometry as w
+  const uint8_t *w2;
+  const uint16_t *sc2;
+  const uint16_t *bi2;
 };
 
 // SPLIT > 1: SPLIT teams share one row, each over a contiguous K segment of
@@ -36,9 +40,14 @@ struct GemvParams {
 // rows are hi = bf16(x) and lo = bf16(x - hi) (|x - hi - lo| <= 2^-18 |x|),
 // split in registers, and their partial sums are added before the team
 // reduction, so the kernel writes one f32 (or bf16) output row (MT == 2).
-template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF = false>
+// SW: SwiGLU form. Team row u alternates between the gate matrix (w, even u)
+// and the up matrix (w2, odd u) at the same row index j = (r0 + u) / 2, and
+// the team writes h[m][j] = silu(gate_j . x) * (up_j . x) (logan-qwen4/src
+// /lib.rs:8803-8812) instead of the two products; the grid covers 2 * O rows.
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF = false, bool SW = false>
 __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   static_assert(!XF || MT == 2, "f32 activations use the two-row operand form");
+  static_assert(!SW || (U % 2 == 0 && !XF), "SwiGLU pairs whole teams of bf16 rows");
   constexpr int MO = XF ? 1 : MT;  // output rows
   constexpr int TEAMS = 256 / LANES;
   constexpr int ROWTEAMS = TEAMS / SPLIT;
@@ -96,22 +105,27 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
     const int r0 = bid * (ROWTEAMS * U) + rteam * U;
     uint32_t wv[U][CPL][BITS];
     uint32_t scr[U][CPL], bir[U][CPL];
+    // row index and matrix of team row u (SW: gate / up alternately)
+    auto row_of = [&](int u) { return SW ? (r0 >> 1) + (u >> 1) : r0 + u; };
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = min(r0 + u, a.O - 1);
+      const int row = min(row_of(u), a.O - 1);
+      const uint16_t *scp = (SW && (u & 1)) ? a.sc2 : a.sc;
+      const uint16_t *bip = (SW && (u & 1)) ? a.bi2 : a.bi;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const size_t pi = (size_t)row * a.ng + gidx[j];
-        scr[u][j] = a.sc[pi];
-        bir[u][j] = a.bi[pi];
+        scr[u][j] = scp[pi];
+        bir[u][j] = bip[pi];
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row = min(r0 + u, a.O - 1);
+      const int row = min(row_of(u), a.O - 1);
+      const uint8_t *wp = (SW && (u & 1)) ? a.w2 : a.w;
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        load_chunk<BITS>(wv[u][j], a.w + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
+        load_chunk<BITS>(wv[u][j], wp + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
     }
     // keep every load above issued before any of their consumers
     __builtin_amdgcn_sched_barrier(0);
@@ -159,7 +173,7 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        const bool live = r0 + u < a.O && cval[j];
+        const bool live = row_of(u) < a.O && cval[j];
         scv[u][j] = live ? aux_to_f32(scr[u][j], a.fp16) : 0.f;
         biv[u][j] = live ? aux_to_f32(bir[u][j], a.fp16) : 0.f;
       }
@@ -185,7 +199,7 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
 #pragma unroll
       for (int u = 0; u < U; ++u) part[u][0] += part[u][1];  // y = W.hi + W.lo
     }
-    if constexpr (LANES == 64 && SPLIT == 1 && U * MO >= 2) {
+    if constexpr (LANES == 64 && SPLIT == 1 && U * MO >= 2 && !SW) {
       // four (row, token) sums per wave_reduce4; row r of lanes gets value r
       constexpr int NV = U * MO;
       float vals[NV];
@@ -238,11 +252,12 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
         __syncthreads();
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int row = r0 + u;
+      for (int u = 0; u < U; u += SW ? 2 : 1) {
+        const int row = row_of(u);
 #pragma unroll
         for (int m = 0; m < MO; ++m) {
-          const float v = tot[u][m];
+          // SW: h = silu(gate) * up of the pair (u, u + 1)
+          const float v = SW ? silu(tot[u][m]) * tot[u + (SW ? 1 : 0)][m] : tot[u][m];
           if (seg == 0 && lane == 0 && row < a.O && (XF || m < a.M)) {
             if (a.y_bf16)
               reinterpret_cast<uint16_t *>(a.y)[(size_t)m * a.y_stride + row] =
@@ -259,6 +274,11 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
 template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT, bool XF>
 __global__ __launch_bounds__(256) void gemv_bf16_kernel(GemvParams a) {
   gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT, XF>(a, blockIdx.x);
+}
+
+template <int BITS, int LANES, int CPL, int U, int MT, int SPLIT>
+__global__ __launch_bounds__(256) void gemv_swiglu_kernel(GemvParams a) {
+  gemv_bf16_body<BITS, LANES, CPL, U, MT, SPLIT, false, true>(a, blockIdx.x);
 }
 
 // Up to kMultiMax matrices sharing one activation in one launch: block b
@@ -407,6 +427,91 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
     else
       e = dot2_rows(m0, mc);
     if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+// ---- gate/up + SwiGLU in one product (h = silu(gate . x) * (up . x)) ----
+
+template <int BITS, int LANES, int CPL, int MT, int SPLIT, int U>
+static hipError_t swiglu_launch_t(const GemvParams &p, hipStream_t st) {
+  constexpr int rows_per_block = (256 / LANES / SPLIT) * U;  // gate and up rows together
+  const int blocks = (2 * p.O + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((gemv_swiglu_kernel<BITS, LANES, CPL, U, MT, SPLIT>), dim3(blocks), dim3(256), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+template <int BITS, int MT>
+static hipError_t swiglu_dispatch_shape(const GemvParams &p, hipStream_t st) {
+  const int C = p.I >> 5;
+  if (C <= 16) return swiglu_launch_t<BITS, 16, 1, MT, 1, 4>(p, st);
+  if (C <= 32) return swiglu_launch_t<BITS, 32, 1, MT, 1, 4>(p, st);
+  if (C <= 64) return swiglu_launch_t<BITS, 64, 1, MT, 1, 4>(p, st);
+  if (C <= 128) return swiglu_launch_t<BITS, 64, 1, MT, 2, 2>(p, st);
+  if (C <= 256) return swiglu_launch_t<BITS, 64, 1, MT, 4, 2>(p, st);
+  if (C <= 512) return swiglu_launch_t<BITS, 64, 2, MT, 4, 2>(p, st);
+  return hipErrorInvalidValue;
+}
+
+template <int MT>
+static hipError_t swiglu_dispatch_bits(const GemvParams &p, int bits, hipStream_t st) {
+  switch (bits) {
+    case 4: return swiglu_dispatch_shape<4, MT>(p, st);
+    case 5: return swiglu_dispatch_shape<5, MT>(p, st);
+    case 6: return swiglu_dispatch_shape<6, MT>(p, st);
+    case 8: return swiglu_dispatch_shape<8, MT>(p, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
+                              void *h, int h_stride, int h_bf16, hipStream_t st) {
+  if (!gemv_bf16_supported(g) || !gemv_bf16_supported(u) || M <= 0) return hipErrorInvalidValue;
+  if (g.I != u.I || g.O != u.O || g.bits != u.bits || g.gs != u.gs || g.fp16 != u.fp16 ||
+      g.row_bytes != u.row_bytes)
+    return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  // 3..32 tokens: the K-split pair, its reduce forming h
+  const DevMat gu[2] = {g, u};
+  for (int m0 = 0; m0 < M; m0 += 32) {
+    const int mc = min(32, M - m0);
+    if (mc >= 3 && affine_splitk_multi_supported(gu, 2, mc)) {
+      void *hm = h_bf16 ? (void *)(reinterpret_cast<uint16_t *>(h) + (size_t)m0 * h_stride)
+                        : (void *)(reinterpret_cast<float *>(h) + (size_t)m0 * h_stride);
+      void *const ys[2] = {hm, hm};
+      const hipError_t e = launch_affine_splitk_multi(gu, 2, x + (size_t)m0 * x_stride, x_stride, mc,
+                                                      ys, h_bf16, st, h_stride);
+      if (e != hipSuccess) return e;
+      continue;
+    }
+    // token pairs through the dot2 kernel
+    GemvParams p;
+    p.w = g.w;
+    p.sc = g.sc;
+    p.bi = g.bi;
+    p.w2 = u.w;
+    p.sc2 = u.sc;
+    p.bi2 = u.bi;
+    p.row_bytes = g.row_bytes;
+    p.I = g.I;
+    p.O = g.O;
+    p.ng = g.ng;
+    p.gsc = g.gs / 32;
+    p.gsc_shift = (p.gsc & (p.gsc - 1)) == 0 ? __builtin_ctz(p.gsc) : -1;
+    p.fp16 = g.fp16;
+    p.x_stride = x_stride;
+    p.y_stride = h_stride;
+    p.y_bf16 = h_bf16;
+    for (int t = m0; t < m0 + mc; t += 2) {
+      const int mt = m0 + mc - t >= 2 ? 2 : 1;
+      p.x = x + (size_t)t * x_stride;
+      p.M = mt;
+      p.y = h_bf16 ? (void *)(reinterpret_cast<uint16_t *>(h) + (size_t)t * h_stride)
+                   : (void *)(reinterpret_cast<float *>(h) + (size_t)t * h_stride);
+      const hipError_t e = mt == 2 ? swiglu_dispatch_bits<2>(p, g.bits, st) : swiglu_dispatch_bits<1>(p, g.bits, st);
+      if (e != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }

@@ -20,6 +20,7 @@
 // share a slot unless more than kSkSlots of them are in flight at once.
 #include <atomic>
 
+#include "affine_dev.hpp"
 #include "lh_internal.hpp"
 #include "mfma_dev.hpp"
 
@@ -58,6 +59,7 @@ struct ReduceMulti {
   int y_stride[kSkMultiMax];
   int start[kSkMultiMax + 1];  // prefix sums of M * N
   int n, KS, M, slot, y_bf16;
+  int swiglu;  // products 0 (gate) and 1 (up) reduce to y[0] = silu(gate) * up
 };
 
 template <int BITS, int MT, bool FP16, bool AUX8>
@@ -202,6 +204,34 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(int slot, int KS, in
 // as in splitk_reduce_kernel).
 __global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r) {
   const float *part = g_sk_part + (size_t)r.slot * kSkSlotFloats;
+  if (r.swiglu) {
+    // h = silu(gate) * up (logan-qwen4/src/lib.rs:8803-8812), each sum in K order
+    const int MN = r.M * r.N[0];
+    const float *pg = part + r.part_off[0], *pu = part + r.part_off[1];
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < MN; i += gridDim.x * 256) {
+      float sg = 0.f, su = 0.f;
+      for (int k0 = 0; k0 < r.KS; k0 += 8) {
+        float vg[8], vu[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          vg[q] = pg[(size_t)min(k0 + q, r.KS - 1) * MN + i];
+          vu[q] = pu[(size_t)min(k0 + q, r.KS - 1) * MN + i];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          sg += k0 + q < r.KS ? vg[q] : 0.f;
+          su += k0 + q < r.KS ? vu[q] : 0.f;
+        }
+      }
+      const float hv = silu(sg) * su;
+      const int m = i / r.N[0], nn = i - m * r.N[0];
+      if (r.y_bf16)
+        reinterpret_cast<uint16_t *>(r.y[0])[(size_t)m * r.y_stride[0] + nn] = (uint16_t)f32_to_bf16_rne(hv);
+      else
+        reinterpret_cast<float *>(r.y[0])[(size_t)m * r.y_stride[0] + nn] = hv;
+    }
+    return;
+  }
   const int total = r.start[r.n];
   for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
     int j = 0;
@@ -328,7 +358,9 @@ bool affine_splitk_multi_supported(const DevMat *ms, int n, int M) {
 // one reduce launch for all of them (gate/up, q/k/v) instead of two launches
 // per product.
 hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
-                                      void *const *ys, int y_bf16, hipStream_t st) {
+                                      void *const *ys, int y_bf16, hipStream_t st, int swiglu_stride) {
+  const bool swiglu = swiglu_stride > 0;
+  if (swiglu && (n != 2 || ms[0].O != ms[1].O)) return hipErrorInvalidValue;
   if (!affine_splitk_multi_supported(ms, n, M)) return hipErrorInvalidValue;
   if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
   SplitMulti mp{};
@@ -368,6 +400,8 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
   r.M = M;
   r.slot = slot;
   r.y_bf16 = y_bf16;
+  r.swiglu = swiglu ? 1 : 0;
+  if (swiglu) r.y_stride[0] = swiglu_stride;
   switch (ms[0].bits) {
     case 4: splitk_multi_launch_bits<4>(mp, KS, M, ms[0].fp16, aux8, st); break;
     case 5: splitk_multi_launch_bits<5>(mp, KS, M, ms[0].fp16, aux8, st); break;
@@ -376,7 +410,7 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  size_t blocks = ((size_t)r.start[n] + 255) / 256;
+  size_t blocks = ((size_t)(swiglu ? r.start[1] : r.start[n]) + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, st, r);
   return hipGetLastError();

@@ -72,8 +72,16 @@ hipError_t launch_affine_skinny(const DevMat &m, const uint16_t *x, int x_stride
 // K split across blocks (gemv_splitk.hip): I % 512 == 0, groups of 64k,
 // 3 <= M <= 32; partial sums in module-scope scratch slots
 bool affine_splitk_multi_supported(const DevMat *ms, int n, int M);
+// swiglu_stride > 0: n == 2 (gate, up) and the reduce writes
+// ys[0][M][swiglu_stride] = silu(gate) * up instead of the two products
 hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
-                                      void *const *ys, int y_bf16, hipStream_t st);
+                                      void *const *ys, int y_bf16, hipStream_t st,
+                                      int swiglu_stride = 0);
+// h[M][h_stride] = silu(gate . x) * (up . x) in one product (gate and up of
+// the same geometry): the dot2 kernel with gate/up row pairs for token pairs,
+// the K-split pair with a SwiGLU reduce for 3..32 tokens
+hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
+                              void *h, int h_stride, int h_bf16, hipStream_t st);
 bool affine_splitk_supported(const DevMat &m, int M);
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);

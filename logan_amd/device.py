@@ -158,6 +158,27 @@ def affine_qmm(w: AffineMatrix, x: torch.Tensor, out: Optional[torch.Tensor] = N
     return out
 
 
+def affine_gemv_swiglu(gate: AffineMatrix, up: AffineMatrix, x: torch.Tensor,
+                       out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+                       stream=None) -> torch.Tensor:
+    """h[M, O] = silu(x . gate^T) * (x . up^T) in one product
+    (logan-qwen4/src/lib.rs:8803-8812)."""
+    if x.dtype != torch.bfloat16:
+        raise LoganHipError("x must be bf16")
+    x2 = x.reshape(-1, gate.I)
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((M, gate.O), dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("out must be bf16 or f32")
+    hd = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    g, u = gate.c(), up.c()
+    rc = L.lib().logan_hip_affine_gemv_swiglu(C.byref(g), C.byref(u), _dev(x2, "x"), M, gate.I,
+                                              _dev(out, "out"), gate.O, hd, _stream(stream))
+    _check(rc, "affine_gemv_swiglu")
+    return out
+
+
 def affine_qmm_multi(ws, x: torch.Tensor, outs=None, out_dtype: torch.dtype = torch.bfloat16,
                      stream=None):
     """Prefill products of up to 8 matrices sharing x in one grid: returns

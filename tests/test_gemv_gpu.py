@@ -572,3 +572,39 @@ def test_host_multi_fast_and_exact_paths(gpu):
             assert err <= 2e-5, f"desc {k} row {r}: {err:.2e}"
     for k in range(len(specs)):
         Tensor(raw[k].tensor or 0).free()
+
+
+SWIGLU_SHAPES = [
+    # (O, I, bits, gs): config 2's gate/up (8-bit 4096 -> 14336, cut to a
+    # slice of rows), the expert shape of config 3, short and odd rows, 5/6-bit
+    (3000, 4096, 8, 64), (512, 2048, 4, 64), (200, 512, 5, 64), (96, 1024, 6, 128),
+    (77, 256, 4, 32), (1000, 16384, 4, 64),
+]
+
+
+@pytest.mark.parametrize("O,I,bits,gs", SWIGLU_SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 33])
+def test_gemv_swiglu_matches_oracle(gpu, O, I, bits, gs, M):
+    """h = silu(gate . x) * (up . x) in one product (logan_hip_affine_gemv_swiglu)
+    against the oracle's f32 GEMVs and silu_mul, f32 h within 5e-5 normwise,
+    bf16 h equal to RNE of the f32 h; M = 33 crosses the 32-token pass."""
+    import torch
+    from logan_amd.device import affine_gemv_swiglu
+
+    print(f"swiglu O={O} I={I} bits={bits} gs={gs} M={M}", flush=True)
+    rng = np.random.default_rng(O * 7 + I + bits + M)
+    g = make_affine(rng, O, I, bits, gs)
+    u = make_affine(rng, O, I, bits, gs)
+    xb = make_x(rng, M, I).reshape(M, I)
+    gm, um = dev_matrix(torch, *g, O, I, bits, gs), dev_matrix(torch, *u, O, I, bits, gs)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    h = affine_gemv_swiglu(gm, um, x, out_dtype=torch.float32)
+    hb = affine_gemv_swiglu(gm, um, x, out_dtype=torch.bfloat16)
+    assert torch.equal(hb, h.to(torch.bfloat16))
+    h = h.cpu().numpy()
+    for m in range(M):
+        xf = bf16_to_f32(xb[m])
+        yg = oracle.affine_gemv(xf, *g, O, I, bits, gs)
+        yu = oracle.affine_gemv(xf, *u, O, I, bits, gs)
+        ref = oracle.silu_mul(yg, yu)
+        assert normwise_rel(h[m], ref) <= 5e-5, m
