@@ -341,6 +341,54 @@ __device__ __forceinline__ float wave_reduce4(float a, float b, float c, float d
   return t;
 }
 
+// One 32-code chunk (LSB-first BITS-bit codes) as 16 f16 pairs (code 2i in
+// the low half, code 2i+1 in the high half). Every code (< 256) is an exact
+// f16: the pair is formed as f16 (1024 + code) by or-ing the code into the
+// mantissa of 1024 (0x6400), then 1024 is subtracted with one packed f16
+// add, which is exact since both operands and the result are integers
+// below 2048.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f16_pair_from_bias1024(uint32_t p) {
+  const half2v v = __builtin_bit_cast(half2v, p | 0x64006400u);
+  return __builtin_bit_cast(uint32_t, v - (half2v){(_Float16)1024.f, (_Float16)1024.f});
+}
+template <int BITS>
+__device__ __forceinline__ void codes_to_f16(const uint32_t (&w)[BITS], uint32_t (&cp)[16]) {
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // even codes in the bytes of lo, odd codes in the bytes of hi; v_perm
+      // picks byte j of each into the two halves (selector 0x0C = zero byte)
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t sel = (uint32_t)j | 0x0C00u | ((uint32_t)(4 + j) << 16) | 0x0C000000u;
+        cp[4 * i + j] = f16_pair_from_bias1024(__builtin_amdgcn_perm(hi, lo, sel));
+      }
+    }
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      cp[2 * i] = f16_pair_from_bias1024(__builtin_amdgcn_perm(0u, w[i], 0x0C010C00u));
+      cp[2 * i + 1] = f16_pair_from_bias1024(__builtin_amdgcn_perm(0u, w[i], 0x0C030C02u));
+    }
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int k = 0; k < 32; k += 2) {
+      uint32_t c[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int bit = (k + q) * BITS, i = bit >> 5, sh = bit & 31;
+        uint32_t v = w[i] >> sh;
+        if (sh + BITS > 32) v |= w[i + 1] << (32 - sh);
+        c[q] = v & mask;
+      }
+      cp[k >> 1] = f16_pair_from_bias1024(c[0] | (c[1] << 16));
+    }
+  }
+}
+
 // sum_k code_k * h_k over one 32-code chunk (LSB-first BITS-bit codes)
 template <int BITS>
 __device__ __forceinline__ float codes_dot(const uint32_t (&w)[BITS], const float (&h)[32]) {

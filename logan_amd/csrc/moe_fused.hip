@@ -13,10 +13,11 @@
 //   w + 8 for all of them. Each wave issues the shared slot's down-row loads
 //   and the shared-expert gate loads before routing and the routed down rows
 //   right after it, so they stream from HBM while A runs; the last wave
-//   computes the shared-expert scalar gate sigmoid(se_g . x). Per slot, a wave waits
-//   for the slot's arrivals, reads the slot's h pairs until every tag is
-//   this launch's (an arrival can overtake the stores it counts), converts h
-//   to bf16 hi/lo x-operands and forms the down products of its rows. The
+//   computes the shared-expert scalar gate sigmoid(se_g . x). While A runs,
+//   each wave turns its down codes into exact f16 pairs. Per slot, a wave
+//   waits for the slot's arrivals, reads the slot's h pairs until every tag
+//   is this launch's (an arrival can overtake the stores it counts) and forms
+//   the down products of its rows, one f16 x f32 fma per code. The
 //   block then combines them per row in rank order:
 //   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
@@ -131,6 +132,50 @@ __device__ __forceinline__ void load_down(uint32_t (&w)[BITS], uint32_t &scr, ui
   const size_t p = (size_t)e * bd.p_stride + (size_t)dd * bd.m.ng + ll / (bd.m.gs >> 5);
   scr = bd.m.sc[p];
   bir = bd.m.bi[p];
+}
+
+// The down products of one slot from f32 h and packed codes converted at
+// use (the instantiations without room for pre-converted codes): h goes
+// through the wave's LDS row to chunk-per-lane, then
+// sum_k (code_k * sc + bi) * h_k = sc * sum_k code_k h_k + bi * sum_k h_k.
+template <int BITS, int PASSES, int RPP, int LANESB, int VPL, int SLOTS>
+__device__ __forceinline__ void down_slot_f32(const MoeArgs &a, int s, bool sh, int d0, int lb, int rsub,
+                                              float *row, const float (&hv)[VPL],
+                                              const uint32_t (&wv)[PASSES][BITS], const uint32_t (&rsc)[PASSES],
+                                              const uint32_t (&rbi)[PASSES], float (&s_y)[RPP * PASSES][SLOTS]) {
+  const int lane = threadIdx.x & 63;
+  const int K = sh ? a.sinter : a.inter;
+#pragma unroll
+  for (int v = 0; v < VPL; v += 4)
+    *reinterpret_cast<float4 *>(row + VPL * lane + v) = make_float4(hv[v], hv[v + 1], hv[v + 2], hv[v + 3]);
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  float xf[32];
+#pragma unroll
+  for (int v = 0; v < 32; v += 4) {
+    const float4 f = *reinterpret_cast<const float4 *>(row + 32 * lb + v);
+    xf[v] = f.x; xf[v + 1] = f.y; xf[v + 2] = f.z; xf[v + 3] = f.w;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  float xt[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) xt[v] = xf[v] + xf[v + 16];
+#pragma unroll
+  for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+    for (int v = 0; v < w; ++v) xt[v] += xt[v + w];
+  const float xs = xt[0];
+  const DevBank &bd = sh ? a.sdown : a.down;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const bool live = d0 + p * RPP + rsub < a.D && lb < (K >> 5);
+    const float sc = live ? aux_to_f32(rsc[p], bd.m.fp16) : 0.f;
+    const float bi = live ? aux_to_f32(rbi[p], bd.m.fp16) : 0.f;
+    float v = fmaf(sc, codes_dot<BITS>(wv[p], xf), bi * xs);
+    v = group_sum_f32<LANESB>(v);
+    if (lb == 0) s_y[p * RPP + rsub][s] = v;
+  }
 }
 
 // VPL consecutive (value, tag) pairs from byte offset off; positions at or
@@ -542,6 +587,34 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     if (lane == 0) s_gsig = gsig;
   }
 
+  // While the gate/up blocks run, turn this wave's down codes into exact f16
+  // pairs and its scale/bias words into f32, so that after the hand-off each
+  // code costs one v_fma_mix_f32 (f16 code x f32 h + f32). The empty asm
+  // operands keep the conversion here, ahead of the wait (the compiler would
+  // otherwise sink it to the first use, behind the hand-off).
+  // (Not with 32-lane down rows at one x chunk per lane: their h pairs
+  // already fill the 128-register budget of that instantiation.)
+  constexpr bool kPreF16 = !(LANESB == 32 && CPLA == 1);
+  uint32_t cp[kSlotsPerWave][PASSES][16];
+  float fsc[kSlotsPerWave][PASSES], fbi[kSlotsPerWave][PASSES];
+#pragma unroll
+  for (int t = 0; t < kSlotsPerWave && kPreF16; ++t) {
+    const int s = wave + t * kWaves;
+    const bool sh = has_shared && s == g.k;
+    const int K = sh ? a.sinter : a.inter;
+    const int fp16 = sh ? a.sdown.m.fp16 : a.down.m.fp16;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const bool live = s < g.slots && d0 + p * RPP + rsub < a.D && lb < (K >> 5);
+      fsc[t][p] = live ? aux_to_f32(rsc[t][p], fp16) : 0.f;
+      fbi[t][p] = live ? aux_to_f32(rbi[t][p], fp16) : 0.f;
+      codes_to_f16<BITS>(wv[t][p], cp[t][p]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(cp[t][p][i]));
+      asm volatile("" : "+v"(fsc[t][p]), "+v"(fbi[t][p]));
+    }
+  }
+
   // Wait for the arrivals of this wave's slots (lane 4 t + q polls
   // sub-counter q of slot wave + 8 t), read their tagged h together until
   // every tag is this launch's, then form the down products slot by slot.
@@ -602,41 +675,49 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 #pragma unroll
   for (int t = 0; t < kSlotsPerWave; ++t) {
     const int s = wave + t * kWaves;
-    if (s < g.slots && !to) {
-      const bool sh = has_shared && s == g.k;
-      const int K = sh ? a.sinter : a.inter;
+    if (s < g.slots && !to && !kPreF16) {
+      down_slot_f32<BITS, PASSES, RPP, LANESB, VPL>(a, s, has_shared && s == g.k, d0, lb, rsub, s_hv[wave],
+                                                  hv[t], wv[t], rsc[t], rbi[t], s_y);
+    } else if (s < g.slots && !to) {
       // through this wave's LDS row to chunk-per-lane (h of chunk lb)
       float *row = s_hv[wave];
 #pragma unroll
       for (int v = 0; v < VPL; v += 4)
         *reinterpret_cast<float4 *>(row + VPL * lane + v) =
             make_float4(hv[t][v], hv[t][v + 1], hv[t][v + 2], hv[t][v + 3]);
+      // sum of h over chunk c, which lanes LPC c .. LPC c + LPC - 1 hold
+      constexpr int LPC = 32 / VPL;
+      static_assert(LPC == 2 || LPC == 4, "h pairs per lane");
+      float hs = 0.f;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) hs += hv[t][v];
+      hs += __shfl_xor(hs, 1);
+      if constexpr (LPC == 4) hs += __shfl_xor(hs, 2);
+      const float xs = __shfl(hs, LPC * lb);
       __builtin_amdgcn_wave_barrier();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      float xf[32];
+      float acc[PASSES];
 #pragma unroll
-      for (int v = 0; v < 32; v += 4) {
-        const float4 f = *reinterpret_cast<const float4 *>(row + 32 * lb + v);
-        xf[v] = f.x; xf[v + 1] = f.y; xf[v + 2] = f.z; xf[v + 3] = f.w;
+      for (int p = 0; p < PASSES; ++p) acc[p] = 0.f;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float4 f = *reinterpret_cast<const float4 *>(row + 32 * lb + 4 * v);
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+          const half2v c0 = __builtin_bit_cast(half2v, cp[t][p][2 * v]);
+          const half2v c1 = __builtin_bit_cast(half2v, cp[t][p][2 * v + 1]);
+          acc[p] = fmaf((float)c0.x, f.x, acc[p]);
+          acc[p] = fmaf((float)c0.y, f.y, acc[p]);
+          acc[p] = fmaf((float)c1.x, f.z, acc[p]);
+          acc[p] = fmaf((float)c1.y, f.w, acc[p]);
+        }
       }
       __builtin_amdgcn_wave_barrier();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      float xt[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) xt[v] = xf[v] + xf[v + 16];
-#pragma unroll
-      for (int w = 8; w > 0; w >>= 1)
-#pragma unroll
-        for (int v = 0; v < w; ++v) xt[v] += xt[v + w];
-      const float xs = xt[0];
-      const DevBank &bd = sh ? a.sdown : a.down;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
-        const bool live = d0 + p * RPP + rsub < a.D && lb < (K >> 5);
-        const float sc = live ? aux_to_f32(rsc[t][p], bd.m.fp16) : 0.f;
-        const float bi = live ? aux_to_f32(rbi[t][p], bd.m.fp16) : 0.f;
         // sum_k (code_k * sc + bi) * h_k = sc * sum_k code_k h_k + bi * sum_k h_k
-        float v = fmaf(sc, codes_dot<BITS>(wv[t][p], xf), bi * xs);
+        float v = fmaf(fsc[t][p], acc[p], fbi[t][p] * xs);
         v = group_sum_f32<LANESB>(v);
         if (lb == 0) s_y[p * RPP + rsub][s] = v;
       }
