@@ -42,34 +42,43 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build logan-hip)")
 
 
-def _compile(src: Path) -> Path:
-    out = OBJ / (src.stem + ".o")
-    cmd = [hipcc(), *HIPFLAGS, "-I", str(INCLUDE), "-c", str(src), "-o", str(out)]
+def _compile(src: Path, obj_dir: Path = OBJ, defines: tuple = ()) -> Path:
+    out = obj_dir / (src.stem + ".o")
+    cmd = [hipcc(), *HIPFLAGS, *(f"-D{d}" for d in defines), "-I", str(INCLUDE), "-c", str(src),
+           "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")
     return out
 
 
-def build(verbose: bool = False) -> Path:
-    OBJ.mkdir(exist_ok=True)
+# The stage-timeline variant of the library (moe_fused.hip built with
+# LOGAN_HIP_TIMELINE; see logan_amd/timeline.py). Never loaded unless named.
+TIMELINE_OBJ = PKG / "_build_tl"
+TIMELINE_LIB = PKG / "liblogan_hip_timeline.so"
+
+
+def build(verbose: bool = False, timeline: bool = False) -> Path:
+    obj_dir, lib, defines = (TIMELINE_OBJ, TIMELINE_LIB, ("LOGAN_HIP_TIMELINE",)) if timeline \
+        else (OBJ, LIB, ())
+    obj_dir.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError("no HIP sources found")
     jobs = min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, obj_dir, defines), srcs))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, timeline="--timeline" in sys.argv[1:])
     sys.exit(0)

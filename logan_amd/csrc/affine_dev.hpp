@@ -273,25 +273,38 @@ __device__ __forceinline__ float chunk_fold(float acc, float sc, float bi, float
 // bytes modulo 16 (4-bit: 16 B, 5-bit: 4 B, 6-bit: 8 B, 8-bit: 32 B).
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x4_a16 __attribute__((ext_vector_type(4)));
 
-template <int BITS>
+// NT: non-temporal loads (the nt cache policy), for weight streams that are
+// read once per launch: they then do not displace from L2 what the launch
+// reads again (activations, routing inputs, hand-off data, its own code).
+template <typename T, bool NT>
+__device__ __forceinline__ T ld_stream(const T *p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+template <int BITS, bool NT = false>
 __device__ __forceinline__ void load_chunk(uint32_t (&w)[BITS], const uint8_t *p) {
   if constexpr (BITS == 4) {
-    const uint4 v = *reinterpret_cast<const uint4 *>(p);
-    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    const u32x4_a16 v = ld_stream<u32x4_a16, NT>(reinterpret_cast<const u32x4_a16 *>(p));
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
   } else if constexpr (BITS == 8) {
-    const uint4 v0 = reinterpret_cast<const uint4 *>(p)[0];
-    const uint4 v1 = reinterpret_cast<const uint4 *>(p)[1];
-    w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
-    w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+    const u32x4_a16 v0 = ld_stream<u32x4_a16, NT>(reinterpret_cast<const u32x4_a16 *>(p));
+    const u32x4_a16 v1 = ld_stream<u32x4_a16, NT>(reinterpret_cast<const u32x4_a16 *>(p + 16));
+    w[0] = v0[0]; w[1] = v0[1]; w[2] = v0[2]; w[3] = v0[3];
+    w[4] = v1[0]; w[5] = v1[1]; w[6] = v1[2]; w[7] = v1[3];
   } else if constexpr (BITS == 6) {
-    const uint2 *q = reinterpret_cast<const uint2 *>(p);
-    const uint2 a = q[0], b = q[1], c = q[2];
-    w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+    const u32x2_a4 *q = reinterpret_cast<const u32x2_a4 *>(p);
+    const u32x2_a4 a = ld_stream<u32x2_a4, NT>(q), b = ld_stream<u32x2_a4, NT>(q + 1),
+                   c = ld_stream<u32x2_a4, NT>(q + 2);
+    w[0] = a[0]; w[1] = a[1]; w[2] = b[0]; w[3] = b[1]; w[4] = c[0]; w[5] = c[1];
   } else {
-    const u32x4_a4 a = *reinterpret_cast<const u32x4_a4 *>(p);
+    const u32x4_a4 a = ld_stream<u32x4_a4, NT>(reinterpret_cast<const u32x4_a4 *>(p));
     w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
-    w[4] = *reinterpret_cast<const uint32_t *>(p + 16);
+    w[4] = ld_stream<uint32_t, NT>(reinterpret_cast<const uint32_t *>(p + 16));
   }
 }
 

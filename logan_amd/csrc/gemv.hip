@@ -6,7 +6,9 @@
 //    operand of the lane's chunks is built once (bf16 pairs in the unpack
 //    order) and kept in VGPRs for every row the team visits. U rows are
 //    loaded before any is consumed to keep several 128-bit loads in flight
-//    per lane. The team sum is a butterfly over LANES lanes.
+//    per lane. The team sum is a butterfly over LANES lanes. For rows of up
+//    to 64 chunks the weights and their scale/bias words are read with
+//    non-temporal loads (read once per launch; x and the code stay in L2).
 //  * gemv_generic_kernel: any bits/group size, f32 activations, f32 output,
 //    per-element exact dequantisation (code*scale+bias, as
 //    logan-qwen4/src/lib.rs:3752-3762); serves the f32 host ABI and shapes
@@ -59,6 +61,10 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   UnpackConsts kc;
   kc.init();
   __shared__ float s_part[SPLIT > 1 ? TEAMS * U * MT : 1];
+  // non-temporal weight loads for the short-row shapes (config 1: 3.39 ->
+  // 3.30 us); the long-row 8-bit shapes measured slower with them (config-2
+  // layer at M = 1: 52 -> 62 us)
+  constexpr bool NT = SPLIT == 1 && CPL == 1;
 
   // Loads are branch-free (row and chunk clamped into the matrix, x rows
   // clamped to M) and issued in the order they are needed: x, the raw
@@ -115,8 +121,8 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const size_t pi = (size_t)row * a.ng + gidx[j];
-        scr[u][j] = scp[pi];
-        bir[u][j] = bip[pi];
+        scr[u][j] = ld_stream<uint16_t, NT>(scp + pi);
+        bir[u][j] = ld_stream<uint16_t, NT>(bip + pi);
       }
     }
 #pragma unroll
@@ -125,7 +131,7 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
       const uint8_t *wp = (SW && (u & 1)) ? a.w2 : a.w;
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        load_chunk<BITS>(wv[u][j], wp + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
+        load_chunk<BITS, NT>(wv[u][j], wp + (size_t)row * a.row_bytes + (size_t)cc[j] * (4 * BITS));
     }
     // keep every load above issued before any of their consumers
     __builtin_amdgcn_sched_barrier(0);

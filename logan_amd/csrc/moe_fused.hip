@@ -22,6 +22,11 @@
 //   out[d] = sum_{r<k} w_r * (down_r . h_r)[d] + gs * (down_shared . h_shared)[d]
 //   (logan-qwen4/src/lib.rs:8692-8711, :7597-7759).
 //
+// Weights and their scale/bias words are read with non-temporal loads: they
+// are read once per launch, and kept out of L2 they do not displace what the
+// launch reads again (logits, x, the hand-off lines, its code): 14.1 -> 13.3
+// us per config-3 layer.
+//
 // Every wave computes the route itself from the router logits, bf16 or f32
 // (top-k with the key (logit desc, index asc): per-lane sorted keys, k rounds
 // of a DPP wave max, and the reference's probability arithmetic instead where
@@ -98,6 +103,49 @@ __device__ __forceinline__ void st_agent(uint32_t *p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------------- stage timeline
+// A build with -DLOGAN_HIP_TIMELINE records, per block, s_memrealtime stamps
+// (100 MHz) of its stages for the last two launches (slot = launch number &
+// 1), read back with logan_hip_fused_timeline(). A blocks: start, route
+// known, gate/up weights consumed (wave 0), arrival added (last wave). B
+// blocks: start, route known, then the latest wave's arrivals seen, h read
+// and down products formed, and the end. Default builds contain none of it.
+#ifdef LOGAN_HIP_TIMELINE
+// one 128-byte line per block (blocks sharing a line slowed the launch by ~5 us)
+constexpr int kTlBlocks = 1024, kTlStamps = 16;
+__device__ unsigned long long g_fused_tl[2][kTlBlocks][kTlStamps];
+#define TL_NOW() __builtin_amdgcn_s_memrealtime()
+#define TL_PUT(lid, i, v)                                                      \
+  do {                                                                         \
+    if (blockIdx.x < (unsigned)kTlBlocks) g_fused_tl[(lid) & 1][blockIdx.x][i] = (v); \
+  } while (0)
+// stamps go to LDS at once (held in registers they would spill)
+#define TL_LDS                                 \
+  __shared__ unsigned long long s_tl[3][kWaves]; \
+  __shared__ unsigned long long s_tlb[3]
+#define TL_BLOCK(i)                              \
+  do {                                           \
+    if (threadIdx.x == 0) s_tlb[i] = TL_NOW();   \
+  } while (0)
+#define TL_WAVE(i) \
+  do {             \
+    if (lane == 0) s_tl[i][wave] = TL_NOW(); \
+  } while (0)
+#define TL_PUT_WAVES(lid, i, j)                                              \
+  do {                                                                       \
+    unsigned long long m_ = 0;                                               \
+    for (int w_ = 0; w_ < kWaves; ++w_) m_ = s_tl[j][w_] > m_ ? s_tl[j][w_] : m_; \
+    TL_PUT(lid, i, m_);                                                      \
+  } while (0)
+#else
+#define TL_NOW() 0ull
+#define TL_PUT(lid, i, v) ((void)0)
+#define TL_LDS
+#define TL_BLOCK(i) ((void)0)
+#define TL_WAVE(i) ((void)0)
+#define TL_PUT_WAVES(lid, i, j) ((void)0)
+#endif
+
 // ---------------------------------------------------------------- kernel
 
 struct FusedGeom {
@@ -127,11 +175,11 @@ template <int BITS>
 __device__ __forceinline__ void load_down(uint32_t (&w)[BITS], uint32_t &scr, uint32_t &bir,
                                           const DevBank &bd, int e, int d, int lb, bool live) {
   const int dd = live ? d : 0, ll = live ? lb : 0;
-  load_chunk<BITS>(w, bd.m.w + (size_t)e * bd.w_stride + (size_t)dd * bd.m.row_bytes +
-                          (size_t)ll * (4 * BITS));
+  load_chunk<BITS, true>(w, bd.m.w + (size_t)e * bd.w_stride + (size_t)dd * bd.m.row_bytes +
+                                (size_t)ll * (4 * BITS));
   const size_t p = (size_t)e * bd.p_stride + (size_t)dd * bd.m.ng + ll / (bd.m.gs >> 5);
-  scr = bd.m.sc[p];
-  bir = bd.m.bi[p];
+  scr = ld_stream<uint16_t, true>(bd.m.sc + p);
+  bir = ld_stream<uint16_t, true>(bd.m.bi + p);
 }
 
 // The down products of one slot from f32 h and packed codes converted at
@@ -252,6 +300,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __shared__ uint32_t s_left;  // A: waves of the block still running
   __shared__ uint32_t s_lid;   // launch number
   __shared__ float s_gsig;
+  TL_LDS;
 
   const int lane = threadIdx.x & 63;
   // wave-uniform for the compiler too, so per-slot bank selection and
@@ -266,6 +315,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 
   if ((int)blockIdx.x < g.nA_blocks) {
     // ------------------------------------------------------------ phase A
+    TL_BLOCK(0);
     const int item = blockIdx.x * kWaves + wave;
     const bool shared = item >= g.k * g.wpr;
     const int slot = shared ? g.k : item / g.wpr;
@@ -346,6 +396,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     __syncthreads();
     const int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
     const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
+    TL_BLOCK(1);
     // bank fields copied once (scalar) rather than re-read per use
     const DevMat gm = shared ? a.sgate.m : a.gate.m;
     const DevMat um = shared ? a.sup.m : a.up.m;
@@ -373,18 +424,18 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       for (int i = 0; i < CPLA; ++i) {
         const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
         const size_t p = (size_t)j * gm.ng + (c >> gsh);
-        rsg[u][i] = gsc[p];
-        rbg[u][i] = gbi[p];
-        rsu[u][i] = usc[p];
-        rbu[u][i] = ubi[p];
+        rsg[u][i] = ld_stream<uint16_t, true>(gsc + p);
+        rbg[u][i] = ld_stream<uint16_t, true>(gbi + p);
+        rsu[u][i] = ld_stream<uint16_t, true>(usc + p);
+        rbu[u][i] = ld_stream<uint16_t, true>(ubi + p);
       }
 #pragma unroll
     for (int u = 0; u < UA; ++u)
 #pragma unroll
       for (int i = 0; i < CPLA; ++i) {
         const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-        load_chunk<BITS>(wg[u][i], gw + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
-        load_chunk<BITS>(wu[u][i], uw + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS, true>(wg[u][i], gw + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+        load_chunk<BITS, true>(wu[u][i], uw + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
       }
     const uint32_t tag = launch_tag(lid);
     // keep every load above issued before any of their consumers
@@ -423,6 +474,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
     // wave totals: lane row r (r = lane / 16) ends up with row j0 + r's h
     // (logan-qwen4/src/lib.rs:8807-8809: h = silu(gate) * up)
+    TL_BLOCK(2);
     float hval;
     if constexpr (UA == 4) {
       const float gv = wave_reduce4(pg[0], pg[1], pg[2], pg[3]);
@@ -443,7 +495,13 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
     // The block's last wave to get here adds the block's arrival, right
     // behind the stores and without waiting for them (B checks the tags).
+    if (threadIdx.x == 0) {
+      TL_PUT(lid, 0, s_tlb[0]);
+      TL_PUT(lid, 1, s_tlb[1]);
+      TL_PUT(lid, 2, s_tlb[2]);
+    }
     if (lane == 0 && atomicSub(&s_left, 1u) == 1u) {
+      TL_PUT(lid, 3, TL_NOW());
       const int first = shared ? g.k * g.wpr / kWaves : slot * (g.wpr / kWaves);
       __hip_atomic_fetch_add(&g_fused_sync.ctr[lid & 1][slot][(blockIdx.x - first) % kSubCtrs][0], 1u,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -453,6 +511,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 
   // -------------------------------------------------------------- phase B
   // lane: chunk lb of row rsub within each pass; wave: slots wave, wave + 8
+  TL_BLOCK(0);
   const int bb = blockIdx.x - g.nA_blocks;
   const int lb = lane % LANESB;
   const int rsub = lane / LANESB;
@@ -526,6 +585,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __syncthreads();
   const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
   const uint32_t tag = launch_tag(lid);
+  TL_BLOCK(1);
   // zero the arrival counters the next launch uses (the previous launch,
   // their last user, has ended): counter j by block j mod nB
   if (wave == 0) {
@@ -638,6 +698,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
   }
+  TL_WAVE(0);
   // lane covers h[VPL*lane .. VPL*lane + VPL) of each slot: first through
   // L2, then (stale or not yet landed) with device-scope loads
   const int slice = (int)(lid % kSlices);
@@ -670,6 +731,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       ok = read_pairs<VPL, kCpolSc1>(hrsrc, off, K - VPL * lane, tag, hv[t]) && ok;
     }
   }
+  TL_WAVE(1);
   if (to && lane == 0)
     __hip_atomic_fetch_or(&g_fused_sync.error[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
@@ -724,7 +786,15 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
   }
   if (lane == 0) s_to[wave] = to;
+  TL_WAVE(2);
   __syncthreads();
+  if (threadIdx.x == 0) {
+    TL_PUT(lid, 0, s_tlb[0]);
+    TL_PUT(lid, 1, s_tlb[1]);
+    TL_PUT_WAVES(lid, 2, 0);
+    TL_PUT_WAVES(lid, 3, 1);
+    TL_PUT_WAVES(lid, 4, 2);
+  }
 
   // rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711) by the first ROWS_B threads
   if ((int)threadIdx.x < ROWS_B) {
@@ -746,6 +816,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
         reinterpret_cast<uint16_t *>(a.out)[dd] = (uint16_t)f32_to_bf16_rne(o);
     }
   }
+  if (threadIdx.x == 0) TL_PUT(lid, 5, TL_NOW());
 
 }
 
@@ -869,3 +940,12 @@ uint32_t moe_fused_sync_errors() {
 }
 
 }  // namespace lh
+
+#ifdef LOGAN_HIP_TIMELINE
+// [2][1024][16] u64 stamps of the timeline build (see above); 0 on success
+extern "C" int logan_hip_fused_timeline(unsigned long long *out, size_t bytes) {
+  if (bytes < sizeof(lh::g_fused_tl)) return -1;
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(lh::g_fused_tl), sizeof(lh::g_fused_tl), 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
