@@ -278,12 +278,28 @@ typedef uint32_t u32x4_a16 __attribute__((ext_vector_type(4)));
 // NT: non-temporal loads (the nt cache policy), for weight streams that are
 // read once per launch: they then do not displace from L2 what the launch
 // reads again (activations, routing inputs, hand-off data, its own code).
+// (the builtin takes scalars and clang vectors: HIP's uint2 / uint4 structs
+// are loaded as the native vector of the same size)
+template <typename T>
+struct NtNative {
+  using type = T;
+};
+template <>
+struct NtNative<uint2> {
+  typedef uint32_t type __attribute__((ext_vector_type(2)));
+};
+template <>
+struct NtNative<uint4> {
+  typedef uint32_t type __attribute__((ext_vector_type(4)));
+};
 template <typename T, bool NT>
 __device__ __forceinline__ T ld_stream(const T *p) {
-  if constexpr (NT)
-    return __builtin_nontemporal_load(p);
-  else
+  if constexpr (NT) {
+    using V = typename NtNative<T>::type;
+    return __builtin_bit_cast(T, __builtin_nontemporal_load(reinterpret_cast<const V *>(p)));
+  } else {
     return *p;
+  }
 }
 
 template <int BITS, bool NT = false>
@@ -297,12 +313,25 @@ __device__ __forceinline__ void load_chunk(uint32_t (&w)[BITS], const uint8_t *p
     w[0] = v0[0]; w[1] = v0[1]; w[2] = v0[2]; w[3] = v0[3];
     w[4] = v1[0]; w[5] = v1[1]; w[6] = v1[2]; w[7] = v1[3];
   } else if constexpr (BITS == 6) {
+    // (the under-aligned vector types go to the builtin directly: as a
+    // template argument their alignment attribute would be dropped)
     const u32x2_a4 *q = reinterpret_cast<const u32x2_a4 *>(p);
-    const u32x2_a4 a = ld_stream<u32x2_a4, NT>(q), b = ld_stream<u32x2_a4, NT>(q + 1),
-                   c = ld_stream<u32x2_a4, NT>(q + 2);
+    u32x2_a4 a, b, c;
+    if constexpr (NT) {
+      a = __builtin_nontemporal_load(q);
+      b = __builtin_nontemporal_load(q + 1);
+      c = __builtin_nontemporal_load(q + 2);
+    } else {
+      a = q[0]; b = q[1]; c = q[2];
+    }
     w[0] = a[0]; w[1] = a[1]; w[2] = b[0]; w[3] = b[1]; w[4] = c[0]; w[5] = c[1];
   } else {
-    const u32x4_a4 a = ld_stream<u32x4_a4, NT>(reinterpret_cast<const u32x4_a4 *>(p));
+    const u32x4_a4 *q = reinterpret_cast<const u32x4_a4 *>(p);
+    u32x4_a4 a;
+    if constexpr (NT)
+      a = __builtin_nontemporal_load(q);
+    else
+      a = *q;
     w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
     w[4] = ld_stream<uint32_t, NT>(reinterpret_cast<const uint32_t *>(p + 16));
   }

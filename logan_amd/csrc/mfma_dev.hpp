@@ -158,17 +158,19 @@ struct MfmaStep {
     }
   }
   // the lane's 16 codes [k, k + 16) of a row (k a multiple of 16)
+  // (NT: non-temporal loads, for weights read once per launch)
+  template <bool NT = false>
   static __device__ __forceinline__ void load_raw(SkRaw<BITS> &r, const uint8_t *row, int k) {
     if constexpr (BITS == 4) {
-      r.v = *reinterpret_cast<const uint2 *>(row + (k >> 1));
+      r.v = ld_stream<uint2, NT>(reinterpret_cast<const uint2 *>(row + (k >> 1)));
     } else if constexpr (BITS == 8) {
-      r.v = *reinterpret_cast<const uint4 *>(row + k);
+      r.v = ld_stream<uint4, NT>(reinterpret_cast<const uint4 *>(row + k));
     } else {
       // dword holding the first code: 5-bit (k * 5) / 32, 6-bit (k * 6) / 32
       const uint32_t *p = reinterpret_cast<const uint32_t *>(row) + ((k * BITS) >> 5);
-      r.w[0] = p[0];
-      r.w[1] = p[1];
-      r.w[2] = p[2];
+      r.w[0] = ld_stream<uint32_t, NT>(p);
+      r.w[1] = ld_stream<uint32_t, NT>(p + 1);
+      r.w[2] = ld_stream<uint32_t, NT>(p + 2);
     }
   }
   // y += s' D + b' X: D = X + 2^(s-7) sum(c x) for codes at mantissa bit s

@@ -497,7 +497,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   constexpr int kHq = LANES / 8;     // float4 of one h row per thread (K <= 32 * LANES)
   constexpr int RPP = 256 / LANES;  // rows per pass of the block
   constexpr int PASSES = down_rows(BITS, LANES) / RPP;
-  const int lane = threadIdx.x & 63;
   const int lb = threadIdx.x % LANES;
   const int rsub = threadIdx.x / LANES;
   // the shared expert's sub-groups first, then the routed ones
