@@ -694,6 +694,236 @@ __global__ __launch_bounds__(512) void affine_qmm256_kernel(QmmMulti p, int mtil
   }
 }
 
+// ---------------------------------------------------------------------------
+// The same 256 x 128 tiles with 16 waves (1024 threads): waves 8 (m) x 2 (n),
+// each a 32 x 64 tile (1 x 2 v_mfma_f32_32x32x16_bf16 tiles), each thread
+// dequantising 8 codes and staging 2 granules of x per step. Same LDS layout,
+// tile order and one-barrier-per-step pipeline as affine_qmm256_kernel, at
+// <= 128 registers so that four waves share a SIMD instead of two: the step's
+// chain of LDS reads -> MFMAs and loads -> dequantisation -> LDS writes ->
+// barrier then overlaps across twice the waves.
+template <int BITS>
+struct Q8Raw {
+  uint32_t w[BITS == 4 ? 1 : 2];
+  uint32_t s, b;
+};
+
+// 8 codes [k, k + 8) of a row (k a multiple of 8) and their group's scale
+// and bias
+template <int BITS>
+__device__ __forceinline__ void q8_load(Q8Raw<BITS> &r, __amdgpu_buffer_rsrc_t wr,
+                                        __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t br,
+                                        int rowoff, int poff, int k) {
+  if constexpr (BITS == 4) {
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, rowoff + (k >> 1), 0, 0);
+  } else if constexpr (BITS == 8) {
+    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, rowoff + k, 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  } else {
+    // the dword holding the first code; the 8 codes end within the next one
+    const uint2 v = __builtin_bit_cast(
+        uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, rowoff + 4 * ((k * BITS) >> 5), 0, 0));
+    r.w[0] = v.x;
+    r.w[1] = v.y;
+  }
+  r.s = __builtin_amdgcn_raw_buffer_load_b16(sr, poff, 0, 0);
+  r.b = __builtin_amdgcn_raw_buffer_load_b16(br, poff, 0, 0);
+}
+
+// bf16(code * s + b) of the 8 codes, packed in pairs (code order); sh is the
+// bit of the first code within r.w[0] (5/6-bit)
+template <int BITS>
+__device__ __forceinline__ void q8_dequant(const Q8Raw<BITS> &r, int sh, bool fp16, uint32_t (&pk)[4]) {
+  const float s = aux_to_f32_sel(r.s, fp16), b = aux_to_f32_sel(r.b, fp16);
+  float f[8];
+  if constexpr (BITS == 4) {
+    const uint32_t lo = r.w[0] & 0x0F0F0F0Fu, hi = (r.w[0] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = (float)((lo >> (8 * i)) & 255u);
+      f[2 * i + 1] = (float)((hi >> (8 * i)) & 255u);
+    }
+  } else if constexpr (BITS == 8) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[4 * d + i] = (float)((r.w[d] >> (8 * i)) & 255u);
+  } else {
+    const uint32_t win[2] = {__builtin_amdgcn_alignbit(r.w[1], r.w[0], sh), r.w[1] >> sh};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int bit = j * BITS, i = bit >> 5, o = bit & 31;
+      uint32_t v = win[i] >> o;
+      if (o + BITS > 32) v |= win[i + 1] << (32 - o);
+      f[j] = (float)(v & ((1u << BITS) - 1u));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf16x2 v;
+    v[0] = (__bf16)fmaf(f[2 * j], s, b);
+    v[1] = (__bf16)fmaf(f[2 * j + 1], s, b);
+    pk[j] = __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(1024) void affine_qmm256w_kernel(QmmMulti p, int mtiles, int ntiles,
+                                                              int ksteps, int slot) {
+  __shared__ __align__(16) uint16_t sX[2][kQ3M * kQ3Ld];
+  __shared__ __align__(16) uint16_t sW[2][kQ3N * kQ3Ld];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int L = blockIdx.x;
+  const int grp = L / (8 * mtiles), rem = L % (8 * mtiles);
+  const int nt = grp * 8 + rem % 8, mt = rem / 8;
+  if (nt >= ntiles) return;
+  int mi = 0;
+#pragma unroll
+  for (int t = 1; t < kQMultiMax; ++t) mi = t < p.n && nt >= p.tile_start[t] ? t : mi;
+  mi = __builtin_amdgcn_readfirstlane(mi);
+  const QmmMat &mat = p.m[mi];
+  const int bm0 = mt * kQ3M, bn0 = (nt - p.tile_start[mi]) * kQ3N;
+  const int N = mat.N;
+
+  // dequantising role: row wr of the W tile, codes [8 q, 8 q + 8) of each step
+  const int wr = tid >> 3, q = tid & 7;
+  const int nrow = min(bn0 + wr, N - 1);
+  const __amdgpu_buffer_rsrc_t wrs = q3_rsrc(mat.w, (long long)N * mat.row_bytes);
+  const __amdgpu_buffer_rsrc_t srs = q3_rsrc(mat.sc, (long long)N * mat.ng * 2);
+  const __amdgpu_buffer_rsrc_t brs = q3_rsrc(mat.bi, (long long)N * mat.ng * 2);
+  const int rowoff = (int)((long long)nrow * mat.row_bytes);
+  const int prow = nrow * mat.ng;
+  const int gsh = __builtin_ctz(p.gs);
+  // first code's bit within its dword: (8 q * BITS) mod 32 (k0 is a multiple of 64)
+  const int shq = (8 * q * BITS) & 31;
+  const int wdst = wr * kQ3Ld + 8 * q;
+
+  // x staging role: 16-byte granules g = 1024 i + tid (i < 2) of the 256 x 8 tile
+  const uint16_t *xsrc[2];
+  int xdst[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int g = 1024 * i + tid;
+    const int r = g >> 3, lg = g & 7;
+    xsrc[i] = p.x + (size_t)min(bm0 + r, p.M - 1) * p.x_stride + 8 * lg;
+    xdst[i] = r * kQ3Ld + 8 * lg;
+  }
+
+  const int z = blockIdx.y;
+  const int kb = z * ksteps * 64;
+  const int nst = (min(p.K, kb + ksteps * 64) - kb) >> 6;
+
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct Set {
+    u32x4 x[2];
+    Q8Raw<BITS> w;
+  };
+  auto load = [&](int s, Set &r) {
+    const int k0 = kb + 64 * s;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r.x[i] = *reinterpret_cast<const u32x4 *>(xsrc[i] + k0);
+    const int k = k0 + 8 * q;
+    q8_load<BITS>(r.w, wrs, srs, brs, rowoff, 2 * (prow + (k >> gsh)), k);
+  };
+  auto stage = [&](const Set &r, int st) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4 *>(sX[st] + xdst[i]) = r.x[i];
+    uint32_t pk[4];
+    q8_dequant<BITS>(r.w, shq, p.fp16 != 0, pk);
+    *reinterpret_cast<uint4 *>(sW[st] + wdst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  };
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) acc[j] = f32x16{};
+  auto mfma = [&](int st) {
+    const uint16_t *xa = sX[st] + (wm * 32 + l32) * kQ3Ld;
+    const uint16_t *wb = sW[st] + (wn * 64 + l32) * kQ3Ld;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int g = 16 * ks + 8 * half;
+      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(xa + g);
+      bf16x8 b[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const bf16x8 *>(wb + 32 * kQ3Ld * j + g);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[j], acc[j], 0, 0, 0);
+    }
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // as affine_qmm256_kernel: step s's operands pass through a register set
+  // loaded two steps earlier and LDS stage s & 1 written one step ahead
+  Set ra, rb;
+  load(0, ra);
+  if (nst > 1) load(1, rb);
+  stage(ra, 0);
+  if (nst > 2) load(2, ra);
+  int s = 0;
+  for (; s + 4 < nst; s += 2) {
+    barrier();
+    mfma(0);
+    stage(rb, 1);
+    load(s + 3, rb);
+    barrier();
+    mfma(1);
+    stage(ra, 0);
+    load(s + 4, ra);
+  }
+  if (s < nst) {
+    barrier();
+    mfma(0);
+    if (s + 1 < nst) stage(rb, 1);
+    if (s + 3 < nst) load(s + 3, rb);
+  }
+  if (s + 1 < nst) {
+    barrier();
+    mfma(1);
+    if (s + 2 < nst) stage(ra, 0);
+    if (s + 4 < nst) load(s + 4, ra);
+  }
+  if (s + 2 < nst) {
+    barrier();
+    mfma(0);
+    if (s + 3 < nst) stage(rb, 1);
+  }
+  if (s + 3 < nst) {
+    barrier();
+    mfma(1);
+  }
+
+  // element e of tile j: row 8 (e / 4) + 4 half + e % 4 of the wave's 32,
+  // column 32 j + l32 of its 64; lanes 0-31 store 32 consecutive columns
+  const bool split = slot >= 0;
+  float *part = split ? g_qmm_part + (size_t)slot * kQSlotFloats + (size_t)z * p.M * p.part_N + mat.col0
+                      : nullptr;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = bn0 + wn * 64 + 32 * j + l32;
+    if (n >= N) continue;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = bm0 + wm * 32 + 8 * (e / 4) + 4 * half + (e % 4);
+      if (m >= p.M) continue;
+      if (split)
+        part[(size_t)m * p.part_N + n] = acc[j][e];
+      else if (p.y_bf16)
+        reinterpret_cast<__bf16 *>(mat.y)[(size_t)m * mat.y_stride + n] = (__bf16)acc[j][e];
+      else
+        reinterpret_cast<float *>(mat.y)[(size_t)m * mat.y_stride + n] = acc[j][e];
+    }
+  }
+}
+
 bool affine_qmm_supported(const DevMat &m) {
   if (!(m.bits == 4 || m.bits == 5 || m.bits == 6 || m.bits == 8)) return false;
   if (m.I <= 0 || m.I % kTile != 0 || m.O <= 0) return false;
@@ -717,6 +947,11 @@ static bool qmm256_ok(const DevMat *ms, int n, int M) {
   }
   return true;
 }
+
+#ifndef QMM_WAVES16
+#define QMM_WAVES16 1
+#endif
+constexpr bool kQmmWaves16 = QMM_WAVES16 != 0;
 
 static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
                                 void *const *ys, const int *y_strides, int y_bf16, hipStream_t st) {
@@ -763,12 +998,22 @@ static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int 
   split = (ksteps_all + ksteps - 1) / ksteps;
   const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
   const dim3 grid(((tiles + 7) / 8) * 8 * mt, split);
-  switch (ms[0].bits) {
-    case 4: hipLaunchKernelGGL(affine_qmm256_kernel<4>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
-    case 5: hipLaunchKernelGGL(affine_qmm256_kernel<5>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
-    case 6: hipLaunchKernelGGL(affine_qmm256_kernel<6>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
-    case 8: hipLaunchKernelGGL(affine_qmm256_kernel<8>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
-    default: return hipErrorInvalidValue;
+  if (kQmmWaves16) {
+    switch (ms[0].bits) {
+      case 4: hipLaunchKernelGGL(affine_qmm256w_kernel<4>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 5: hipLaunchKernelGGL(affine_qmm256w_kernel<5>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 6: hipLaunchKernelGGL(affine_qmm256w_kernel<6>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 8: hipLaunchKernelGGL(affine_qmm256w_kernel<8>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (ms[0].bits) {
+      case 4: hipLaunchKernelGGL(affine_qmm256_kernel<4>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 5: hipLaunchKernelGGL(affine_qmm256_kernel<5>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 6: hipLaunchKernelGGL(affine_qmm256_kernel<6>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+      case 8: hipLaunchKernelGGL(affine_qmm256_kernel<8>, grid, dim3(512), 0, st, p, mt, tiles, ksteps, slot); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
