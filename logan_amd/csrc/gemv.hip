@@ -471,6 +471,11 @@ static hipError_t swiglu_dispatch_bits(const GemvParams &p, int bits, hipStream_
   return hipErrorInvalidValue;
 }
 
+#ifndef SWIGLU_FULLK
+#define SWIGLU_FULLK 1
+#endif
+constexpr bool kSwigluFullK = SWIGLU_FULLK != 0;
+
 hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
                               void *h, int h_stride, int h_bf16, hipStream_t st) {
   if (!gemv_bf16_supported(g) || !gemv_bf16_supported(u) || M <= 0) return hipErrorInvalidValue;
@@ -482,6 +487,14 @@ hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *
   const DevMat gu[2] = {g, u};
   for (int m0 = 0; m0 < M; m0 += 32) {
     const int mc = min(32, M - m0);
+    if (mc >= 3 && kSwigluFullK && swiglu_fullk_supported(g, u, mc)) {
+      void *hm = h_bf16 ? (void *)(reinterpret_cast<uint16_t *>(h) + (size_t)m0 * h_stride)
+                        : (void *)(reinterpret_cast<float *>(h) + (size_t)m0 * h_stride);
+      const hipError_t e = launch_swiglu_fullk(g, u, x + (size_t)m0 * x_stride, x_stride, mc, hm, h_stride,
+                                               h_bf16, st);
+      if (e != hipSuccess) return e;
+      continue;
+    }
     if (mc >= 3 && affine_splitk_multi_supported(gu, 2, mc)) {
       void *hm = h_bf16 ? (void *)(reinterpret_cast<uint16_t *>(h) + (size_t)m0 * h_stride)
                         : (void *)(reinterpret_cast<float *>(h) + (size_t)m0 * h_stride);

@@ -255,6 +255,173 @@ __global__ __launch_bounds__(256) void splitk_reduce_multi_kernel(ReduceMulti r)
   }
 }
 
+// ---------------------------------------------------------------------------
+// gate/up + SwiGLU over the full K, for the pairs with enough rows to fill the
+// chip without a K split (the config-2 4096 -> 2 x 14336 product): block b
+// owns row indices [64 b, 64 b + 64); waves 0-3 stream those gate rows and
+// waves 4-7 the same up rows, 16 each, over all of K in chunks of 512 codes.
+// Each chunk's x rows are staged once in LDS (double-buffered, the layout of
+// splitk_block) and its weights, scale and bias words are issued one chunk
+// ahead of their MFMAs. The gate waves hand their sums to the up waves
+// through LDS, which write h = silu(gate) * up (logan-qwen4/src/lib.rs
+// :8807-8809): no partial sums and no reduce launch.
+#ifndef FULLK_WPM
+#define FULLK_WPM 4
+#endif
+constexpr int kFkWpm = FULLK_WPM;     // waves per matrix in a block
+constexpr int kFkRows = 16 * kFkWpm;  // row indices per block
+constexpr int kFkThreads = 128 * kFkWpm;
+
+struct FullKParams {
+  const uint8_t *w[2];  // gate, up
+  const uint16_t *sc[2];
+  const uint16_t *bi[2];
+  const uint16_t *x;
+  void *h;
+  long long row_bytes;
+  int N, K, ng, gsteps, x_stride, M, h_stride, h_bf16;
+};
+
+template <int BITS, int MT, bool AUX8>
+struct FkChunk {
+  static constexpr int NV = 16 * MT * (kSkKc / 8) / kFkThreads;  // x granules per thread
+  uint4 v[NV];
+  SkRaw<BITS> wr[kSkSteps];
+  uint32_t sr[AUX8 ? 1 : kSkSteps], br[AUX8 ? 1 : kSkSteps];
+  uint4 vs, vb;
+};
+
+template <int BITS, int MT, bool FP16, bool AUX8>
+__global__ __launch_bounds__(kFkThreads) void swiglu_fullk_kernel(FullKParams p) {
+  __shared__ __align__(16) uint16_t sx[2][16 * MT * kSkKc];
+  __shared__ float sg[kFkWpm][64][4 * MT];
+  using S = MfmaStep<BITS>;
+  using C = FkChunk<BITS, MT, AUX8>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int mat = wave / kFkWpm;  // 0: gate, 1: up
+  const int n = blockIdx.x * kFkRows + (wave % kFkWpm) * 16 + r16;
+  const int row = min(n, p.N - 1);
+  const uint8_t *wrow = (mat ? p.w[1] : p.w[0]) + (size_t)row * p.row_bytes;
+  const uint16_t *srow = (mat ? p.sc[1] : p.sc[0]) + (size_t)row * p.ng;
+  const uint16_t *brow = (mat ? p.bi[1] : p.bi[0]) + (size_t)row * p.ng;
+  const int nch = p.K / kSkKc;
+  const int lim = p.M * (kSkKc / 8);
+
+  // loads of chunk c in the order they are needed: x, scale/bias, weights
+  auto issue = [&](int c, C &q) {
+    const int k0 = c * kSkKc;
+#pragma unroll
+    for (int i = 0; i < C::NV; ++i) {
+      const int gq = min(tid + kFkThreads * i, lim - 1);
+      q.v[i] = *reinterpret_cast<const uint4 *>(p.x + (size_t)(gq >> 6) * p.x_stride + k0 + 8 * (gq & 63));
+    }
+    if constexpr (AUX8) {
+      q.vs = *reinterpret_cast<const uint4 *>(srow + (k0 >> 6));
+      q.vb = *reinterpret_cast<const uint4 *>(brow + (k0 >> 6));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSkSteps; ++u) {
+        const int gi = ((k0 >> 6) + u) / p.gsteps;
+        q.sr[u] = srow[gi];
+        q.br[u] = brow[gi];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSkSteps; ++u) S::load_raw(q.wr[u], wrow, k0 + u * 64 + 16 * g);
+  };
+  // x of a chunk into LDS buffer b (granules past row M - 1 fill rows no
+  // stored output depends on)
+  auto stage = [&](const C &q, int b) {
+#pragma unroll
+    for (int i = 0; i < C::NV; ++i) {
+      const int gq = tid + kFkThreads * i;
+      const int m = gq >> 6, qq = gq & 63;
+      const uint4 o = BITS == 4 ? __builtin_bit_cast(uint4, a_nibble_order(q.v[i])) : q.v[i];
+      *reinterpret_cast<uint4 *>(sx[b] + m * kSkKc + 8 * swz(m, qq)) = o;
+    }
+  };
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const C &q, int b) {
+#pragma unroll
+    for (int u = 0; u < kSkSteps; ++u) {
+      uint32_t su, bu;
+      if constexpr (AUX8) {
+        const uint32_t ws[4] = {q.vs.x, q.vs.y, q.vs.z, q.vs.w}, wb[4] = {q.vb.x, q.vb.y, q.vb.z, q.vb.w};
+        su = (ws[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+        bu = (wb[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+      } else {
+        su = q.sr[u];
+        bu = q.br[u];
+      }
+      bf16x8_t b0, b1;
+      S::b_ops(q.wr[u], kc, b0, b1);
+      const float sf = aux_f32<FP16>(su), bf = aux_f32<FP16>(bu);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        bf16x8_t a0, a1;
+        const int m = 16 * t + r16;
+        S::a_ops(sx[b] + m * kSkKc, (u * 64 + 16 * g) >> 3, m, a0, a1);
+        const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+        f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+        S::fold(acc[t], d, xs, sf, bf);
+      }
+    }
+  };
+
+  // two chunks per trip, so each register set is a fixed one: chunk c is
+  // multiplied from LDS buffer c & 1 while chunk c + 1's loads are in flight
+  C qa, qb;
+  issue(0, qa);
+  stage(qa, 0);
+  if (nch > 1) issue(1, qb);
+  __syncthreads();
+  for (int c = 0; c < nch; c += 2) {
+    compute(qa, 0);
+    if (c + 1 < nch) stage(qb, 1);
+    if (c + 2 < nch) issue(c + 2, qa);
+    __syncthreads();
+    if (c + 1 < nch) {
+      compute(qb, 1);
+      if (c + 2 < nch) stage(qa, 0);
+      if (c + 3 < nch) issue(c + 3, qb);
+      __syncthreads();
+    }
+  }
+
+  // accumulator element i of lane l: token 16 t + 4 (l / 16) + i, row n
+  if (mat == 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sg[wave][lane][4 * t + i] = acc[t][i];
+  }
+  __syncthreads();
+  if (mat == 1 && n < p.N) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 16 * t + 4 * g + i;
+        if (m >= p.M) continue;
+        const float hv = silu(sg[wave - kFkWpm][lane][4 * t + i]) * acc[t][i];
+        if (p.h_bf16)
+          reinterpret_cast<uint16_t *>(p.h)[(size_t)m * p.h_stride + n] = (uint16_t)f32_to_bf16_rne(hv);
+        else
+          reinterpret_cast<float *>(p.h)[(size_t)m * p.h_stride + n] = hv;
+      }
+  }
+}
+
 bool affine_splitk_supported(const DevMat &m, int M) {
   if (m.bits < 4 || m.bits > 8 || m.bits == 7) return false;
   if (M < 3 || M > 32 || m.I % kSkKc != 0) return false;
@@ -413,6 +580,70 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
   size_t blocks = ((size_t)(swiglu ? r.start[1] : r.start[n]) + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, st, r);
+  return hipGetLastError();
+}
+
+// The full-K pair serves gate/up pairs of one geometry whose 64-row blocks
+// cover at least three quarters of the CUs (N >= 12288), at up to 16 tokens
+// (one 16-token MFMA tile: more would spill registers); other pairs keep the
+// K split.
+bool swiglu_fullk_supported(const DevMat &g, const DevMat &u, int M) {
+  if (M > 16) return false;
+  if (!affine_splitk_supported(g, M) || !affine_splitk_supported(u, M)) return false;
+  if (g.I != u.I || g.O != u.O || g.bits != u.bits || g.gs != u.gs || g.fp16 != u.fp16 ||
+      g.row_bytes != u.row_bytes)
+    return false;
+  return g.O >= 12288;
+}
+
+template <int BITS, int MT>
+static void fullk_launch_t(const FullKParams &p, bool fp16, bool aux8, hipStream_t st) {
+  const dim3 grid((p.N + kFkRows - 1) / kFkRows);
+  if (fp16) {
+    if (aux8) hipLaunchKernelGGL((swiglu_fullk_kernel<BITS, MT, true, true>), grid, dim3(kFkThreads), 0, st, p);
+    else hipLaunchKernelGGL((swiglu_fullk_kernel<BITS, MT, true, false>), grid, dim3(kFkThreads), 0, st, p);
+  } else {
+    if (aux8) hipLaunchKernelGGL((swiglu_fullk_kernel<BITS, MT, false, true>), grid, dim3(kFkThreads), 0, st, p);
+    else hipLaunchKernelGGL((swiglu_fullk_kernel<BITS, MT, false, false>), grid, dim3(kFkThreads), 0, st, p);
+  }
+}
+
+template <int BITS>
+static void fullk_launch_bits(const FullKParams &p, bool fp16, bool aux8, hipStream_t st) {
+  fullk_launch_t<BITS, 1>(p, fp16, aux8, st);
+}
+
+hipError_t launch_swiglu_fullk(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
+                               void *h, int h_stride, int h_bf16, hipStream_t st) {
+  if (!swiglu_fullk_supported(g, u, M)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  FullKParams p;
+  p.w[0] = g.w;
+  p.w[1] = u.w;
+  p.sc[0] = g.sc;
+  p.sc[1] = u.sc;
+  p.bi[0] = g.bi;
+  p.bi[1] = u.bi;
+  p.x = x;
+  p.h = h;
+  p.row_bytes = g.row_bytes;
+  p.N = g.O;
+  p.K = g.I;
+  p.ng = g.ng;
+  p.gsteps = g.gs / 64;
+  p.x_stride = x_stride;
+  p.M = M;
+  p.h_stride = h_stride;
+  p.h_bf16 = h_bf16;
+  const bool aux8 = g.gs == 64 && (g.ng % 8) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(g.sc) | reinterpret_cast<uintptr_t>(g.bi) |
+                      reinterpret_cast<uintptr_t>(u.sc) | reinterpret_cast<uintptr_t>(u.bi)) & 15) == 0;
+  switch (g.bits) {
+    case 4: fullk_launch_bits<4>(p, g.fp16, aux8, st); break;
+    case 5: fullk_launch_bits<5>(p, g.fp16, aux8, st); break;
+    case 6: fullk_launch_bits<6>(p, g.fp16, aux8, st); break;
+    default: fullk_launch_bits<8>(p, g.fp16, aux8, st); break;
+  }
   return hipGetLastError();
 }
 

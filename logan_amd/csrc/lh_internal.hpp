@@ -82,6 +82,11 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
 // the K-split pair with a SwiGLU reduce for 3..32 tokens
 hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
                               void *h, int h_stride, int h_bf16, hipStream_t st);
+// gate/up + SwiGLU for 3..16 tokens over the full K (no partial sums), for
+// pairs with at least 12288 rows
+bool swiglu_fullk_supported(const DevMat &g, const DevMat &u, int M);
+hipError_t launch_swiglu_fullk(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
+                               void *h, int h_stride, int h_bf16, hipStream_t st);
 bool affine_splitk_supported(const DevMat &m, int M);
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);

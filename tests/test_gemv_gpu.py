@@ -608,3 +608,42 @@ def test_gemv_swiglu_matches_oracle(gpu, O, I, bits, gs, M):
         yu = oracle.affine_gemv(xf, *u, O, I, bits, gs)
         ref = oracle.silu_mul(yg, yu)
         assert normwise_rel(h[m], ref) <= 5e-5, m
+
+
+FULLK_SHAPES = [
+    # (O, I, bits, gs, fp16): gate/up pairs with >= 12288 rows take the full-K
+    # kernel at 3..16 tokens: config 2's 4096 -> 14336 at 8-bit, 4/5/6-bit,
+    # a row count that is not a multiple of the 64-row block, groups of 128
+    # (scale/bias per step, not per 512-code run), fp16 sidecars
+    (14336, 4096, 8, 64, False), (12288, 1024, 4, 64, False), (12300, 512, 5, 64, False),
+    (12352, 1024, 6, 128, False), (12288, 1536, 4, 64, True),
+]
+
+
+@pytest.mark.parametrize("O,I,bits,gs,fp16", FULLK_SHAPES)
+@pytest.mark.parametrize("M", [3, 4, 8, 16, 17, 33])
+def test_gemv_swiglu_full_k_matches_oracle(gpu, O, I, bits, gs, fp16, M):
+    """The gate/up + SwiGLU product over the full K (no partial sums, h
+    formed in the kernel) against the oracle's f32 GEMVs and silu_mul: f32 h
+    within 5e-5 normwise, bf16 h equal to RNE of the f32 h. M = 17 and 33
+    take the K-split pair (and the dot2 kernel for the 33rd token)."""
+    import torch
+    from logan_amd.device import affine_gemv_swiglu
+
+    print(f"swiglu full-K O={O} I={I} bits={bits} gs={gs} fp16={fp16} M={M}", flush=True)
+    rng = np.random.default_rng(O + I * 3 + bits + M + int(fp16))
+    g = make_affine(rng, O, I, bits, gs, fp16)
+    u = make_affine(rng, O, I, bits, gs, fp16)
+    xb = make_x(rng, M, I).reshape(M, I)
+    gm = dev_matrix(torch, *g, O, I, bits, gs, fp16)
+    um = dev_matrix(torch, *u, O, I, bits, gs, fp16)
+    x = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    h = affine_gemv_swiglu(gm, um, x, out_dtype=torch.float32)
+    hb = affine_gemv_swiglu(gm, um, x, out_dtype=torch.bfloat16)
+    assert torch.equal(hb, h.to(torch.bfloat16))
+    h = h.cpu().numpy()
+    for m in range(M):
+        xf = bf16_to_f32(xb[m])
+        ref = oracle.silu_mul(oracle.affine_gemv(xf, *g, O, I, bits, gs, fp16=fp16),
+                              oracle.affine_gemv(xf, *u, O, I, bits, gs, fp16=fp16))
+        assert normwise_rel(h[m], ref) <= 5e-5, m
