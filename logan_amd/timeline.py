@@ -4,7 +4,7 @@
 the library with moe_fused.hip compiled under LOGAN_HIP_TIMELINE, whose blocks
 record s_memrealtime stamps (100 MHz) of their stages. `python -m
 logan_amd.timeline` then runs config-3 layers (B = 1, 4-bit g64, E = 512,
-top-10 + one shared expert, D = 2048, inter = 512; each layer its own seeded
+top-10 + one shared expert, D = 2048, inter = 512, `--bits` 4/5/6/8; each layer its own seeded
 weights, x and router logits) as one HIP graph of `--layers` fused launches,
 replays it, reads the stamps of the graph's last two launches and prints, per
 stage, the distribution over blocks in microseconds from the first block
@@ -27,16 +27,20 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 
-E, TOPK, D, INTER, BITS, GS = 512, 10, 2048, 512, 4, 64
-# grid of the 4-bit D = 2048 instantiation: 4 gate/up rows per A wave, 8 waves
-# per block, (k + 1) * inter / 32 A blocks; 8 output rows per B block
-N_A = (TOPK + 1) * INTER // (4 * 8)
+E, TOPK, D, INTER, GS = 512, 10, 2048, 512, 64
+# grid of the D = 2048 instantiations: 4 gate/up rows per A wave (2 for 8-bit
+# codes), 8 waves per block, (k + 1) * inter / (8 * rows) A blocks; 8 output
+# rows per B block
 N_B = D // 8
+
+
+def n_a(bits: int) -> int:
+    return (TOPK + 1) * INTER // ((2 if bits == 8 else 4) * 8)
 A_STAGES = ("start", "route known", "gate/up weights consumed", "arrival added")
 B_STAGES = ("start", "route known", "arrivals seen", "h read", "down products", "end")
 
 
-def _layers(torch, device, synth, n):
+def _layers(torch, device, synth, n, BITS):
     layers = []
     for l in range(n):
         s = 1000 * l
@@ -58,6 +62,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--bits", type=int, default=4, choices=(4, 5, 6, 8))
     args = ap.parse_args(argv)
 
     from logan_amd import build as b
@@ -73,7 +78,8 @@ def main(argv=None) -> int:
     from logan_amd import _lib, device, synth
 
     L = args.layers
-    layers = _layers(torch, device, synth, L)
+    N_A = n_a(args.bits)
+    layers = _layers(torch, device, synth, L, args.bits)
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
     xs = torch.randn((L, 1, D), device="cuda", generator=g).to(torch.bfloat16)
@@ -114,7 +120,7 @@ def main(argv=None) -> int:
     t = st[last, :nb].astype(np.int64)
     t0 = t[:, 0].min()
     gap = (t0 - int(st[prev, N_A:nb, 5].max())) / 100.0
-    print(f"config 3 B=1, {L} layers: {us:.2f} us per launch (graph replay, timeline build); "
+    print(f"config 3 B=1 ({args.bits}-bit), {L} layers: {us:.2f} us per launch (graph replay, timeline build); "
           f"{N_A} A + {N_B} B blocks")
     print(f"previous launch's last block end -> this launch's first block start: {gap:.2f} us")
     print("| blocks | stage | min | median | p90 | max |")

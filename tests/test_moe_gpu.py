@@ -309,6 +309,9 @@ def test_moe_fused_agrees_with_multi_launch(gpu):
     (64, 6, 1024, 640, None, 6, 32, True, False),
     (32, 11, 512, 512, None, 6, 64, True, True),    # 12 slots, the most one launch serves
     (1024, 10, 2048, 512, None, 4, 64, True, False),
+    (64, 1, 512, 256, None, 4, 64, True, False),    # k = 1: two slots, most B waves own none
+    (128, 2, 1024, 256, None, 8, 64, False, False), # k = 2, no shared expert
+    (256, 8, 2048, 512, None, 5, 64, True, False),  # E between the 64 and 512 lane blocks
 ])
 def test_moe_fused_shapes(gpu, fused_mode, E, k, D, inter, sinter, bits, gs, shared, fp16):
     """Single-token block over the shapes the one-launch kernel serves (row
