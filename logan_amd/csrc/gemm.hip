@@ -948,10 +948,9 @@ static bool qmm256_ok(const DevMat *ms, int n, int M) {
   return true;
 }
 
-#ifndef QMM_WAVES16
-#define QMM_WAVES16 1
-#endif
-constexpr bool kQmmWaves16 = QMM_WAVES16 != 0;
+// 16 waves per block where K is split (short k ranges: the 2048-row output
+// projections, 23 -> 19.6 us), 8 where it is not (the 12352-row grids of one
+// k range, 45.4 -> 43 us)
 
 static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
                                 void *const *ys, const int *y_strides, int y_bf16, hipStream_t st) {
@@ -998,7 +997,7 @@ static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int 
   split = (ksteps_all + ksteps - 1) / ksteps;
   const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
   const dim3 grid(((tiles + 7) / 8) * 8 * mt, split);
-  if (kQmmWaves16) {
+  if (split > 1) {
     switch (ms[0].bits) {
       case 4: hipLaunchKernelGGL(affine_qmm256w_kernel<4>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
       case 5: hipLaunchKernelGGL(affine_qmm256w_kernel<5>, grid, dim3(1024), 0, st, p, mt, tiles, ksteps, slot); break;
