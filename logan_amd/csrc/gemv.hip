@@ -426,7 +426,9 @@ hipError_t launch_gemv_bf16(const DevMat &m, const uint16_t *x, int x_stride, in
                       : (void *)(reinterpret_cast<float *>(y) + (size_t)m0 * y_stride);
     const uint16_t *xm = x + (size_t)m0 * x_stride;
     hipError_t e;
-    if (mc >= 3 && affine_splitk_supported(m, mc))
+    if (mc >= 3 && affine_kwave_supported(m, mc))
+      e = launch_affine_kwave(m, xm, x_stride, mc, ym, y_stride, y_bf16, st);
+    else if (mc >= 3 && affine_splitk_supported(m, mc))
       e = launch_affine_splitk(m, xm, x_stride, mc, ym, y_stride, y_bf16, st);
     else if (affine_skinny_supported(m))
       e = launch_affine_skinny(m, xm, x_stride, mc, ym, y_stride, y_bf16, st);

@@ -19,6 +19,7 @@
 // picks slots round-robin, so launches that overlap on one device do not
 // share a slot unless more than kSkSlots of them are in flight at once.
 #include <atomic>
+#include <type_traits>
 
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
@@ -420,6 +421,280 @@ __global__ __launch_bounds__(kFkThreads) void swiglu_fullk_kernel(FullKParams p)
           reinterpret_cast<float *>(p.h)[(size_t)m * p.h_stride + n] = hv;
       }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Small-batch product (3..8 tokens) with K split across the waves of one
+// block instead of across blocks: block b owns rows [16 b, 16 b + 16), and
+// each of its W waves owns a run of cpw 512-code chunks (K = 512 W cpw). The
+// waves' K ranges are disjoint, so each wave stages its own x rows: per
+// chunk, one coalesced 1 KB load per row (MX rows, MX = 4 or 8; rows past
+// M - 1 repeat row M - 1 and their outputs are discarded) into an LDS tile
+// of its own, read back in the MFMA operand order. A wave keeps one chunk of
+// weights in flight behind the step it computes (a step's registers are
+// reissued for the next chunk as soon as the step's products have read them)
+// and the next chunk's x one chunk ahead. The waves' sums meet in LDS and
+// are added in K order (wave 0 first, the order the K-split reduce adds its
+// partials in), and the block writes y: no partial sums and no reduce
+// launch.
+//
+// Measured against a plain read of the same bytes in the same pattern (9 us
+// for the config-2 down product, 4096 x 14336 codes): the kernel's loads
+// alone run at that rate and its arithmetic alone (8-bit code conversion,
+// MFMA, fold) takes 7.5 us, and the two add up rather than overlap. Each CU
+// holds a bounded number of vector-memory instructions in flight; a wave
+// with more outstanding waits at issue and cannot compute meanwhile. Holding
+// two chunks per wave in registers (next chunk issued before the current
+// one's products) made the issue stalls longer, not the layer faster
+// (per-wave s_memrealtime stamps: up to 8 us before a wave's first chunk
+// was accepted), and copying x with global_load_lds makes the compiler wait
+// for every load before each LDS read.
+#ifndef SKINNY_KWAVE
+#define SKINNY_KWAVE 1
+#endif
+constexpr bool kSkinnyKwave = SKINNY_KWAVE != 0;
+constexpr int kKwMaxW = 8;
+
+struct KwaveParams {
+  const uint8_t *w;
+  const uint16_t *sc;
+  const uint16_t *bi;
+  const uint16_t *x;
+  void *y;
+  long long row_bytes;
+  int N, ng, gsteps, x_stride, M, cpw, y_stride, y_bf16;
+};
+
+// dynamic LDS of the kernel: W waves x 2 buffers x MX rows x 512 bf16
+__host__ __device__ constexpr size_t kwave_lds_bytes(int W, int MX) {
+  return (size_t)W * 2 * MX * kSkKc * 2;
+}
+
+template <int BITS, int MX, bool FP16, bool AUX8>
+__global__ __launch_bounds__(64 * kKwMaxW) void skinny_kwave_kernel(KwaveParams p) {
+  using S = MfmaStep<BITS>;
+  extern __shared__ __align__(16) uint16_t kw_lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int W = blockDim.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n = blockIdx.x * 16 + r16;
+  const int row = min(n, p.N - 1);
+  const uint8_t *wrow = p.w + (size_t)row * p.row_bytes;
+  const uint16_t *srow = p.sc + (size_t)row * p.ng;
+  const uint16_t *brow = p.bi + (size_t)row * p.ng;
+  const int kb = wave * p.cpw * kSkKc;
+  uint16_t *sxw = kw_lds + (size_t)wave * 2 * MX * kSkKc;  // this wave's two x tiles
+  const int mr = min(r16, MX - 1);                          // operand row read by this lane
+
+  SkRaw<BITS> wr[kSkSteps];
+  uint4 xg[MX];                          // x granule `lane` of rows 0..MX-1 of a chunk
+  uint4 vs, vb;                          // AUX8: the chunk's 8 scale / bias words
+  uint32_t sr[kSkSteps], br[kSkSteps];  // otherwise one word per step
+  auto issue_aux = [&](int k0) {
+    if constexpr (AUX8) {
+      vs = *reinterpret_cast<const uint4 *>(srow + (k0 >> 6));
+      vb = *reinterpret_cast<const uint4 *>(brow + (k0 >> 6));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSkSteps; ++u) {
+        const int gi = ((k0 >> 6) + u) / p.gsteps;
+        sr[u] = srow[gi];
+        br[u] = brow[gi];
+      }
+    }
+  };
+  auto issue_w = [&](int u, int k0) { S::load_raw(wr[u], wrow, k0 + u * 64 + 16 * g); };
+  // every load unconditional (rows past M - 1 repeat row M - 1), so the
+  // compiler's wait counts stay exact
+  auto issue_x = [&](int k0) {
+#pragma unroll
+    for (int m = 0; m < MX; ++m)
+      xg[m] = *reinterpret_cast<const uint4 *>(p.x + (size_t)min(m, p.M - 1) * p.x_stride + k0 + 8 * lane);
+  };
+  auto store_x = [&](int buf) {
+    uint16_t *t = sxw + buf * MX * kSkKc;
+#pragma unroll
+    for (int m = 0; m < MX; ++m) {
+      const uint4 o = BITS == 4 ? __builtin_bit_cast(uint4, a_nibble_order(xg[m])) : xg[m];
+      *reinterpret_cast<uint4 *>(t + m * kSkKc + 8 * swz(m, lane)) = o;
+    }
+  };
+
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // one chunk's eight steps from x tile `buf`; with REISSUE each step's
+  // weight registers are loaded again for the chunk at knext once the step's
+  // products have read them (the last chunk is peeled off, so no load is
+  // conditional)
+  auto chunk = [&](auto reissue, int buf, int knext) {
+    constexpr bool REISSUE = decltype(reissue)::value;
+    uint32_t scur[kSkSteps], bcur[kSkSteps];
+    if constexpr (AUX8) {
+      const uint32_t ws[4] = {vs.x, vs.y, vs.z, vs.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+      for (int u = 0; u < kSkSteps; ++u) {
+        scur[u] = (ws[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+        bcur[u] = (wb[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSkSteps; ++u) {
+        scur[u] = sr[u];
+        bcur[u] = br[u];
+      }
+    }
+    if constexpr (REISSUE) issue_aux(knext);
+    const uint16_t *rowp = sxw + buf * MX * kSkKc + mr * kSkKc;
+#pragma unroll
+    for (int u = 0; u < kSkSteps; ++u) {
+      bf16x8_t b0, b1, a0, a1;
+      S::b_ops(wr[u], kc, b0, b1);
+      S::a_ops(rowp, (u * 64 + 16 * g) >> 3, mr, a0, a1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      // the reissue after the step's operands are formed, so the loads land
+      // in place (no copies, and no waits, at the loop head); the barrier
+      // keeps it there (the scheduler would otherwise sink every load of the
+      // next chunk below the last step: one round trip per chunk)
+      if constexpr (REISSUE) issue_w(u, knext);
+      __builtin_amdgcn_sched_barrier(0);
+      S::fold(acc, d, xs, aux_f32<FP16>(scur[u]), aux_f32<FP16>(bcur[u]));
+    }
+  };
+
+  issue_x(kb);
+  issue_aux(kb);
+#pragma unroll
+  for (int u = 0; u < kSkSteps; ++u) issue_w(u, kb);
+  store_x(0);
+  // x one chunk ahead (the last chunk's x is read again on the last round)
+  issue_x(kb + min(1, p.cpw - 1) * kSkKc);
+  for (int c = 0; c + 1 < p.cpw; ++c) {
+    chunk(std::true_type{}, c & 1, kb + (c + 1) * kSkKc);
+    store_x((c + 1) & 1);
+    issue_x(kb + min(c + 2, p.cpw - 1) * kSkKc);
+  }
+  chunk(std::false_type{}, (p.cpw - 1) & 1, 0);
+
+  // the waves' sums, added in K order
+  __syncthreads();
+  float *red = reinterpret_cast<float *>(kw_lds);  // [W][4][64]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+  __syncthreads();
+  if (tid < 256) {
+    const int i = tid >> 6, l = tid & 63;
+    float s = 0.f;
+    for (int w = 0; w < W; ++w) s += red[(w * 4 + i) * 64 + l];
+    const int m = 4 * (l >> 4) + i, nn = blockIdx.x * 16 + (l & 15);
+    if (m < p.M && nn < p.N) {
+      if (p.y_bf16)
+        reinterpret_cast<uint16_t *>(p.y)[(size_t)m * p.y_stride + nn] = (uint16_t)f32_to_bf16_rne(s);
+      else
+        reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + nn] = s;
+    }
+  }
+}
+
+// waves per block for nch 512-code chunks, `blocks` blocks and MX x rows:
+// the largest divisor of nch in [4, 8] that leaves each wave at least two
+// chunks (the config-2 o product, 8 chunks: 6.7 us with 4 waves of two
+// against 7.6 us with 8 of one) and keeps the whole grid resident on the 256
+// CUs (the kernel holds up to about 200 VGPRs: two waves per SIMD, 2048
+// waves; and the blocks of one CU share its 160 KB of LDS); failing that,
+// the largest that fits; 0 if none
+static int kwave_waves(int nch, int blocks, int MX) {
+  const int per_cu = (blocks + 255) / 256;
+  auto fits = [&](int w) {
+    return nch % w == 0 && (long long)blocks * w <= 2048 &&
+           (size_t)per_cu * kwave_lds_bytes(w, MX) <= 160 * 1024;
+  };
+  for (int w = kKwMaxW; w >= 4; --w)
+    if (fits(w) && nch / w >= 2) return w;
+  for (int w = kKwMaxW; w >= 4; --w)
+    if (fits(w)) return w;
+  return 0;
+}
+
+static int kwave_mx(int M) { return M <= 4 ? 4 : 8; }
+
+bool affine_kwave_supported(const DevMat &m, int M) {
+  if (!kSkinnyKwave) return false;
+  if (m.bits < 4 || m.bits > 8 || m.bits == 7) return false;
+  if (M < 3 || M > 8 || m.I % kSkKc != 0) return false;
+  if (m.gs <= 0 || m.gs % 64 != 0 || m.I % m.gs != 0) return false;
+  if (m.row_bytes != (long long)m.I * m.bits / 8) return false;
+  const uintptr_t need = m.bits == 4 ? 7 : m.bits == 8 ? 15 : 3;
+  if ((reinterpret_cast<uintptr_t>(m.w) & need) != 0 || (m.row_bytes & (long long)need) != 0) return false;
+  // at least 256 blocks of 16 rows (one per CU); fewer rows fill the chip
+  // better with the K split across blocks
+  if (m.O < 16 * 256) return false;
+  return kwave_waves(m.I / kSkKc, (m.O + 15) / 16, kwave_mx(M)) != 0;
+}
+
+template <int BITS, int MX, bool FP16, bool AUX8>
+static void kwave_launch_t(const KwaveParams &p, int W, hipStream_t st) {
+  auto *k = skinny_kwave_kernel<BITS, MX, FP16, AUX8>;
+  const size_t lds = kwave_lds_bytes(W, MX);
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)kwave_lds_bytes(kKwMaxW, MX));
+  (void)attr;
+  hipLaunchKernelGGL(k, dim3((p.N + 15) / 16), dim3(64 * W), lds, st, p);
+}
+
+template <int BITS, int MX>
+static void kwave_launch_mx(const KwaveParams &p, int W, bool fp16, bool aux8, hipStream_t st) {
+  if (fp16) {
+    if (aux8) kwave_launch_t<BITS, MX, true, true>(p, W, st);
+    else kwave_launch_t<BITS, MX, true, false>(p, W, st);
+  } else {
+    if (aux8) kwave_launch_t<BITS, MX, false, true>(p, W, st);
+    else kwave_launch_t<BITS, MX, false, false>(p, W, st);
+  }
+}
+
+template <int BITS>
+static void kwave_launch_bits(const KwaveParams &p, int W, bool fp16, bool aux8, hipStream_t st) {
+  if (kwave_mx(p.M) == 4) kwave_launch_mx<BITS, 4>(p, W, fp16, aux8, st);
+  else kwave_launch_mx<BITS, 8>(p, W, fp16, aux8, st);
+}
+
+hipError_t launch_affine_kwave(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                               int y_stride, int y_bf16, hipStream_t st) {
+  if (!affine_kwave_supported(m, M)) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) != 0 || (x_stride & 7) != 0) return hipErrorInvalidValue;
+  const int nch = m.I / kSkKc, W = kwave_waves(nch, (m.O + 15) / 16, kwave_mx(M));
+  KwaveParams p;
+  p.w = m.w;
+  p.sc = m.sc;
+  p.bi = m.bi;
+  p.x = x;
+  p.y = y;
+  p.row_bytes = m.row_bytes;
+  p.N = m.O;
+  p.ng = m.ng;
+  p.gsteps = m.gs / 64;
+  p.x_stride = x_stride;
+  p.M = M;
+  p.cpw = nch / W;
+  p.y_stride = y_stride;
+  p.y_bf16 = y_bf16;
+  const bool aux8 = m.gs == 64 && (m.ng % 8) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(m.sc) | reinterpret_cast<uintptr_t>(m.bi)) & 15) == 0;
+  switch (m.bits) {
+    case 4: kwave_launch_bits<4>(p, W, m.fp16, aux8, st); break;
+    case 5: kwave_launch_bits<5>(p, W, m.fp16, aux8, st); break;
+    case 6: kwave_launch_bits<6>(p, W, m.fp16, aux8, st); break;
+    default: kwave_launch_bits<8>(p, W, m.fp16, aux8, st); break;
+  }
+  return hipGetLastError();
 }
 
 bool affine_splitk_supported(const DevMat &m, int M) {

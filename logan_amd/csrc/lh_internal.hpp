@@ -87,6 +87,11 @@ hipError_t launch_gemv_swiglu(const DevMat &g, const DevMat &u, const uint16_t *
 bool swiglu_fullk_supported(const DevMat &g, const DevMat &u, int M);
 hipError_t launch_swiglu_fullk(const DevMat &g, const DevMat &u, const uint16_t *x, int x_stride, int M,
                                void *h, int h_stride, int h_bf16, hipStream_t st);
+// K split across the waves of a block (3..8 tokens, at least 4096 rows,
+// I / 512 with a divisor in [4, 8]): y written by the one launch
+bool affine_kwave_supported(const DevMat &m, int M);
+hipError_t launch_affine_kwave(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
+                               int y_stride, int y_bf16, hipStream_t st);
 bool affine_splitk_supported(const DevMat &m, int M);
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st);

@@ -91,6 +91,39 @@ def test_gemv_bf16_matches_oracle(gpu, O, I, bits, gs, M):
         assert bf16_ulp_ok(y16[r][big], ref[big], 1)
 
 
+# (O, I, bits, gs, fp16): the shapes that take the K-split-across-waves kernel
+# at 3..8 tokens (at least 4096 rows, I / 512 with a divisor in [4, 8]; M = 16
+# takes the K split across blocks): config 2's q/k/v, o and down products,
+# odd wave counts (5, 6, 7), ragged rows, groups of 128, fp16 sidecars
+KWAVE_SHAPES = [
+    (6144, 4096, 8, 64, False), (4096, 4096, 8, 64, False), (4096, 14336, 8, 64, False),
+    (4100, 2560, 5, 64, False), (4111, 3072, 6, 128, False), (4096, 3584, 4, 64, True),
+    (5000, 4096, 4, 128, False),
+]
+
+
+@pytest.mark.parametrize("O,I,bits,gs,fp16", KWAVE_SHAPES)
+@pytest.mark.parametrize("M", [3, 4, 8, 16])
+def test_gemv_kwave_matches_oracle(gpu, O, I, bits, gs, fp16, M):
+    import torch
+    from logan_amd.device import affine_gemv
+
+    print(f"kwave O={O} I={I} bits={bits} gs={gs} fp16={fp16} M={M}", flush=True)
+    rng = np.random.default_rng(O + I * 3 + bits * 11 + M)
+    w, sc, bi = make_affine(rng, O, I, bits, gs, fp16)
+    xb = make_x(rng, M, I)
+    m = dev_matrix(torch, w, sc, bi, O, I, bits, gs, fp16)
+    xd = to_dev(xb.view(np.int16), torch).view(torch.bfloat16)
+    y32 = affine_gemv(m, xd, out_dtype=torch.float32).cpu().numpy()
+    y16 = affine_gemv(m, xd, out_dtype=torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(y16, bf16_bits(y32))
+    xf = bf16_to_f32(xb)
+    for r in range(M):
+        ref = oracle.affine_gemv(xf[r], w, sc, bi, O, I, bits, gs, fp16=fp16)
+        err = normwise_rel(y32[r], ref)
+        assert err <= 2e-5, f"row {r}: normwise {err:.3e}"
+
+
 def test_gemv_fp16_sidecar(gpu):
     import torch
     from logan_amd.device import affine_gemv
