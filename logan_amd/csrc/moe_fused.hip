@@ -378,14 +378,17 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       // slot's rank then comes from the reference's own arithmetic
       const float m = RK::logit(sel[0]), ls = RK::logit(mine);
       if (LF || !bf16_rank_tie_free(m, ls)) {
-        bool cand = false, pair = false;
+        // consecutive selected ranks checked lane-parallel (lane r: ranks r,
+        // r + 1), the unselected keys per lane
+        Key kr = 0;
+#pragma unroll
+        for (int r = 0; r < kFusedMaxSlots; ++r) kr = lane == r ? sel[r] : kr;
+        const float lr = RK::logit(kr), lnext = __shfl(lr, (lane + 1) & 63, 64);
+        bool cand = lane < slot && tie_pair(lr, lnext, m);
 #pragma unroll
         for (int i = 0; i < KPL; ++i)
           cand = cand || (rk.key[i] != Key(0) && tie_other(RK::logit(rk.key[i]), ls, m));
-#pragma unroll
-        for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
-          pair = pair || (r < slot && tie_pair(RK::logit(sel[r]), RK::logit(sel[r + 1]), m));
-        if (__any(cand) || pair || tie_global(m, ls)) {
+        if (__any(cand) || tie_global(m, ls)) {
           const RouteLane rl = route_exact<KPL, LF>(a.logits, 0, a.E, a.k);
           ex = __builtin_amdgcn_readlane(rl.idx, slot);
         }
@@ -551,14 +554,14 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     for (int r = 0; r < kFusedMaxSlots; ++r) llast = r == g.k - 1 ? RK::logit(sel0[r]) : llast;
     bool exact = false;
     if (LF || !bf16_ranks_tie_free(m, llast)) {
-      bool cand = false, pair = false;
-#pragma unroll
-      for (int r = 0; r + 1 < kFusedMaxSlots; ++r)
-        pair = pair || (r + 1 < g.k && tie_pair(RK::logit(sel0[r]), RK::logit(sel0[r + 1]), m));
+      // consecutive selected ranks checked lane-parallel (lane r: ranks r,
+      // r + 1), the unselected keys per lane
+      const float lr = RK::logit(mine), lnext = __shfl(lr, (lane + 1) & 63, 64);
+      bool cand = lane + 1 < g.k && tie_pair(lr, lnext, m);
 #pragma unroll
       for (int i = 0; i < KPL; ++i)
         cand = cand || (rk.key[i] != Key(0) && tie_other(RK::logit(rk.key[i]), llast, m));
-      exact = __any(cand) || pair || tie_global(m, llast);
+      exact = __any(cand) || tie_global(m, llast);
     }
     float wr;
     uint32_t enc;  // 0xffff - expert of rank `lane`, 0 past the route

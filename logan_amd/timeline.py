@@ -4,7 +4,8 @@
 the library with moe_fused.hip compiled under LOGAN_HIP_TIMELINE, whose blocks
 record s_memrealtime stamps (100 MHz) of their stages. `python -m
 logan_amd.timeline` then runs config-3 layers (B = 1, 4-bit g64, E = 512,
-top-10 + one shared expert, D = 2048, inter = 512, `--bits` 4/5/6/8; each layer its own seeded
+top-10 + one shared expert, D = 2048, inter = 512, `--bits` 4/5/6/8, bf16 logits or
+`--f32-logits`; each layer its own seeded
 weights, x and router logits) as one HIP graph of `--layers` fused launches,
 replays it, reads the stamps of the graph's last two launches and prints, per
 stage, the distribution over blocks in microseconds from the first block
@@ -63,6 +64,8 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--bits", type=int, default=4, choices=(4, 5, 6, 8))
+    ap.add_argument("--f32-logits", action="store_true",
+                    help="f32 router logits (64-bit selection keys) instead of bf16")
     args = ap.parse_args(argv)
 
     from logan_amd import build as b
@@ -83,7 +86,9 @@ def main(argv=None) -> int:
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
     xs = torch.randn((L, 1, D), device="cuda", generator=g).to(torch.bfloat16)
-    lg = torch.randn((L, 1, E), device="cuda", generator=g).to(torch.bfloat16)
+    lg = torch.randn((L, 1, E), device="cuda", generator=g)
+    if not args.f32_logits:
+        lg = lg.to(torch.bfloat16)
     out = torch.empty((L, 1, D), dtype=torch.bfloat16, device="cuda")
     ws = torch.empty(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
 
@@ -120,7 +125,8 @@ def main(argv=None) -> int:
     t = st[last, :nb].astype(np.int64)
     t0 = t[:, 0].min()
     gap = (t0 - int(st[prev, N_A:nb, 5].max())) / 100.0
-    print(f"config 3 B=1 ({args.bits}-bit), {L} layers: {us:.2f} us per launch (graph replay, timeline build); "
+    kind = "f32" if args.f32_logits else "bf16"
+    print(f"config 3 B=1 ({args.bits}-bit, {kind} logits), {L} layers: {us:.2f} us per launch (graph replay, timeline build); "
           f"{N_A} A + {N_B} B blocks")
     print(f"previous launch's last block end -> this launch's first block start: {gap:.2f} us")
     print("| blocks | stage | min | median | p90 | max |")
