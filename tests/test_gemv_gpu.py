@@ -103,7 +103,7 @@ KWAVE_SHAPES = [
 
 
 @pytest.mark.parametrize("O,I,bits,gs,fp16", KWAVE_SHAPES)
-@pytest.mark.parametrize("M", [3, 4, 8, 16])
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 16])
 def test_gemv_kwave_matches_oracle(gpu, O, I, bits, gs, fp16, M):
     import torch
     from logan_amd.device import affine_gemv
