@@ -75,21 +75,61 @@ __device__ __forceinline__ void qmm_store(const GemmParams &p, int slot, int z, 
     reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = v;
 }
 
-__global__ __launch_bounds__(256) void qmm_reduce_kernel(GemmParams p, int slot, int KS) {
+// all KS loads of a thread issued before the first add; V = 4 when rows are
+// a multiple of 4 columns (16-byte partial loads), the y store then one 8- or
+// 16-byte store when y rows are 16-byte aligned (yvec)
+template <int KS, int V>
+__global__ __launch_bounds__(256) void qmm_reduce_kernel(GemmParams p, int slot, int yvec) {
+  typedef float fv __attribute__((ext_vector_type(V)));
   const float *part = g_qmm_part + (size_t)slot * kQSlotFloats;
-  const size_t MN = (size_t)p.M * p.N;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-    float v[16];
+  const size_t MN = (size_t)p.M * p.N, nv = MN / V;
+  for (size_t v = (size_t)blockIdx.x * 256 + threadIdx.x; v < nv; v += (size_t)gridDim.x * 256) {
+    const size_t i = v * V;
+    fv t[KS];
 #pragma unroll
-    for (int z = 0; z < 16; ++z) v[z] = z < KS ? part[z * MN + i] : 0.f;
-    float s = v[0];
+    for (int z = 0; z < KS; ++z) t[z] = __builtin_nontemporal_load(reinterpret_cast<const fv *>(part + z * MN + i));
+    fv s = t[0];
 #pragma unroll
-    for (int z = 1; z < 16; ++z) s += z < KS ? v[z] : 0.f;  // in k order
-    const int m = (int)(i / p.N), n = (int)(i % p.N);
-    if (p.y_bf16)
-      reinterpret_cast<__bf16 *>(p.y)[(size_t)m * p.y_stride + n] = (__bf16)s;
-    else
-      reinterpret_cast<float *>(p.y)[(size_t)m * p.y_stride + n] = s;
+    for (int z = 1; z < KS; ++z) s += t[z];  // in k order
+    const size_t o = (i / p.N) * p.y_stride + i % p.N;
+    if (p.y_bf16) {
+      __bf16 *y = reinterpret_cast<__bf16 *>(p.y) + o;
+      if constexpr (V == 4) {
+        if (yvec) {
+          typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<b4 *>(y) = b4{(__bf16)s[0], (__bf16)s[1], (__bf16)s[2], (__bf16)s[3]};
+          continue;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[e] = (__bf16)s[e];
+    } else {
+      float *y = reinterpret_cast<float *>(p.y) + o;
+      if constexpr (V == 4) {
+        if (yvec) {
+          *reinterpret_cast<fv *>(y) = s;
+          continue;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[e] = s[e];
+    }
+  }
+}
+
+template <int V>
+static void launch_qmm_reduce(const GemmParams &p, int slot, int KS, hipStream_t st) {
+  const size_t nv = (size_t)p.M * p.N / V;
+  const dim3 grid((unsigned)std::min<size_t>((nv + 255) / 256, 4096));
+  const int es = p.y_bf16 ? 2 : 4;
+  const int yvec = (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && ((long long)p.y_stride * es) % 16 == 0;
+  switch (KS) {
+#define LH_QRED(k) \
+  case k: hipLaunchKernelGGL((qmm_reduce_kernel<k, V>), grid, dim3(256), 0, st, p, slot, yvec); break;
+    LH_QRED(2) LH_QRED(3) LH_QRED(4) LH_QRED(5) LH_QRED(6) LH_QRED(7) LH_QRED(8) LH_QRED(9)
+    LH_QRED(10) LH_QRED(11) LH_QRED(12) LH_QRED(13) LH_QRED(14) LH_QRED(15) LH_QRED(16)
+#undef LH_QRED
+    default: break;
   }
 }
 
@@ -450,26 +490,67 @@ __device__ __forceinline__ void q3_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(256) void qmm_reduce_multi_kernel(QmmMulti p, int slot, int KS) {
+// sums the KS partial slices of a split product in k order (z = 0, 1, ...):
+// all KS loads of a thread are issued before the first add. V = 4: a thread
+// takes 4 consecutive columns of one row with 16-byte loads (partial rows and
+// every matrix's first column a multiple of 4 columns, vec bit 1), so the 4
+// never cross a matrix or a row; the y store is then one 8- or 16-byte store
+// when y rows are 16-byte aligned (vec bit 0).
+template <int KS, int V>
+__global__ __launch_bounds__(256) void qmm_reduce_multi_kernel(QmmMulti p, int slot) {
+  typedef float fv __attribute__((ext_vector_type(V)));
   const float *part = g_qmm_part + (size_t)slot * kQSlotFloats;
-  const size_t MN = (size_t)p.M * p.part_N;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-    float v[16];
+  const size_t MN = (size_t)p.M * p.part_N, nv = MN / V;
+  for (size_t v = (size_t)blockIdx.x * 256 + threadIdx.x; v < nv; v += (size_t)gridDim.x * 256) {
+    const size_t i = v * V;
+    fv t[KS];
 #pragma unroll
-    for (int z = 0; z < 16; ++z) v[z] = z < KS ? part[z * MN + i] : 0.f;
-    float s = v[0];
+    for (int z = 0; z < KS; ++z) t[z] = __builtin_nontemporal_load(reinterpret_cast<const fv *>(part + z * MN + i));
+    fv s = t[0];
 #pragma unroll
-    for (int z = 1; z < 16; ++z) s += z < KS ? v[z] : 0.f;  // in k order
+    for (int z = 1; z < KS; ++z) s += t[z];  // in k order
     const int m = (int)(i / p.part_N), c = (int)(i % p.part_N);
     int mi = 0;
 #pragma unroll
-    for (int t = 1; t < kQMultiMax; ++t) mi = t < p.n && c >= p.m[t].col0 ? t : mi;
+    for (int u = 1; u < kQMultiMax; ++u) mi = u < p.n && c >= p.m[u].col0 ? u : mi;
     const QmmMat &q = p.m[mi];
-    const int n = c - q.col0;
-    if (p.y_bf16)
-      reinterpret_cast<__bf16 *>(q.y)[(size_t)m * q.y_stride + n] = (__bf16)s;
-    else
-      reinterpret_cast<float *>(q.y)[(size_t)m * q.y_stride + n] = s;
+    const size_t o = (size_t)m * q.y_stride + (c - q.col0);
+    if (p.y_bf16) {
+      __bf16 *y = reinterpret_cast<__bf16 *>(q.y) + o;
+      if constexpr (V == 4) {
+        if (p.vec & 1) {
+          typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<b4 *>(y) = b4{(__bf16)s[0], (__bf16)s[1], (__bf16)s[2], (__bf16)s[3]};
+          continue;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[e] = (__bf16)s[e];
+    } else {
+      float *y = reinterpret_cast<float *>(q.y) + o;
+      if constexpr (V == 4) {
+        if (p.vec & 1) {
+          *reinterpret_cast<fv *>(y) = s;
+          continue;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[e] = s[e];
+    }
+  }
+}
+
+template <int V>
+static void launch_qmm_reduce_multi(const QmmMulti &p, int slot, int KS, hipStream_t st) {
+  const size_t nv = (size_t)p.M * p.part_N / V;
+  const dim3 grid((unsigned)std::min<size_t>((nv + 255) / 256, 4096));
+  switch (KS) {
+#define LH_QRED(k) \
+  case k: hipLaunchKernelGGL((qmm_reduce_multi_kernel<k, V>), grid, dim3(256), 0, st, p, slot); break;
+    LH_QRED(2) LH_QRED(3) LH_QRED(4) LH_QRED(5) LH_QRED(6) LH_QRED(7) LH_QRED(8) LH_QRED(9)
+    LH_QRED(10) LH_QRED(11) LH_QRED(12) LH_QRED(13) LH_QRED(14) LH_QRED(15) LH_QRED(16)
+#undef LH_QRED
+    default: break;
   }
 }
 
@@ -1016,9 +1097,10 @@ static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
-  const size_t mn = (size_t)M * cols;
-  const int rblocks = (int)std::min<size_t>((mn + 255) / 256, 4096);
-  hipLaunchKernelGGL(qmm_reduce_multi_kernel, dim3(rblocks), dim3(256), 0, st, p, slot, split);
+  if (p.vec & 2)
+    launch_qmm_reduce_multi<4>(p, slot, split, st);
+  else
+    launch_qmm_reduce_multi<1>(p, slot, split, st);
   return hipGetLastError();
 }
 
@@ -1094,9 +1176,10 @@ hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, i
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || split == 1) return e;
-  const size_t mn = (size_t)M * m.O;
-  const int rblocks = (int)std::min<size_t>((mn + 255) / 256, 4096);
-  hipLaunchKernelGGL(qmm_reduce_kernel, dim3(rblocks), dim3(256), 0, st, p, slot, split);
+  if ((m.O & 3) == 0)
+    launch_qmm_reduce<4>(p, slot, split, st);
+  else
+    launch_qmm_reduce<1>(p, slot, split, st);
   return hipGetLastError();
 }
 

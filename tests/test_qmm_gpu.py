@@ -178,6 +178,19 @@ MULTI_CASES = [
 ]
 
 
+KSLAB_CASES = [
+    # grids short of 192 tiles of 256 x 128 with K a multiple of 1024: 64 x 64
+    # tiles, K split across the 8 waves of a block (2, 4 or 6 steps per wave)
+    (300, [2048], 1024, 5, 32, True),
+    (270, [200, 130], 2048, 6, 128, False),        # ragged N and M
+    (511, [1000], 3072, 8, 64, False),
+    (256, [64, 96, 40], 1024, 4, 64, True),
+    (257, [520, 33], 2048, 4, 32, False),          # one row in the last M tile
+]
+
+MULTI_CASES += KSLAB_CASES
+
+
 @pytest.mark.parametrize("M,Os,I,bits,gs,fp16", MULTI_CASES, ids=lambda v: str(v))
 def test_qmm_multi_matches_oracle(gpu, M, Os, I, bits, gs, fp16):
     """Matrices that share x in one product launch (logan_hip_affine_qmm_multi):
