@@ -204,12 +204,18 @@ __global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, M
 #ifndef MOE_GU
 #define MOE_GU 4
 #endif
+// Two block shapes: 8 waves (128 rows, one block per CU) for large batches,
+// 4 waves (64 rows) with two blocks resident per CU for batches of up to
+// kMGuSmallB tokens, whose few tiles per expert leave the chip short of
+// blocks (config 4 B = 32: 140 -> 128 µs per 5-bit layer; the B = 512
+// prefill chunk 2 % slower with 4 waves)
 #ifndef MOE_GU_WAVES
 #define MOE_GU_WAVES 8
 #endif
 #ifndef MOE_GU_MINW
-#define MOE_GU_MINW 1  // minimum waves per SIMD (register cap)
+#define MOE_GU_MINW 1  // minimum waves per SIMD (register cap) of the 8-wave shape
 #endif
+constexpr int kMGuSmallB = 128;
 
 // scale/bias words of GU steps for one lane's row: with 64-code groups the GU
 // consecutive u16 come in one load
@@ -257,7 +263,7 @@ struct GuBatch {
 };
 
 template <int BITS, int GU, int WAVES, bool GS64, bool FP16>
-__global__ __launch_bounds__(WAVES * 64, MOE_GU_MINW) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
+__global__ __launch_bounds__(WAVES * 64, WAVES <= 4 ? 2 : MOE_GU_MINW) void moe_gateup_mfma_kernel(MoeArgs a, MoeMWs w, int ipt) {
   __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
   constexpr int NT = WAVES * 64;
   constexpr int RPB = 16 * WAVES;
@@ -615,11 +621,10 @@ bool moe_mfma_supported(const MoeArgs &a) {
   return true;
 }
 
-template <int BITS>
-static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
+template <int BITS, int WV>
+static hipError_t moe_gateup_launch(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
   const int kmax = a.inter > a.sinter ? a.inter : a.sinter;
   {
-    constexpr int WV = MOE_GU_WAVES;
     const int ipt = (kmax + 16 * WV - 1) / (16 * WV);
     // one aligned load of GU consecutive u16 scale (bias) words per batch
     const bool gs64 = a.gate.m.gs == 64 && (!a.sgate.m.w || a.sgate.m.gs == 64) &&
@@ -632,8 +637,15 @@ static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t s
       if (gs64) hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, true, false>), grid, block, 0, st, a, w, ipt);
       else hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, false, false>), grid, block, 0, st, a, w, ipt);
     }
-    if (hipGetLastError() != hipSuccess) return -1;
   }
+  return hipGetLastError();
+}
+
+template <int BITS>
+static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
+  const hipError_t ge = a.B <= kMGuSmallB ? moe_gateup_launch<BITS, 4>(a, w, st)
+                                          : moe_gateup_launch<BITS, MOE_GU_WAVES>(a, w, st);
+  if (ge != hipSuccess) return -1;
   {
     const int ipt = (a.D + 127) / 128;
     if (a.down.m.fp16)

@@ -367,7 +367,8 @@ def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
                                                 (8, 5, False, True), (4, 40, True, True),
                                                 (8, 33, True, False), (5, 40, True, True),
                                                 (6, 32, True, True), (5, 3, False, False),
-                                                (6, 17, False, True)])
+                                                (6, 17, False, True),
+                                                (5, 136, True, True)])   # 8-wave gate/up blocks
 def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
     """The token-batch MFMA path (forced for every B) against the oracle:
     routing bit-exact, outputs at f32-accumulation level; Zipf routes put
