@@ -182,11 +182,12 @@ typedef struct LoganHipAffine {
 /* y[M][y_stride] = x[M][x_stride] . W^T  (matmul_mlx_affine_storage,
  * logan-qwen4/src/lib.rs:3729-3764, per activation row). x bf16, y bf16 or
  * f32 (y_dtype). f32 accumulation. 1 ok, 0 unsupported geometry, -1 launch
- * failure. With M >= 3 (I a multiple of 512, groups of 64k) the product is
- * split over K and its partial sums pass through one of 4 library-owned
- * scratch slots taken round-robin per call; calls on one device whose
- * executions overlap (different streams) therefore stay correct while at
- * most 4 of them are in flight. */
+ * failure. With M >= 3 (I a multiple of 512, groups of 64k) the product may
+ * be split over K, its partial sums passing through one of 4 library-owned
+ * scratch slots: a call waits on the device (an event wait on its stream)
+ * for the previous user of its slot, so calls on any number of streams stay
+ * correct. Calls made inside a stream capture skip that wait: replays of a
+ * captured graph are ordered by their own stream only. */
 int logan_hip_affine_gemv(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                           int y_stride, int y_dtype, void *stream);
 
@@ -223,7 +224,9 @@ int logan_hip_affine_gemv_swiglu(const LoganHipAffine *gate, const LoganHipAffin
  * rounded to bf16 (RNE) before bf16 x bf16 products are accumulated in f32.
  * x bf16 [M][x_stride], y bf16 (RNE) or f32. I must be a multiple of 64 and
  * group_size a multiple of 32. 1 ok, 0 unsupported geometry, -1 launch
- * failure. */
+ * failure. Grids short of blocks split K and pass partial sums through one
+ * of 2 library-owned scratch slots, ordered across streams as in
+ * logan_hip_affine_gemv (the same capture caveat applies). */
 int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_stride, void *y,
                          int y_stride, int y_dtype, void *stream);
 
@@ -233,7 +236,8 @@ int logan_hip_affine_qmm(const LoganHipAffine *w, const void *x, int M, int x_st
  * column tiles form one grid (the reference encodes its batch of products
  * into one command buffer, backend_metal.mm:2290-2493); otherwise one launch
  * per matrix. Every matrix has the same I, bits, group_size and aux type. 1
- * ok, 0 unsupported, -1 launch failure. */
+ * ok, 0 unsupported, -1 launch failure. Split grids share
+ * logan_hip_affine_qmm's scratch slots and their cross-stream ordering. */
 int logan_hip_affine_qmm_multi(const LoganHipAffine *ws, int count, const void *x, int M,
                                int x_stride, void *const *ys, int y_dtype, void *stream);
 
@@ -318,7 +322,8 @@ size_t logan_hip_llama_workspace_bytes(const LoganHipLlamaLayer *L, int pos);
 
 /* The decode layer of logan_hip_host_llama_layer on device buffers: x[D] f32
  * in place, K[pos] and V[pos] written to the caches (pos < cache_tokens),
- * attention over positions 0..pos. 1 ok, 0 unsupported, -1 launch failure. */
+ * attention over positions 0..pos. x, the two norm weights and ws must be
+ * 16-byte aligned. 1 ok, 0 unsupported (or unaligned), -1 launch failure. */
 int logan_hip_llama_layer(const LoganHipLlamaLayer *L, float *x, int pos, void *ws, size_t ws_bytes,
                           void *stream);
 

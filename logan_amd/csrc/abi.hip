@@ -1448,6 +1448,10 @@ int logan_hip_llama_layer(const LoganHipLlamaLayer *L, float *x, int pos, void *
   lh::LlamaDims dims;
   if (!x || !ws || pos < 0 || !llama_from(L, mats, dims)) return 0;
   if (!L->in_norm || !L->post_norm || !L->k_cache || !L->v_cache || pos >= L->cache_tokens) return 0;
+  // x and the norm weights are read as float4, the workspace's activation
+  // pairs as 16-byte vectors
+  const auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!a16(x) || !a16(L->in_norm) || !a16(L->post_norm) || !a16(ws)) return 0;
   if (ws_bytes < lh::llama_workspace_bytes(dims, pos + 1)) return 0;
   return rc_from(lh::launch_llama_layer(mats, L->in_norm, L->post_norm, dims, x, L->k_cache,
                                         L->v_cache, pos, ws, reinterpret_cast<hipStream_t>(stream)));

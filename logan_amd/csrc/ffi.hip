@@ -162,7 +162,7 @@ int32_t metalio_active(void) { return 0; }
 void metalio_shutdown(void) {}
 int32_t metalio_file_add(const char *) { return -1; }
 int32_t metalio_slot_alloc(size_t) { return -1; }
-int32_t metalio_slot_alloc_alias(void *, size_t) { return 0; }
+int32_t metalio_slot_alloc_alias(void *, size_t) { return -1; }
 void metalio_slot_free(int32_t) {}
 void *metalio_slot_ptr(int32_t) { return nullptr; }
 size_t metalio_slot_bytes(int32_t) { return 0; }

@@ -57,10 +57,10 @@ __device__ __forceinline__ uint32_t code_of(const uint32_t (&w)[DeqGeom<BITS>::D
 }
 
 // Split-K: the blocks of one tile that share a k range write f32 partial
-// sums part[z][m][n] into one of kQSlots module-scope slots (taken round-robin
-// per call, so calls whose executions overlap on one device stay correct
-// while at most kQSlots are in flight); qmm_reduce_kernel adds them in z
-// order and writes y. slot < 0: one k range, y written directly.
+// sums part[z][m][n] into one of kQSlots module-scope slots (a SlotRing
+// lease: calls on any streams that would overlap on a slot are ordered on
+// the device); qmm_reduce_kernel adds them in z order and writes y.
+// slot < 0: one k range, y written directly.
 constexpr int kQSlots = 2;
 constexpr size_t kQSlotFloats = size_t(1) << 23;  // 32 MB per slot
 static __device__ __align__(256) float g_qmm_part[kQSlots * kQSlotFloats];
@@ -242,7 +242,7 @@ constexpr int kQ2Ld = 72;    // bf16 per LDS row: 64 + 8 pad
 #endif
 constexpr int kQ2MinTiles = QMM_MIN_TILES;
 constexpr int kQTargetBlocks = 512;  // about two blocks per CU
-static std::atomic<unsigned> g_qmm_next{0};
+static SlotRing g_qmm_slots(kQSlots);
 
 template <int BITS>
 __global__ __launch_bounds__(256) void affine_qmm128_kernel(GemmParams p, int mtiles, int ntiles,
@@ -1076,7 +1076,12 @@ static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int 
     split *= 2;
   const int ksteps = (ksteps_all + split - 1) / split;
   split = (ksteps_all + ksteps - 1) / ksteps;
-  const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
+  SlotRing::Lease lease;
+  if (split > 1) {
+    const hipError_t le = g_qmm_slots.take(st, lease);
+    if (le != hipSuccess) return le;
+  }
+  const int slot = split > 1 ? lease.slot() : -1;
   const dim3 grid(((tiles + 7) / 8) * 8 * mt, split);
   if (split > 1) {
     switch (ms[0].bits) {
@@ -1101,7 +1106,9 @@ static hipError_t launch_qmm256(const DevMat *ms, int n, const uint16_t *x, int 
     launch_qmm_reduce_multi<4>(p, slot, split, st);
   else
     launch_qmm_reduce_multi<1>(p, slot, split, st);
-  return hipGetLastError();
+  e = hipGetLastError();
+  const hipError_t le = lease.done();
+  return e != hipSuccess ? e : le;
 }
 
 hipError_t launch_affine_qmm_multi(const DevMat *ms, int n, const uint16_t *x, int x_stride, int M,
@@ -1156,7 +1163,12 @@ hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, i
     split *= 2;
   const int ksteps = (ksteps_all + split - 1) / split;
   split = (ksteps_all + ksteps - 1) / ksteps;
-  const int slot = split > 1 ? (int)(g_qmm_next.fetch_add(1, std::memory_order_relaxed) % kQSlots) : -1;
+  SlotRing::Lease lease;
+  if (split > 1) {
+    const hipError_t le = g_qmm_slots.take(st, lease);
+    if (le != hipSuccess) return le;
+  }
+  const int slot = split > 1 ? lease.slot() : -1;
   if (big) {
     const dim3 grid(((nt + 7) / 8) * 8 * mt, split);
     switch (m.bits) {
@@ -1180,7 +1192,9 @@ hipError_t launch_affine_qmm(const DevMat &m, const uint16_t *x, int x_stride, i
     launch_qmm_reduce<4>(p, slot, split, st);
   else
     launch_qmm_reduce<1>(p, slot, split, st);
-  return hipGetLastError();
+  e = hipGetLastError();
+  const hipError_t le = lease.done();
+  return e != hipSuccess ? e : le;
 }
 
 }  // namespace lh

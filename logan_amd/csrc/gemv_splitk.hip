@@ -15,9 +15,9 @@
 // measured slower: 87.9 against 84.4 us for a config-2 layer at M = 8, since
 // one block then reads every partial of its rows in series.)
 //
-// Scratch: kSkSlots module-scope slots of kSkSlotFloats floats; the host
-// picks slots round-robin, so launches that overlap on one device do not
-// share a slot unless more than kSkSlots of them are in flight at once.
+// Scratch: kSkSlots module-scope slots of kSkSlotFloats floats, leased from
+// a SlotRing: launches on any streams that would overlap on a slot are
+// ordered on the device.
 #include <atomic>
 #include <type_traits>
 
@@ -726,7 +726,7 @@ static void splitk_launch_bits(const SplitParams &p, bool fp16, bool aux8, hipSt
   else splitk_launch_t<BITS, 2>(p, fp16, aux8, st);
 }
 
-static std::atomic<unsigned> g_sk_next{0};
+static SlotRing g_sk_slots(kSkSlots);
 
 hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride, int M, void *y,
                                 int y_stride, int y_bf16, hipStream_t st) {
@@ -744,7 +744,12 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
   p.gsteps = m.gs / 64;
   p.x_stride = x_stride;
   p.M = M;
-  p.slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
+  SlotRing::Lease lease;
+  {
+    const hipError_t le = g_sk_slots.take(st, lease);
+    if (le != hipSuccess) return le;
+  }
+  p.slot = lease.slot();
   p.part_off = 0;
   // 16-byte runs of eight u16 scale/bias words per 512 codes
   const bool aux8 = m.gs == 64 && (m.ng % 8) == 0 &&
@@ -762,7 +767,9 @@ hipError_t launch_affine_splitk(const DevMat &m, const uint16_t *x, int x_stride
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.slot, m.I / kSkKc, M,
                      m.O, y, y_stride, y_bf16);
-  return hipGetLastError();
+  e = hipGetLastError();
+  const hipError_t le = lease.done();
+  return e != hipSuccess ? e : le;
 }
 
 template <int BITS, int MT>
@@ -808,7 +815,12 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
   SplitMulti mp{};
   ReduceMulti r{};
   const int KS = ms[0].I / kSkKc;
-  const int slot = (int)(g_sk_next.fetch_add(1, std::memory_order_relaxed) % kSkSlots);
+  SlotRing::Lease lease;
+  {
+    const hipError_t le = g_sk_slots.take(st, lease);
+    if (le != hipSuccess) return le;
+  }
+  const int slot = lease.slot();
   bool aux8 = true;
   size_t off = 0;
   for (int i = 0; i < n; ++i) {
@@ -855,7 +867,9 @@ hipError_t launch_affine_splitk_multi(const DevMat *ms, int n, const uint16_t *x
   size_t blocks = ((size_t)(swiglu ? r.start[1] : r.start[n]) + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(splitk_reduce_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, st, r);
-  return hipGetLastError();
+  e = hipGetLastError();
+  const hipError_t le = lease.done();
+  return e != hipSuccess ? e : le;
 }
 
 // The full-K pair serves gate/up pairs of one geometry whose 64-row blocks

@@ -7,6 +7,52 @@
 
 namespace lh {
 
+// ---- scratch slots shared by launches on any stream of one device ----
+// Split products write partial sums into a module-scope slot with one kernel
+// and add them up with a second on the same stream. SlotRing hands the slots
+// out round-robin; a lease holds its slot's host lock from take() until
+// done(), makes its stream wait (on the device) for the event the slot's
+// previous user recorded after its last kernel on the slot, and done()
+// records the lease's own event there. Launches on different streams
+// therefore never overlap on a slot, whatever their number. Inside a stream
+// capture neither the wait nor the record is made: a captured graph's slot
+// is fixed at capture time and its replays are ordered by their own stream
+// only (a replay that overlaps another call on another stream may share the
+// slot).
+class SlotRing {
+ public:
+  static constexpr int kMaxSlots = 8, kMaxDevices = 16;
+  explicit SlotRing(int nslots) : n_(nslots) {}
+  class Lease {
+   public:
+    Lease() = default;
+    Lease(const Lease &) = delete;
+    Lease &operator=(const Lease &) = delete;
+    ~Lease() { release(true); }
+    int slot() const { return slot_; }
+    // after the last kernel that touches the slot: record, unlock (the
+    // destructor does the same for a lease left held on an error path)
+    hipError_t done() { return release(true); }
+
+   private:
+    friend class SlotRing;
+    hipError_t release(bool record);
+    SlotRing *ring_ = nullptr;
+    int dev_ = 0, slot_ = -1;
+    bool capturing_ = false;
+    hipStream_t st_ = nullptr;
+  };
+  // takes the next slot for stream st (blocks while another host thread
+  // holds it); on failure lease.slot() < 0
+  hipError_t take(hipStream_t st, Lease &lease);
+
+ private:
+  struct Dev;
+  Dev *dev(int d);
+  int n_;
+  Dev *devs_[kMaxDevices] = {};
+};
+
 // One MLX-affine matrix resident in device memory.
 struct DevMat {
   const uint8_t *w;     // rows * row_bytes, 16-byte aligned

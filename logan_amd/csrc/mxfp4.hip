@@ -16,6 +16,21 @@
 // groups l, l + LANES, ..., the next group's loads in flight while the
 // current one is used. Up to kMx4MaxDescs matrices (each with its own x and
 // y) share one launch.
+//
+// The group-scaled sums equal the reference's per-element sum
+// (acc += x * MX4[code] * scale in column order, lib.rs:2948-2961; planes
+// added in order, :2985-3038) up to f32 rounding order only while no term or
+// partial sum can reach the overflow range and scale and x are finite. A row
+// with a group that breaks this (scale byte 255, i.e. scale = +inf, where a
+// zero code or zero x gives NaN and terms of both signs give NaN; terms or
+// sums that may overflow, whose inf/NaN outcome depends on the summation
+// order; inf/NaN activations) is recomputed by one lane in the reference's
+// own order, bit for bit. The test uses the group's largest activation
+// exponent e (bf16 field, |x| < 2^(e - 126)) and scale byte s: each term is
+// below 2^(e + s - 250), a 32-term group below 2^(e + s - 245), the row's
+// C groups and at most 3 planes below 2^(e + s - 243 + ceil(log2 C)), so
+// e + s <= 370 - ceil(log2 C) keeps every partial sum, in any order, under
+// 2^127.
 #include "affine_dev.hpp"
 #include "lh_internal.hpp"
 
@@ -23,6 +38,7 @@ namespace lh {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMx4U = 4;  // rows per team
 
@@ -45,7 +61,53 @@ template <bool XF>
 struct Mx4X {
   uint32_t hi[16];
   uint32_t lo[XF ? 16 : 1];
+  uint32_t xe;  // largest bf16 exponent field among the group's hi halves
 };
+
+// largest exponent field of 32 bf16 values held as 16 pairs (an upper bound
+// for f32 activations: RNE to bf16 never lowers the exponent)
+__device__ __forceinline__ uint32_t mx4_max_exp(const uint32_t (&h)[16]) {
+  uint32_t m = h[0] & 0x7fff7fffu;
+#pragma unroll
+  for (int k = 1; k < 16; ++k)
+    m = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
+                                         __builtin_bit_cast(u16x2_t, m),
+                                         __builtin_bit_cast(u16x2_t, h[k] & 0x7fff7fffu)));
+  return max(m & 0xffffu, m >> 16) >> 7;
+}
+
+// one row the reference's way (flagged rows only): each term
+// fl(fl(x * MX4) * scale) added in column order, plane results added in
+// plane order; x re-read from memory (the f32 original, not its bf16 halves)
+template <bool XF>
+__device__ __noinline__ float mx4_row_exact(const Mx4Desc d, int row) {
+  // no FMA contraction: a product must round (to inf when it overflows)
+  // before it is added, as the reference's separate multiply and add do
+#pragma clang fp contract(off)
+  const int rb = d.I >> 1, ng = d.I >> 5;
+  float tot = 0.f;
+  for (int p = 0; p < d.planes; ++p) {
+    const uint8_t *wr = d.w + (size_t)p * d.wplane + (size_t)row * rb;
+    const uint8_t *sr = d.sc + (size_t)p * d.splane + (size_t)row * ng;
+    float acc = 0.f;
+    for (int j = 0; j < rb; ++j) {
+      const f32x2_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)wr[j], 1.0f, 0);
+      const float scale = e8m0(sr[j >> 4]);
+      float x0, x1;
+      if constexpr (XF) {
+        x0 = reinterpret_cast<const float *>(d.x)[2 * j];
+        x1 = reinterpret_cast<const float *>(d.x)[2 * j + 1];
+      } else {
+        x0 = bf16_to_f32(reinterpret_cast<const uint16_t *>(d.x)[2 * j]);
+        x1 = bf16_to_f32(reinterpret_cast<const uint16_t *>(d.x)[2 * j + 1]);
+      }
+      acc = acc + (x0 * v[0]) * scale;
+      acc = acc + (x1 * v[1]) * scale;
+    }
+    tot = p == 0 ? acc : tot + acc;
+  }
+  return tot;
+}
 
 template <bool XF>
 __device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
@@ -64,6 +126,7 @@ __device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
         o.lo[2 * v + q / 2] = l0 | (l1 << 16);
       }
     }
+    o.xe = mx4_max_exp(o.hi);
   } else {
     const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + 32 * c);
 #pragma unroll
@@ -74,6 +137,7 @@ __device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
       o.hi[4 * v + 2] = t.z;
       o.hi[4 * v + 3] = t.w;
     }
+    o.xe = mx4_max_exp(o.hi);
   }
 }
 
@@ -93,6 +157,11 @@ __global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
   float tot[kMx4U];
 #pragma unroll
   for (int u = 0; u < kMx4U; ++u) tot[u] = 0.f;
+  // rows the group-scaled sums may not serve (see the file comment)
+  bool risky[kMx4U];
+#pragma unroll
+  for (int u = 0; u < kMx4U; ++u) risky[u] = false;
+  const uint32_t lim = 370u - (C > 1 ? 32u - (uint32_t)__clz(C - 1) : 0u);
   for (int p = 0; p < d.planes; ++p) {
     const uint8_t *wp = d.w + (size_t)p * d.wplane;
     const uint8_t *sp = d.sc + (size_t)p * d.splane;
@@ -126,6 +195,7 @@ __global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
           for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.lo[k], g);
         }
         acc[u] = fmaf(g, e8m0(s[u]), acc[u]);  // g * 2^(s - 127) is exact
+        risky[u] = risky[u] || s[u] == 255u || xv.xe == 255u || s[u] + xv.xe > lim;
       }
     };
     for (; c < C; c += 2 * LANES) {
@@ -143,6 +213,12 @@ __global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
       tot[u] += team_sum<LANES>(acc[u]);
       acc[u] = 0.f;
     }
+  }
+  const uint64_t team_mask = (LANES == 64 ? ~0ull : ((1ull << LANES) - 1)) << ((threadIdx.x & 63) & ~(LANES - 1));
+#pragma unroll
+  for (int u = 0; u < kMx4U; ++u) {
+    const bool redo = (__ballot(risky[u]) & team_mask) != 0ull;
+    if (redo && lane == 0 && r0 + u < d.O) tot[u] = mx4_row_exact<XF>(d, r0 + u);
   }
   if (lane == 0) {
 #pragma unroll

@@ -71,8 +71,14 @@ __device__ __forceinline__ float group_sum_f32(float v) {
 
 // ---------------------------------------------------------------- routing
 
+// Order-preserving 16-bit key of a bf16 value. Every NaN, either sign, maps
+// to the top key: rank 0 is then NaN, its maximum fails tie_global's
+// finiteness test and the token takes route_exact, which reproduces the
+// reference's NaN sum (ranks 0..k-1 = experts 0..k-1, NaN weights). A NaN
+// left below the selected ranks would skip that path on the bf16 shortcut.
 __device__ __forceinline__ uint32_t ord16(uint32_t b) {
-  if (b == 0x8000u) b = 0;  // -0 == +0
+  if ((b & 0x7fffu) > 0x7f80u) return 0xffffu;  // NaN
+  if (b == 0x8000u) b = 0;                     // -0 == +0
   return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
 }
 
@@ -106,9 +112,11 @@ __device__ __forceinline__ int sel_expert(uint32_t key) { return (int)(0xffffu -
 
 // ---- f32 logits: 64-bit keys (ordered f32 << 32 | ~index) -----------------
 
+// f32 counterpart of ord16, NaN (either sign) first as there
 __device__ __forceinline__ uint32_t ord32f(float f) {
   uint32_t u = __float_as_uint(f);
-  if (u == 0x80000000u) u = 0;  // -0 == +0
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN
+  if (u == 0x80000000u) u = 0;                            // -0 == +0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 

@@ -150,3 +150,26 @@ def test_declines_without_a_device(so):
     assert lib.logan_hip_shared_expert(0, 0, d, 3, x, y, 64, 64) == 0
     assert lib.logan_hip_matmul_multi(x, 1, d, 0) == 0
     assert lib.logan_hip_matmul_multi(x, 1, d, 17) == 0
+
+
+def test_integration_build_rs_builds_every_source():
+    """INTEGRATION.md's build.rs compiles what logan_amd/build.py compiles:
+    the same source directory and extension filter (so every csrc/*.hip,
+    not a fixed list that can drift), include path and hipcc flags."""
+    from logan_amd import build
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```rust\n(.*?)```", text, flags=re.S)
+    snip = [b for b in blocks if "build.rs" in b]
+    assert len(snip) == 1
+    rs = snip[0]
+    consts = dict(re.findall(r'const (CSRC|INCLUDE): &str = "([^"]+)";', rs))
+    assert (ROOT / consts["CSRC"]).resolve() == build.CSRC
+    assert (ROOT / consts["INCLUDE"]).resolve() == build.INCLUDE
+    flags = re.search(r"const HIPFLAGS: &\[&str\] = &\[(.*?)\];", rs, flags=re.S).group(1)
+    assert re.findall(r'"([^"]+)"', flags) == build.HIPFLAGS
+    # sources: read_dir(CSRC) filtered on the .hip extension, as build.py's glob
+    assert "fs::read_dir(CSRC)" in rs and 'x == "hip"' in rs
+    assert ".args(HIPFLAGS)" in rs and ".arg(INCLUDE)" in rs
+    srcs = sorted(p.name for p in build.CSRC.glob("*.hip"))
+    assert "ffi.hip" in srcs and "abi.hip" in srcs and len(srcs) >= 10

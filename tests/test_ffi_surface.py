@@ -111,8 +111,8 @@ IMPLEMENTED = {"coli_metal_init", "coli_metal_available", "coli_metal_profile_se
 ADVISORY = {"coli_metal_wrap_stats", "coli_metal_register", "coli_metal_unregister",
             "coli_metal_ptr_registered"}
 # MetalIO failure values as its Rust callers test them (lib.rs:2890-2990, :3050, :3301)
-MINUS_ONE = {"metalio_file_add", "metalio_slot_alloc", "metalio_loadv", "metalio_wait",
-             "metalio_batch_wait", "metalio_probe"}
+MINUS_ONE = {"metalio_file_add", "metalio_slot_alloc", "metalio_slot_alloc_alias",
+             "metalio_loadv", "metalio_wait", "metalio_batch_wait", "metalio_probe"}
 
 
 def test_every_declining_entry_declines(so):

@@ -233,6 +233,12 @@ def test_device_llama_layer_rejects(gpu):
     x = torch.zeros(D, dtype=torch.float32, device="cuda")
     with pytest.raises(LoganHipError):  # position beyond the cache
         llama_layer(layer, x, 4)
+    xo = torch.zeros(D + 1, dtype=torch.float32, device="cuda")[1:]
+    with pytest.raises(LoganHipError):  # x not 16-byte aligned (read as float4)
+        llama_layer(layer, xo, 0)
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(LoganHipError):  # workspace not 16-byte aligned
+        llama_layer(layer, x, 0, workspace=ws[8:])
     layer.head_dim = 512  # more than 256
     with pytest.raises(LoganHipError):
         llama_layer(layer, x, 0)

@@ -48,16 +48,29 @@ def dev_mx(torch, w, sc, O, I):
                        torch.from_numpy(np.ascontiguousarray(sc)).cuda(), O, I, w.shape[0])
 
 
+def same_bits_or_nan(got, want):
+    """f32 arrays equal bit for bit, except that a NaN only has to be a NaN
+    (its payload and sign are the platform's: 0 * inf is 0x7FC00000 on the
+    GPU, 0xFFC00000 on x86)."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan = np.isnan(want)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
 def test_mxfp4_dequant_bit_exact(gpu):
-    """The decode instruction against the oracle, every code under scale bytes
-    1..254 (the golden canonical-order bytes first), sign of zero included."""
+    """The decode instruction against the oracle, every code under every scale
+    byte 0..255 (the golden canonical-order bytes first), sign of zero
+    included; byte 0 is a zero scale, byte 255 an infinite one (zero codes
+    then decode to NaN, as the reference's product gives)."""
     import torch
 
     from logan_amd.device import mxfp4_dequant
 
     rng = np.random.default_rng(7)
     O, I = 96, 512
-    w, sc = make_mx(rng, O, I, 1, 1, 255)
+    w, sc = make_mx(rng, O, I, 1, 0, 256)
+    sc[0, 1:, :2] = [0, 255]  # every row holds both extremes
     c = GOLDEN["mxfp4_order"]
     w[0, 0, :8] = c["bytes"]
     sc[0, 0, 0] = c["scale_byte"]
@@ -70,10 +83,11 @@ def test_mxfp4_dequant_bit_exact(gpu):
         for j in range(I):
             b = int(w[0, r, j // 2])
             want[r, j] = lib.lo_mxfp4_value(b & 0xF if j % 2 == 0 else b >> 4, int(sc[0, r, j // 32]))
-    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.isnan(want).any() and np.isinf(want).any() and (want[:, :32] == 0).any()
+    same_bits_or_nan(got, want)
     # a row window
     part = mxfp4_dequant(dev_mx(torch, w, sc, O, I), 37, 5).cpu().numpy()
-    np.testing.assert_array_equal(part.view(np.uint32), want[37:42].view(np.uint32))
+    same_bits_or_nan(part, want[37:42])
 
 
 @pytest.mark.parametrize("planes", [1, 2, 3])
@@ -100,6 +114,87 @@ def test_mxfp4_gemv_matches_oracle(gpu, planes, O, I, xdt):
     bound = 2e-5 * abs_dot(w, sc, x, O, I)
     assert np.abs(y - want).max() <= bound
     # bf16 output: the same f32 sum rounded once (RNE)
+    (yb,) = mxfp4_gemv([m], [xd], out_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), bf16_bits(y))
+
+
+def row_abs_dot(w, sc, x, O, I):
+    """sum_j |w_rj x_j| per row over the summed planes (float64)."""
+    tot = np.zeros(O)
+    ax = np.abs(x.astype(np.float64))
+    for p in range(w.shape[0]):
+        codes = np.stack([w[p] & 0xF, w[p] >> 4], axis=-1).reshape(O, I)
+        wa = np.abs(MX4[codes] * np.repeat(2.0 ** (sc[p].astype(np.float64) - 127), 32, axis=1))
+        tot += wa @ ax
+    return tot
+
+
+def full_range_case(planes, xdt):
+    """Scale bytes over all of 0..255 (see test_mxfp4_gemv_full_scale_range):
+    (w, sc, x, want) with the oracle's output."""
+    rng = np.random.default_rng(2550 + planes + (xdt == "bf16"))
+    O, I = 320, 1024
+    w, sc = make_mx(rng, O, I, planes, 0, 256)
+    sc[:, O // 2:] = rng.integers(0, 201, sc[:, O // 2:].shape)
+    sc[0, :8] = rng.integers(110, 140, (8, I // 32))  # planted rows: moderate elsewhere
+    x = rng.standard_normal(I).astype(np.float32)
+    x[:32] = np.abs(x[:32]) + np.float32(0.5)  # group 0: positive, >= 0.5
+    x[96:128] = np.abs(x[96:128]) + np.float32(0.5)
+    x[100] = 0.0                               # group 3: positive but one zero
+    if xdt == "bf16":
+        x = bf16_to_f32(bf16_bits(x))
+    pos = rng.integers(1, 8, (8, 16)).astype(np.uint8)  # codes 1..7: positive, nonzero
+    w[0, :8, :16] = pos | (pos << 4)
+    sc[0, 0, 0] = 255                       # +inf
+    sc[0, 1, 0] = 255
+    w[0, 1, 5] &= 0xF0                      # one zero code -> NaN
+    sc[0, 2, 3] = 255                       # group 3 holds x[100] = 0 -> NaN
+    w[0, 2, 48:64] = pos[2] | (pos[2] << 4)
+    sc[0, 3, 0] = 255
+    w[0, 3, 7] |= 0x08                      # one negative code -> NaN
+    sc[0, 4, 0] = 254
+    w[0, 4, 3] = 0x7F                       # 6 and -6 at 2^127: both overflow -> NaN
+    sc[0, 5, 0] = 254                       # 6 * x * 2^127 with x >= 0.5 -> +inf
+    w[0, 5, :16] = 0x77
+    for r in (6, 7):                        # byte-0 groups only: exact zeros
+        sc[:, r] = 0
+    want = oracle.mxfp4_gemv(x, w, sc, O, I, planes)
+    return w, sc, x, want
+
+
+@pytest.mark.parametrize("planes", [1, 3])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_mxfp4_gemv_full_scale_range(gpu, planes, xdt):
+    """Scale bytes over all of 0..255 against the reference's per-element
+    product (acc += x * MX4[code] * scale, logan-qwen4/src/lib.rs:2948-2961):
+    where the oracle's row is NaN or +-inf the kernel's is the same, finite
+    rows within 2e-5 of the row's sum_j |w_rj x_j| (plus 1e-40 for terms in
+    the subnormal range, which the reference rounds one by one). Rows 0-5
+    plant byte-255 groups: all codes nonzero and positive with x > 0 (+inf),
+    one zero code, a zero x, codes of both signs (NaN each); byte-254 groups
+    whose terms overflow with both signs (NaN) and with one sign (+inf); rows
+    6-7 hold only byte-0 groups (zero); the other rows of the first half draw
+    bytes from 0..255, the second half from 0..200 (finite rows with tiny
+    and zero scales)."""
+    import torch
+
+    from logan_amd.device import mxfp4_gemv
+
+    w, sc, x, want = full_range_case(planes, xdt)
+    O, I = want.shape[0], x.shape[0]
+    m = dev_mx(torch, w, sc, O, I)
+    if xdt == "f32":
+        xd = torch.from_numpy(x).cuda()
+    else:
+        xd = torch.from_numpy(bf16_bits(x).view(np.int16)).cuda().view(torch.bfloat16)
+    (y,) = mxfp4_gemv([m], [xd])
+    y = y.cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(y), np.isnan(want))
+    inf = np.isinf(want)
+    np.testing.assert_array_equal(y[inf], want[inf])
+    fin = np.isfinite(want)
+    bound = 2e-5 * row_abs_dot(w, sc, x, O, I)[fin] + 1e-40
+    assert (np.abs(y[fin].astype(np.float64) - want[fin]) <= bound).all()
     (yb,) = mxfp4_gemv([m], [xd], out_dtype=torch.bfloat16)
     np.testing.assert_array_equal(yb.cpu().view(torch.int16).numpy().view(np.uint16), bf16_bits(y))
 

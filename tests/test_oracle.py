@@ -19,6 +19,8 @@ from logan_amd.synth import bf16_bits, bf16_to_f32, make_affine, make_logits, ma
 
 from _util import dequant_f64, pack_codes, unpack_codes
 
+import test_mxfp4_gpu
+
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "kat_vectors.json").read_text())
 
 
@@ -626,3 +628,17 @@ def test_dense_gemv_fmt15_equals_fmt5_of_loader_weights():
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
     ref = bf16_to_f32(w5).astype(np.float64) @ x.astype(np.float64)
     assert np.abs(a - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("planes", [1, 3])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_full_range_case_is_what_it_claims(planes, xdt):
+    """CPU: the planted rows give the oracle outputs the GPU test relies on."""
+    w, sc, x, want = test_mxfp4_gpu.full_range_case(planes, xdt)
+    O = want.shape[0]
+    if planes == 1:
+        assert want[0] == np.inf and np.isnan(want[1:5]).all() and want[5] == np.inf
+    assert (want[6:8] == 0).all()
+    assert np.isnan(want[:O // 2]).any() and np.isinf(want[:O // 2]).any()
+    assert np.isfinite(want[O // 2:]).all()
+    assert (sc[:, O // 2:] <= 40).any() and (sc == 0).any() and (sc == 255).any()

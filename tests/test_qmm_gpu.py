@@ -224,3 +224,48 @@ def test_qmm_multi_matches_oracle(gpu, M, Os, I, bits, gs, fp16):
         bis = bi.reshape(O, ng)[cols].reshape(-1)
         ref = oracle.affine_qmm_bf16(xf, ws, scs, bis, len(cols), I, bits, gs, fp16)
         assert normwise_rel(y.cpu().numpy()[:, cols], ref) <= 1e-5, O
+
+
+def test_split_qmm_on_three_overlapping_streams(gpu):
+    """Split-K products pass their partial sums through 2 library-owned
+    slots. Three streams, each issuing four split products back to back
+    with no synchronisation between the streams, so more calls are in flight
+    than there are slots: every output equals the single-stream result
+    bitwise (the kernels are deterministic), and one per stream matches the
+    oracle."""
+    import torch
+    from logan_amd.device import affine_gemv, affine_qmm
+
+    M, O, I, bits, gs = 64, 512, 4096, 4, 64  # 8 tiles: the grid splits K
+    mats, xs, hosts = [], [], []
+    for s in range(3):
+        rng = np.random.default_rng(900 + s)
+        w, sc, bi = make_affine(rng, O, I, bits, gs)
+        xb = make_x(rng, M, I).reshape(M, I)
+        mats.append(dev_matrix(torch, w, sc, bi, O, I, bits, gs))
+        xs.append(to_dev(xb.view(np.int16), torch).view(torch.bfloat16))
+        hosts.append((w, sc, bi, xb))
+    serial = [affine_qmm(mats[s], xs[s], out_dtype=torch.float32) for s in range(3)]
+    serial_g = [affine_gemv(mats[s], xs[s][:8], out_dtype=torch.float32) for s in range(3)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    outs = [[torch.full((M, O), float("nan"), device="cuda") for _ in range(4)] for _ in range(3)]
+    outs_g = [[torch.full((8, O), float("nan"), device="cuda") for _ in range(4)] for _ in range(3)]
+    torch.cuda.synchronize()
+    for r in range(4):
+        for s in range(3):
+            with torch.cuda.stream(streams[s]):
+                affine_qmm(mats[s], xs[s], out=outs[s][r], stream=streams[s])
+                affine_gemv(mats[s], xs[s][:8], out=outs_g[s][r], stream=streams[s])
+    torch.cuda.synchronize()
+    for s in range(3):
+        for r in range(4):
+            assert torch.equal(outs[s][r], serial[s]), (s, r)
+            assert torch.equal(outs_g[s][r], serial_g[s]), (s, r)
+        w, sc, bi, xb = hosts[s]
+        cols = np.arange(0, O, 37)
+        ng = I // gs
+        ref = oracle.affine_qmm_bf16(bf16_to_f32(xb).reshape(M, I), w.reshape(O, -1)[cols],
+                                     sc.reshape(O, ng)[cols].reshape(-1),
+                                     bi.reshape(O, ng)[cols].reshape(-1), len(cols), I, bits, gs)
+        assert normwise_rel(serial[s].cpu().numpy()[:, cols], ref) <= 1e-5

@@ -16,7 +16,11 @@ only non-decreasing in the logit, so distinct logits can tie in p:
 * "ulp": f32 logits one ulp apart whose probabilities stay distinct (the
   recomputed selection must agree with the logit order there);
 * "nan": one NaN logit makes every probability NaN; the reference's
-  comparisons are then all false and it keeps experts 0..k-1.
+  comparisons are then all false and it keeps experts 0..k-1;
+* "negnan": the same with NaN bit patterns that have the sign bit set
+  (0xFFC0 and others, bf16-exact): an ordered-bits key would sort such a NaN
+  below every number, so the selection must treat any NaN as NaN whatever
+  its sign (x86 arithmetic produces the negative default NaN).
 
 Every case checks its own premise on the CPU: that the logit order and the
 oracle's probability order really differ (where that is the point), and that
@@ -37,9 +41,12 @@ from logan_amd.synth import bf16_bits, bf16_to_f32, make_x
 from _util import normwise_rel
 
 E, K = 512, 10
-BF16_KINDS = ["subtract", "underflow", "neginf", "nan"]
+BF16_KINDS = ["subtract", "underflow", "neginf", "nan", "negnan"]
+NAN_KINDS = {"nan", "negnan"}
+# NaN bit patterns (f32, each bf16-exact), one per seed in turn
+NEG_NANS = [0xFFC00000, 0xFF810000, 0xFFFF0000, 0x7F810000]
 F32_KINDS = BF16_KINDS + ["nearmax", "divtie", "ulp"]
-ORDER_DIFFERS = {"subtract", "underflow", "neginf", "nearmax", "divtie", "nan"}
+ORDER_DIFFERS = {"subtract", "underflow", "neginf", "nearmax", "divtie", "nan", "negnan"}
 
 
 def tie_logits(kind: str, seed: int) -> np.ndarray:
@@ -71,6 +78,10 @@ def tie_logits(kind: str, seed: int) -> np.ndarray:
     elif kind == "nan":
         lf[:] = bf16_to_f32(bf16_bits(rng.standard_normal(E).astype(np.float32)))
         lf[rng.integers(0, E)] = np.nan
+    elif kind == "negnan":
+        lf[:] = bf16_to_f32(bf16_bits(rng.standard_normal(E).astype(np.float32)))
+        pat = NEG_NANS[seed % len(NEG_NANS)]
+        lf[rng.integers(K, E)] = np.uint32(pat).view(np.float32)
     else:
         raise ValueError(kind)
     return lf
@@ -95,7 +106,7 @@ def test_tie_cases_are_what_they_claim(kind):
     lf = tie_logits(kind, 1)
     ridx, rw = oracle_route(lf, K)
     finite = lf[np.isfinite(lf)]
-    if kind != "nan":
+    if kind not in NAN_KINDS:
         m = np.float32(finite.max())
         d = (lf - m).astype(np.float32)
         expf = _libm_expf()
@@ -108,9 +119,22 @@ def test_tie_cases_are_what_they_claim(kind):
         assert not np.array_equal(ridx, logit_order), "case does not separate the two orders"
     else:
         np.testing.assert_array_equal(ridx, logit_order)
-    if kind == "nan":
+    if kind in NAN_KINDS:
         np.testing.assert_array_equal(ridx, np.arange(K))
         assert np.isnan(rw).all()
+    if kind == "negnan":
+        # the planted NaN is the sign-bit kind for most seeds, below the top k,
+        # and a key of its ordered bits would rank it last: the old shortcut's
+        # answer (the finite logits' top k) differs from the reference's
+        for seed in range(len(NEG_NANS)):
+            lfs = tie_logits(kind, seed)
+            pos = np.flatnonzero(np.isnan(lfs))
+            assert len(pos) == 1 and pos[0] >= K
+            bits = int(lfs[pos[0]:pos[0] + 1].view(np.uint32)[0])
+            assert bits == NEG_NANS[seed]
+            assert bf16_bits(lfs[pos])[0] == bits >> 16
+        lfin = np.where(np.isnan(lf), -np.inf, lf)
+        assert not np.array_equal(np.argsort(-lfin, kind="stable")[:K], ridx)
 
 
 def to_dev(a, torch, dtype=None):
@@ -129,7 +153,7 @@ def dev_logits(torch, lf, dtype):
 def check_route(idx, w, lf, k, kind):
     ridx, rw = oracle_route(lf, k)
     np.testing.assert_array_equal(idx, ridx)
-    if kind == "nan":
+    if kind in NAN_KINDS:
         assert np.isnan(w).all()
     else:
         # the recomputed path is the reference's arithmetic: bit-exact weights
@@ -156,7 +180,9 @@ def test_route_topk_probability_ties(gpu, dtype, kind):
 
 MOE_TIE_CASES = [(1, "bf16", "subtract"), (1, "bf16", "underflow"), (1, "bf16", "neginf"),
                  (1, "f32", "divtie"), (1, "f32", "nearmax"), (16, "bf16", "subtract"),
-                 (16, "f32", "divtie"), (64, "bf16", "underflow"), (64, "f32", "divtie")]
+                 (16, "f32", "divtie"), (64, "bf16", "underflow"), (64, "f32", "divtie"),
+                 (1, "bf16", "negnan"), (1, "f32", "negnan"), (1, "bf16", "nan"),
+                 (16, "bf16", "negnan"), (64, "bf16", "negnan"), (64, "f32", "negnan")]
 
 
 # B > 1 takes the multi-launch path either way: only B = 1 runs both ways
@@ -188,7 +214,10 @@ def test_moe_block_probability_ties(gpu, fused, B, dtype, kind):
         for t in range(B):
             ref, ridx, _ = layer.ref(xf[t], lf[t])
             np.testing.assert_array_equal(idx[t], ridx)
-            assert normwise_rel(out[t], ref) <= 5e-5
+            if kind in NAN_KINDS:  # NaN weights: the reference's output is NaN throughout
+                assert np.isnan(ref).all() and np.isnan(out[t]).all()
+            else:
+                assert normwise_rel(out[t], ref) <= 5e-5
     finally:
         _lib.lib().logan_hip_set_moe_fused(1)
     assert _lib.lib().logan_hip_moe_sync_errors() == 0
