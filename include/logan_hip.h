@@ -412,7 +412,8 @@ int logan_hip_moe_block_static(const LoganHipMoeBlock *blk, const void *x, const
  * current device: 0 = healthy; bit 0 = a phase hand-off wait timed out (the
  * output of that call was not valid); bit 1 = a launch counter not on a
  * launch boundary, bit 2 = launch counters out of step (both checked between
- * launches). */
+ * launches); bit 3 = a routed expert missing from logan_hip_moe_block_cached's
+ * map (that call's output was not valid). */
 void logan_hip_set_moe_fused(int on);
 uint32_t logan_hip_moe_sync_errors(void);
 
@@ -512,6 +513,78 @@ int logan_hip_plan_mlx_quantized_experts(const LoganHipStFile *st, const char *n
                                          int count, int experts, int O, int I,
                                          LoganHipQuantWt *out);
 void logan_hip_quant_free(LoganHipQuantWt *w);
+
+/* ---- Route-driven expert cache (banks not kept resident) ----------------
+ * The reference's EXP-069 RouteCache and EXP-067 RouteArena
+ * (logan-qwen4/src/lib.rs:12110-12300; builders try_build_route_cache /
+ * try_build_route_arena :12959-13140; cache_fetch_route :12697-12903) in
+ * one HBM allocation of expert blocks. A block holds one routed expert's
+ * gate, up and down matrices (packed weights, scales, biases) in io_plan's
+ * order (:13550-13590), each part 256-byte aligned. Each layer owns
+ * blocks_per_layer retained blocks (the reference's LOGAN_ROUTE_CACHE
+ * blocks: tags, a replacement cursor that skips the blocks the current
+ * route has claimed, hit / miss / eviction counts); 2 x topk more blocks are
+ * the route arena (one set of topk per layer parity) for the ranks the
+ * cache does not retain. Affine banks only. */
+typedef struct LoganHipExpertCache LoganHipExpertCache;
+
+typedef struct LoganHipExpertCacheStats {
+  uint64_t hits, misses, evictions; /* retained ranks (:12775-12789) */
+  uint64_t streamed;                /* ranks loaded through the route arena */
+  uint64_t bytes_loaded;            /* host -> HBM bytes of all fills */
+  uint64_t generation;              /* bumped per block reuse (:12163) */
+  uint64_t block_bytes, device_bytes;
+  int layers, blocks_per_layer, topk;
+} LoganHipExpertCacheStats;
+
+/* Blocks sized from layer 0 expert 0's banks
+ * model.layers.{L}.mlp.switch_mlp.{gate,up,down}_proj of `st` (stacked
+ * [experts] banks, gate/up d_hidden x d_model, down d_model x d_hidden, the
+ * loader's checks). layers 0: counted from the tensor table as
+ * try_build_route_cache does (:12965-12975). blocks_per_layer 0: every rank
+ * streams through the arena. topk <= 32. `st` must stay open while the
+ * cache lives. NULL on error (logan_hip_last_error). */
+LoganHipExpertCache *logan_hip_expert_cache_create(const LoganHipStFile *st, int layers, int experts,
+                                                   int d_model, int d_hidden, int blocks_per_layer,
+                                                   int topk);
+/* Waits for the device, frees the blocks. */
+void logan_hip_expert_cache_destroy(LoganHipExpertCache *c);
+/* cache_fetch_route for one token's route experts[0..k-1] (rank order) of
+ * `layer`: ranks below min(blocks_per_layer, k) are looked up / reserved in
+ * the layer's cache (RouteCache::reserve, :12190-12228), the others take the
+ * layer parity's arena blocks; misses and arena ranks are read from the
+ * checkpoint through the loader's pinned staging ring and copied on the
+ * loader's stream after the work already queued on `stream` (which may
+ * still read those blocks), and `stream` then waits for the copies (the
+ * host returns once the reads are staged). blocks_out[r] = the block of rank
+ * r, for logan_hip_moe_block_cached. 1 ok; 0 declined (k > topk, an id out
+ * of range, a layer whose banks differ from the cache's layout); -1 read or
+ * device failure (the blocks this call claimed are dropped from the cache;
+ * the reference disables its cache instead). Calls on one cache
+ * serialise. */
+int logan_hip_expert_cache_fetch(LoganHipExpertCache *c, int layer, const int32_t *experts, int k,
+                                 int32_t *blocks_out, void *stream);
+void logan_hip_expert_cache_stats(const LoganHipExpertCache *c, LoganHipExpertCacheStats *out);
+/* The layer's block tags (expert per retained block, -1 empty) into
+ * tags_out[blocks_per_layer]. 1 ok, 0 bad arguments. */
+int logan_hip_expert_cache_tags(const LoganHipExpertCache *c, int layer, int32_t *tags_out);
+
+/* logan_hip_moe_block for one token (B = 1) whose routed experts come from
+ * an expert cache: experts[r] / blocks[r] are the route and the blocks
+ * logan_hip_expert_cache_fetch returned (the engine's authoritative route,
+ * e.g. logan_hip_route_topk on the same logits, so the block's own routing
+ * selects the same experts). blk supplies top_k (== k), the shared expert,
+ * its gate vector and the routed geometry (gate.E = experts, O, I, bits,
+ * group_size, aux_fp16 equal to the cache's); its routed weight pointers are
+ * not read. The output is bit-identical to logan_hip_moe_block on resident
+ * banks holding the same bytes. A routed expert missing from the map sets
+ * bit 3 of logan_hip_moe_sync_errors (the launch reads a mapped block, in
+ * bounds). 1 ok, 0 unsupported, -1 failure. */
+int logan_hip_moe_block_cached(const LoganHipMoeBlock *blk, const LoganHipExpertCache *c,
+                               const int32_t *experts, const int32_t *blocks, int k, const void *x,
+                               const void *logits, int logits_dtype, void *out, int out_dtype,
+                               int32_t *idx_out, float *w_out, void *workspace,
+                               size_t workspace_bytes, void *stream);
 
 /* Library version string. */
 const char *logan_hip_version(void);

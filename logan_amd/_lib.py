@@ -132,6 +132,22 @@ class QuantWt(C.Structure):
     ]
 
 
+class ExpertCacheStats(C.Structure):
+    _fields_ = [
+        ("hits", C.c_uint64),
+        ("misses", C.c_uint64),
+        ("evictions", C.c_uint64),
+        ("streamed", C.c_uint64),
+        ("bytes_loaded", C.c_uint64),
+        ("generation", C.c_uint64),
+        ("block_bytes", C.c_uint64),
+        ("device_bytes", C.c_uint64),
+        ("layers", C.c_int),
+        ("blocks_per_layer", C.c_int),
+        ("topk", C.c_int),
+    ]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _SZ = C.c_size_t
@@ -205,6 +221,13 @@ SIGNATURES = {
     "logan_hip_plan_mlx_quantized_experts": (_I, [_P, C.c_char_p, _I, _I, _I, _I, _I,
                                                   C.POINTER(QuantWt)]),
     "logan_hip_quant_free": (None, [C.POINTER(QuantWt)]),
+    "logan_hip_expert_cache_create": (_P, [_P, _I, _I, _I, _I, _I, _I]),
+    "logan_hip_expert_cache_destroy": (None, [_P]),
+    "logan_hip_expert_cache_fetch": (_I, [_P, _I, _P, _I, _P, _P]),
+    "logan_hip_expert_cache_stats": (None, [_P, C.POINTER(ExpertCacheStats)]),
+    "logan_hip_expert_cache_tags": (_I, [_P, _I, _P]),
+    "logan_hip_moe_block_cached": (_I, [C.POINTER(MoeBlock), _P, _P, _P, _I, _P, _P, _I, _P, _I, _P,
+                                        _P, _P, _SZ, _P]),
 }
 
 _lib = None

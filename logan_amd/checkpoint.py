@@ -16,6 +16,8 @@ from __future__ import annotations
 import ctypes as C
 from typing import Dict, List, Optional
 
+import numpy as np
+
 from . import _lib as L
 
 DTYPES = ("F32", "I32", "I64", "U32", "U8", "BF16", "F16", "F8_E4M3", "F8_E4M3FN")
@@ -275,3 +277,96 @@ def load_mlx_quantized_bank(st: StFile, name: str, experts: int, o: int, i: int,
     if rc != 1:
         raise CheckpointError(_err())
     return _wrap(q, bank=True)
+
+
+class CachedBankGeometry:
+    """A routed bank whose experts live in an ExpertCache: only its geometry
+    (the protocol of device.AffineBank's c(), weight pointers null)."""
+
+    def __init__(self, E: int, O: int, I: int, bits: int, group_size: int, aux_fp16: bool = False):
+        self.E, self.O, self.I, self.bits = E, O, I, bits
+        self.group_size, self.aux_fp16 = group_size, aux_fp16
+
+    def c(self) -> L.AffineBank:
+        return L.AffineBank(None, None, None, self.E, self.O, self.I, self.bits, self.group_size,
+                            int(self.aux_fp16))
+
+
+class ExpertCache:
+    """The reference's route-driven expert cache and route arena
+    (RouteCache / RouteArena, logan-qwen4/src/lib.rs:12110-12300,
+    cache_fetch_route :12697-12903) in HBM, filled from this checkpoint
+    (logan_hip_expert_cache_*): `fetch` places one token's routed experts and
+    returns their blocks for device.moe_block_cached."""
+
+    def __init__(self, st: StFile, experts: int, d_model: int, d_hidden: int,
+                 blocks_per_layer: int, topk: int, layers: int = 0):
+        self._st = st  # the cache reads the checkpoint's descriptors: keep it open
+        self.experts, self.d_model, self.d_hidden = experts, d_model, d_hidden
+        h = L.lib().logan_hip_expert_cache_create(st.handle, layers, experts, d_model, d_hidden,
+                                                  blocks_per_layer, topk)
+        if not h:
+            raise CheckpointError(_err())
+        self._h = h
+        s = self.stats()
+        self.layers, self.blocks_per_layer, self.topk = s["layers"], s["blocks_per_layer"], s["topk"]
+
+    @property
+    def handle(self) -> int:
+        if not self._h:
+            raise CheckpointError("expert cache is closed")
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            L.lib().logan_hip_expert_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def fetch(self, layer: int, experts, stream=None) -> np.ndarray:
+        """Blocks of the route's experts (rank order); loads the misses and the
+        arena ranks, ordered after `stream`'s queued work, and makes `stream`
+        wait for them. None when the cache declines the route."""
+        e = np.ascontiguousarray(experts, dtype=np.int32)
+        blocks = np.empty(len(e), np.int32)
+        st = None
+        if stream is not None:
+            st = stream.cuda_stream or None
+        else:
+            try:
+                import torch
+
+                if torch.cuda.is_available():
+                    st = torch.cuda.current_stream().cuda_stream or None
+            except ImportError:
+                pass
+        rc = L.lib().logan_hip_expert_cache_fetch(self.handle, layer, e.ctypes.data, len(e),
+                                                  blocks.ctypes.data, st)
+        if rc == 0:
+            return None
+        if rc != 1:
+            raise CheckpointError(_err())
+        return blocks
+
+    def stats(self) -> Dict[str, int]:
+        s = L.ExpertCacheStats()
+        L.lib().logan_hip_expert_cache_stats(self.handle, C.byref(s))
+        return {name: int(getattr(s, name)) for name, _ in L.ExpertCacheStats._fields_}
+
+    def tags(self, layer: int) -> np.ndarray:
+        out = np.empty(max(self.blocks_per_layer, 1), np.int32)
+        if L.lib().logan_hip_expert_cache_tags(self.handle, layer, out.ctypes.data) != 1:
+            raise CheckpointError("bad layer")
+        return out[:self.blocks_per_layer]
+
+    def geometry(self, bits: int, group_size: int, aux_fp16: bool = False, down_group_size=None):
+        """(gate, up, down) CachedBankGeometry for a device.MoeLayer."""
+        dg = group_size if down_group_size is None else down_group_size
+        return (CachedBankGeometry(self.experts, self.d_hidden, self.d_model, bits, group_size, aux_fp16),
+                CachedBankGeometry(self.experts, self.d_hidden, self.d_model, bits, group_size, aux_fp16),
+                CachedBankGeometry(self.experts, self.d_model, self.d_hidden, bits, dg, aux_fp16))

@@ -1293,23 +1293,10 @@ size_t logan_hip_moe_workspace_bytes(const LoganHipMoeBlock *blk, int B) {
   return lh::moe_workspace_bytes(B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
 }
 
-int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *logits,
-                        int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
-                        float *w_out, void *workspace, size_t workspace_bytes, void *stream) {
-  lh::MoeArgs a;
-  if (!fill_moe_args(blk, a) || !x || !logits || !out || B <= 0) return 0;
-  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
-  if (out_dtype != LOGAN_HIP_F32 && out_dtype != LOGAN_HIP_BF16) return 0;
-  a.x = reinterpret_cast<const uint16_t *>(x);
-  a.logits = logits;
-  a.logits_f32 = logits_dtype == LOGAN_HIP_F32;
-  a.B = B;
-  a.out = out;
-  a.out_f32 = out_dtype == LOGAN_HIP_F32;
-  a.idx_out = idx_out;
-  a.w_out = w_out;
+// the MoE launch on the caller's workspace, or on the library-owned one
+static int run_moe_block(lh::MoeArgs &a, void *workspace, size_t workspace_bytes, void *stream) {
   const size_t need =
-      lh::moe_workspace_bytes(B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
+      lh::moe_workspace_bytes(a.B, a.D, a.inter, a.sgate.m.w ? a.sinter : 0, a.E, a.k);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (workspace) {
     if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return 0;
@@ -1326,6 +1313,60 @@ int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *
   a.ws = g_ws.p;
   a.ws_bytes = g_ws.n;
   return lh::launch_moe_block(a, st);
+}
+
+int logan_hip_moe_block(const LoganHipMoeBlock *blk, const void *x, const void *logits,
+                        int logits_dtype, int B, void *out, int out_dtype, int32_t *idx_out,
+                        float *w_out, void *workspace, size_t workspace_bytes, void *stream) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || !x || !logits || !out || B <= 0) return 0;
+  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
+  if (out_dtype != LOGAN_HIP_F32 && out_dtype != LOGAN_HIP_BF16) return 0;
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.logits = logits;
+  a.logits_f32 = logits_dtype == LOGAN_HIP_F32;
+  a.B = B;
+  a.out = out;
+  a.out_f32 = out_dtype == LOGAN_HIP_F32;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  return run_moe_block(a, workspace, workspace_bytes, stream);
+}
+
+int logan_hip_moe_block_cached(const LoganHipMoeBlock *blk, const LoganHipExpertCache *c,
+                               const int32_t *experts, const int32_t *blocks, int k, const void *x,
+                               const void *logits, int logits_dtype, void *out, int out_dtype,
+                               int32_t *idx_out, float *w_out, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  lh::MoeArgs a;
+  if (!fill_moe_args(blk, a) || !c || !experts || !blocks || !x || !logits || !out) return 0;
+  if (k != a.k || k < 1 || k > lh::kMoeMapMax) return 0;
+  if (logits_dtype != LOGAN_HIP_F32 && logits_dtype != LOGAN_HIP_BF16) return 0;
+  if (out_dtype != LOGAN_HIP_F32 && out_dtype != LOGAN_HIP_BF16) return 0;
+  // the routed banks: views of the cache's blocks, in the caller's geometry
+  const lh::DevBank want[3] = {a.gate, a.up, a.down};
+  int nblocks = 0;
+  if (!lh::expert_cache_banks(c, &a.gate, &a.up, &a.down, &nblocks)) return 0;
+  const lh::DevBank *got[3] = {&a.gate, &a.up, &a.down};
+  for (int m = 0; m < 3; ++m) {
+    const lh::DevMat &w = want[m].m, &g = got[m]->m;
+    if (w.O != g.O || w.I != g.I || w.bits != g.bits || w.gs != g.gs || w.fp16 != g.fp16) return 0;
+  }
+  a.nmap = k;
+  for (int r = 0; r < k; ++r) {
+    if (experts[r] < 0 || experts[r] >= a.E || blocks[r] < 0 || blocks[r] >= nblocks) return 0;
+    a.map_e[r] = experts[r];
+    a.map_b[r] = blocks[r];
+  }
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.logits = logits;
+  a.logits_f32 = logits_dtype == LOGAN_HIP_F32;
+  a.B = 1;
+  a.out = out;
+  a.out_f32 = out_dtype == LOGAN_HIP_F32;
+  a.idx_out = idx_out;
+  a.w_out = w_out;
+  return run_moe_block(a, workspace, workspace_bytes, stream);
 }
 
 int logan_hip_moe_block_routed(const LoganHipMoeBlock *blk, const LoganHipAffine *router,
@@ -1459,7 +1500,7 @@ int logan_hip_llama_layer(const LoganHipLlamaLayer *L, float *x, int pos, void *
 
 void logan_hip_set_moe_fused(int on) { lh::set_moe_fused_enabled(on ? 1 : 0); }
 
-uint32_t logan_hip_moe_sync_errors(void) { return lh::moe_fused_sync_errors(); }
+uint32_t logan_hip_moe_sync_errors(void) { return lh::moe_fused_sync_errors() | lh::moe_map_errors(); }
 
 void logan_hip_set_moe_mfma_min_batch(int b) { lh::set_moe_mfma_min_batch(b); }
 

@@ -250,14 +250,34 @@ struct MoeArgs {
   float *w_out;                    // optional [B, k]
   void *ws;                        // workspace
   size_t ws_bytes;
+  // Routed experts held in an expert cache's arena (expert_cache.hip): the
+  // routed banks are views of its blocks (block stride as w_stride /
+  // p_stride) and expert map_e[i] sits in block map_b[i]. nmap == 0: the
+  // banks hold every expert, indexed by expert id.
+  int nmap;
+  int32_t map_e[32], map_b[32];
 };
+constexpr int kMoeMapMax = 32;
+// The bank index of routed expert e: its block when a map is set (an expert
+// missing from the map reads block map_b[0], so the launch stays in bounds,
+// and sets *miss), else e itself.
+__device__ __forceinline__ int moe_bank_index(const MoeArgs &a, int e, bool &miss) {
+  if (a.nmap == 0) return e;
+  int b = -1;
+  for (int i = 0; i < a.nmap; ++i) b = a.map_e[i] == e ? a.map_b[i] : b;
+  miss = b < 0;
+  return b < 0 ? a.map_b[0] : b;
+}
 size_t moe_workspace_bytes(int B, int D, int inter, int sinter, int E, int k);
 // single-launch B = 1 path (moe_fused.hip): 1 launched, 0 not applicable
 int launch_moe_fused_b1(const MoeArgs &a, hipStream_t st);
 size_t moe_fused_workspace_bytes(int slots, int inter, int sinter);
 // sticky error bits of the fused path (bit 0: a wait timed out; bits 1-2:
-// arrival counters not at rest)
+// arrival counters not at rest; bit 3: a routed expert missing from the
+// expert-cache map)
 uint32_t moe_fused_sync_errors();
+// bit 3 of the same word for the per-token path (moe.hip)
+uint32_t moe_map_errors();
 // 0 disables the fused B = 1 path (LOGAN_HIP_MOE_FUSED=0); default on
 void set_moe_fused_enabled(int on);
 // token-batch path on MFMA (moe_mfma.hip): 4/5/6/8-bit codes, groups of 64k,
@@ -278,5 +298,12 @@ size_t moe_mfma_workspace_bytes(int B, int D, int inter, int sinter, int E, int 
 void set_moe_mfma_min_batch(int b);
 // 1 ok, 0 unsupported geometry (nothing launched), -1 launch failure
 int launch_moe_block(const MoeArgs &a, hipStream_t st);
+}  // namespace lh
+
+struct LoganHipExpertCache;
+namespace lh {
+// the routed banks as views of an expert cache's blocks (expert_cache.hip);
+// *nblocks = blocks in the cache's allocation
+bool expert_cache_banks(const LoganHipExpertCache *c, DevBank *g, DevBank *u, DevBank *d, int *nblocks);
 
 }  // namespace lh

@@ -28,24 +28,16 @@ bool pread_all(int fd, uint64_t off, void *dst, size_t n);
 }  // namespace st
 }  // namespace lh
 
-namespace {
+namespace lh {
+namespace ld {
 
-constexpr size_t kSlotBytes = 32u << 20;  // one staging slot
-constexpr int kSlots = 4;                 // reads run up to 3 slots ahead of the DMA
-constexpr int kMaxReaders = 8;            // pread threads per slot
-
-struct Stager {
-  bool ready = false;
-  int dev = -1;
-  hipStream_t st = nullptr;
-  void *buf[kSlots] = {};
-  hipEvent_t ev[kSlots] = {};
-  bool pending[kSlots] = {};
-  int readers = 1;
-};
+constexpr int kMaxReaders = 8;  // pread threads per slot
 
 std::mutex g_load_mtx;  // one load at a time per process (the staging ring is shared)
 Stager g_stage;
+
+std::mutex &load_mutex() { return g_load_mtx; }
+Stager &stager() { return g_stage; }
 
 bool stager_ready(std::string *err) {
   int dev = 0;
@@ -136,6 +128,13 @@ bool stage_region(const lh::st::File &f, const lh::st::Region &r, char *ddst, in
   }
   return true;
 }
+
+}  // namespace ld
+}  // namespace lh
+
+namespace {
+
+using namespace lh::ld;
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 

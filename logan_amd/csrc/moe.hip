@@ -42,6 +42,9 @@
 
 namespace lh {
 
+// sticky: bit 3 = a routed expert missing from the expert-cache map
+static __device__ uint32_t g_moe_map_err;
+
 constexpr int kMaxE = 1024;  // 16 keys per lane
 constexpr int kMaxK = 32;
 
@@ -381,7 +384,12 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
   const long long uws = shared ? a.sup.w_stride : a.up.w_stride;
   const long long gps = shared ? a.sgate.p_stride : a.gate.p_stride;
   const long long ups = shared ? a.sup.p_stride : a.up.p_stride;
-  const int e = __builtin_amdgcn_readfirstlane(ge);
+  int e = __builtin_amdgcn_readfirstlane(ge);
+  if (!shared && a.nmap) {  // the expert's block in an expert cache's arena
+    bool miss = false;
+    e = moe_bank_index(a, e, miss);
+    if (miss && threadIdx.x == 0) atomicOr(&g_moe_map_err, 8u);
+  }
   const int rows = shared ? a.sinter : a.inter;
   const uint8_t *gwb = gm.w + (size_t)e * gws;
   const uint8_t *uwb = um.w + (size_t)e * uws;
@@ -516,7 +524,11 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   const DevMat dm = shared ? a.sdown.m : a.down.m;
   const long long dws = shared ? a.sdown.w_stride : a.down.w_stride;
   const long long dps = shared ? a.sdown.p_stride : a.down.p_stride;
-  const int e = __builtin_amdgcn_readfirstlane(ge);
+  int e = __builtin_amdgcn_readfirstlane(ge);
+  if (!shared && a.nmap) {
+    bool miss = false;  // (reported by the gate/up blocks)
+    e = moe_bank_index(a, e, miss);
+  }
   const int K = shared ? a.sinter : a.inter;  // columns of down
   const int Ck = K >> 5;
   const uint8_t *wb = dm.w + (size_t)e * dws;
@@ -678,6 +690,14 @@ static int moe_launch_bits(const MoeArgs &a, const MoeWs &w, hipStream_t st) {
   return 1;
 }
 
+uint32_t moe_map_errors() {
+  uint32_t v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_moe_map_err), sizeof(v), 0, hipMemcpyDeviceToHost) !=
+      hipSuccess)
+    return 0xffffffffu;
+  return v;
+}
+
 static bool bank_ok(const DevBank &b, int O, int I, int bits, int gs) {
   const DevMat &m = b.m;
   if (!m.w || !m.sc || !m.bi) return false;
@@ -723,7 +743,14 @@ int launch_moe_block(const MoeArgs &a, hipStream_t st) {
   if (!(bits == 4 || bits == 5 || bits == 6 || bits == 8)) return 0;
   if (!bank_ok(a.gate, a.inter, a.D, bits, gs) || !bank_ok(a.up, a.inter, a.D, bits, gs)) return 0;
   if (!bank_ok(a.down, a.D, a.inter, bits, a.down.m.gs)) return 0;
-  if (a.gate.E < a.E || a.up.E < a.E || a.down.E < a.E) return 0;
+  if (a.nmap < 0 || a.nmap > kMoeMapMax) return 0;
+  if (a.nmap == 0 && (a.gate.E < a.E || a.up.E < a.E || a.down.E < a.E)) return 0;
+  for (int i = 0; i < a.nmap; ++i)  // cache blocks: inside every bank view
+    if (a.map_b[i] < 0 || a.map_b[i] >= a.gate.E || a.map_b[i] >= a.up.E || a.map_b[i] >= a.down.E)
+      return 0;
+  // a map covers the experts of one token's route: B = 1, on the fused or
+  // per-token path (the token-batch MFMA path never takes B = 1)
+  if (a.nmap > 0 && a.B != 1) return 0;
   if (a.sgate.m.w) {
     if (a.sinter <= 0 || a.sinter % 32 != 0) return 0;
     if (!bank_ok(a.sgate, a.sinter, a.D, bits, gs) || !bank_ok(a.sup, a.sinter, a.D, bits, gs)) return 0;

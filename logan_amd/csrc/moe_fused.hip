@@ -397,7 +397,13 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
     if (threadIdx.x == 0) s_lid = launch_number(tk);
     __syncthreads();
-    const int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
+    int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
+    if (!shared && a.nmap) {  // the expert's block in an expert cache's arena
+      bool miss = false;
+      e = moe_bank_index(a, e, miss);
+      if (miss && threadIdx.x == 0)
+        __hip_atomic_fetch_or(&g_fused_sync.error[0], 8u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
     TL_BLOCK(1);
     // bank fields copied once (scalar) rather than re-read per use
@@ -600,7 +606,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     const int s = wave + t * kWaves;
     if (s < g.k) {
       const uint32_t kk = __builtin_amdgcn_readfirstlane(s_sel[s]);
-      const int e = sel_expert(kk);
+      bool miss = false;  // (reported by the A blocks, which route the same way)
+      const int e = moe_bank_index(a, sel_expert(kk), miss);
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
         const int d = d0 + p * RPP + rsub;

@@ -3,9 +3,11 @@
 // parsing and validation) and loader.hip (upload into HBM).
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -60,6 +62,30 @@ bool plan_experts(const File &f, const std::string &name, long long e0, long lon
                   long long experts, long long o, long long i, QuantPlan *p, std::string *err);
 
 }  // namespace st
+
+// The loader's pinned staging ring (loader.hip), shared by the expert cache's
+// fills: kSlots pinned host slots filled by pread()s and drained by async
+// copies on the loader's own stream, one event per slot.
+namespace ld {
+constexpr size_t kSlotBytes = 32u << 20;  // one staging slot
+constexpr int kSlots = 4;                 // reads run up to 3 slots ahead of the DMA
+struct Stager {
+  bool ready = false;
+  int dev = -1;
+  hipStream_t st = nullptr;
+  void *buf[kSlots] = {};
+  hipEvent_t ev[kSlots] = {};
+  bool pending[kSlots] = {};
+  int readers = 1;
+};
+// held for a whole load (the ring is shared)
+std::mutex &load_mutex();
+Stager &stager();
+// the ring on the current device (built on first use); false with *err set
+bool stager_ready(std::string *err);
+// [off, off + n) of fd into dst with up to `readers` threads
+bool parallel_read(int fd, uint64_t off, char *dst, size_t n, int readers);
+}  // namespace ld
 
 // Thread-local message of the last failed loader/stfile call.
 void set_last_error(const std::string &m);

@@ -10,6 +10,7 @@ import ctypes as C
 from dataclasses import dataclass
 from typing import Optional
 
+import numpy as np
 import torch
 
 from . import _lib as L
@@ -440,6 +441,47 @@ def moe_block(layer: MoeLayer, x: torch.Tensor, logits: torch.Tensor,
                                      w.data_ptr() if w is not None else None, ws_ptr, ws_bytes,
                                      _stream(stream))
     _check(rc, "moe_block")
+    if return_routing:
+        return out, idx, w
+    return out
+
+
+def moe_block_cached(layer: MoeLayer, cache, experts, blocks, x: torch.Tensor,
+                     logits: torch.Tensor, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None, return_routing: bool = False,
+                     out_dtype: torch.dtype = torch.bfloat16, stream=None):
+    """moe_block for one token whose routed experts sit in an ExpertCache
+    (logan_amd.checkpoint): experts / blocks are the route and the blocks
+    ExpertCache.fetch returned; layer supplies top_k, the shared expert and
+    the routed geometry (logan_hip_moe_block_cached)."""
+    if x.dtype != torch.bfloat16 or x.numel() != x.shape[-1]:
+        raise LoganHipError("x must be one bf16 token")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise LoganHipError("logits must be bf16 or f32")
+    D = x.shape[-1]
+    if out is None:
+        out = torch.empty((1, D), dtype=out_dtype, device=x.device)
+    od = L.LOGAN_HIP_BF16 if out.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    e = np.ascontiguousarray(experts, dtype=np.int32)
+    b = np.ascontiguousarray(blocks, dtype=np.int32)
+    if len(e) != len(b):
+        raise LoganHipError("experts and blocks differ in length")
+    idx = w = None
+    if return_routing:
+        idx = torch.empty((1, layer.top_k), dtype=torch.int32, device=x.device)
+        w = torch.empty((1, layer.top_k), dtype=torch.float32, device=x.device)
+    blk = layer.c()
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = _dev(workspace, "workspace"), workspace.numel() * workspace.element_size()
+    dt = L.LOGAN_HIP_BF16 if logits.dtype == torch.bfloat16 else L.LOGAN_HIP_F32
+    rc = L.lib().logan_hip_moe_block_cached(C.byref(blk), cache.handle, e.ctypes.data, b.ctypes.data,
+                                            len(e), _dev(x, "x"), _dev(logits, "logits"), dt,
+                                            _dev(out, "out"), od,
+                                            idx.data_ptr() if idx is not None else None,
+                                            w.data_ptr() if w is not None else None, ws_ptr,
+                                            ws_bytes, _stream(stream))
+    _check(rc, "moe_block_cached")
     if return_routing:
         return out, idx, w
     return out
