@@ -41,7 +41,10 @@ one a HIP graph of the product entry points timed with HIP events):
     math between the projections is outside the path: its inputs are
     synthetic activations of the right shape;
   * loader: one config-3 layer's switch_mlp banks (906 MB) from a
-    safetensors file into HBM, whole banks and one expert at a time.
+    safetensors file into HBM, whole banks and one expert at a time;
+  * expert cache: the same banks served by the route-driven expert cache
+    (route on device, route to the host, fetch, block on cached experts)
+    cold (every rank streamed) and warm (every rank retained).
 """
 from __future__ import annotations
 
@@ -85,9 +88,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs",
-                    default="gemv,dense8,llama,moe3,stack5,moe4,dropin,router,mxfp4,loader",
+                    default="gemv,dense8,llama,moe3,stack5,moe4,dropin,router,mxfp4,loader,cache",
                     help="secondary legs to run (comma list of gemv, dense8, llama, moe3, stack5, "
-                         "moe4, dropin, router, mxfp4, loader; 'none' for none)")
+                         "moe4, dropin, router, mxfp4, loader, cache; 'none' for none)")
     ap.add_argument("--no-gemv", action="store_true", help="skip the config-1 GEMV leg")
     ap.add_argument("--no-secondary", action="store_true", help="same as --legs none")
     ap.add_argument("--reps", type=int, default=5, help="graph replays per secondary measurement")
@@ -513,6 +516,104 @@ def bench_loader(torch, args):
                                       bytes=TOPK * PER_EXPERT,
                                       gbps=round(TOPK * PER_EXPERT / ex_s / 1e9, 2)),
                 source="page cache (file just written); median of 3 after one warm-up")
+
+
+def bench_cache(torch, device, synth, args, layers):
+    """Route-driven expert cache (logan_hip_expert_cache_*, the reference's
+    RouteCache / RouteArena) at config 3: one layer's switch_mlp banks
+    (512 experts, 4-bit g64, fp16 sidecars) in a safetensors file, the
+    shared expert resident. Per token-layer, wall time of what an engine
+    does on this path: route on device (logan_hip_route_topk), the route to
+    the host (one synchronisation), fetch (cache bookkeeping plus the loads
+    of missed and arena ranks from the file through the pinned staging ring
+    into HBM, ordered before the block), the block on the cached experts,
+    then a synchronisation. cold: no retained blocks, every rank streams
+    through the route arena (10 experts, 17.7 MB per token-layer, from the
+    page cache); warm: 10 retained blocks and one route repeated, every
+    rank hits; resident: the same route / sync / block sequence on resident
+    banks (no fetch), the floor of the host round trip."""
+    import tempfile
+
+    import numpy as np
+
+    from safetensors.numpy import save_file
+
+    from logan_amd import checkpoint
+
+    rng = np.random.default_rng(88)
+    tensors = {}
+    for role, O, I in (("gate_proj", INTER, D), ("up_proj", INTER, D), ("down_proj", D, INTER)):
+        w, sc, bi = synth.make_affine(rng, O, I, BITS, GS, fp16=True, E=E)
+        tensors[f"model.layers.0.mlp.switch_mlp.{role}.weight"] = w.view(np.uint32)
+        tensors[f"model.layers.0.mlp.switch_mlp.{role}.scales"] = sc.view(np.float16)
+        tensors[f"model.layers.0.mlp.switch_mlp.{role}.biases"] = bi.view(np.float16)
+    tmpdir = os.environ.get("TMPDIR", "/tmp")
+    fd, path = tempfile.mkstemp(suffix=".safetensors", dir=tmpdir)
+    os.close(fd)
+    res = {}
+    try:
+        save_file(tensors, path)
+        del tensors
+        n = 40
+        g = torch.Generator(device="cuda")
+        g.manual_seed(4242)
+        xs = torch.randn((n, 1, D), device="cuda", generator=g).to(torch.bfloat16)
+        lgs = torch.randn((n, 1, E), device="cuda", generator=g).to(torch.bfloat16)
+        out = torch.empty((1, D), dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(layers[0].workspace_bytes(1), dtype=torch.uint8, device="cuda")
+        base = layers[0]
+        with checkpoint.StFile.open(path) as st:
+            for mode, blocks, same in (("cold", 0, False), ("warm", TOPK, True)):
+                cache = checkpoint.ExpertCache(st, E, D, INTER, blocks_per_layer=blocks, topk=TOPK,
+                                               layers=1)
+                lay = device.MoeLayer(*cache.geometry(BITS, GS, aux_fp16=True), TOPK,
+                                      base.shared_gate, base.shared_up, base.shared_down,
+                                      base.shared_gate_vec)
+
+                def token(i):
+                    j = 0 if same else i
+                    idx, _ = device.route_topk(lgs[j], TOPK)
+                    ex = idx.cpu().numpy()[0]
+                    bl = cache.fetch(0, ex)
+                    device.moe_block_cached(lay, cache, ex, bl, xs[i], lgs[j], out=out, workspace=ws)
+
+                for i in range(3):
+                    token(i)
+                torch.cuda.synchronize()
+                s0 = cache.stats()
+                t0 = time.perf_counter()
+                for i in range(3, n):
+                    token(i)
+                torch.cuda.synchronize()
+                us = (time.perf_counter() - t0) / (n - 3) * 1e6
+                s1 = cache.stats()
+                loaded = s1["bytes_loaded"] - s0["bytes_loaded"]
+                res[mode] = dict(us_per_token_layer=round(us, 1),
+                                 hits=s1["hits"] - s0["hits"], misses=s1["misses"] - s0["misses"],
+                                 streamed=s1["streamed"] - s0["streamed"],
+                                 bytes_loaded_per_token=loaded // (n - 3),
+                                 load_gbps=round(loaded / (us * 1e-6 * (n - 3)) / 1e9, 2))
+                log(f"expert cache {mode}: {us:.1f} us/token-layer, {res[mode]}")
+                cache.close()
+        # the same host round trip on resident banks
+        for i in range(3):
+            idx, _ = device.route_topk(lgs[i], TOPK)
+            idx.cpu()
+            device.moe_block(base, xs[i], lgs[i], out=out, workspace=ws)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(3, n):
+            idx, _ = device.route_topk(lgs[i], TOPK)
+            idx.cpu()
+            device.moe_block(base, xs[i], lgs[i], out=out, workspace=ws)
+        torch.cuda.synchronize()
+        res["resident"] = dict(us_per_token_layer=round((time.perf_counter() - t0) / (n - 3) * 1e6, 1))
+        log(f"expert cache resident floor: {res['resident']}")
+    finally:
+        os.unlink(path)
+    res["block_bytes"] = PER_EXPERT
+    res["source"] = "page cache (file just written); wall time per token-layer, 37 tokens"
+    return res
 
 
 # Qwen3-Next-80B-A3B projections per layer (hidden 2048; 16 q heads x 256 with
@@ -997,6 +1098,8 @@ def main():
             secondary["mxfp4"] = bench_mxfp4(torch, device, args)
         if "loader" in legs:
             secondary["loader"] = bench_loader(torch, args)
+        if "cache" in legs:
+            secondary["expert_cache"] = bench_cache(torch, device, synth, args, layers)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")

@@ -155,12 +155,17 @@ int run_jobs(LoganHipExpertCache *c, const std::vector<Job> &jobs, hipStream_t s
     }
     g.pending[slot] = false;
     char *buf = reinterpret_cast<char *>(g.buf[slot]);
-    // one reader thread per expert image, up to the ring's reader count
+    // one reader thread per expert image, up to the ring's reader count; each
+    // image's copy is queued as soon as it is read, so reads and copies overlap
     const int t = (int)std::min<size_t>(n, (size_t)std::max(1, g.readers));
     std::vector<char> ok(n, 0);
     auto work = [&](int w) {
-      for (size_t i = (size_t)w; i < n; i += (size_t)t)
-        ok[i] = read_job(c, jobs[j0 + i], buf + i * c->stride);
+      for (size_t i = (size_t)w; i < n; i += (size_t)t) {
+        char *src = buf + i * c->stride;
+        if (!read_job(c, jobs[j0 + i], src)) continue;
+        char *dst = c->base + (size_t)jobs[j0 + i].block * c->stride;
+        ok[i] = hipMemcpyAsync(dst, src, c->stride, hipMemcpyHostToDevice, g.st) == hipSuccess ? 1 : 2;
+      }
     };
     if (t == 1) {
       work(0);
@@ -169,25 +174,20 @@ int run_jobs(LoganHipExpertCache *c, const std::vector<Job> &jobs, hipStream_t s
       for (int w = 0; w < t; ++w) th.emplace_back(work, w);
       for (auto &x : th) x.join();
     }
+    // the slot's event after every copy queued from it, even on failure
+    const hipError_t re = hipEventRecord(g.ev[slot], g.st);
+    g.pending[slot] = re == hipSuccess;
     for (size_t i = 0; i < n; ++i)
-      if (!ok[i]) {
-        *err = "expert cache: read of layer " + std::to_string(jobs[j0 + i].layer) + " expert " +
-               std::to_string(jobs[j0 + i].expert) + " failed";
+      if (ok[i] != 1) {
+        *err = ok[i] == 0 ? "expert cache: read of layer " + std::to_string(jobs[j0 + i].layer) +
+                                " expert " + std::to_string(jobs[j0 + i].expert) + " failed"
+                          : std::string("expert cache: hipMemcpyAsync failed");
         return -1;
       }
-    for (size_t i = 0; i < n; ++i) {
-      char *dst = c->base + (size_t)jobs[j0 + i].block * c->stride;
-      if (hipMemcpyAsync(dst, buf + i * c->stride, c->stride, hipMemcpyHostToDevice, g.st) !=
-          hipSuccess) {
-        *err = "expert cache: hipMemcpyAsync failed";
-        return -1;
-      }
-    }
-    if (hipEventRecord(g.ev[slot], g.st) != hipSuccess) {
+    if (re != hipSuccess) {
       *err = "expert cache: event record failed";
       return -1;
     }
-    g.pending[slot] = true;
     slot = (slot + 1) % lh::ld::kSlots;
   }
   if (hipEventRecord(c->ev_done, g.st) != hipSuccess || hipStreamWaitEvent(st, c->ev_done, 0) != hipSuccess) {
