@@ -28,7 +28,7 @@ class SlotRing {
     Lease() = default;
     Lease(const Lease &) = delete;
     Lease &operator=(const Lease &) = delete;
-    ~Lease() { release(true); }
+    ~Lease() { (void)release(true); }
     int slot() const { return slot_; }
     // after the last kernel that touches the slot: record, unlock (the
     // destructor does the same for a lease left held on an error path)

@@ -368,12 +368,26 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
     if (!shared && wave == 0) {
+      int ex = -1;
+      if constexpr (LF) {
+        // 32-bit keys first (route_dev.hpp: select_fast / fast_ok)
+        uint32_t fs[kFusedMaxSlots + 1];
+        rk.select_fast(a.E, slot + 1, fs);
+        float v, m;
+        if (rk.fast_ok(fs, slot, v, m)) {
+          uint32_t ks = fs[0];
+#pragma unroll
+          for (int r = 1; r < kFusedMaxSlots; ++r) ks = r == slot ? fs[r] : ks;
+          ex = RK::expert32(ks);
+        }
+      }
+      if (ex < 0) {
       Key sel[kFusedMaxSlots];
       rk.select(a.E, slot + 1, sel);
       Key mine = sel[0];
 #pragma unroll
       for (int r = 1; r < kFusedMaxSlots; ++r) mine = r == slot ? sel[r] : mine;
-      int ex = RK::expert(mine);
+      ex = RK::expert(mine);
       // a probability tie the logit order cannot see (route_dev.hpp): this
       // slot's rank then comes from the reference's own arithmetic
       const float m = RK::logit(sel[0]), ls = RK::logit(mine);
@@ -392,6 +406,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
           const RouteLane rl = route_exact<KPL, LF>(a.logits, 0, a.E, a.k);
           ex = __builtin_amdgcn_readlane(rl.idx, slot);
         }
+      }
       }
       if (lane == 0) s_sel[0] = 0xffffu - (uint32_t)ex;
     }
@@ -549,6 +564,26 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
   }
   if (wave == 0) {
+    float wr = 0.f;
+    uint32_t enc = 0u;  // 0xffff - expert of rank `lane`, 0 past the route
+    bool routed = false;
+    if constexpr (LF) {
+      // 32-bit keys first (route_dev.hpp: select_fast / fast_ok)
+      uint32_t fs[kFusedMaxSlots + 1];
+      rk.select_fast(a.E, g.k, fs);
+      float v, m;
+      if (rk.fast_ok(fs, g.k - 1, v, m)) {
+        uint32_t kr = 0u;
+#pragma unroll
+        for (int r = 0; r < kFusedMaxSlots; ++r) kr = lane == r ? fs[r] : kr;
+        // combine weights, one rank per lane (logan-qwen4/src/lib.rs:8694)
+        const float ev = lane < g.k ? __expf(v - m) : 0.f;
+        wr = ev / wave_sum_f32(ev);
+        enc = lane < g.k ? 0xffffu - (uint32_t)RK::expert32(kr) : 0u;
+        routed = true;
+      }
+    }
+    if (!routed) {
     Key sel0[kFusedMaxSlots];
     rk.select(a.E, g.k, sel0);
     Key mine = 0;
@@ -569,8 +604,6 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
         cand = cand || (rk.key[i] != Key(0) && tie_other(RK::logit(rk.key[i]), llast, m));
       exact = __any(cand) || tie_global(m, llast);
     }
-    float wr;
-    uint32_t enc;  // 0xffff - expert of rank `lane`, 0 past the route
     if (exact) {
       // a probability tie the logit order cannot see (route_dev.hpp)
       const RouteLane rl = route_exact<KPL, LF>(a.logits, 0, a.E, g.k);
@@ -582,6 +615,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       const float ev = lane < g.k ? __expf(RK::logit(mine) - m) : 0.f;
       wr = ev / wave_sum_f32(ev);
       enc = lane < g.k ? 0xffffu - (uint32_t)RK::expert(mine) : 0u;
+    }
     }
     if (lane < kFusedMaxSlots) s_sel[lane] = enc;
     if (lane < kFusedMaxSlots) s_w[lane] = wr;

@@ -263,6 +263,82 @@ struct WaveKeys {
     if constexpr (LF) return (int)(0xffffffffu - (uint32_t)k);
     else return (int)(0xffffu - (k & 0xffffu));
   }
+
+  // ---- f32 logits on 32-bit keys (LF only; before select) ----------------
+  // Key = the upper 32 - IB bits of the ordered f32 (its prefix) above an
+  // IB-bit inverted expert index. Distinct prefixes order as the values do,
+  // so where the keys that decide the ranks have pairwise distinct prefixes
+  // the 32-bit selection equals the selection on (value desc, index asc),
+  // with each round a 32-bit wave max like the bf16 keys'. fast_ok says when
+  // that holds and no probability tie can reach the ranks; otherwise the
+  // caller selects on the 64-bit keys (select) instead. The raw logits stay
+  // in key[] until select converts them.
+  static constexpr int IB = KPL <= 8 ? 9 : 10;
+  static constexpr uint32_t IM = (1u << IB) - 1u;
+  __device__ static __forceinline__ int expert32(uint32_t k) { return (int)(IM - (k & IM)); }
+  // exact logit of expert e (lane-varying): lane e % 64 holds it in key[e / 64]
+  __device__ __forceinline__ float value_lane(int e) const {
+    float out = 0.f;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const float t = __shfl(__uint_as_float((uint32_t)key[i]), e & 63, 64);
+      out = (e >> 6) == i ? t : out;
+    }
+    return out;
+  }
+  // sel[r] for r <= rounds: the keys of ranks 0 .. rounds (0 past E)
+  template <int NSEL>
+  __device__ __forceinline__ void select_fast(int E, int rounds, uint32_t (&sel)[NSEL]) const {
+    static_assert(LF, "f32 keys");
+    const int lane = threadIdx.x & 63;
+    uint32_t k32[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int e = i * 64 + lane;
+      k32[i] = e < E ? ((ord32f(__uint_as_float((uint32_t)key[i])) & ~IM) | (IM - (uint32_t)e)) : 0u;
+    }
+    sort_desc<KPL>(k32);
+#pragma unroll
+    for (int r = 0; r < NSEL; ++r) {
+      sel[r] = 0u;
+      if (r <= rounds) {
+        const uint32_t m = wave_max_u32(k32[0]);
+        sel[r] = m;
+        const bool mine = k32[0] == m;  // keys are unique
+#pragma unroll
+        for (int i = 0; i < KPL - 1; ++i) k32[i] = mine ? k32[i + 1] : k32[i];
+        k32[KPL - 1] = mine ? 0u : k32[KPL - 1];
+      }
+    }
+  }
+  // True when ranks 0 .. R of select_fast's keys (sel[0 .. R + 1] filled)
+  // are the reference's: no two of the keys of ranks 0 .. R + 1 share a
+  // prefix, no probability tie joins consecutive ranks up to R, no logit of
+  // the best unselected prefix can tie with rank R, and rank 0 / rank R pass
+  // tie_global (route_dev.hpp's tie rules, on exact values). Lane r <= R
+  // gets rank r's exact logit in v, every lane the maximum in m.
+  template <int NSEL>
+  __device__ __forceinline__ bool fast_ok(const uint32_t (&sel)[NSEL], int R, float &v, float &m) const {
+    const int lane = threadIdx.x & 63;
+    uint32_t kr = 0u;
+#pragma unroll
+    for (int r = 0; r < NSEL; ++r) kr = lane == r ? sel[r] : kr;
+    const uint32_t knext = __shfl(kr, (lane + 1) & 63, 64);
+    // every lane runs the cross-lane reads (a lane outside a branch would
+    // not supply its registers to them)
+    const float vall = value_lane(expert32(kr));
+    v = lane <= R ? vall : 0.f;
+    m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+    const float vR = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), R));
+    const float vnext = __shfl(v, (lane + 1) & 63, 64);
+    bool bad = lane <= R && knext != 0u && (kr >> IB) == (knext >> IB);
+    bad = bad || (lane < R && tie_pair(v, vnext, m));
+    if (lane == R + 1 && kr != 0u) {
+      const float bhi = unord32f(kr | IM);  // largest logit with this prefix
+      bad = bad || fabsf((bhi - m) - (vR - m)) <= kTieGap;
+    }
+    return !__any(bad) && !tie_global(m, vR);
+  }
   __device__ static __forceinline__ float logit(K k) {
     if constexpr (LF) return unord32f((uint32_t)(k >> 32));
     else return unord16(k >> 16);

@@ -17,6 +17,9 @@ only non-decreasing in the logit, so distinct logits can tie in p:
   recomputed selection must agree with the logit order there);
 * "nan": one NaN logit makes every probability NaN; the reference's
   comparisons are then all false and it keeps experts 0..k-1;
+* "prefix": f32 logits 2^-16 apart next to 2.0 (distinct probabilities,
+  logit order) that share the upper bits the 32-bit selection keys keep, so
+  that selection must hand over to the 64-bit keys;
 * "negnan": the same with NaN bit patterns that have the sign bit set
   (0xFFC0 and others, bf16-exact): an ordered-bits key would sort such a NaN
   below every number, so the selection must treat any NaN as NaN whatever
@@ -45,7 +48,7 @@ BF16_KINDS = ["subtract", "underflow", "neginf", "nan", "negnan"]
 NAN_KINDS = {"nan", "negnan"}
 # NaN bit patterns (f32, each bf16-exact), one per seed in turn
 NEG_NANS = [0xFFC00000, 0xFF810000, 0xFFFF0000, 0x7F810000]
-F32_KINDS = BF16_KINDS + ["nearmax", "divtie", "ulp"]
+F32_KINDS = BF16_KINDS + ["nearmax", "divtie", "ulp", "prefix"]
 ORDER_DIFFERS = {"subtract", "underflow", "neginf", "nearmax", "divtie", "nan", "negnan"}
 
 
@@ -68,9 +71,9 @@ def tie_logits(kind: str, seed: int) -> np.ndarray:
         lf[1::2] = -120.0 - 2.0 * rng.integers(0, 8, E // 2)
         pos = rng.choice(E, 6, replace=False)
         lf[pos] = np.float32([3.0, 2.5, 2.0, 1.5, 1.0, 0.5])
-    elif kind in ("nearmax", "divtie", "ulp"):
+    elif kind in ("nearmax", "divtie", "ulp", "prefix"):
         m, step = {"nearmax": (0.25, 2.0 ** -26), "divtie": (0.75, 2.0 ** -24),
-                   "ulp": (2.0, 2.0 ** -22)}[kind]
+                   "ulp": (2.0, 2.0 ** -22), "prefix": (2.0, 2.0 ** -16)}[kind]
         m, step = np.float32(m), np.float32(step)
         lf[:] = (m - np.float32([3.0, 4.5, 6.0, 7.5]))[rng.integers(0, 4, E)]
         pos = np.sort(rng.choice(E, 12, replace=False))
@@ -155,6 +158,10 @@ def check_route(idx, w, lf, k, kind):
     np.testing.assert_array_equal(idx, ridx)
     if kind in NAN_KINDS:
         assert np.isnan(w).all()
+    elif kind == "prefix":
+        # no probability tie: the fast weights exp(l_r - l_0) / sum, which
+        # equal the reference's val_r / wsum up to rounding
+        np.testing.assert_allclose(w, rw, rtol=2e-6, atol=0)
     else:
         # the recomputed path is the reference's arithmetic: bit-exact weights
         np.testing.assert_array_equal(w, rw)
@@ -182,7 +189,9 @@ MOE_TIE_CASES = [(1, "bf16", "subtract"), (1, "bf16", "underflow"), (1, "bf16", 
                  (1, "f32", "divtie"), (1, "f32", "nearmax"), (16, "bf16", "subtract"),
                  (16, "f32", "divtie"), (64, "bf16", "underflow"), (64, "f32", "divtie"),
                  (1, "bf16", "negnan"), (1, "f32", "negnan"), (1, "bf16", "nan"),
-                 (16, "bf16", "negnan"), (64, "bf16", "negnan"), (64, "f32", "negnan")]
+                 (16, "bf16", "negnan"), (64, "bf16", "negnan"), (64, "f32", "negnan"),
+                 (1, "f32", "prefix"), (16, "f32", "prefix"), (64, "f32", "prefix"),
+                 (1, "f32", "nan")]
 
 
 # B > 1 takes the multi-launch path either way: only B = 1 runs both ways
