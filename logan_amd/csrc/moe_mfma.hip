@@ -397,6 +397,227 @@ __global__ __launch_bounds__(WAVES * 64, WAVES <= 4 ? 2 : MOE_GU_MINW) void moe_
 }
 
 // ---------------------------------------------------------------------------
+// 3b. gate/up with the weights staged in LDS (4- and 8-bit codes, 8 waves, the
+//     large-batch shape). The register form above has each lane load its own
+//     8 or 16 bytes of 16 rows per step: one load instruction touches 16
+//     lines 32 bytes at a time, the same line again on each of the next
+//     three steps, and 8 waves x 32 rows of lines in flight per CU do not
+//     stay in its L1. Here each wave copies its 16 gate and 16 up rows batch
+//     by batch (128 bytes of every row: 4 steps of 4-bit codes, 2 of 8-bit)
+//     straight into a private two-batch LDS ring with global_load_lds: 8
+//     lanes cover one row's 128 bytes, so each instruction reads whole lines
+//     of 8 rows, each line once. The 16-byte chunks of a row are XOR-swizzled
+//     by the row (source chunk c of row r at position c ^ (r & 7)), so the
+//     16 rows of an MFMA operand read spread over the banks. Scale/bias
+//     words, the x tile, the MFMA steps and the fold are those of the
+//     register form.
+
+// Direct global -> LDS copies whose LDS writes the compiler does not see, so it
+// inserts no waits for them before LDS reads (it would wait for every copy in
+// flight, the ring's next batch included); the kernel waits with vmcnt
+// itself. Lane l writes its 16 (4) bytes at lds + 16 l (4 l); lds is the
+// wave-uniform LDS byte address.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const uint8_t *)p);
+}
+__device__ __forceinline__ void lds_copy16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+
+template <int BITS, bool FP16>
+__global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMWs w, int ipt) {
+  static_assert(BITS == 4 || BITS == 8, "128-byte row batches of 4- or 8-bit codes");
+  constexpr int WAVES = 8, NT = WAVES * 64, RPB = 16 * WAVES;
+  constexpr int GU = BITS == 4 ? 4 : 2;  // steps per batch: 128 bytes of each row
+  constexpr int NB = 2;                  // batches in a wave's ring
+  // per wave and batch: gate rows, up rows (16 x 128 B each), then the
+  // scale / bias words of the batch's GU steps (groups of 64) of both
+  constexpr int AUXB = BITS == 4 ? 512 : 256;
+  constexpr int SLOT = 4096 + AUXB;
+  constexpr int NI = BITS == 4 ? 6 : 5;  // copies per batch
+  __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
+  __shared__ __align__(16) uint8_t swt[NB][WAVES][SLOT];
+  __shared__ int s_tok[kMTok];
+  using S = MfmaStep<BITS>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
+  if (tile >= *w.n_tiles) return;
+  const int4 tr = w.tiles[tile];
+  const int e = __builtin_amdgcn_readfirstlane(tr.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
+  const bool shared = e < 0;
+  const int rows = shared ? a.sinter : a.inter;
+  if (rb * RPB >= rows) return;
+  const DevBank &gbk = shared ? a.sgate : a.gate;
+  const DevBank &ubk = shared ? a.sup : a.up;
+  const size_t eo = shared ? 0 : (size_t)e;
+  const int jw = rb * RPB + wave * 16;  // the wave's first row
+  // weight copies: 8 lanes per row, rows 8 i + lr; the lane takes source
+  // chunk lc ^ lr of its row (position lc), so chunk c of row r sits at c ^ (r & 7)
+  const int lr = lane >> 3, lc = lane & 7;
+  const int jl0 = min(jw + lr, rows - 1), jl1 = min(jw + 8 + lr, rows - 1);
+  const int sc = 16 * (lc ^ lr);
+  const uint8_t *gb = gbk.m.w + eo * gbk.w_stride;
+  const uint8_t *ub = ubk.m.w + eo * ubk.w_stride;
+  const uint8_t *gw0 = gb + (size_t)jl0 * gbk.m.row_bytes + sc, *gw1 = gb + (size_t)jl1 * gbk.m.row_bytes + sc;
+  const uint8_t *uw0 = ub + (size_t)jl0 * ubk.m.row_bytes + sc, *uw1 = ub + (size_t)jl1 * ubk.m.row_bytes + sc;
+  // scale/bias copies (u16 index of the batch's first step is added per batch)
+  const uint16_t *ax0, *ax1 = nullptr;
+  if constexpr (BITS == 4) {
+    // copy m: lanes 0-31 scales, 32-63 biases; row (l & 31) / 2, dword l & 1
+    const int ar = min(jw + ((lane & 31) >> 1), rows - 1);
+    const size_t po = eo * gbk.p_stride + (size_t)ar * gbk.m.ng + 2 * (lane & 1);
+    ax0 = (lane < 32 ? gbk.m.sc : gbk.m.bi) + po;
+    ax1 = (lane < 32 ? ubk.m.sc : ubk.m.bi) + eo * ubk.p_stride + (size_t)ar * ubk.m.ng + 2 * (lane & 1);
+  } else {
+    // one copy: lanes 0-15 gate scales, 16-31 gate biases, 32-47 up scales,
+    // 48-63 up biases; row l & 15
+    const int ar = min(jw + (lane & 15), rows - 1);
+    const DevBank &bk = lane < 32 ? gbk : ubk;
+    const uint16_t *base = ((lane >> 4) & 1) ? bk.m.bi : bk.m.sc;
+    ax0 = base + eo * bk.p_stride + (size_t)ar * bk.m.ng;
+  }
+  const int nslots = a.B * a.k;
+  const int chunk = a.D < kMChunk ? a.D : kMChunk;
+  const int nch = a.D / chunk;
+  const int bpc = (chunk >> 6) / GU;  // batches per chunk
+  const uint16_t *xsrc = BITS == 4 ? w.xop : a.x;  // x in the operand order
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+  if (tid < kMTok) s_tok[tid] = shared ? row0 - nslots + min(tid, cnt - 1) : w.tok[row0 + min(tid, cnt - 1)];
+  __syncthreads();
+
+  // batch b (absolute: bytes [128 b, 128 b + 128) of every row, steps
+  // [GU b, GU b + GU)) into ring slot b % NB
+  auto issue = [&](int b) {
+    const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(&swt[b % NB][wave][0]));
+    const size_t o = (size_t)b * 128;
+    lds_copy16(gw0 + o, d);
+    lds_copy16(gw1 + o, d + 1024);
+    lds_copy16(uw0 + o, d + 2048);
+    lds_copy16(uw1 + o, d + 3072);
+    lds_copy4(ax0 + (size_t)b * GU, d + 4096);
+    if constexpr (BITS == 4) lds_copy4(ax1 + (size_t)b * GU, d + 4096 + 256);
+  };
+  // the lane's 16 codes of step u of batch b, matrix m (0 gate, 1 up)
+  auto raw = [&](const uint8_t *slot, int m, int u, SkRaw<BITS> &r) {
+    const uint8_t *row = slot + m * 2048 + r16 * 128;
+    if constexpr (BITS == 4) {
+      const int c = 2 * u + (g >> 1);
+      r.v = *reinterpret_cast<const uint2 *>(row + ((c ^ (r16 & 7)) << 4) + 8 * (g & 1));
+    } else {
+      const int c = 4 * u + g;
+      r.v = *reinterpret_cast<const uint4 *>(row + ((c ^ (r16 & 7)) << 4));
+    }
+  };
+  auto step = [&](int b, int bl) {
+    const uint8_t *slot = &swt[b % NB][wave][0];
+    // this lane's output row's scale / bias words of the batch's GU steps
+    uint32_t gs_w[GU / 2], gb_w[GU / 2], us_w[GU / 2], ub_w[GU / 2];
+    if constexpr (BITS == 4) {
+      const uint2 a0 = *reinterpret_cast<const uint2 *>(slot + 4096 + 8 * r16);
+      const uint2 a1 = *reinterpret_cast<const uint2 *>(slot + 4096 + 128 + 8 * r16);
+      const uint2 a2 = *reinterpret_cast<const uint2 *>(slot + 4096 + 256 + 8 * r16);
+      const uint2 a3 = *reinterpret_cast<const uint2 *>(slot + 4096 + 384 + 8 * r16);
+      gs_w[0] = a0.x; gs_w[1] = a0.y; gb_w[0] = a1.x; gb_w[1] = a1.y;
+      us_w[0] = a2.x; us_w[1] = a2.y; ub_w[0] = a3.x; ub_w[1] = a3.y;
+    } else {
+      gs_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 4 * r16);
+      gb_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 64 + 4 * r16);
+      us_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 128 + 4 * r16);
+      ub_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 192 + 4 * r16);
+    }
+#pragma unroll
+    for (int u = 0; u < GU; ++u) {
+      bf16x8_t a0, a1, b0, b1;
+      S::a_ops(sx + r16 * chunk, ((bl * GU + u) * 64 + 16 * g) >> 3, r16, a0, a1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      SkRaw<BITS> rg, ru;
+      raw(slot, 0, u, rg);
+      raw(slot, 1, u, ru);
+      const int sh = 16 * (u & 1);
+      S::b_ops(rg, kc, b0, b1);
+      f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      S::fold(accg, d, xs, aux_f32<FP16>((gs_w[u >> 1] >> sh) & 0xffffu),
+              aux_f32<FP16>((gb_w[u >> 1] >> sh) & 0xffffu));
+      S::b_ops(ru, kc, b0, b1);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+      S::fold(accu, d, xs, aux_f32<FP16>((us_w[u >> 1] >> sh) & 0xffffu),
+              aux_f32<FP16>((ub_w[u >> 1] >> sh) & 0xffffu));
+    }
+  };
+
+  for (int c = 0; c < nch; ++c) {
+    const int b0 = c * bpc;
+    // the x tile's copies and the chunk's first batch, then one full wait
+    if (c > 0) __syncthreads();
+    {
+      constexpr int NV = kMTok * kMChunk / 8 / NT;
+      const int gpr = chunk >> 3;  // granules per row (>= 32)
+      auto dma = [&](int base) {
+        const int pg = base + lane;
+        const int m = pg / gpr, qq = swz(m, pg % gpr);
+        lds_dma16(xsrc + (size_t)s_tok[m] * a.D + c * chunk + 8 * qq, sx + 8 * base);
+      };
+      if (chunk == kMChunk) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) dma(NT * i + 64 * wave);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+          if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
+      }
+    }
+    issue(b0);
+    lds_dma_wait();
+    __syncthreads();
+    // batch bl + 1 in flight while batch bl is multiplied: wait for all but
+    // the NI copies of the batch issued last. An issue past the chunk end
+    // copies its last batch again (into the slot just released), so the
+    // count of copies behind every batch stays NI.
+    for (int bl = 0; bl < bpc; ++bl) {
+      issue(b0 + min(bl + 1, bpc - 1));
+      lds_dma_wait_behind<NI>();
+      step(b0 + bl, bl);
+      // the slot read by step() is the next issue's destination: its LDS
+      // reads are complete once their values are used, which step() did
+    }
+  }
+  // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16,
+  // each at its place in the down pass's operand order
+  const int jj = jw + r16;
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  if (jj < rows) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * g + i;
+      if (m < cnt) {
+        const float h = silu(accg[i]) * accu[i];
+        const uint32_t hi = f32_to_bf16_rne(h);
+        const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
+        const size_t o = (size_t)(row0 + m) * hmax + S::op_pos(jj);
+        w.h_hi[o] = (uint16_t)hi;
+        w.h_lo[o] = (uint16_t)lo;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 4. down: block = (tile, 128 rows), wave = 2 x 16 rows, K <= 512: h copied
 //    into LDS first, then every scale/bias and weight load of the wave, and
 //    each step waits only for its own weights
@@ -630,6 +851,14 @@ static hipError_t moe_gateup_launch(const MoeArgs &a, const MoeMWs &w, hipStream
     const bool gs64 = a.gate.m.gs == 64 && (!a.sgate.m.w || a.sgate.m.gs == 64) &&
                       a.gate.m.ng % (MOE_GU < 4 ? 4 : MOE_GU) == 0;
     const dim3 grid(w.max_tiles * ipt), block(WV * 64);
+    if constexpr (WV == 8 && (BITS == 4 || BITS == 8)) {
+      // the large-batch shape with the weights staged in LDS (groups of 64)
+      if (gs64 && a.gate.m.gs == 64) {
+        if (a.gate.m.fp16) hipLaunchKernelGGL((moe_gateup_lds_kernel<BITS, true>), grid, block, 0, st, a, w, ipt);
+        else hipLaunchKernelGGL((moe_gateup_lds_kernel<BITS, false>), grid, block, 0, st, a, w, ipt);
+        return hipGetLastError();
+      }
+    }
     if (a.gate.m.fp16) {
       if (gs64) hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, true, true>), grid, block, 0, st, a, w, ipt);
       else hipLaunchKernelGGL((moe_gateup_mfma_kernel<BITS, MOE_GU, WV, false, true>), grid, block, 0, st, a, w, ipt);

@@ -368,7 +368,9 @@ def _check_tokens(layer, xb, lb, out32, idx, w, tokens):
                                                 (8, 33, True, False), (5, 40, True, True),
                                                 (6, 32, True, True), (5, 3, False, False),
                                                 (6, 17, False, True),
-                                                (5, 136, True, True)])   # 8-wave gate/up blocks
+                                                (5, 136, True, True),    # 8-wave gate/up blocks
+                                                (4, 200, True, True),    # LDS-staged 8-wave blocks
+                                                (8, 150, True, True)])
 def test_moe_mfma_path_matches_oracle(gpu, mfma_min_b, bits, B, zipf, shared):
     """The token-batch MFMA path (forced for every B) against the oracle:
     routing bit-exact, outputs at f32-accumulation level; Zipf routes put
@@ -404,6 +406,26 @@ def test_moe_mfma_fp16_sidecars(gpu, mfma_min_b, bits):
     lb = make_logits(rng, B, 128)
     out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
     _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(B))
+
+
+@pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
+@pytest.mark.parametrize("bits,fp16,D,sinter", [(4, True, 2048, 512), (8, True, 1024, 384),
+                                                 (4, False, 1024, 384), (8, False, 2048, 256)])
+def test_moe_mfma_large_batch_staged_weights(gpu, mfma_min_b, bits, fp16, D, sinter):
+    """Batches above 128 tokens take the 8-wave gate/up blocks whose 4- and
+    8-bit weights are staged in LDS: fp16 and bf16 sidecars, D = 1024 (one
+    x chunk shorter than the LDS tile) and 2048, a shared expert of another
+    size; every 7th token against the oracle."""
+    import torch
+
+    print(f"moe mfma staged bits={bits} fp16={fp16} D={D} sinter={sinter}", flush=True)
+    layer = Layer(torch, 256, 8, D, 512, bits, 64, seed=71 + bits + D, fp16=fp16, sinter=sinter)
+    rng = np.random.default_rng(72 + D)
+    B = 160
+    xb = make_x(rng, B, D)
+    lb = make_logits(rng, B, 256, zipf_s=1.1)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    _check_tokens(layer, xb, lb, out32.cpu().numpy(), idx, w, range(0, B, 7))
 
 
 @pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
