@@ -404,18 +404,15 @@ __global__ __launch_bounds__(WAVES * 64, WAVES <= 4 ? 2 : MOE_GU_MINW) void moe_
 //     three steps, and 8 waves x 32 rows of lines in flight per CU do not
 //     stay in its L1. Here each wave copies its 16 gate and 16 up rows batch
 //     by batch (128 bytes of every row: 4 steps of 4-bit codes, 2 of 8-bit)
-//     straight into a private two-batch LDS ring with global_load_lds: 8
-//     lanes cover one row's 128 bytes, so each instruction reads whole lines
-//     of 8 rows, each line once. The 16-byte chunks of a row are XOR-swizzled
-//     by the row (source chunk c of row r at position c ^ (r & 7)), so the
-//     16 rows of an MFMA operand read spread over the banks. Scale/bias
-//     words, the x tile, the MFMA steps and the fold are those of the
-//     register form.
+//     straight into a private LDS ring with global_load_lds: 8 lanes cover
+//     one row's 128 bytes, so each instruction reads whole lines of 8 rows,
+//     each line once. Scale/bias words, the x tile, the MFMA steps and the
+//     fold are those of the register form.
 
 // Direct global -> LDS copies whose LDS writes the compiler does not see, so it
 // inserts no waits for them before LDS reads (it would wait for every copy in
-// flight, the ring's next batch included); the kernel waits with vmcnt
-// itself. Lane l writes its 16 (4) bytes at lds + 16 l (4 l); lds is the
+// flight, the ring's next batches included); the kernels wait with vmcnt
+// themselves. Lane l writes its 16 (4) bytes at lds + 16 l (4 l); lds is the
 // wave-uniform LDS byte address.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const uint8_t *)p);
@@ -429,19 +426,99 @@ __device__ __forceinline__ void lds_copy4(const void *src, uint32_t lds) {
                :: "v"(src), "s"(lds) : "memory", "m0");
 }
 
+// One slot of a wave's LDS ring: a batch of two 16-row groups (m = 0, 1) x
+// 128 bytes of BITS-bit codes (GU steps of 64), groups of 64 codes. Bytes
+// [2048 m, 2048 m + 2048): group m's rows, 128 bytes each, the 16-byte chunk
+// c of row r at position c ^ (r & 7) (the 16 rows of an MFMA operand read
+// spread over the banks); then the scale and bias words of the GU steps:
+// 4-bit: [128 m + 0: m's scales (8 bytes per row) | +128: biases] per group,
+// 8-bit: [64 (2m): m's scales (4 bytes per row) | 64 (2m + 1): biases].
+template <int BITS>
+struct RingSlot {
+  static_assert(BITS == 4 || BITS == 8, "128-byte row batches of 4- or 8-bit codes");
+  static constexpr int GU = BITS == 4 ? 4 : 2;  // steps per batch
+  static constexpr int BYTES = 4096 + (BITS == 4 ? 512 : 256);
+  static constexpr int NI = BITS == 4 ? 6 : 5;  // copies per batch
+
+  // the copies of one batch into slot d: row pointers wr[i] (rows 8 i + lane / 8
+  // of the slot, already at the batch's first byte plus the lane's source chunk
+  // 16 ((lane & 7) ^ (lane >> 3))), scale/bias pointers of the batch (aux1
+  // 4-bit only) as laid out by aux_ptr
+  static __device__ __forceinline__ void issue(uint32_t d, const uint8_t *wr[4], const uint16_t *aux0,
+                                               const uint16_t *aux1) {
+    lds_copy16(wr[0], d);
+    lds_copy16(wr[1], d + 1024);
+    lds_copy16(wr[2], d + 2048);
+    lds_copy16(wr[3], d + 3072);
+    lds_copy4(aux0, d + 4096);
+    if constexpr (BITS == 4) lds_copy4(aux1, d + 4096 + 256);
+  }
+  // the lane's first scale/bias word to copy (u16 index of the batch's first
+  // step added per batch) for groups whose rows are rowm[0], rowm[1] + (the
+  // lane's row inside its group, chosen here): 4-bit: copy m, lanes 0-31
+  // scales, 32-63 biases, row (l & 31) / 2, dword l & 1; 8-bit: one copy,
+  // lanes 0-15 group 0 scales, 16-31 its biases, 32-63 group 1 likewise, row l & 15
+  static __device__ __forceinline__ void aux_ptr(int lane, const DevBank &b0, const DevBank &b1,
+                                                 size_t eo, const int (&rowm)[2], int rmax,
+                                                 const uint16_t *(&aux)[2]) {
+    if constexpr (BITS == 4) {
+      const int rl = (lane & 31) >> 1;
+      const int r0 = min(rowm[0] + rl, rmax), r1 = min(rowm[1] + rl, rmax);
+      aux[0] = (lane < 32 ? b0.m.sc : b0.m.bi) + eo * b0.p_stride + (size_t)r0 * b0.m.ng + 2 * (lane & 1);
+      aux[1] = (lane < 32 ? b1.m.sc : b1.m.bi) + eo * b1.p_stride + (size_t)r1 * b1.m.ng + 2 * (lane & 1);
+    } else {
+      const int m = lane >> 5;
+      const DevBank &bk = m ? b1 : b0;
+      const int r = min(rowm[m] + (lane & 15), rmax);
+      aux[0] = (((lane >> 4) & 1) ? bk.m.bi : bk.m.sc) + eo * bk.p_stride + (size_t)r * bk.m.ng;
+      aux[1] = aux[0];
+    }
+  }
+  // the lane's 16 codes of step u, group m (lane = 16 g + r16)
+  static __device__ __forceinline__ void raw(const uint8_t *slot, int m, int u, int r16, int g,
+                                             SkRaw<BITS> &r) {
+    const uint8_t *row = slot + m * 2048 + r16 * 128;
+    if constexpr (BITS == 4) {
+      const int c = 2 * u + (g >> 1);
+      r.v = *reinterpret_cast<const uint2 *>(row + ((c ^ (r16 & 7)) << 4) + 8 * (g & 1));
+    } else {
+      const int c = 4 * u + g;
+      r.v = *reinterpret_cast<const uint4 *>(row + ((c ^ (r16 & 7)) << 4));
+    }
+  }
+  // output row r16's scale / bias words of the batch's steps, two u16 per word
+  static __device__ __forceinline__ void aux(const uint8_t *slot, int r16, uint32_t (&sw)[2][GU / 2],
+                                             uint32_t (&bw)[2][GU / 2]) {
+    if constexpr (BITS == 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint2 s2 = *reinterpret_cast<const uint2 *>(slot + 4096 + 256 * m + 8 * r16);
+        const uint2 b2 = *reinterpret_cast<const uint2 *>(slot + 4096 + 256 * m + 128 + 8 * r16);
+        sw[m][0] = s2.x; sw[m][1] = s2.y;
+        bw[m][0] = b2.x; bw[m][1] = b2.y;
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        sw[m][0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 128 * m + 4 * r16);
+        bw[m][0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 128 * m + 64 + 4 * r16);
+      }
+    }
+  }
+  // step u's u16 of a word pair
+  template <bool FP16>
+  static __device__ __forceinline__ float word(const uint32_t (&v)[GU / 2], int u) {
+    return aux_f32<FP16>((v[u >> 1] >> (16 * (u & 1))) & 0xffffu);
+  }
+};
+
 template <int BITS, bool FP16>
 __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMWs w, int ipt) {
-  static_assert(BITS == 4 || BITS == 8, "128-byte row batches of 4- or 8-bit codes");
   constexpr int WAVES = 8, NT = WAVES * 64, RPB = 16 * WAVES;
-  constexpr int GU = BITS == 4 ? 4 : 2;  // steps per batch: 128 bytes of each row
-  constexpr int NB = 2;                  // batches in a wave's ring
-  // per wave and batch: gate rows, up rows (16 x 128 B each), then the
-  // scale / bias words of the batch's GU steps (groups of 64) of both
-  constexpr int AUXB = BITS == 4 ? 512 : 256;
-  constexpr int SLOT = 4096 + AUXB;
-  constexpr int NI = BITS == 4 ? 6 : 5;  // copies per batch
+  using R = RingSlot<BITS>;
+  constexpr int GU = R::GU, NB = 2;  // two batches in a wave's ring
   __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
-  __shared__ __align__(16) uint8_t swt[NB][WAVES][SLOT];
+  __shared__ __align__(16) uint8_t swt[NB][WAVES][R::BYTES];
   __shared__ int s_tok[kMTok];
   using S = MfmaStep<BITS>;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -460,31 +537,14 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   const DevBank &ubk = shared ? a.sup : a.up;
   const size_t eo = shared ? 0 : (size_t)e;
   const int jw = rb * RPB + wave * 16;  // the wave's first row
-  // weight copies: 8 lanes per row, rows 8 i + lr; the lane takes source
-  // chunk lc ^ lr of its row (position lc), so chunk c of row r sits at c ^ (r & 7)
-  const int lr = lane >> 3, lc = lane & 7;
+  // ring group 0 = the gate rows, group 1 = the same rows of up
+  const int lr = lane >> 3, sc = 16 * ((lane & 7) ^ lr);
   const int jl0 = min(jw + lr, rows - 1), jl1 = min(jw + 8 + lr, rows - 1);
-  const int sc = 16 * (lc ^ lr);
-  const uint8_t *gb = gbk.m.w + eo * gbk.w_stride;
-  const uint8_t *ub = ubk.m.w + eo * ubk.w_stride;
-  const uint8_t *gw0 = gb + (size_t)jl0 * gbk.m.row_bytes + sc, *gw1 = gb + (size_t)jl1 * gbk.m.row_bytes + sc;
-  const uint8_t *uw0 = ub + (size_t)jl0 * ubk.m.row_bytes + sc, *uw1 = ub + (size_t)jl1 * ubk.m.row_bytes + sc;
-  // scale/bias copies (u16 index of the batch's first step is added per batch)
-  const uint16_t *ax0, *ax1 = nullptr;
-  if constexpr (BITS == 4) {
-    // copy m: lanes 0-31 scales, 32-63 biases; row (l & 31) / 2, dword l & 1
-    const int ar = min(jw + ((lane & 31) >> 1), rows - 1);
-    const size_t po = eo * gbk.p_stride + (size_t)ar * gbk.m.ng + 2 * (lane & 1);
-    ax0 = (lane < 32 ? gbk.m.sc : gbk.m.bi) + po;
-    ax1 = (lane < 32 ? ubk.m.sc : ubk.m.bi) + eo * ubk.p_stride + (size_t)ar * ubk.m.ng + 2 * (lane & 1);
-  } else {
-    // one copy: lanes 0-15 gate scales, 16-31 gate biases, 32-47 up scales,
-    // 48-63 up biases; row l & 15
-    const int ar = min(jw + (lane & 15), rows - 1);
-    const DevBank &bk = lane < 32 ? gbk : ubk;
-    const uint16_t *base = ((lane >> 4) & 1) ? bk.m.bi : bk.m.sc;
-    ax0 = base + eo * bk.p_stride + (size_t)ar * bk.m.ng;
-  }
+  const uint8_t *gb = gbk.m.w + eo * gbk.w_stride + sc, *ub = ubk.m.w + eo * ubk.w_stride + sc;
+  const uint8_t *const wrow[4] = {gb + (size_t)jl0 * gbk.m.row_bytes, gb + (size_t)jl1 * gbk.m.row_bytes,
+                                  ub + (size_t)jl0 * ubk.m.row_bytes, ub + (size_t)jl1 * ubk.m.row_bytes};
+  const uint16_t *arow[2];
+  R::aux_ptr(lane, gbk, ubk, eo, {jw, jw}, rows - 1, arow);
   const int nslots = a.B * a.k;
   const int chunk = a.D < kMChunk ? a.D : kMChunk;
   const int nch = a.D / chunk;
@@ -493,7 +553,7 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   UnpackConsts kc;
   kc.init();
   const bf16x8_t ones = mfma_ones();
-  f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // gate, up
   if (tid < kMTok) s_tok[tid] = shared ? row0 - nslots + min(tid, cnt - 1) : w.tok[row0 + min(tid, cnt - 1)];
   __syncthreads();
 
@@ -502,41 +562,13 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   auto issue = [&](int b) {
     const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(&swt[b % NB][wave][0]));
     const size_t o = (size_t)b * 128;
-    lds_copy16(gw0 + o, d);
-    lds_copy16(gw1 + o, d + 1024);
-    lds_copy16(uw0 + o, d + 2048);
-    lds_copy16(uw1 + o, d + 3072);
-    lds_copy4(ax0 + (size_t)b * GU, d + 4096);
-    if constexpr (BITS == 4) lds_copy4(ax1 + (size_t)b * GU, d + 4096 + 256);
-  };
-  // the lane's 16 codes of step u of batch b, matrix m (0 gate, 1 up)
-  auto raw = [&](const uint8_t *slot, int m, int u, SkRaw<BITS> &r) {
-    const uint8_t *row = slot + m * 2048 + r16 * 128;
-    if constexpr (BITS == 4) {
-      const int c = 2 * u + (g >> 1);
-      r.v = *reinterpret_cast<const uint2 *>(row + ((c ^ (r16 & 7)) << 4) + 8 * (g & 1));
-    } else {
-      const int c = 4 * u + g;
-      r.v = *reinterpret_cast<const uint4 *>(row + ((c ^ (r16 & 7)) << 4));
-    }
+    const uint8_t *wr[4] = {wrow[0] + o, wrow[1] + o, wrow[2] + o, wrow[3] + o};
+    R::issue(d, wr, arow[0] + (size_t)b * GU, arow[1] + (size_t)b * GU);
   };
   auto step = [&](int b, int bl) {
     const uint8_t *slot = &swt[b % NB][wave][0];
-    // this lane's output row's scale / bias words of the batch's GU steps
-    uint32_t gs_w[GU / 2], gb_w[GU / 2], us_w[GU / 2], ub_w[GU / 2];
-    if constexpr (BITS == 4) {
-      const uint2 a0 = *reinterpret_cast<const uint2 *>(slot + 4096 + 8 * r16);
-      const uint2 a1 = *reinterpret_cast<const uint2 *>(slot + 4096 + 128 + 8 * r16);
-      const uint2 a2 = *reinterpret_cast<const uint2 *>(slot + 4096 + 256 + 8 * r16);
-      const uint2 a3 = *reinterpret_cast<const uint2 *>(slot + 4096 + 384 + 8 * r16);
-      gs_w[0] = a0.x; gs_w[1] = a0.y; gb_w[0] = a1.x; gb_w[1] = a1.y;
-      us_w[0] = a2.x; us_w[1] = a2.y; ub_w[0] = a3.x; ub_w[1] = a3.y;
-    } else {
-      gs_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 4 * r16);
-      gb_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 64 + 4 * r16);
-      us_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 128 + 4 * r16);
-      ub_w[0] = *reinterpret_cast<const uint32_t *>(slot + 4096 + 192 + 4 * r16);
-    }
+    uint32_t sw[2][GU / 2], bw[2][GU / 2];
+    R::aux(slot, r16, sw, bw);
 #pragma unroll
     for (int u = 0; u < GU; ++u) {
       bf16x8_t a0, a1, b0, b1;
@@ -544,20 +576,15 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
       const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
       f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
       xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
-      SkRaw<BITS> rg, ru;
-      raw(slot, 0, u, rg);
-      raw(slot, 1, u, ru);
-      const int sh = 16 * (u & 1);
-      S::b_ops(rg, kc, b0, b1);
-      f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
-      S::fold(accg, d, xs, aux_f32<FP16>((gs_w[u >> 1] >> sh) & 0xffffu),
-              aux_f32<FP16>((gb_w[u >> 1] >> sh) & 0xffffu));
-      S::b_ops(ru, kc, b0, b1);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
-      S::fold(accu, d, xs, aux_f32<FP16>((us_w[u >> 1] >> sh) & 0xffffu),
-              aux_f32<FP16>((ub_w[u >> 1] >> sh) & 0xffffu));
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        SkRaw<BITS> rw;
+        R::raw(slot, m, u, r16, g, rw);
+        S::b_ops(rw, kc, b0, b1);
+        f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, z, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+        S::fold(acc[m], d, xs, R::template word<FP16>(sw[m], u), R::template word<FP16>(bw[m], u));
+      }
     }
   };
 
@@ -586,17 +613,17 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
     lds_dma_wait();
     __syncthreads();
     // batch bl + 1 in flight while batch bl is multiplied: wait for all but
-    // the NI copies of the batch issued last. An issue past the chunk end
-    // copies its last batch again (into the slot just released), so the
-    // count of copies behind every batch stays NI.
+    // the NI copies of the batch issued last. At the chunk's last batch the
+    // issue copies that batch again into its own slot (the same bytes, so
+    // step() reads them whether or not the copy has landed), which keeps
+    // the count of copies behind every batch at NI.
     for (int bl = 0; bl < bpc; ++bl) {
       issue(b0 + min(bl + 1, bpc - 1));
-      lds_dma_wait_behind<NI>();
+      lds_dma_wait_behind<R::NI>();
       step(b0 + bl, bl);
-      // the slot read by step() is the next issue's destination: its LDS
-      // reads are complete once their values are used, which step() did
     }
   }
+  lds_dma_wait();  // no copy into LDS outlives the block
   // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16,
   // each at its place in the down pass's operand order
   const int jj = jw + r16;
@@ -606,7 +633,7 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
     for (int i = 0; i < 4; ++i) {
       const int m = 4 * g + i;
       if (m < cnt) {
-        const float h = silu(accg[i]) * accu[i];
+        const float h = silu(acc[0][i]) * acc[1][i];
         const uint32_t hi = f32_to_bf16_rne(h);
         const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
         const size_t o = (size_t)(row0 + m) * hmax + S::op_pos(jj);
@@ -750,6 +777,171 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
 }
 
 // ---------------------------------------------------------------------------
+// 4b. down with the weights staged in LDS (4- and 8-bit codes, groups of 64,
+//     K a multiple of 128 code bytes): block = (tile, 512 rows), 8 waves x 2
+//     pairs of 16-row groups. h (hi, lo) is staged once per 512 output rows
+//     (the register form stages it per 128), and each wave streams its rows'
+//     codes batch by batch through a three-slot ring of RingSlot batches
+//     (group 0 = rows 32 p + [0, 16), group 1 = rows 32 p + [16, 32) of pair
+//     p), two batches in flight while one is multiplied. The sums of h over
+//     each step (the fold's bias term) are formed once and kept.
+
+constexpr int kMDownLdsRows = 512;  // output rows per block
+
+template <int BITS, bool FP16>
+__global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs w, int ipt) {
+  constexpr int WAVES = 8, NT = WAVES * 64, PW = 2;
+  static_assert(32 * PW * WAVES == kMDownLdsRows, "rows per block");
+  using R = RingSlot<BITS>;
+  constexpr int GU = R::GU, NB = 3;
+  constexpr int NS = kMDownK / 64;      // steps at most
+  constexpr int KBM = NS / GU;           // batches per pair at most
+  __shared__ __align__(16) uint16_t shi[kMTok * kMDownK];
+  __shared__ __align__(16) uint16_t slo[kMTok * kMDownK];
+  __shared__ __align__(16) uint8_t swt[NB][WAVES][R::BYTES];
+  using S = MfmaStep<BITS>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
+  if (tile >= *w.n_tiles) return;
+  const int4 tr = w.tiles[tile];
+  const int e = __builtin_amdgcn_readfirstlane(tr.x);
+  const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
+  const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
+  const bool shared = e < 0;
+  const DevBank &dbk = shared ? a.sdown : a.down;
+  const int K = shared ? a.sinter : a.inter;
+  const size_t eo = shared ? 0 : (size_t)e;
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
+  const int kbn = (K >> 6) / GU;  // batches per pair
+  const int nbw = PW * kbn;       // batches of the wave
+  const int jw = rb * kMDownLdsRows + wave * 32 * PW;  // the wave's first row
+  // the copy sources of both pairs, formed here: the bank's fields are loaded
+  // into registers, and such a load inside the ring loop would wait for every
+  // copy in flight. Pair p's batch: rows jw + 32 p + 8 i + lane / 8 (i < 4, at
+  // the lane's source chunk), scale / bias words of rows jw + 32 p + [0, 32).
+  const int lr = lane >> 3, sc = 16 * ((lane & 7) ^ lr);
+  const uint8_t *wrow[PW][4];
+  const uint16_t *arow[PW][2];
+  {
+    const uint8_t *wb = dbk.m.w + eo * dbk.w_stride + sc;
+    const size_t rbytes = dbk.m.row_bytes;
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int rp = jw + 32 * p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wrow[p][i] = wb + (size_t)min(rp + 8 * i + lr, a.D - 1) * rbytes;
+      R::aux_ptr(lane, dbk, dbk, eo, {rp, rp + 16}, a.D - 1, arow[p]);
+    }
+  }
+  static_assert(PW == 2, "pair of a batch index");
+  auto issue = [&](int b) {
+    const bool p1 = b >= kbn;
+    const int kb = p1 ? b - kbn : b;
+    const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(&swt[b % NB][wave][0]));
+    const uint8_t *wr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[i] = (p1 ? wrow[1][i] : wrow[0][i]) + 128 * kb;
+    R::issue(d, wr, (p1 ? arow[1][0] : arow[0][0]) + kb * GU, (p1 ? arow[1][1] : arow[0][1]) + kb * GU);
+  };
+  {
+    // stage h (hi, lo) of the tile's rows (physical granule P of row m holds
+    // logical granule P ^ (m & 15)); rows past the tile repeat its last row,
+    // which no operand of a stored output reads
+    constexpr int NQ = kMTok * kMDownK / 8 / NT;
+    const int gpr = K >> 3;
+    auto dma = [&](int base) {
+      const int pg = base + lane;
+      const int m = pg / gpr, qq = swz(m, pg % gpr);
+      const size_t o = (size_t)(row0 + min(m, cnt - 1)) * hmax + 8 * qq;
+      lds_dma16(w.h_hi + o, shi + 8 * base);
+      lds_dma16(w.h_lo + o, slo + 8 * base);
+    };
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
+  }
+  // the ring's first two batches behind the h copies (a wave with no rows
+  // inside D copies clamped rows and stores nothing)
+  issue(0);
+  issue(min(1, nbw - 1));
+  lds_dma_wait_behind<2 * R::NI>();
+  __syncthreads();
+  UnpackConsts kc;
+  kc.init();
+  const bf16x8_t ones = mfma_ones();
+  // sum of h over each step's 64 k (hi and lo): the fold's bias term
+  f32x4_t xs[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (u < kbn * GU) {
+      bf16x8_t h0, h1, l0, l1;
+      const int q0 = (u * 64 + 16 * g) >> 3;
+      S::a_ops(shi + r16 * K, q0, r16, h0, h1);
+      S::a_ops(slo + r16 * K, q0, r16, l0, l1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      xs[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, ones, z, 0, 0, 0);
+      xs[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, ones, xs[u], 0, 0, 0);
+      xs[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, ones, xs[u], 0, 0, 0);
+      xs[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, ones, xs[u], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PW; ++p) {
+    f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kb = 0; kb < KBM; ++kb) {
+      if (kb < kbn) {
+        // two batches in flight behind this one; past the wave's last batch
+        // the issue copies that batch again into its own slot (the same
+        // bytes), which keeps the count behind every batch at 2 NI
+        const int b = p * kbn + kb;
+        issue(min(b + 2, nbw - 1));
+        lds_dma_wait_behind<2 * R::NI>();
+        const uint8_t *slot = &swt[b % NB][wave][0];
+        uint32_t sw[2][GU / 2], bw[2][GU / 2];
+        R::aux(slot, r16, sw, bw);
+#pragma unroll
+        for (int ul = 0; ul < GU; ++ul) {
+          const int u = kb * GU + ul;
+          const int q0 = (u * 64 + 16 * g) >> 3;
+          bf16x8_t h0, h1, l0, l1;
+          S::a_ops(shi + r16 * K, q0, r16, h0, h1);
+          S::a_ops(slo + r16 * K, q0, r16, l0, l1);
+          const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            SkRaw<BITS> rw;
+            bf16x8_t b0, b1;
+            R::raw(slot, m, ul, r16, g, rw);
+            S::b_ops(rw, kc, b0, b1);
+            f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, b0, z, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, b1, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, b0, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, b1, d, 0, 0, 0);
+            S::fold(acc[m], d, xs[u], R::template word<FP16>(sw[m], ul),
+                    R::template word<FP16>(bw[m], ul));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int d = jw + 32 * p + 16 * m + r16;
+      if (d < a.D) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 4 * g + i;
+          if (t < cnt) w.y[(size_t)(row0 + t) * a.D + d] = acc[m][i];
+        }
+      }
+    }
+  }
+  lds_dma_wait();  // no copy into LDS outlives the block
+}
+
+// ---------------------------------------------------------------------------
 // 5. rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711)
 
 __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) {
@@ -871,18 +1063,36 @@ static hipError_t moe_gateup_launch(const MoeArgs &a, const MoeMWs &w, hipStream
 }
 
 template <int BITS>
+static hipError_t moe_down_launch(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
+  if constexpr (BITS == 4 || BITS == 8) {
+    // the large-batch shape with the weights staged in LDS: groups of 64, K a
+    // multiple of one batch (128 code bytes) on the routed and shared experts
+    constexpr int KB = 128 * 8 / BITS;
+    const bool lds = a.B > kMGuSmallB && a.down.m.gs == 64 && a.inter % KB == 0 &&
+                     (!a.sdown.m.w || (a.sdown.m.gs == 64 && a.sinter % KB == 0));
+    if (lds) {
+      const int ipt = (a.D + kMDownLdsRows - 1) / kMDownLdsRows;
+      if (a.down.m.fp16)
+        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, true>), dim3(w.max_tiles * ipt), dim3(512), 0, st, a, w, ipt);
+      else
+        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, false>), dim3(w.max_tiles * ipt), dim3(512), 0, st, a, w, ipt);
+      return hipGetLastError();
+    }
+  }
+  const int ipt = (a.D + 127) / 128;
+  if (a.down.m.fp16)
+    hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, true>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+  else
+    hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, false>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
+  return hipGetLastError();
+}
+
+template <int BITS>
 static int moe_mfma_launch_bits(const MoeArgs &a, const MoeMWs &w, hipStream_t st) {
   const hipError_t ge = a.B <= kMGuSmallB ? moe_gateup_launch<BITS, 4>(a, w, st)
                                           : moe_gateup_launch<BITS, MOE_GU_WAVES>(a, w, st);
   if (ge != hipSuccess) return -1;
-  {
-    const int ipt = (a.D + 127) / 128;
-    if (a.down.m.fp16)
-      hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, true>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
-    else
-      hipLaunchKernelGGL((moe_down_mfma_kernel<BITS, false>), dim3(w.max_tiles * ipt), dim3(256), 0, st, a, w, ipt);
-    if (hipGetLastError() != hipSuccess) return -1;
-  }
+  if (moe_down_launch<BITS>(a, w, st) != hipSuccess) return -1;
   {
     long long n = (long long)a.B * (a.D >> 2);
     long long blocks = (n + 255) / 256;

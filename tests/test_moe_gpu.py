@@ -410,12 +410,15 @@ def test_moe_mfma_fp16_sidecars(gpu, mfma_min_b, bits):
 
 @pytest.mark.parametrize("mfma_min_b", [1], indirect=True)
 @pytest.mark.parametrize("bits,fp16,D,sinter", [(4, True, 2048, 512), (8, True, 1024, 384),
-                                                 (4, False, 1024, 384), (8, False, 2048, 256)])
+                                                 (4, False, 1024, 384), (8, False, 2048, 256),
+                                                 (4, False, 768, 256)])
 def test_moe_mfma_large_batch_staged_weights(gpu, mfma_min_b, bits, fp16, D, sinter):
-    """Batches above 128 tokens take the 8-wave gate/up blocks whose 4- and
+    """Batches above 128 tokens take the gate/up and down blocks whose 4- and
     8-bit weights are staged in LDS: fp16 and bf16 sidecars, D = 1024 (one
-    x chunk shorter than the LDS tile) and 2048, a shared expert of another
-    size; every 7th token against the oracle."""
+    x chunk shorter than the LDS tile), 2048, and 768 (down blocks of 512
+    rows running past D); shared experts whose down K is one, two or three
+    batches, or (4-bit, K = 384) not a whole number of them (the register
+    down blocks); every 7th token against the oracle."""
     import torch
 
     print(f"moe mfma staged bits={bits} fp16={fp16} D={D} sinter={sinter}", flush=True)
