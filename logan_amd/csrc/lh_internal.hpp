@@ -196,6 +196,11 @@ struct DenseDesc {
   float *y;                       // [O]
   const float *res;               // y = res + W x when set (may alias y)
   int O, I;
+  // SwiGLU pair when w2 is set: w is gate, w2 up (same format and shape);
+  // instead of y, hhl[2][O] receives the hi/lo halves of silu(W x) * (W2 x)
+  const void *w2;
+  const uint16_t *sc2, *bi2;
+  uint16_t *hhl;
 };
 constexpr int kDenseMaxDescs = 8;
 struct DenseBatch {

@@ -86,7 +86,11 @@ __global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
   while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
   const DenseDesc d = b.d[di];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = ((int)blockIdx.x - b.block_start[di]) * kDU;
+  // a SwiGLU pair's block holds rows r0, r0 + 1 of gate (u = 0, 1) and of up
+  // (u = 2, 3); every row's sum is formed as for a single product
+  const bool pair = d.w2 != nullptr;
+  const int rpb = pair ? kDU / 2 : kDU;
+  const int r0 = ((int)blockIdx.x - b.block_start[di]) * rpb;
   const int C = d.I >> 4;
   const uint16_t *xh = d.xhl, *xl = d.xhl + d.I;
   constexpr int WD = FMT == 5 ? 8 : 4;  // dwords of one row's 16-column chunk
@@ -99,19 +103,21 @@ __global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
     const int cc = c < C ? c : C - 1;
 #pragma unroll
     for (int u = 0; u < kDU; ++u) {
-      const int row = min(r0 + u, d.O - 1);
+      const bool second = pair && u >= kDU / 2;
+      const int row = min(r0 + (second ? u - kDU / 2 : u), d.O - 1);
+      const void *wm = second ? d.w2 : d.w;
       if constexpr (FMT == 5) {
         const uint4 *p = reinterpret_cast<const uint4 *>(
-            reinterpret_cast<const uint16_t *>(d.w) + (size_t)row * d.I + 16 * (size_t)cc);
+            reinterpret_cast<const uint16_t *>(wm) + (size_t)row * d.I + 16 * (size_t)cc);
         const uint4 a = p[0], bq = p[1];
         k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
         k.w[u][4] = bq.x; k.w[u][5] = bq.y; k.w[u][6] = bq.z; k.w[u][7] = bq.w;
       } else {
-        const uint4 a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(d.w) +
+        const uint4 a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(wm) +
                                                          (size_t)row * d.I + 16 * (size_t)cc);
         k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
         const size_t g = (size_t)row * (d.I >> 6) + (cc >> 2);
-        k.sb[u] = (uint32_t)d.sc[g] | ((uint32_t)d.bi[g] << 16);
+        k.sb[u] = (uint32_t)(second ? d.sc2 : d.sc)[g] | ((uint32_t)(second ? d.bi2 : d.bi)[g] << 16);
       }
     }
     const uint4 *ph = reinterpret_cast<const uint4 *>(xh + 16 * (size_t)cc);
@@ -170,11 +176,20 @@ __global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
     if (lane == 0) red[wave][u] = t;
   }
   __syncthreads();
-  if (threadIdx.x < kDU) {
-    const int row = r0 + threadIdx.x;
-    float t = red[0][threadIdx.x];
+  auto row_sum = [&](int u) {
+    float t = red[0][u];
 #pragma unroll
-    for (int w = 1; w < kLT / 64; ++w) t += red[w][threadIdx.x];
+    for (int w = 1; w < kLT / 64; ++w) t += red[w][u];
+    return t;
+  };
+  if (pair) {
+    // h = silu(gate) * up (logan-llama/src/model.rs:888-890) as hi/lo halves
+    const int row = r0 + threadIdx.x;
+    if (threadIdx.x < kDU / 2 && row < d.O)
+      put_hl(d.hhl, d.O, row, silu(row_sum(threadIdx.x)) * row_sum(threadIdx.x + kDU / 2));
+  } else if (threadIdx.x < kDU) {
+    const float t = row_sum(threadIdx.x);
+    const int row = r0 + threadIdx.x;
     if (row < d.O) d.y[row] = d.res ? d.res[row] + t : t;
   }
 }
@@ -192,10 +207,15 @@ hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
   b.block_start[0] = 0;
   for (int i = 0; i < b.n; ++i) {
     const DenseDesc &d = b.d[i];
-    if (!dense_supported(fmt, d.O, d.I, d.w) || !d.xhl || !d.y) return hipErrorInvalidValue;
+    if (!dense_supported(fmt, d.O, d.I, d.w) || !d.xhl) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(d.xhl) & 15) != 0) return hipErrorInvalidValue;
     if (fmt == 15 && (!d.sc || !d.bi)) return hipErrorInvalidValue;
-    b.block_start[i + 1] = b.block_start[i] + (d.O + rows_per_block - 1) / rows_per_block;
+    const bool pair = d.w2 != nullptr;
+    if (pair ? !dense_supported(fmt, d.O, d.I, d.w2) || !d.hhl || (fmt == 15 && (!d.sc2 || !d.bi2))
+             : !d.y)
+      return hipErrorInvalidValue;
+    const int rpb = pair ? rows_per_block / 2 : rows_per_block;
+    b.block_start[i + 1] = b.block_start[i] + (d.O + rpb - 1) / rpb;
   }
   const dim3 grid(b.block_start[b.n]);
   if (fmt == 5) hipLaunchKernelGGL(dense_gemv_kernel<5>, grid, dim3(kLT), 0, st, b);
@@ -208,10 +228,12 @@ hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
 // out = hi/lo halves of x * (1 / sqrt(sum x^2 / n + eps)) * w (a_rmsnorm,
 // backend_metal.mm:705-714; rms_norm_into, logan-llama/src/model.rs
 // :1067-1073). One block; n a multiple of 4; loads unrolled so each thread's
-// are in flight together.
+// are in flight together. Also zeroes ctr[0, nctr) (the attention's
+// per-kv-head counters, when this is the layer's first kernel).
 __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const float *w, int n,
-                                                         float eps, uint16_t *out) {
+                                                         float eps, uint16_t *out, int *ctr, int nctr) {
   __shared__ float red[kLT / 64];
+  for (int i = threadIdx.x; i < nctr; i += kLT) ctr[i] = 0;
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
   const float4 *w4 = reinterpret_cast<const float4 *>(w);
   const int n4 = n >> 2;
@@ -236,133 +258,247 @@ __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const f
   }
 }
 
-// RoPE on the q and k heads of qkv [q | k | v] (pairs j, j + hd/2, angle
-// pos / theta^(2j/hd), logan-llama/src/model.rs:786-796, :1087-1100;
-// llama_qkv_rope, backend_metal.mm:1328-1356), then K[pos] = k, V[pos] = v
-// (llama_cache_store :1358-1368).
-__global__ __launch_bounds__(kLT) void rope_store_kernel(float *qkv, float *kc, float *vc, int H,
-                                                         int KH, int hd, int pos, float theta) {
-  const int half = hd >> 1, qdim = H * hd, kvdim = KH * hd;
-  const int rope_tasks = (H + KH) * half;
-  const int t = blockIdx.x * kLT + threadIdx.x;
-  if (t < rope_tasks) {
-    const int head = t / half, j = t % half;
+// Attention for one token at position pos over T = pos + 1 cached positions,
+// with RoPE and the cache store fused in (logan-llama/src/model.rs:786-869;
+// llama_qkv_rope, llama_cache_store, llama_attn_score, spark_softmax,
+// llama_attn_ctx: backend_metal.mm:1290-1408):
+//   RoPE on q and k (pairs j, j + hd/2, angle pos / theta^(2j/hd));
+//   K[pos], V[pos] = k, v;
+//   per head h (kv head h / G, G = H / KH): s_t = q.K[t] / sqrt(hd), t <= pos;
+//   p = softmax(s); att_h = sum_t p_t V[t], stored as hi/lo halves.
+// Block (kv head kh, slice sl of kAttnTS positions) serves the G query heads
+// of kh, so each K/V row is read once: the angles' cos/sin formed once per
+// block, RoPE on the G q rows and, in the slice holding pos, on the new k row
+// (that block alone stores k and v at pos; the slice's own reads of position
+// pos take them from LDS), the scores (4 threads per position, a quarter of
+// the row each), per head the slice max m, l = sum exp(s - m) and
+// o = sum exp(s_t - m) V[t]. The last block of kh to finish (a counter per kv
+// head, zeroed by the layer's first kernel and reset by that block) joins the
+// slices in order, rescaling each by exp(m_slice - m_max), and writes o / l.
+constexpr int kAttnTS = 64;  // positions per slice
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kAttnGMax = 16;  // query heads per kv head
+
+__global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float *vc, float *part,
+                                                   int *ctr, uint16_t *att, int H, int KH, int hd,
+                                                   int pos, float theta) {
+  static_assert(kAttnTS * 4 == kLT, "4 threads per position");
+  __shared__ float cs[128], sn[128];          // cos / sin of the hd/2 angles
+  __shared__ float qs[kAttnGMax * 256 / 4];  // G roped q rows (G * hd <= 1024)
+  __shared__ float kn[256], vn[256];          // the new k (roped) and v rows
+  __shared__ float es[kAttnGMax][kAttnTS];   // exp(s - m) per head and position
+  __shared__ float ml[kAttnGMax][2];
+  __shared__ float red[kLT / 64 * 1024];      // per wave and head: o partials (G * hd <= 1024)
+  __shared__ int s_last;
+  const int kh = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
+  const int G = H / KH, half = hd >> 1, qdim = H * hd, kvdim = KH * hd;
+  const int T = pos + 1, t0 = sl * kAttnTS, nt = min(kAttnTS, T - t0);
+  const bool has_pos = pos < t0 + kAttnTS;  // the last slice
+  const int tid = threadIdx.x;
+  // every load of the block first: the K and V rows of the slice (position pos
+  // read too, and replaced by the new rows below), the q pairs and the new k, v
+  const int t = tid >> 2, qd = tid & 3, q4 = hd >> 4;  // scores: position, quarter
+  const int C4 = hd >> 2, PG = kLT / C4, c4 = tid % C4, pg = tid / C4;  // o: column, group
+  constexpr int NPM = kAttnTS / 4;  // positions per thread in o at most (hd <= 256)
+  const int np = kAttnTS / PG;
+  float4 kv[16], vv[NPM];
+  {
+    const int tt = t0 + min(t, nt - 1);
+    const float4 *krow = reinterpret_cast<const float4 *>(kc + (size_t)tt * kvdim + kh * hd);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i < q4) kv[i] = krow[qd * q4 + i];
+#pragma unroll
+    for (int i = 0; i < NPM; ++i) {
+      if (i < np) {
+        const int tv = t0 + min(pg + PG * i, nt - 1);
+        vv[i] = reinterpret_cast<const float4 *>(vc + (size_t)tv * kvdim + kh * hd)[c4];
+      }
+    }
+  }
+  float qa[2], qb[2];  // pairs tid and tid + kLT of the G q rows (G * hd / 2 <= 512)
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = tid + r * kLT;
+    if (i < G * half) {
+      const float *q = qkv + (kh * G + i / half) * hd + i % half;
+      qa[r] = q[0];
+      qb[r] = q[half];
+    }
+  }
+  float ka = 0.f, kb = 0.f, vnew = 0.f;
+  if (has_pos) {
+    if (tid < half) {
+      ka = qkv[qdim + kh * hd + tid];
+      kb = qkv[qdim + kh * hd + tid + half];
+    }
+    if (tid < hd) vnew = qkv[qdim + kvdim + kh * hd + tid];
+  }
+  if (tid < half) {
     // the angle as the CPU path forms it, in f32: pos / powf(theta, 2j / hd)
-    const float ex = __fdiv_rn((float)(2 * j), (float)hd);
+    const float ex = __fdiv_rn((float)(2 * tid), (float)hd);
     const float pw = (float)pow((double)theta, (double)ex);
     const float ang = __fdiv_rn((float)pos, pw);
     const float co = (float)cos((double)ang), si = (float)sin((double)ang);
-    float *v = qkv + (head < H ? head * hd : qdim + (head - H) * hd);
-    const float a = v[j], bb = v[j + half];
-    const float ra = a * co - bb * si, rb = a * si + bb * co;
-    v[j] = ra;
-    v[j + half] = rb;
-    if (head >= H) {
-      float *kr = kc + (size_t)pos * kvdim + (head - H) * hd;
-      kr[j] = ra;
-      kr[j + half] = rb;
+    cs[tid] = co;
+    sn[tid] = si;
+    if (has_pos) {
+      // the new k row, roped, and v: into LDS and (this block alone) the cache
+      const float ra = ka * co - kb * si, rb = ka * si + kb * co;
+      float *kr = kc + (size_t)pos * kvdim + kh * hd;
+      kn[tid] = ra;
+      kn[tid + half] = rb;
+      kr[tid] = ra;
+      kr[tid + half] = rb;
     }
-  } else if (t < rope_tasks + kvdim) {
-    const int i = t - rope_tasks;
-    vc[(size_t)pos * kvdim + i] = qkv[qdim + kvdim + i];
   }
-}
-
-// Attention over T = pos + 1 cached positions (logan-llama/src/model.rs
-// :838-869; llama_attn_score / spark_softmax / llama_attn_ctx,
-// backend_metal.mm:1290-1302, :1370-1408): s_t = q.K[t] / sqrt(hd),
-// p = softmax(s), att = sum_t p_t V[t], split over T in slices of kAttnTS
-// positions. Block (h, slice) forms its slice's scores, their max m, the
-// sum l of exp(s - m) and o = sum exp(s_t - m) V[t]; a second kernel joins
-// the slices in order, rescaling each by exp(m_slice - m_max), and writes
-// att = o / l as hi/lo halves.
-constexpr int kAttnQ = 16;   // q values per lane: head_dim <= 256
-constexpr int kAttnTS = 64;  // positions per slice
-
-__global__ __launch_bounds__(kLT) void attn_slice_kernel(const float *qkv, const float *kc,
-                                                         const float *vc, float *part, int H,
-                                                         int KH, int hd, int T) {
-  __shared__ float red[kLT / 64];
-  __shared__ float es[kAttnTS];
-  __shared__ float ps[kLT];
-  const int h = blockIdx.x, sl = blockIdx.y, S = gridDim.y;
-  const int kh = h / (H / KH), kvdim = KH * hd;
-  const int t0 = sl * kAttnTS, nt = min(kAttnTS, T - t0);
-  const int sub = threadIdx.x & 15, grp = threadIdx.x >> 4;
-  const float *q = qkv + h * hd;
+  if (has_pos && tid < hd) {
+    vn[tid] = vnew;
+    vc[(size_t)pos * kvdim + kh * hd + tid] = vnew;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i = tid + r * kLT;
+    if (i < G * half) {
+      const int g = i / half, j = i % half;
+      qs[g * hd + j] = qa[r] * cs[j] - qb[r] * sn[j];
+      qs[g * hd + j + half] = qa[r] * sn[j] + qb[r] * cs[j];
+    }
+  }
+  if (has_pos) {
+    // position pos: the new rows, not the cache's
+    if (t0 + min(t, nt - 1) == pos) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (i < q4) kv[i] = reinterpret_cast<const float4 *>(kn)[qd * q4 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < NPM; ++i)
+      if (i < np && t0 + min(pg + PG * i, nt - 1) == pos) vv[i] = reinterpret_cast<const float4 *>(vn)[c4];
+  }
+  __syncthreads();
+  // scores: position t, the row's quarter qd (hd / 16 float4)
   const float rs = sqrtf((float)hd);
-  float qr[kAttnQ];
-#pragma unroll
-  for (int i = 0; i < kAttnQ; ++i) qr[i] = sub + 16 * i < hd ? q[sub + 16 * i] : 0.f;
-  const float *kb = kc + kh * hd + sub;
-  // scores: 16 groups of 16 lanes, 4 positions per group, loads together
-  float a[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = t0 + min(16 * j + grp, nt - 1);
-    const float *k = kb + (size_t)t * kvdim;
+  for (int g = 0; g < G; ++g) {
+    const float *q = qs + g * hd + 4 * qd * q4;
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < kAttnQ; ++i)
-      if (sub + 16 * i < hd) acc = fmaf(qr[i], k[16 * i], acc);
-    a[j] = acc;
+    for (int i = 0; i < 16; ++i) {
+      if (i < q4) {
+        acc = fmaf(q[4 * i], kv[i].x, acc);
+        acc = fmaf(q[4 * i + 1], kv[i].y, acc);
+        acc = fmaf(q[4 * i + 2], kv[i].z, acc);
+        acc = fmaf(q[4 * i + 3], kv[i].w, acc);
+      }
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (qd == 0) es[g][t] = __fdiv_rn(acc, rs);
   }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float sc = __fdiv_rn(team_sum<16>(a[j]), rs);
-    a[j] = sc;
-    if (16 * j + grp < nt) mx = fmaxf(mx, sc);
-  }
-  mx = block_max(mx, red);
-  float l = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tl = 16 * j + grp;
-    const float e = tl < nt ? __expf(a[j] - mx) : 0.f;
-    if (sub == 0) es[tl] = e;
-    if (sub == 0) l += e;
-  }
-  l = block_sum(l, red);  // its barriers publish es[]
-  // o[d] = sum_t e_t V[t][d]: P partitions of hd threads, positions p, p + P, ...
-  const int P = kLT / hd;
-  const int d = threadIdx.x % hd, p = threadIdx.x / hd;
-  float o = 0.f;
-  if (p < P) {
-    const float *vcol = vc + (size_t)t0 * kvdim + kh * hd + d;
-#pragma unroll 8
-    for (int t = p; t < nt; t += P) o = fmaf(es[t], vcol[(size_t)t * kvdim], o);
-  }
-  ps[threadIdx.x] = o;
   __syncthreads();
-  float *pr = part + ((size_t)h * S + sl) * (hd + 2);
-  if (threadIdx.x < hd) {
+  // softmax over the slice, one wave per head
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int g = wave; g < G; g += kLT / 64) {
+    const float sc = es[g][lane];
+    float mx = lane < nt ? sc : -INFINITY;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float e = lane < nt ? __expf(sc - mx) : 0.f;
+    const float l = team_sum<64>(e);
+    es[g][lane] = e;
+    if (lane == 0) {
+      ml[g][0] = mx;
+      ml[g][1] = l;
+    }
+  }
+  __syncthreads();
+  // o = sum_t e_t V[t]: column float4 c4, positions pg, pg + PG, ...; the
+  // position groups of a wave added by shuffles, then the waves' in wave order
+  for (int g = 0; g < G; ++g) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < NPM; ++i) {
+      if (i < np) {
+        const float e = es[g][pg + PG * i];  // 0 past the slice's positions
+        o.x = fmaf(e, vv[i].x, o.x);
+        o.y = fmaf(e, vv[i].y, o.y);
+        o.z = fmaf(e, vv[i].z, o.z);
+        o.w = fmaf(e, vv[i].w, o.w);
+      }
+    }
+    for (int off = C4; off < 64; off <<= 1) {
+      o.x += __shfl_xor(o.x, off, 64);
+      o.y += __shfl_xor(o.y, off, 64);
+      o.z += __shfl_xor(o.z, off, 64);
+      o.w += __shfl_xor(o.w, off, 64);
+    }
+    if (lane < C4) reinterpret_cast<float4 *>(red)[(wave * G + g) * C4 + c4] = o;
+  }
+  __syncthreads();
+  // The slice partials go out as device-scope stores and the joining block
+  // reads them with device-scope loads, coherent across the XCDs' L2s; each
+  // block's stores complete (vmcnt) before its counter increment. (An
+  // agent-scope fence would write back / invalidate the whole L2 instead.)
+  for (int i = tid; i < G * hd; i += kLT) {
+    const int g = i / hd, d = i % hd;
     float v = 0.f;
-    for (int pp = 0; pp < P; ++pp) v += ps[pp * hd + threadIdx.x];
-    pr[2 + threadIdx.x] = v;
+    for (int w = 0; w < kLT / 64; ++w) v += red[(w * G + g) * hd + d];
+    float *pr = part + ((size_t)(kh * G + g) * S + sl) * (hd + 2);
+    st_dev(pr + 2 + d, v);
+    if (d == 0) {
+      st_dev(pr, ml[g][0]);
+      st_dev(pr + 1, ml[g][1]);
+    }
   }
-  if (threadIdx.x == 0) {
-    pr[0] = mx;
-    pr[1] = l;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // the last block of kv head kh joins its heads' slices
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&ctr[kh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  __syncthreads();
+  if (!s_last) return;
+  for (int i = tid; i < G * hd; i += kLT) {
+    const int h = kh * G + i / hd, d = i % hd;
+    const float *pr = part + (size_t)h * S * (hd + 2);
+    // slices in groups of 8, their (m, l, o) loads in flight together
+    float m = -INFINITY;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      float mv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mv[j] = s0 + j < S ? ld_dev(pr + (size_t)(s0 + j) * (hd + 2)) : -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, mv[j]);
+    }
+    float l = 0.f, o = 0.f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      float mv[8], lv[8], ov[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < S) {
+          const float *q = pr + (size_t)(s0 + j) * (hd + 2);
+          mv[j] = ld_dev(q);
+          lv[j] = ld_dev(q + 1);
+          ov[j] = ld_dev(q + 2 + d);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < S) {
+          const float f = __expf(mv[j] - m);
+          l = fmaf(lv[j], f, l);
+          o = fmaf(ov[j], f, o);
+        }
+      }
+    }
+    put_hl(att, qdim, h * hd + d, __fdiv_rn(o, l));
   }
-}
-
-__global__ __launch_bounds__(kLT) void attn_join_kernel(const float *part, uint16_t *att, int H,
-                                                        int hd, int S) {
-  const int i = blockIdx.x * kLT + threadIdx.x;
-  if (i >= H * hd) return;
-  const int h = i / hd, d = i % hd;
-  const float *pr = part + (size_t)h * S * (hd + 2);
-  float m = -INFINITY;
-  for (int sl = 0; sl < S; ++sl) m = fmaxf(m, pr[(size_t)sl * (hd + 2)]);
-  float l = 0.f, o = 0.f;
-  for (int sl = 0; sl < S; ++sl) {
-    const float *q = pr + (size_t)sl * (hd + 2);
-    const float f = __expf(q[0] - m);
-    l = fmaf(q[1], f, l);
-    o = fmaf(q[2 + d], f, o);
-  }
-  put_hl(att, H * hd, i, __fdiv_rn(o, l));
+  if (tid == 0) __hip_atomic_store(&ctr[kh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // h = silu(g) * u (logan-llama/src/model.rs:888-890; moe_silu,
@@ -381,6 +517,7 @@ inline size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 struct LlamaWs {
   uint16_t *xhl, *atthl, *pnhl, *hhl;
   float *qkv, *part, *mg, *mu;
+  int *ctr;
 };
 
 size_t llama_ws_layout(const LlamaDims &m, int T, uint8_t *base, LlamaWs *w) {
@@ -396,7 +533,9 @@ size_t llama_ws_layout(const LlamaDims &m, int T, uint8_t *base, LlamaWs *w) {
   uint8_t *prt = take((size_t)m.H * S * (m.hd + 2) * 4), *att = take((size_t)2 * qdim * 2);
   uint8_t *pn = take((size_t)2 * m.D * 2), *mg = take((size_t)m.inter * 4);
   uint8_t *mu = take((size_t)m.inter * 4), *hh = take((size_t)2 * m.inter * 2);
+  uint8_t *ctr = take((size_t)m.KH * 4);
   if (w) {
+    w->ctr = reinterpret_cast<int *>(ctr);
     w->xhl = reinterpret_cast<uint16_t *>(xhl);
     w->qkv = reinterpret_cast<float *>(qkv);
     w->part = reinterpret_cast<float *>(prt);
@@ -440,7 +579,11 @@ size_t llama_workspace_bytes(const LlamaDims &m, int T) { return llama_ws_layout
 
 bool llama_supported(const LlamaDims &m, const DenseMat mats[7]) {
   if (m.D <= 0 || m.inter <= 0 || m.H <= 0 || m.KH <= 0 || m.H % m.KH != 0) return false;
-  if (m.hd <= 0 || m.hd % 2 != 0 || m.hd > 16 * kAttnQ || !(m.theta > 0.f) || !(m.eps > 0.f))
+  // head size 16, 32, 64, 128 or 256 (float4 columns that divide the block),
+  // at most kAttnGMax query heads per kv head, G * hd <= 1024
+  const int G = m.H / m.KH;
+  if (m.hd < 16 || m.hd > 256 || (m.hd & (m.hd - 1)) != 0 || G > kAttnGMax || G * m.hd > 1024 ||
+      !(m.theta > 0.f) || !(m.eps > 0.f))
     return false;
   if (m.D % 16 != 0) return false;  // the norms' float4 loads; the GEMVs need it too
   const int qdim = m.H * m.hd, kvdim = m.KH * m.hd;
@@ -459,32 +602,42 @@ hipError_t launch_llama_layer(const DenseMat mats[7], const float *in_norm, cons
                               void *ws, hipStream_t st) {
   if (!llama_supported(m, mats) || pos < 0 || !x || !kc || !vc || !ws || !in_norm || !post_norm)
     return hipErrorInvalidValue;
+  // the attention reads cache rows as float4
+  if ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15) return hipErrorInvalidValue;
   const int T = pos + 1, qdim = m.H * m.hd, kvdim = m.KH * m.hd;
   LlamaWs w;
   llama_ws_layout(m, T, reinterpret_cast<uint8_t *>(ws), &w);
-  hipLaunchKernelGGL(rmsnorm_hl_kernel, dim3(1), dim3(kLT), 0, st, x, in_norm, m.D, m.eps, w.xhl);
+  hipLaunchKernelGGL(rmsnorm_hl_kernel, dim3(1), dim3(kLT), 0, st, x, in_norm, m.D, m.eps, w.xhl,
+                     w.ctr, m.KH);
   const DenseDesc qkv[3] = {ddesc(mats[0], w.xhl, w.qkv, nullptr),
                             ddesc(mats[1], w.xhl, w.qkv + qdim, nullptr),
                             ddesc(mats[2], w.xhl, w.qkv + qdim + kvdim, nullptr)};
   hipError_t e = launch_dense_set(mats, qkv, 3, st);
   if (e != hipSuccess) return e;
-  const int rs_tasks = (m.H + m.KH) * (m.hd / 2) + kvdim;
-  hipLaunchKernelGGL(rope_store_kernel, dim3((rs_tasks + kLT - 1) / kLT), dim3(kLT), 0, st, w.qkv,
-                     kc, vc, m.H, m.KH, m.hd, pos, m.theta);
   const int S = (T + kAttnTS - 1) / kAttnTS;
-  hipLaunchKernelGGL(attn_slice_kernel, dim3(m.H, S), dim3(kLT), 0, st, w.qkv, kc, vc, w.part,
-                     m.H, m.KH, m.hd, T);
-  hipLaunchKernelGGL(attn_join_kernel, dim3((m.H * m.hd + kLT - 1) / kLT), dim3(kLT), 0, st,
-                     w.part, w.atthl, m.H, m.hd, S);
+  hipLaunchKernelGGL(attn_kernel, dim3(m.KH, S), dim3(kLT), 0, st, w.qkv, kc, vc, w.part, w.ctr,
+                     w.atthl, m.H, m.KH, m.hd, pos, m.theta);
   const DenseDesc od = ddesc(mats[3], w.atthl, x, x);
   e = launch_dense_set(mats + 3, &od, 1, st);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(rmsnorm_hl_kernel, dim3(1), dim3(kLT), 0, st, x, post_norm, m.D, m.eps, w.pnhl);
-  const DenseDesc gu[2] = {ddesc(mats[4], w.pnhl, w.mg, nullptr), ddesc(mats[5], w.pnhl, w.mu, nullptr)};
-  e = launch_dense_set(mats + 4, gu, 2, st);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(silu_mul_hl_kernel, dim3((m.inter + kLT - 1) / kLT), dim3(kLT), 0, st, w.mg,
-                     w.mu, m.inter, w.hhl);
+  hipLaunchKernelGGL(rmsnorm_hl_kernel, dim3(1), dim3(kLT), 0, st, x, post_norm, m.D, m.eps, w.pnhl,
+                     nullptr, 0);
+  if (mats[4].fmt == mats[5].fmt) {
+    // gate and up as one SwiGLU pair: h straight from the product
+    DenseDesc gu = ddesc(mats[4], w.pnhl, nullptr, nullptr);
+    gu.w2 = mats[5].w;
+    gu.sc2 = mats[5].sc;
+    gu.bi2 = mats[5].bi;
+    gu.hhl = w.hhl;
+    e = launch_dense_set(mats + 4, &gu, 1, st);
+    if (e != hipSuccess) return e;
+  } else {
+    const DenseDesc gu[2] = {ddesc(mats[4], w.pnhl, w.mg, nullptr), ddesc(mats[5], w.pnhl, w.mu, nullptr)};
+    e = launch_dense_set(mats + 4, gu, 2, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(silu_mul_hl_kernel, dim3((m.inter + kLT - 1) / kLT), dim3(kLT), 0, st, w.mg,
+                       w.mu, m.inter, w.hhl);
+  }
   const DenseDesc dd = ddesc(mats[6], w.hhl, x, x);
   e = launch_dense_set(mats + 6, &dd, 1, st);
   if (e != hipSuccess) return e;
