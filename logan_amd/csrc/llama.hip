@@ -32,7 +32,6 @@ namespace lh {
 namespace {
 
 constexpr int kLT = 256;  // threads per block
-constexpr int kDU = 4;    // rows per block in the dense GEMV
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -47,6 +46,16 @@ __device__ __forceinline__ void put_hl(uint16_t *hl, int n, int i, float v) {
   const uint32_t hi = f32_to_bf16_rne(v);
   hl[i] = (uint16_t)hi;
   hl[n + i] = (uint16_t)f32_to_bf16_rne(v - bf16_to_f32(hi));  // v - hi is exact
+}
+
+// Device-scope (sc1) stores and loads: coherent across the XCDs' L2s, for
+// values one block of a running kernel hands to another (an agent-scope
+// fence would write back / invalidate the whole L2 instead).
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ float block_sum(float v, float *red) {
@@ -74,162 +83,14 @@ __device__ float block_max(float v, float *red) {
 
 }  // namespace
 
-// ---- dense GEMV: y[r] = (res ? res[r] : 0) + sum_j w[r][j] x[j] ----------
-//
-// A block owns kDU rows; its 4 waves split the 16-column chunks of those
-// rows (wave w, lane l: chunks 64 w + l, + 256, ...), the next chunk's loads
-// in flight while the current one is used; the 4 wave partials of a row are
-// added in wave order.
-template <int FMT>
-__global__ __launch_bounds__(kLT) void dense_gemv_kernel(DenseBatch b) {
-  int di = 0;
-  while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
-  const DenseDesc d = b.d[di];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // a SwiGLU pair's block holds rows r0, r0 + 1 of gate (u = 0, 1) and of up
-  // (u = 2, 3); every row's sum is formed as for a single product
-  const bool pair = d.w2 != nullptr;
-  const int rpb = pair ? kDU / 2 : kDU;
-  const int r0 = ((int)blockIdx.x - b.block_start[di]) * rpb;
-  const int C = d.I >> 4;
-  const uint16_t *xh = d.xhl, *xl = d.xhl + d.I;
-  constexpr int WD = FMT == 5 ? 8 : 4;  // dwords of one row's 16-column chunk
-  struct Chunk {
-    uint32_t w[kDU][WD];
-    uint32_t sb[FMT == 5 ? 1 : kDU];  // fmt 15: scale | bias << 16
-    uint32_t hi[8], lo[8];
-  };
-  auto load = [&](int c, Chunk &k) {
-    const int cc = c < C ? c : C - 1;
-#pragma unroll
-    for (int u = 0; u < kDU; ++u) {
-      const bool second = pair && u >= kDU / 2;
-      const int row = min(r0 + (second ? u - kDU / 2 : u), d.O - 1);
-      const void *wm = second ? d.w2 : d.w;
-      if constexpr (FMT == 5) {
-        const uint4 *p = reinterpret_cast<const uint4 *>(
-            reinterpret_cast<const uint16_t *>(wm) + (size_t)row * d.I + 16 * (size_t)cc);
-        const uint4 a = p[0], bq = p[1];
-        k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
-        k.w[u][4] = bq.x; k.w[u][5] = bq.y; k.w[u][6] = bq.z; k.w[u][7] = bq.w;
-      } else {
-        const uint4 a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(wm) +
-                                                         (size_t)row * d.I + 16 * (size_t)cc);
-        k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
-        const size_t g = (size_t)row * (d.I >> 6) + (cc >> 2);
-        k.sb[u] = (uint32_t)(second ? d.sc2 : d.sc)[g] | ((uint32_t)(second ? d.bi2 : d.bi)[g] << 16);
-      }
-    }
-    const uint4 *ph = reinterpret_cast<const uint4 *>(xh + 16 * (size_t)cc);
-    const uint4 *pl = reinterpret_cast<const uint4 *>(xl + 16 * (size_t)cc);
-    const uint4 h0 = ph[0], h1 = ph[1], l0 = pl[0], l1 = pl[1];
-    k.hi[0] = h0.x; k.hi[1] = h0.y; k.hi[2] = h0.z; k.hi[3] = h0.w;
-    k.hi[4] = h1.x; k.hi[5] = h1.y; k.hi[6] = h1.z; k.hi[7] = h1.w;
-    k.lo[0] = l0.x; k.lo[1] = l0.y; k.lo[2] = l0.z; k.lo[3] = l0.w;
-    k.lo[4] = l1.x; k.lo[5] = l1.y; k.lo[6] = l1.z; k.lo[7] = l1.w;
-  };
-  float acc[kDU];
-#pragma unroll
-  for (int u = 0; u < kDU; ++u) acc[u] = 0.f;
-  auto use = [&](int c, const Chunk &k) {
-    if (c >= C) return;
-#pragma unroll
-    for (int u = 0; u < kDU; ++u) {
-      uint32_t pr[8];
-      if constexpr (FMT == 5) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) pr[q] = k.w[u][q];
-      } else {
-        const float sc = bf16_to_f32(k.sb[u] & 0xffffu), bi = bf16_to_f32(k.sb[u] >> 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t v = k.w[u][q];
-          const float w0 = fmaf(sc, (float)(v & 0xffu), bi);
-          const float w1 = fmaf(sc, (float)((v >> 8) & 0xffu), bi);
-          const float w2 = fmaf(sc, (float)((v >> 16) & 0xffu), bi);
-          const float w3 = fmaf(sc, (float)(v >> 24), bi);
-          pr[2 * q] = pk_bf16(w0, w1);
-          pr[2 * q + 1] = pk_bf16(w2, w3);
-        }
-      }
-      float a = acc[u];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) a = dot2(pr[q], k.hi[q], a);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) a = dot2(pr[q], k.lo[q], a);
-      acc[u] = a;
-    }
-  };
-  Chunk k0, k1;
-  int c = wave * 64 + lane;
-  load(c, k0);
-  for (; c < C; c += 512) {
-    load(c + 256, k1);
-    use(c, k0);
-    load(c + 512, k0);
-    use(c + 256, k1);
-  }
-  __shared__ float red[kLT / 64][kDU];
-#pragma unroll
-  for (int u = 0; u < kDU; ++u) {
-    const float t = team_sum<64>(acc[u]);
-    if (lane == 0) red[wave][u] = t;
-  }
-  __syncthreads();
-  auto row_sum = [&](int u) {
-    float t = red[0][u];
-#pragma unroll
-    for (int w = 1; w < kLT / 64; ++w) t += red[w][u];
-    return t;
-  };
-  if (pair) {
-    // h = silu(gate) * up (logan-llama/src/model.rs:888-890) as hi/lo halves
-    const int row = r0 + threadIdx.x;
-    if (threadIdx.x < kDU / 2 && row < d.O)
-      put_hl(d.hhl, d.O, row, silu(row_sum(threadIdx.x)) * row_sum(threadIdx.x + kDU / 2));
-  } else if (threadIdx.x < kDU) {
-    const float t = row_sum(threadIdx.x);
-    const int row = r0 + threadIdx.x;
-    if (row < d.O) d.y[row] = d.res ? d.res[row] + t : t;
-  }
-}
-
-bool dense_supported(int fmt, int O, int I, const void *w) {
-  if (O <= 0 || I <= 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0) return false;
-  if (fmt == 5) return I % 16 == 0;
-  if (fmt == 15) return I % 64 == 0;
-  return false;
-}
-
-hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
-  if (b.n <= 0 || b.n > kDenseMaxDescs) return hipErrorInvalidValue;
-  constexpr int rows_per_block = kDU;
-  b.block_start[0] = 0;
-  for (int i = 0; i < b.n; ++i) {
-    const DenseDesc &d = b.d[i];
-    if (!dense_supported(fmt, d.O, d.I, d.w) || !d.xhl) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(d.xhl) & 15) != 0) return hipErrorInvalidValue;
-    if (fmt == 15 && (!d.sc || !d.bi)) return hipErrorInvalidValue;
-    const bool pair = d.w2 != nullptr;
-    if (pair ? !dense_supported(fmt, d.O, d.I, d.w2) || !d.hhl || (fmt == 15 && (!d.sc2 || !d.bi2))
-             : !d.y)
-      return hipErrorInvalidValue;
-    const int rpb = pair ? rows_per_block / 2 : rows_per_block;
-    b.block_start[i + 1] = b.block_start[i] + (d.O + rpb - 1) / rpb;
-  }
-  const dim3 grid(b.block_start[b.n]);
-  if (fmt == 5) hipLaunchKernelGGL(dense_gemv_kernel<5>, grid, dim3(kLT), 0, st, b);
-  else hipLaunchKernelGGL(dense_gemv_kernel<15>, grid, dim3(kLT), 0, st, b);
-  return hipGetLastError();
-}
-
-// ---- the layer's small kernels --------------------------------------------
-
 // out = hi/lo halves of x * (1 / sqrt(sum x^2 / n + eps)) * w (a_rmsnorm,
 // backend_metal.mm:705-714; rms_norm_into, logan-llama/src/model.rs
 // :1067-1073). One block; n a multiple of 4; loads unrolled so each thread's
 // are in flight together. Also zeroes ctr[0, nctr) (the attention's
-// per-kv-head counters, when this is the layer's first kernel).
+// per-kv-head counters, when this is the layer's first kernel). (Forming the
+// norm inside the product blocks instead, the input one in every q/k/v block
+// and the post-attention one in the output projection's last block,
+// measured 1.5-2.5 us slower per config-2 layer.)
 __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const float *w, int n,
                                                          float eps, uint16_t *out, int *ctr, int nctr) {
   __shared__ float red[kLT / 64];
@@ -258,6 +119,177 @@ __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const f
   }
 }
 
+// ---- dense GEMV: y[r] = (res ? res[r] : 0) + sum_j w[r][j] x[j] ----------
+//
+// A block of NT threads owns DU rows; its waves split the 16-column chunks of
+// those rows (thread i: chunks i, i + NT, ...). With NCH = 1 (K <= 16 NT) a
+// thread loads its one chunk; with NCH = 0 (any K) it keeps the next chunk's
+// loads in flight while it uses the current one. The wave partials of a row
+// are added in wave order.
+template <int FMT, int DU, int NT, int NCH>
+__global__ __launch_bounds__(NT) void dense_gemv_kernel(DenseBatch b) {
+  int di = 0;
+  while (di + 1 < b.n && (int)blockIdx.x >= b.block_start[di + 1]) ++di;
+  const DenseDesc d = b.d[di];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // a SwiGLU pair's block holds rows [r0, r0 + DU / 2) of gate (u < DU / 2)
+  // and of up; every row's sum is formed as for a single product
+  const bool pair = d.w2 != nullptr;
+  const int rpb = pair ? DU / 2 : DU;
+  const int r0 = ((int)blockIdx.x - b.block_start[di]) * rpb;
+  const int C = d.I >> 4;
+  const uint16_t *xh = d.xhl, *xl = d.xhl + d.I;
+  constexpr int WD = FMT == 5 ? 8 : 4;  // dwords of one row's 16-column chunk
+  struct Chunk {
+    uint32_t w[DU][WD];
+    uint32_t sb[FMT == 5 ? 1 : DU];  // fmt 15: scale | bias << 16
+    uint32_t hi[8], lo[8];
+  };
+  auto load = [&](int c, Chunk &k) {
+    const int cc = c < C ? c : C - 1;
+#pragma unroll
+    for (int u = 0; u < DU; ++u) {
+      const bool second = pair && u >= DU / 2;
+      const int row = min(r0 + (second ? u - DU / 2 : u), d.O - 1);
+      const void *wm = second ? d.w2 : d.w;
+      if constexpr (FMT == 5) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(
+            reinterpret_cast<const uint16_t *>(wm) + (size_t)row * d.I + 16 * (size_t)cc);
+        const uint4 a = p[0], bq = p[1];
+        k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
+        k.w[u][4] = bq.x; k.w[u][5] = bq.y; k.w[u][6] = bq.z; k.w[u][7] = bq.w;
+      } else {
+        const uint4 a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(wm) +
+                                                         (size_t)row * d.I + 16 * (size_t)cc);
+        k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
+        const size_t g = (size_t)row * (d.I >> 6) + (cc >> 2);
+        k.sb[u] = (uint32_t)(second ? d.sc2 : d.sc)[g] | ((uint32_t)(second ? d.bi2 : d.bi)[g] << 16);
+      }
+    }
+    const uint4 *ph = reinterpret_cast<const uint4 *>(xh + 16 * (size_t)cc);
+    const uint4 *pl = reinterpret_cast<const uint4 *>(xl + 16 * (size_t)cc);
+    const uint4 h0 = ph[0], h1 = ph[1], l0 = pl[0], l1 = pl[1];
+    k.hi[0] = h0.x; k.hi[1] = h0.y; k.hi[2] = h0.z; k.hi[3] = h0.w;
+    k.hi[4] = h1.x; k.hi[5] = h1.y; k.hi[6] = h1.z; k.hi[7] = h1.w;
+    k.lo[0] = l0.x; k.lo[1] = l0.y; k.lo[2] = l0.z; k.lo[3] = l0.w;
+    k.lo[4] = l1.x; k.lo[5] = l1.y; k.lo[6] = l1.z; k.lo[7] = l1.w;
+  };
+  float acc[DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u) acc[u] = 0.f;
+  auto use = [&](int c, const Chunk &k) {
+    if (c >= C) return;
+#pragma unroll
+    for (int u = 0; u < DU; ++u) {
+      uint32_t pr[8];
+      if constexpr (FMT == 5) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pr[q] = k.w[u][q];
+      } else {
+        const float sc = bf16_to_f32(k.sb[u] & 0xffffu), bi = bf16_to_f32(k.sb[u] >> 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t v = k.w[u][q];
+          const float w0 = fmaf(sc, (float)(v & 0xffu), bi);
+          const float w1 = fmaf(sc, (float)((v >> 8) & 0xffu), bi);
+          const float w2 = fmaf(sc, (float)((v >> 16) & 0xffu), bi);
+          const float w3 = fmaf(sc, (float)(v >> 24), bi);
+          pr[2 * q] = pk_bf16(w0, w1);
+          pr[2 * q + 1] = pk_bf16(w2, w3);
+        }
+      }
+      float a = acc[u];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) a = dot2(pr[q], k.hi[q], a);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) a = dot2(pr[q], k.lo[q], a);
+      acc[u] = a;
+    }
+  };
+  int c = threadIdx.x;
+  if constexpr (NCH == 1) {
+    Chunk k0;
+    load(c, k0);
+    use(c, k0);
+  } else {
+    static_assert(NCH == 0, "one chunk up front, or the loop");
+    Chunk k0, k1;
+    load(c, k0);
+    for (; c < C; c += 2 * NT) {
+      load(c + NT, k1);
+      use(c, k0);
+      load(c + 2 * NT, k0);
+      use(c + NT, k1);
+    }
+  }
+  __shared__ float red[NT / 64][DU];
+#pragma unroll
+  for (int u = 0; u < DU; ++u) {
+    const float t = team_sum<64>(acc[u]);
+    if (lane == 0) red[wave][u] = t;
+  }
+  __syncthreads();
+  auto row_sum = [&](int u) {
+    float t = red[0][u];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) t += red[w][u];
+    return t;
+  };
+  if (pair) {
+    // h = silu(gate) * up (logan-llama/src/model.rs:888-890) as hi/lo halves
+    const int row = r0 + threadIdx.x;
+    if (threadIdx.x < DU / 2 && row < d.O)
+      put_hl(d.hhl, d.O, row, silu(row_sum(threadIdx.x)) * row_sum(threadIdx.x + DU / 2));
+  } else if (threadIdx.x < DU) {
+    const float t = row_sum(threadIdx.x);
+    const int row = r0 + threadIdx.x;
+    if (row < d.O) d.y[row] = d.res ? d.res[row] + t : t;
+  }
+}
+
+bool dense_supported(int fmt, int O, int I, const void *w) {
+  if (O <= 0 || I <= 0 || (reinterpret_cast<uintptr_t>(w) & 15) != 0) return false;
+  if (fmt == 5) return I % 16 == 0;
+  if (fmt == 15) return I % 64 == 0;
+  return false;
+}
+
+hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
+  if (b.n <= 0 || b.n > kDenseMaxDescs) return hipErrorInvalidValue;
+  // by the longest K: at most one 16-column chunk per thread (K <= 4096): 8
+  // rows per block, each thread's loads issued at once; longer: 4 rows, the
+  // next chunk in flight while one is used (two chunks per thread of 512
+  // threads measured no faster for the 4096 x 14336 down product)
+  int kmax = 0;
+  for (int i = 0; i < b.n; ++i) kmax = b.d[i].I > kmax ? b.d[i].I : kmax;
+  const bool one = kmax <= 16 * kLT;
+  const int rows_per_block = one ? 8 : 4;
+  b.block_start[0] = 0;
+  for (int i = 0; i < b.n; ++i) {
+    const DenseDesc &d = b.d[i];
+    if (!dense_supported(fmt, d.O, d.I, d.w) || !d.xhl) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(d.xhl) & 15) != 0) return hipErrorInvalidValue;
+    if (fmt == 15 && (!d.sc || !d.bi)) return hipErrorInvalidValue;
+    const bool pair = d.w2 != nullptr;
+    if (pair ? !dense_supported(fmt, d.O, d.I, d.w2) || !d.hhl || (fmt == 15 && (!d.sc2 || !d.bi2))
+             : !d.y)
+      return hipErrorInvalidValue;
+    const int rpb = pair ? rows_per_block / 2 : rows_per_block;
+    b.block_start[i + 1] = b.block_start[i] + (d.O + rpb - 1) / rpb;
+  }
+  const dim3 grid(b.block_start[b.n]), block(kLT);
+  if (fmt == 5) {
+    if (one) hipLaunchKernelGGL((dense_gemv_kernel<5, 8, kLT, 1>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((dense_gemv_kernel<5, 4, kLT, 0>), grid, block, 0, st, b);
+  } else {
+    if (one) hipLaunchKernelGGL((dense_gemv_kernel<15, 8, kLT, 1>), grid, block, 0, st, b);
+    else hipLaunchKernelGGL((dense_gemv_kernel<15, 4, kLT, 0>), grid, block, 0, st, b);
+  }
+  return hipGetLastError();
+}
+
+// ---- the layer's small kernels --------------------------------------------
+
 // Attention for one token at position pos over T = pos + 1 cached positions,
 // with RoPE and the cache store fused in (logan-llama/src/model.rs:786-869;
 // llama_qkv_rope, llama_cache_store, llama_attn_score, spark_softmax,
@@ -276,12 +308,6 @@ __global__ __launch_bounds__(kLT) void rmsnorm_hl_kernel(const float *x, const f
 // head, zeroed by the layer's first kernel and reset by that block) joins the
 // slices in order, rescaling each by exp(m_slice - m_max), and writes o / l.
 constexpr int kAttnTS = 64;  // positions per slice
-__device__ __forceinline__ void st_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float *p) {
-  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 constexpr int kAttnGMax = 16;  // query heads per kv head
 
 __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float *vc, float *part,
@@ -442,9 +468,8 @@ __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float 
   }
   __syncthreads();
   // The slice partials go out as device-scope stores and the joining block
-  // reads them with device-scope loads, coherent across the XCDs' L2s; each
-  // block's stores complete (vmcnt) before its counter increment. (An
-  // agent-scope fence would write back / invalidate the whole L2 instead.)
+  // reads them with device-scope loads; each block's stores complete (vmcnt)
+  // before its counter increment.
   for (int i = tid; i < G * hd; i += kLT) {
     const int g = i / hd, d = i % hd;
     float v = 0.f;
@@ -533,7 +558,7 @@ size_t llama_ws_layout(const LlamaDims &m, int T, uint8_t *base, LlamaWs *w) {
   uint8_t *prt = take((size_t)m.H * S * (m.hd + 2) * 4), *att = take((size_t)2 * qdim * 2);
   uint8_t *pn = take((size_t)2 * m.D * 2), *mg = take((size_t)m.inter * 4);
   uint8_t *mu = take((size_t)m.inter * 4), *hh = take((size_t)2 * m.inter * 2);
-  uint8_t *ctr = take((size_t)m.KH * 4);
+  uint8_t *ctr = take((size_t)m.KH * 4);  // the attention's, per kv head
   if (w) {
     w->ctr = reinterpret_cast<int *>(ctr);
     w->xhl = reinterpret_cast<uint16_t *>(xhl);
