@@ -266,14 +266,23 @@ constexpr int kMoeMapMax = 32;
 // The bank index of routed expert e: its block when a map is set (an expert
 // missing from the map reads block map_b[0], so the launch stays in bounds,
 // and sets *miss), else e itself.
-// The map is read at constant indices only: an index the compiler cannot
-// resolve into the by-value kernel argument makes it copy the whole MoeArgs
-// to scratch in every thread (which made the per-token kernels 4x slower).
+// CONST_IDX: the map is read at constant indices only (an unrolled scan of
+// all kMoeMapMax entries). In the per-token kernels, which also select bank
+// references inside the by-value MoeArgs at run time, a scan at run-time
+// indices makes the compiler copy the whole MoeArgs to scratch in every
+// thread (4x slower); in the fused B = 1 kernel the run-time scan stays in
+// registers and the unrolled one costs 11 % of its time. The kernels' scratch
+// use is checked by a CPU test.
+template <bool CONST_IDX>
 __device__ __forceinline__ int moe_bank_index(const MoeArgs &a, int e, bool &miss) {
   if (a.nmap == 0) return e;
   int b = -1;
+  if constexpr (CONST_IDX) {
 #pragma unroll
-  for (int i = 0; i < kMoeMapMax; ++i) b = i < a.nmap && a.map_e[i] == e ? a.map_b[i] : b;
+    for (int i = 0; i < kMoeMapMax; ++i) b = i < a.nmap && a.map_e[i] == e ? a.map_b[i] : b;
+  } else {
+    for (int i = 0; i < a.nmap; ++i) b = a.map_e[i] == e ? a.map_b[i] : b;
+  }
   miss = b < 0;
   return b < 0 ? a.map_b[0] : b;
 }

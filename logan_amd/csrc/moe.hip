@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
   int e = __builtin_amdgcn_readfirstlane(ge);
   if (!shared && a.nmap) {  // the expert's block in an expert cache's arena
     bool miss = false;
-    e = moe_bank_index(a, e, miss);
+    e = moe_bank_index<true>(a, e, miss);
     if (miss && threadIdx.x == 0) atomicOr(&g_moe_map_err, 8u);
   }
   const int rows = shared ? a.sinter : a.inter;
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
   int e = __builtin_amdgcn_readfirstlane(ge);
   if (!shared && a.nmap) {
     bool miss = false;  // (reported by the gate/up blocks)
-    e = moe_bank_index(a, e, miss);
+    e = moe_bank_index<true>(a, e, miss);
   }
   const int K = shared ? a.sinter : a.inter;  // columns of down
   const int Ck = K >> 5;

@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     int e = shared ? 0 : sel_expert(__builtin_amdgcn_readfirstlane(s_sel[0]));
     if (!shared && a.nmap) {  // the expert's block in an expert cache's arena
       bool miss = false;
-      e = moe_bank_index(a, e, miss);
+      e = moe_bank_index<false>(a, e, miss);
       if (miss && threadIdx.x == 0)
         __hip_atomic_fetch_or(&g_fused_sync.error[0], 8u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -641,7 +641,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     if (s < g.k) {
       const uint32_t kk = __builtin_amdgcn_readfirstlane(s_sel[s]);
       bool miss = false;  // (reported by the A blocks, which route the same way)
-      const int e = moe_bank_index(a, sel_expert(kk), miss);
+      const int e = moe_bank_index<false>(a, sel_expert(kk), miss);
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
         const int d = d0 + p * RPP + rsub;
