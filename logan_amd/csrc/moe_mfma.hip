@@ -342,8 +342,7 @@ __global__ __launch_bounds__(WAVES * 64, WAVES <= 4 ? 2 : MOE_GU_MINW) void moe_
     issue(s0, B0);
     // stage x of the tile's tokens, codes [c*chunk, (c+1)*chunk), straight
     // into LDS: lane granule pg of the 16-row tile is physical granule P of
-    // row m, which holds logical granule P ^ (m & 15); rows past the tile
-    // repeat its last token (no operand of a stored output reads them)
+    // row m, which holds logical granule P ^ (m & 15)
     if (c > 0) __syncthreads();
     {
       constexpr int NV = kMTok * kMChunk / 8 / NT;
@@ -353,15 +352,11 @@ __global__ __launch_bounds__(WAVES * 64, WAVES <= 4 ? 2 : MOE_GU_MINW) void moe_
         const int m = pg / gpr, qq = swz(m, pg % gpr);
         lds_dma16(xsrc + (size_t)s_tok[m] * a.D + c * chunk + 8 * qq, sx + 8 * base);
       };
-      if (chunk == kMChunk) {
-        // full tile: every copy unconditional, all in flight together
+      // rows from cnt on are not staged: their LDS rows keep what an earlier
+      // block left there, and feed only MFMA output rows that are not stored
 #pragma unroll
-        for (int i = 0; i < NV; ++i) dma(NT * i + 64 * wave);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-          if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
-      }
+      for (int i = 0; i < NV; ++i)
+        if (NT * i + 64 * wave < cnt * gpr) dma(NT * i + 64 * wave);
       lds_dma_wait();
     }
     __syncthreads();
@@ -600,14 +595,11 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
         const int m = pg / gpr, qq = swz(m, pg % gpr);
         lds_dma16(xsrc + (size_t)s_tok[m] * a.D + c * chunk + 8 * qq, sx + 8 * base);
       };
-      if (chunk == kMChunk) {
+      // rows from cnt on are not staged: their LDS rows keep what an earlier
+      // block left there, and feed only MFMA output rows that are not stored
 #pragma unroll
-        for (int i = 0; i < NV; ++i) dma(NT * i + 64 * wave);
-      } else {
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-          if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
-      }
+      for (int i = 0; i < NV; ++i)
+        if (NT * i + 64 * wave < cnt * gpr) dma(NT * i + 64 * wave);
     }
     issue(b0);
     lds_dma_wait();
@@ -679,8 +671,7 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
     // stage h (hi, lo) of the tile's rows straight into LDS, first: loads
     // complete in issue order, so the steps' weights (issued last) may still
     // be in flight when the copies are waited for (physical granule P of row
-    // m holds logical granule P ^ (m & 15)); rows past the tile repeat its
-    // last row, which no operand of a stored output reads
+    // m holds logical granule P ^ (m & 15))
     constexpr int NQ = kMTok * kMDownK / 8 / 256;
     const int gpr = K >> 3;  // >= 16
     auto dma = [&](int base) {
@@ -690,14 +681,10 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
       lds_dma16(w.h_hi + o, shi + 8 * base);
       lds_dma16(w.h_lo + o, slo + 8 * base);
     };
-    if (K == kMDownK) {
+    // rows from cnt on are not staged (they feed only output rows not stored)
 #pragma unroll
-      for (int i = 0; i < NQ; ++i) dma(256 * i + 64 * wave);
-    } else {
-#pragma unroll
-      for (int i = 0; i < NQ; ++i)
-        if (256 * i + 64 * wave < kMTok * gpr) dma(256 * i + 64 * wave);
-    }
+    for (int i = 0; i < NQ; ++i)
+      if (256 * i + 64 * wave < cnt * gpr) dma(256 * i + 64 * wave);
   }
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -847,8 +834,7 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
   };
   {
     // stage h (hi, lo) of the tile's rows (physical granule P of row m holds
-    // logical granule P ^ (m & 15)); rows past the tile repeat its last row,
-    // which no operand of a stored output reads
+    // logical granule P ^ (m & 15))
     constexpr int NQ = kMTok * kMDownK / 8 / NT;
     const int gpr = K >> 3;
     auto dma = [&](int base) {
@@ -858,9 +844,10 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
       lds_dma16(w.h_hi + o, shi + 8 * base);
       lds_dma16(w.h_lo + o, slo + 8 * base);
     };
+    // rows from cnt on are not staged (they feed only output rows not stored)
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
-      if (NT * i + 64 * wave < kMTok * gpr) dma(NT * i + 64 * wave);
+      if (NT * i + 64 * wave < cnt * gpr) dma(NT * i + 64 * wave);
   }
   // the ring's first two batches behind the h copies (a wave with no rows
   // inside D copies clamped rows and stores nothing)
