@@ -302,18 +302,22 @@ hipError_t launch_dense_gemv(DenseBatch &b, int fmt, hipStream_t st) {
 // of kh, so each K/V row is read once: the angles' cos/sin formed once per
 // block, RoPE on the G q rows and, in the slice holding pos, on the new k row
 // (that block alone stores k and v at pos; the slice's own reads of position
-// pos take them from LDS), the scores (4 threads per position, a quarter of
-// the row each), per head the slice max m, l = sum exp(s - m) and
+// pos take them from LDS), the scores (kAttnTP threads per position, a part
+// of the row each), per head the slice max m, l = sum exp(s - m) and
 // o = sum exp(s_t - m) V[t]. The last block of kh to finish (a counter per kv
 // head, zeroed by the layer's first kernel and reset by that block) joins the
 // slices in order, rescaling each by exp(m_slice - m_max), and writes o / l.
-constexpr int kAttnTS = 64;  // positions per slice
+// positions per slice (32: 1.5-2.5 us per config-2 layer below 64; 16 no
+// better than 32)
+constexpr int kAttnTS = 32;
+constexpr int kAttnTP = kLT / kAttnTS;  // threads per position in the scores
 constexpr int kAttnGMax = 16;  // query heads per kv head
 
 __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float *vc, float *part,
                                                    int *ctr, uint16_t *att, int H, int KH, int hd,
                                                    int pos, float theta) {
-  static_assert(kAttnTS * 4 == kLT, "4 threads per position");
+  static_assert(kAttnTP * kAttnTS == kLT && (kAttnTP == 4 || kAttnTP == 8 || kAttnTP == 16),
+                "threads per position");
   __shared__ float cs[128], sn[128];          // cos / sin of the hd/2 angles
   __shared__ float qs[kAttnGMax * 256 / 4];  // G roped q rows (G * hd <= 1024)
   __shared__ float kn[256], vn[256];          // the new k (roped) and v rows
@@ -328,16 +332,18 @@ __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float 
   const int tid = threadIdx.x;
   // every load of the block first: the K and V rows of the slice (position pos
   // read too, and replaced by the new rows below), the q pairs and the new k, v
-  const int t = tid >> 2, qd = tid & 3, q4 = hd >> 4;  // scores: position, quarter
+  // scores: position t, its row's part qd of hd / kAttnTP values (q4 float4)
+  const int t = tid / kAttnTP, qd = tid % kAttnTP, q4 = hd / (4 * kAttnTP);
   const int C4 = hd >> 2, PG = kLT / C4, c4 = tid % C4, pg = tid / C4;  // o: column, group
   constexpr int NPM = kAttnTS / 4;  // positions per thread in o at most (hd <= 256)
+  constexpr int KQ = 64 / kAttnTP;   // float4 of a row part at most (hd <= 256)
   const int np = kAttnTS / PG;
-  float4 kv[16], vv[NPM];
+  float4 kv[KQ], vv[NPM];
   {
     const int tt = t0 + min(t, nt - 1);
     const float4 *krow = reinterpret_cast<const float4 *>(kc + (size_t)tt * kvdim + kh * hd);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < KQ; ++i)
       if (i < q4) kv[i] = krow[qd * q4 + i];
 #pragma unroll
     for (int i = 0; i < NPM; ++i) {
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float 
     // position pos: the new rows, not the cache's
     if (t0 + min(t, nt - 1) == pos) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
+      for (int i = 0; i < KQ; ++i)
         if (i < q4) kv[i] = reinterpret_cast<const float4 *>(kn)[qd * q4 + i];
     }
 #pragma unroll
@@ -415,7 +421,7 @@ __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float 
     const float *q = qs + g * hd + 4 * qd * q4;
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < KQ; ++i) {
       if (i < q4) {
         acc = fmaf(q[4 * i], kv[i].x, acc);
         acc = fmaf(q[4 * i + 1], kv[i].y, acc);
@@ -423,21 +429,21 @@ __global__ __launch_bounds__(kLT) void attn_kernel(float *qkv, float *kc, float 
         acc = fmaf(q[4 * i + 3], kv[i].w, acc);
       }
     }
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
+#pragma unroll
+    for (int o = 1; o < kAttnTP; o <<= 1) acc += __shfl_xor(acc, o, 64);
     if (qd == 0) es[g][t] = __fdiv_rn(acc, rs);
   }
   __syncthreads();
   // softmax over the slice, one wave per head
   const int lane = tid & 63, wave = tid >> 6;
   for (int g = wave; g < G; g += kLT / 64) {
-    const float sc = es[g][lane];
+    const float sc = lane < kAttnTS ? es[g][lane] : 0.f;
     float mx = lane < nt ? sc : -INFINITY;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     const float e = lane < nt ? __expf(sc - mx) : 0.f;
     const float l = team_sum<64>(e);
-    es[g][lane] = e;
+    if (lane < kAttnTS) es[g][lane] = e;
     if (lane == 0) {
       ml[g][0] = mx;
       ml[g][1] = l;
@@ -604,10 +610,11 @@ size_t llama_workspace_bytes(const LlamaDims &m, int T) { return llama_ws_layout
 
 bool llama_supported(const LlamaDims &m, const DenseMat mats[7]) {
   if (m.D <= 0 || m.inter <= 0 || m.H <= 0 || m.KH <= 0 || m.H % m.KH != 0) return false;
-  // head size 16, 32, 64, 128 or 256 (float4 columns that divide the block),
+  // head size 32, 64, 128 or 256 (float4 columns that divide the block, and
+  // a float4 per score thread),
   // at most kAttnGMax query heads per kv head, G * hd <= 1024
   const int G = m.H / m.KH;
-  if (m.hd < 16 || m.hd > 256 || (m.hd & (m.hd - 1)) != 0 || G > kAttnGMax || G * m.hd > 1024 ||
+  if (m.hd < 4 * kAttnTP || m.hd > 256 || (m.hd & (m.hd - 1)) != 0 || G > kAttnGMax || G * m.hd > 1024 ||
       !(m.theta > 0.f) || !(m.eps > 0.f))
     return false;
   if (m.D % 16 != 0) return false;  // the norms' float4 loads; the GEMVs need it too
