@@ -57,16 +57,49 @@ struct DevBuf {
 DevBuf g_xbuf, g_ybuf, g_ws;
 DevBuf g_hlbuf, g_y2buf;  // hi/lo activation pairs and pair products of matmul_multi
 
+// Pinned host staging (hipHostMalloc) for the host-pointer entry points: the
+// caller's pageable rows are copied into it on the host and DMA'd from it
+// asynchronously, results come back into it (pageable source or destination
+// made each copy a staged, synchronous transfer: config-1 drop-in matmul
+// 39-48 -> 32 us wall per call).
+struct HostBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  // Grows the buffer; the caller guarantees no in-flight copy uses it.
+  bool ensure(size_t bytes) {
+    if (bytes <= n) return true;
+    if (p) hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+      p = nullptr;
+      return false;
+    }
+    n = bytes;
+    return true;
+  }
+  void release() {
+    if (p) hipHostFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+HostBuf g_hxbuf, g_hybuf;  // matmul_multi's x rows in, y rows out
+
 // Device buffers of one route-island submission: x [D], gate/up outputs
-// [2 K M], expert outputs [K D]. Each pending handle owns one set from the
-// pool until finish/discard, so calls made between begin and finish (the
-// shared expert, other GEMVs, another begin) never touch it.
+// [2 K M], expert outputs [K D], and the pinned host staging of x and of the
+// outputs. Each pending handle owns one set from the pool until
+// finish/discard, so calls made between begin and finish (the shared
+// expert, other GEMVs, another begin) never touch it.
 struct RouteBufs {
   DevBuf x, gu, out;
+  HostBuf hx, hout;
   void release() {
     x.release();
     gu.release();
     out.release();
+    hx.release();
+    hout.release();
   }
 };
 std::vector<RouteBufs *> g_route_pool;  // idle sets
@@ -80,7 +113,8 @@ RouteBufs *route_bufs_take(size_t xb, size_t gub, size_t outb) {
     b = new (std::nothrow) RouteBufs();
     if (!b) return nullptr;
   }
-  if (!b->x.ensure(xb) || !b->gu.ensure(gub) || !b->out.ensure(outb)) {
+  if (!b->x.ensure(xb) || !b->gu.ensure(gub) || !b->out.ensure(outb) || !b->hx.ensure(xb) ||
+      !b->hout.ensure(outb)) {
     g_route_pool.push_back(b);
     return nullptr;
   }
@@ -553,6 +587,8 @@ void logan_hip_shutdown(void) {
   g_xbuf.release();
   g_ybuf.release();
   g_ws.release();
+  g_hxbuf.release();
+  g_hybuf.release();
   for (RouteBufs *b : g_route_pool) {
     b->release();
     delete b;
@@ -722,13 +758,15 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   }
   uint64_t t1 = now_ns();
   prof_add(0, t1 - t0);
-  hipError_t e = hipSuccess;
-  if (shared_I > 0)
-    e = hipMemcpyAsync(dx, x, (size_t)S * shared_I * 4, hipMemcpyHostToDevice, g_stream);
-  for (int i = 0; i < count && e == hipSuccess; ++i)
-    if (descs[i].x)
-      e = hipMemcpyAsync(dx + xoff[i], descs[i].x, (size_t)descs[i].S * descs[i].I * 4,
-                         hipMemcpyHostToDevice, g_stream);
+  // every row in through one pinned staging copy (the previous call's copies
+  // ended with its stream synchronisation)
+  if (!g_hxbuf.ensure(xn * 4 + 16) || !g_hybuf.ensure(yn * 4 + 16)) return 0;
+  float *hx = reinterpret_cast<float *>(g_hxbuf.p);
+  float *hy = reinterpret_cast<float *>(g_hybuf.p);
+  if (shared_I > 0) memcpy(hx, x, (size_t)S * shared_I * 4);
+  for (int i = 0; i < count; ++i)
+    if (descs[i].x) memcpy(hx + xoff[i], descs[i].x, (size_t)descs[i].S * descs[i].I * 4);
+  hipError_t e = hipMemcpyAsync(dx, hx, xn * 4, hipMemcpyHostToDevice, g_stream);
   if (e != hipSuccess) return -1;
   if (g_prof_on) hipEventRecord(g_prof_ev0, g_stream);
   if (!row_m.empty()) e = launch_f32x_groups(row_m, row_x, row_y, g_stream);
@@ -747,14 +785,14 @@ int logan_hip_matmul_multi(const float *x, int S, LoganHipMatmulDesc *descs, int
   if (g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
   uint64_t t2 = now_ns();
   prof_add(1, t2 - t1);
-  for (int i = 0; i < count && e == hipSuccess; ++i) {
-    const int s = descs[i].x ? descs[i].S : S;
-    e = hipMemcpyAsync(descs[i].y, dy + yoff[i], (size_t)s * descs[i].O * 4,
-                       hipMemcpyDeviceToHost, g_stream);
-  }
+  e = hipMemcpyAsync(hy, dy, yn * 4, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-  prof_add(2, now_ns() - t2);
   if (e != hipSuccess) return -1;
+  for (int i = 0; i < count; ++i) {
+    const int s = descs[i].x ? descs[i].S : S;
+    memcpy(descs[i].y, hy + yoff[i], (size_t)s * descs[i].O * 4);
+  }
+  prof_add(2, now_ns() - t2);
   prof_kernel_time();
   return 1;
 }
@@ -808,7 +846,8 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
   float *gu = reinterpret_cast<float *>(p->bufs->gu.p);
   float *out = reinterpret_cast<float *>(p->bufs->out.p);
   uint64_t t1 = now_ns();
-  hipError_t e = hipMemcpyAsync(dx, x, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
+  memcpy(p->bufs->hx.p, x, (size_t)D * 4);
+  hipError_t e = hipMemcpyAsync(dx, p->bufs->hx.p, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
   if (g_prof_on && hipEventCreate(&p->pev0) == hipSuccess && hipEventCreate(&p->pev1) == hipSuccess)
     hipEventRecord(p->pev0, g_stream);
   if (fast) {
@@ -852,6 +891,10 @@ void *logan_hip_moe_route_begin(uint64_t model_id, int layer, LoganHipMatmulDesc
     if (e == hipSuccess) e = launch_descs(s2, g_stream);
   }
   if (p->pev1) hipEventRecord(p->pev1, g_stream);
+  // the expert outputs come back into the handle's pinned buffer in stream
+  // order; finish waits for the event and copies them out on the host
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p->bufs->hout.p, out, (size_t)K * D * 4, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipEventRecord(p->ev, g_stream);
   prof_add(1, now_ns() - t1);
   if (e != hipSuccess) {
@@ -879,8 +922,7 @@ int logan_hip_moe_route_finish(void *pending, float *out, int count) {
     rc = -1;
   } else {
     const int K = std::min(count, p->K);
-    if (hipMemcpy(out, p->bufs->out.p, (size_t)K * p->D * 4, hipMemcpyDeviceToHost) != hipSuccess)
-      rc = -1;
+    memcpy(out, p->bufs->hout.p, (size_t)K * p->D * 4);
   }
   prof_add(2, now_ns() - t0);
   float ms = 0.f;
@@ -1036,10 +1078,15 @@ int logan_hip_host_llama_layer(uint64_t model_id, int layer, LoganHipMatmulDesc 
   LlamaCtx *c = llama_ctx_locked(model_id, layer, in_norm, post_norm, dims);
   if (!c || c->tokens != pos || !llama_grow_locked(c, pos + 1)) return 0;
   if (!c->ws.ensure(lh::llama_workspace_bytes(dims, pos + 1))) return 0;
+  // x in, then x, k and v out, through the pinned staging buffers
+  if (!g_hxbuf.ensure((size_t)D * 4) || !g_hybuf.ensure((size_t)(D + 2 * kvdim) * 4)) return 0;
+  float *hx = reinterpret_cast<float *>(g_hxbuf.p);
+  float *hy = reinterpret_cast<float *>(g_hybuf.p);
   float *dx = reinterpret_cast<float *>(c->x.p);
   const uint64_t t1 = now_ns();
   prof_add(0, t1 - t0);
-  hipError_t e = hipMemcpyAsync(dx, x, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
+  memcpy(hx, x, (size_t)D * 4);
+  hipError_t e = hipMemcpyAsync(dx, hx, (size_t)D * 4, hipMemcpyHostToDevice, g_stream);
   if (e == hipSuccess && g_prof_on) hipEventRecord(g_prof_ev0, g_stream);
   if (e == hipSuccess)
     e = lh::launch_llama_layer(mats, c->in_norm, c->post_norm, dims, dx, c->kc, c->vc, pos, c->ws.p,
@@ -1047,19 +1094,22 @@ int logan_hip_host_llama_layer(uint64_t model_id, int layer, LoganHipMatmulDesc 
   if (e == hipSuccess && g_prof_on) hipEventRecord(g_prof_ev1, g_stream);
   const uint64_t t2 = now_ns();
   prof_add(1, t2 - t1);
-  if (e == hipSuccess) e = hipMemcpyAsync(x, dx, (size_t)D * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(hy, dx, (size_t)D * 4, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(k_out, c->kc + (size_t)pos * kvdim, (size_t)kvdim * 4, hipMemcpyDeviceToHost,
+    e = hipMemcpyAsync(hy + D, c->kc + (size_t)pos * kvdim, (size_t)kvdim * 4, hipMemcpyDeviceToHost,
                        g_stream);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(v_out, c->vc + (size_t)pos * kvdim, (size_t)kvdim * 4, hipMemcpyDeviceToHost,
-                       g_stream);
+    e = hipMemcpyAsync(hy + D + kvdim, c->vc + (size_t)pos * kvdim, (size_t)kvdim * 4,
+                       hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-  prof_add(2, now_ns() - t2);
   if (e != hipSuccess) {
     hipStreamSynchronize(g_stream);
     return -1;
   }
+  memcpy(x, hy, (size_t)D * 4);
+  memcpy(k_out, hy + D, (size_t)kvdim * 4);
+  memcpy(v_out, hy + D + kvdim, (size_t)kvdim * 4);
+  prof_add(2, now_ns() - t2);
   prof_kernel_time();
   c->tokens = pos + 1;
   return 1;
@@ -1102,14 +1152,26 @@ int host_ew(float *dst, size_t n_dst, const float *src, size_t n_src,
   std::lock_guard<std::mutex> lk(g_mtx);
   if (!g_ok) return 0;
   if (!g_xbuf.ensure(n_dst * 4 + 16) || !g_ybuf.ensure(n_src * 4 + 16)) return 0;
+  if (!g_hxbuf.ensure(n_dst * 4 + 16) || !g_hybuf.ensure(n_src * 4 + 16)) return 0;
   float *dd = reinterpret_cast<float *>(g_xbuf.p);
   float *ds = reinterpret_cast<float *>(g_ybuf.p);
-  hipError_t e = hipMemcpyAsync(dd, dst, n_dst * 4, hipMemcpyHostToDevice, g_stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(ds, src, n_src * 4, hipMemcpyHostToDevice, g_stream);
+  // through the pinned staging buffers: dst in and out of g_hxbuf, src in
+  // from g_hybuf (the copies run in stream order)
+  float *hd = reinterpret_cast<float *>(g_hxbuf.p);
+  float *hs = reinterpret_cast<float *>(g_hybuf.p);
+  memcpy(hd, dst, n_dst * 4);
+  memcpy(hs, src, n_src * 4);
+  hipError_t e = hipMemcpyAsync(dd, hd, n_dst * 4, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(ds, hs, n_src * 4, hipMemcpyHostToDevice, g_stream);
   if (e == hipSuccess) e = run(dd, ds, g_stream, arg);
-  if (e == hipSuccess) e = hipMemcpyAsync(dst, dd, n_dst * 4, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(hd, dd, n_dst * 4, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-  return e == hipSuccess ? 1 : -1;
+  if (e != hipSuccess) {
+    hipStreamSynchronize(g_stream);
+    return -1;
+  }
+  memcpy(dst, hd, n_dst * 4);
+  return 1;
 }
 struct RmsArg {
   int n, nrows;
