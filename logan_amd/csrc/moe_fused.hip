@@ -11,8 +11,8 @@
 //
 //   B blocks: a block owns ROWS_B output rows d; wave w owns slots w and
 //   w + 8 for all of them. Each wave issues the shared slot's down-row loads
-//   and the shared-expert gate loads before routing and the routed down rows
-//   right after it, so they stream from HBM while A runs; the last wave
+//   and the shared-expert gate loads before the route is known and the routed
+//   down rows right after it, so they stream from HBM while A runs; the last wave
 //   computes the shared-expert scalar gate sigmoid(se_g . x). While A runs,
 //   each wave turns its down codes into exact f16 pairs. Per slot, a wave
 //   waits for the slot's arrivals, reads the slot's h pairs until every tag
@@ -27,15 +27,22 @@
 // launch reads again (logits, x, the hand-off lines, its code): 14.1 -> 13.3
 // us per config-3 layer.
 //
-// Every wave computes the route itself from the router logits, bf16 or f32
-// (top-k with the key (logit desc, index asc): per-lane sorted keys, k rounds
-// of a DPP wave max, and the reference's probability arithmetic instead where
-// a tie in probability could reorder it), so no block waits for another
-// before streaming weights.
+// Routing, from the router logits, bf16 or f32 (top-k with the key (logit
+// desc, index asc): per-lane sorted keys, k rounds of a DPP wave max, and the
+// reference's probability arithmetic instead where a tie in probability could
+// reorder it): each A block's wave 0 selects its own slot's expert, so no A
+// block waits before streaming weights. B block 0's wave 0 selects every rank
+// and publishes the route (expert and combine weight per rank) as tagged
+// 16-byte records; the other B blocks read them, their routed down-row loads
+// behind it (the shared slot's are issued first). One selecting B wave
+// instead of one per B block: the 256 B waves' selection rounds competed for
+// the CUs with the A blocks' routing (13.33 -> 13.21 us per config-3 layer).
 //
-// Progress: A blocks never wait on another block. Workgroups are dispatched in
-// ID order, and every A block precedes every B block, so a B block can only be
-// resident after all A blocks were dispatched: the waits always end. They are
+// Progress: A blocks never wait on another block, and B block 0 waits for
+// none before it publishes the route. Workgroups are dispatched in ID order,
+// every A block precedes every B block and B block 0 the other B blocks, so
+// a block can only be resident after the blocks it waits for were
+// dispatched: the waits always end. They are
 // also bounded: after kSpinLimit polls a B wave stops waiting, raises the
 // sticky error word and its block finishes without writing its rows (the
 // host can read the word with logan_hip_moe_sync_errors(); results of later
@@ -299,6 +306,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __shared__ __align__(16) float s_xsp[64 * CPLA][kWaves]; // A: partial sums of x' (pairs)
   __shared__ uint32_t s_left;  // A: waves of the block still running
   __shared__ uint32_t s_lid;   // launch number
+  __shared__ uint32_t s_rto;   // B: the route did not arrive
   __shared__ float s_gsig;
   TL_LDS;
 
@@ -542,11 +550,14 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   const int d0 = bb * ROWS_B;
   const bool has_shared = a.sdown.m.w != nullptr;
 
-  // wave 0 routes for the block
+  // B block 0's wave 0 routes and publishes the route; the other B blocks
+  // read it (one wave selecting instead of one per block: the selection
+  // rounds of 256 waves competed with the A blocks' own routing)
   unsigned long long tk = 0;
   if (threadIdx.x == 0) tk = take_ticket();
+  const bool pub = bb == 0;
   RK rk;
-  if (wave == 0) rk.load(a.logits, a.E);
+  if (pub && wave == 0) rk.load(a.logits, a.E);
 
   // route-independent loads first: the shared slot's down rows
   uint32_t wv[kSlotsPerWave][PASSES][BITS];
@@ -563,9 +574,9 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
       }
     }
   }
-  if (wave == 0) {
-    float wr = 0.f;
-    uint32_t enc = 0u;  // 0xffff - expert of rank `lane`, 0 past the route
+  float wr = 0.f;
+  uint32_t enc = 0u;  // publisher: 0xffff - expert of rank `lane`, 0 past the route
+  if (pub && wave == 0) {
     bool routed = false;
     if constexpr (LF) {
       // 32-bit keys first (route_dev.hpp: select_fast / fast_ok)
@@ -619,7 +630,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     }
     if (lane < kFusedMaxSlots) s_sel[lane] = enc;
     if (lane < kFusedMaxSlots) s_w[lane] = wr;
-    if (bb == 0 && lane < g.k) {
+    if (lane < g.k) {
       if (a.idx_out) a.idx_out[lane] = sel_expert(enc);
       if (a.w_out) a.w_out[lane] = wr;
     }
@@ -628,6 +639,53 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __syncthreads();
   const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
   const uint32_t tag = launch_tag(lid);
+  // The route records: one 16 bytes (0xffff - expert, tag, weight bits, tag)
+  // per rank, kSlices rotating slices after the h pairs of the workspace.
+  const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<char *>(a.ws) + (size_t)kSlices * g.slots * hmax * sizeof(uint64_t), (short)0,
+      kSlices * kFusedMaxSlots * 16, kBufWord3);
+  const int roff = ((int)(lid % kSlices) * kFusedMaxSlots + (lane < kFusedMaxSlots ? lane : 0)) * 16;
+  if (pub && wave == 0 && lane < g.k) {
+    // device-scope 64-bit halves, each carrying the tag
+    uint64_t *rec = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(a.ws) + (size_t)kSlices * g.slots * hmax *
+                                                 sizeof(uint64_t) + roff);
+    const uint64_t tg = (uint64_t)tag << 32;
+    __hip_atomic_store(rec, tg | enc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rec + 1, tg | __float_as_uint(wr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!pub && wave == 0) {
+    // read the ranks' records with device-scope loads until every tag is this
+    // launch's (the few record lines stay in an XCD's L2 from earlier
+    // launches, so a first read through L2 would mostly find stale tags)
+    const bool mine = lane < g.k;
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    bool ok = !mine;
+    if (mine) {
+      q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rrs, roff, 0, kCpolSc1));
+      ok = q.y == tag && q.w == tag;
+    }
+    uint32_t rto = 0;
+    for (uint32_t spins = 0; !__all(ok);) {
+      __builtin_amdgcn_s_sleep(1);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (++spins > kSpinLimit) {
+        rto = 1;
+        break;
+      }
+      if (!ok) {
+        q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rrs, roff, 0, kCpolSc1));
+        ok = q.y == tag && q.w == tag;
+      }
+    }
+    // a route that never came: expert 0 everywhere (valid addresses), no output
+    if (lane < kFusedMaxSlots) s_sel[lane] = mine ? (rto ? 0xffffu : q.x) : 0u;
+    if (lane < kFusedMaxSlots) s_w[lane] = mine && !rto ? __uint_as_float(q.z) : 0.f;
+    if (lane == 0) s_rto = rto;
+    if (rto && lane == 0)
+      __hip_atomic_fetch_or(&g_fused_sync.error[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (pub && wave == 0 && lane == 0) s_rto = 0u;
+  __syncthreads();
   TL_BLOCK(1);
   // zero the arrival counters the next launch uses (the previous launch,
   // their last user, has ended): counter j by block j mod nB
@@ -847,6 +905,7 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
     uint32_t anyto = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) anyto |= s_to[w];
+    anyto |= s_rto;
     float acc = 0.f;
 #pragma unroll
     for (int q = 0; q < kFusedMaxSlots; ++q)
@@ -868,7 +927,8 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
 
 size_t moe_fused_workspace_bytes(int slots, int inter, int sinter) {
   const size_t hmax = (size_t)(inter > sinter ? inter : sinter);
-  return (size_t)kSlices * slots * hmax * sizeof(uint64_t);  // (value, tag) pairs
+  // (value, tag) h pairs, then the published route records
+  return (size_t)kSlices * slots * hmax * sizeof(uint64_t) + (size_t)kSlices * kFusedMaxSlots * 16;
 }
 
 // Launches of this kernel on one device share the module-scope ticket and
