@@ -639,16 +639,15 @@ __global__ __launch_bounds__(kWaves * 64, CPLA == 1 ? 4 : 2) void moe_fused_b1_k
   __syncthreads();
   const uint32_t lid = __builtin_amdgcn_readfirstlane(s_lid);
   const uint32_t tag = launch_tag(lid);
-  // The route records: one 16 bytes (0xffff - expert, tag, weight bits, tag)
-  // per rank, kSlices rotating slices after the h pairs of the workspace.
-  const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-      reinterpret_cast<char *>(a.ws) + (size_t)kSlices * g.slots * hmax * sizeof(uint64_t), (short)0,
-      kSlices * kFusedMaxSlots * 16, kBufWord3);
+  // The route records: 16 bytes (0xffff - expert, tag, weight bits, tag) per
+  // rank, in kSlices rotating slices after the h pairs of the workspace.
+  char *const rbase = reinterpret_cast<char *>(a.ws) + (size_t)kSlices * g.slots * hmax * sizeof(uint64_t);
+  const __amdgpu_buffer_rsrc_t rrs =
+      __builtin_amdgcn_make_buffer_rsrc(rbase, (short)0, kSlices * kFusedMaxSlots * 16, kBufWord3);
   const int roff = ((int)(lid % kSlices) * kFusedMaxSlots + (lane < kFusedMaxSlots ? lane : 0)) * 16;
   if (pub && wave == 0 && lane < g.k) {
     // device-scope 64-bit halves, each carrying the tag
-    uint64_t *rec = reinterpret_cast<uint64_t *>(reinterpret_cast<char *>(a.ws) + (size_t)kSlices * g.slots * hmax *
-                                                 sizeof(uint64_t) + roff);
+    uint64_t *rec = reinterpret_cast<uint64_t *>(rbase + roff);
     const uint64_t tg = (uint64_t)tag << 32;
     __hip_atomic_store(rec, tg | enc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(rec + 1, tg | __float_as_uint(wr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
