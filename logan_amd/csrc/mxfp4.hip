@@ -109,13 +109,26 @@ __device__ __noinline__ float mx4_row_exact(const Mx4Desc d, int row) {
   return tot;
 }
 
+// one group's activation words as loaded: 32 f32 (8 x 16 bytes) or 32 bf16
 template <bool XF>
-__device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
+struct Mx4XRaw {
+  uint4 v[XF ? 8 : 4];
+};
+
+template <bool XF>
+__device__ __forceinline__ void mx4_load_x_raw(const void *x, int c, Mx4XRaw<XF> &r) {
+  const uint4 *src = XF ? reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(x) + 32 * c)
+                        : reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + 32 * c);
+#pragma unroll
+  for (int v = 0; v < (XF ? 8 : 4); ++v) r.v[v] = src[v];
+}
+
+template <bool XF>
+__device__ __forceinline__ void mx4_x_from_raw(const Mx4XRaw<XF> &r, Mx4X<XF> &o) {
   if constexpr (XF) {
-    const float4 *src = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(x) + 32 * c);
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      const float4 f = src[v];
+      const float4 f = __builtin_bit_cast(float4, r.v[v]);
       const float e[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
       for (int q = 0; q < 4; q += 2) {
@@ -126,19 +139,23 @@ __device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
         o.lo[2 * v + q / 2] = l0 | (l1 << 16);
       }
     }
-    o.xe = mx4_max_exp(o.hi);
   } else {
-    const uint4 *src = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + 32 * c);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const uint4 t = src[v];
-      o.hi[4 * v] = t.x;
-      o.hi[4 * v + 1] = t.y;
-      o.hi[4 * v + 2] = t.z;
-      o.hi[4 * v + 3] = t.w;
+      o.hi[4 * v] = r.v[v].x;
+      o.hi[4 * v + 1] = r.v[v].y;
+      o.hi[4 * v + 2] = r.v[v].z;
+      o.hi[4 * v + 3] = r.v[v].w;
     }
-    o.xe = mx4_max_exp(o.hi);
   }
+  o.xe = mx4_max_exp(o.hi);
+}
+
+template <bool XF>
+__device__ __forceinline__ void mx4_load_x(const void *x, int c, Mx4X<XF> &o) {
+  Mx4XRaw<XF> r;
+  mx4_load_x_raw<XF>(x, c, r);
+  mx4_x_from_raw<XF>(r, o);
 }
 
 template <int LANES, bool XF>
@@ -162,6 +179,54 @@ __global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
 #pragma unroll
   for (int u = 0; u < kMx4U; ++u) risky[u] = false;
   const uint32_t lim = 370u - (C > 1 ? 32u - (uint32_t)__clz(C - 1) : 0u);
+  auto use = [&](int cg, const uint4 (&q)[kMx4U], const uint32_t (&s)[kMx4U], const Mx4X<XF> &xv) {
+    if (cg >= C) return;
+#pragma unroll
+    for (int u = 0; u < kMx4U; ++u) {
+      uint32_t pr[16];
+      mx4_pairs(q[u], pr);
+      float g = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.hi[k], g);
+      if constexpr (XF) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.lo[k], g);
+      }
+      acc[u] = fmaf(g, e8m0(s[u]), acc[u]);  // g * 2^(s - 127) is exact
+      risky[u] = risky[u] || s[u] == 255u || xv.xe == 255u || s[u] + xv.xe > lim;
+    }
+  };
+  if (C <= LANES) {
+    // One group per lane (rows of up to 32 LANES codes): x first, then the
+    // plane's scale bytes and codes of the team's rows, all in flight at
+    // once; the weights with non-temporal loads (read once per launch, they
+    // leave x and the kernel's code in L2). Loads complete in issue order, so
+    // the x conversion waits for x alone.
+    const int cc = lane < C ? lane : C - 1;
+    Mx4XRaw<XF> xr;
+    mx4_load_x_raw<XF>(d.x, cc, xr);
+    for (int p = 0; p < d.planes; ++p) {
+      const uint8_t *wp = d.w + (size_t)p * d.wplane;
+      const uint8_t *sp = d.sc + (size_t)p * d.splane;
+      uint4 q[kMx4U];
+      uint32_t sb[kMx4U];
+#pragma unroll
+      for (int u = 0; u < kMx4U; ++u) sb[u] = ld_stream<uint8_t, true>(sp + (size_t)min(r0 + u, d.O - 1) * C + cc);
+#pragma unroll
+      for (int u = 0; u < kMx4U; ++u)
+        q[u] = ld_stream<uint4, true>(reinterpret_cast<const uint4 *>(wp + (size_t)min(r0 + u, d.O - 1) * rb +
+                                                                      16 * (size_t)cc));
+      __builtin_amdgcn_sched_barrier(0);
+      Mx4X<XF> xv;
+      mx4_x_from_raw<XF>(xr, xv);
+      use(lane, q, sb, xv);
+#pragma unroll
+      for (int u = 0; u < kMx4U; ++u) {
+        tot[u] += team_sum<LANES>(acc[u]);
+        acc[u] = 0.f;
+      }
+    }
+  } else
   for (int p = 0; p < d.planes; ++p) {
     const uint8_t *wp = d.w + (size_t)p * d.wplane;
     const uint8_t *sp = d.sc + (size_t)p * d.splane;
@@ -181,23 +246,6 @@ __global__ __launch_bounds__(256) void mxfp4_gemv_kernel(Mx4Batch b) {
     int c = lane;
     load(c, q0, s0);
     mx4_load_x<XF>(d.x, c < C ? c : C - 1, x0);
-    auto use = [&](int cg, const uint4 (&q)[kMx4U], const uint32_t (&s)[kMx4U], const Mx4X<XF> &xv) {
-      if (cg >= C) return;
-#pragma unroll
-      for (int u = 0; u < kMx4U; ++u) {
-        uint32_t pr[16];
-        mx4_pairs(q[u], pr);
-        float g = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.hi[k], g);
-        if constexpr (XF) {
-#pragma unroll
-          for (int k = 0; k < 16; ++k) g = dot2(pr[k], xv.lo[k], g);
-        }
-        acc[u] = fmaf(g, e8m0(s[u]), acc[u]);  // g * 2^(s - 127) is exact
-        risky[u] = risky[u] || s[u] == 255u || xv.xe == 255u || s[u] + xv.xe > lim;
-      }
-    };
     for (; c < C; c += 2 * LANES) {
       load(c + LANES, q1, s1);
       mx4_load_x<XF>(d.x, c + LANES < C ? c + LANES : C - 1, x1);
