@@ -425,18 +425,18 @@ __global__ __launch_bounds__(256, 3) void moe_gateup_kernel(MoeArgs a, MoeWs w, 
     for (int i = 0; i < CPL; ++i) {
       const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
       const size_t p = (size_t)j * gm.ng + (c >> gshift);
-      rsg[u][i] = gsc[p];
-      rbg[u][i] = gbi[p];
-      rsu[u][i] = usc[p];
-      rbu[u][i] = ubi[p];
+      rsg[u][i] = ld_stream<uint16_t, true>(gsc + p);
+      rbg[u][i] = ld_stream<uint16_t, true>(gbi + p);
+      rsu[u][i] = ld_stream<uint16_t, true>(usc + p);
+      rbu[u][i] = ld_stream<uint16_t, true>(ubi + p);
     }
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int j = min(j0 + u, rows - 1), c = min(lane + 64 * i, C - 1);
-      load_chunk<BITS>(wg[u][i], gwb + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
-      load_chunk<BITS>(wu[u][i], uwb + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
+      load_chunk<BITS, true>(wg[u][i], gwb + (size_t)j * gm.row_bytes + (size_t)c * (4 * BITS));
+      load_chunk<BITS, true>(wu[u][i], uwb + (size_t)j * um.row_bytes + (size_t)c * (4 * BITS));
     }
   __builtin_amdgcn_sched_barrier(0);
   // the packed rows stay in registers; each token unpacks them again (groups
@@ -557,13 +557,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a, MoeWs w, int i
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const int d = min(d0 + p * RPP + rsub, a.D - 1);
-    rs[p] = scb[(size_t)d * dm.ng + gi];
-    rbi[p] = bib[(size_t)d * dm.ng + gi];
+    rs[p] = ld_stream<uint16_t, true>(scb + (size_t)d * dm.ng + gi);
+    rbi[p] = ld_stream<uint16_t, true>(bib + (size_t)d * dm.ng + gi);
   }
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     const int d = min(d0 + p * RPP + rsub, a.D - 1);
-    load_chunk<BITS>(wv[p], wb + (size_t)d * dm.row_bytes + (size_t)cl * (4 * BITS));
+    load_chunk<BITS, true>(wv[p], wb + (size_t)d * dm.row_bytes + (size_t)cl * (4 * BITS));
   }
   __builtin_amdgcn_sched_barrier(0);
   float sc[PASSES], bi[PASSES];
