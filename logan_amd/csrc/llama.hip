@@ -159,11 +159,15 @@ __global__ __launch_bounds__(NT) void dense_gemv_kernel(DenseBatch b) {
         k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
         k.w[u][4] = bq.x; k.w[u][5] = bq.y; k.w[u][6] = bq.z; k.w[u][7] = bq.w;
       } else {
-        const uint4 a = *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(wm) +
-                                                         (size_t)row * d.I + 16 * (size_t)cc);
+        // fmt 15: non-temporal loads (codes and scale/bias words are read
+        // once per launch): config-2 layer 79.5-80.7 -> 76.3-76.8 us; the
+        // raw bf16 rows of fmt 5 measured slower with them (105-107 -> 116 us)
+        const uint4 a = ld_stream<uint4, true>(reinterpret_cast<const uint4 *>(
+            reinterpret_cast<const uint8_t *>(wm) + (size_t)row * d.I + 16 * (size_t)cc));
         k.w[u][0] = a.x; k.w[u][1] = a.y; k.w[u][2] = a.z; k.w[u][3] = a.w;
         const size_t g = (size_t)row * (d.I >> 6) + (cc >> 2);
-        k.sb[u] = (uint32_t)(second ? d.sc2 : d.sc)[g] | ((uint32_t)(second ? d.bi2 : d.bi)[g] << 16);
+        k.sb[u] = (uint32_t)ld_stream<uint16_t, true>((second ? d.sc2 : d.sc) + g) |
+                  ((uint32_t)ld_stream<uint16_t, true>((second ? d.bi2 : d.bi) + g) << 16);
       }
     }
     const uint4 *ph = reinterpret_cast<const uint4 *>(xh + 16 * (size_t)cc);
