@@ -62,9 +62,11 @@ __device__ __forceinline__ void gemv_bf16_body(const GemvParams &a, int bid) {
   kc.init();
   __shared__ float s_part[SPLIT > 1 ? TEAMS * U * MT : 1];
   // non-temporal weight loads for the short-row shapes (config 1: 3.39 ->
-  // 3.30 us); the long-row 8-bit shapes measured slower with them (config-2
-  // layer at M = 1: 52 -> 62 us)
-  constexpr bool NT = SPLIT == 1 && CPL == 1;
+  // 3.30 us) and the two-wave rows of narrow codes (config-5 decode, 4-bit
+  // K = 4096 output projections: 1090-1097 -> 1066-1070 us per token); the
+  // long-row 8-bit shapes measured slower with them (config-2 layer at
+  // M = 1: 52 -> 62 us, 55 -> 59 us with the 4096-code products alone)
+  constexpr bool NT = (SPLIT == 1 && CPL == 1) || (SPLIT == 2 && CPL == 1 && !SW && BITS < 8);
 
   // Loads are branch-free (row and chunk clamped into the matrix, x rows
   // clamped to M) and issued in the order they are needed: x, the raw
