@@ -765,20 +765,33 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(MoeArgs a, MoeMWs w,
 
 // ---------------------------------------------------------------------------
 // 4b. down with the weights staged in LDS (4- and 8-bit codes, groups of 64,
-//     K a multiple of 128 code bytes): block = (tile, 512 rows), 8 waves x 2
-//     pairs of 16-row groups. h (hi, lo) is staged once per 512 output rows
-//     (the register form stages it per 128), and each wave streams its rows'
+//     K a multiple of 128 code bytes): 8 waves, each wave a run of 32-row
+//     pairs of 16-row groups. h (hi, lo) is staged once per block (the
+//     register form stages it per 128 rows), and each wave streams its rows'
 //     codes batch by batch through a three-slot ring of RingSlot batches
 //     (group 0 = rows 32 p + [0, 16), group 1 = rows 32 p + [16, 32) of pair
-//     p), two batches in flight while one is multiplied. The sums of h over
-//     each step (the fold's bias term) are formed once and kept.
+//     p), two batches in flight while one is multiplied, the ring running on
+//     from one pair into the next. The sums of h over each step (the fold's
+//     bias term) are formed once and kept.
+//
+//     One block per CU (the ring and the h tile fill its LDS), so blocks run
+//     in rounds and a block's start (h copy, first batches) and end (last
+//     batches multiplied, nothing in flight) are paid per block. A block over
+//     a whole tile (all D rows, npw = D / 256 pairs per wave) pays them once
+//     per tile (config-5 chunk: 39 us per 2048-row block against 4 x 13.1 us
+//     for 512-row blocks), but 544 such blocks on 256 CUs leave most of the
+//     last round idle. So the first tiles take whole-tile blocks and the last
+//     kMDownSmallUnits 512-row units (npw = 2) follow them in grid order: the
+//     CUs whose whole-tile blocks end first take the small ones (config-5
+//     chunk: 118-119 us per layer with 512-row blocks only, 98 us so; 110 us
+//     with 128 small units, 103 with 512).
 
-constexpr int kMDownLdsRows = 512;  // output rows per block
+constexpr int kMDownLdsRows = 512;      // rows of a small block (32 x 2 pairs x 8 waves)
+constexpr int kMDownSmallUnits = 256;   // 512-row units left to small blocks (one round on 256 CUs)
 
 template <int BITS, bool FP16>
-__global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs w, int ipt) {
-  constexpr int WAVES = 8, NT = WAVES * 64, PW = 2;
-  static_assert(32 * PW * WAVES == kMDownLdsRows, "rows per block");
+__global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs w, int upt) {
+  constexpr int WAVES = 8, NT = WAVES * 64;
   using R = RingSlot<BITS>;
   constexpr int GU = R::GU, NB = 3;
   constexpr int NS = kMDownK / 64;      // steps at most
@@ -790,8 +803,23 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
-  if (tile >= *w.n_tiles) return;
+  // blocks [0, nbt) take whole tiles; then the tiles from nbt on in 512-row
+  // units (upt = ceil(D / 512) per tile; the grid holds max_tiles x upt)
+  const int nt = __builtin_amdgcn_readfirstlane(*w.n_tiles);
+  const int units = nt * upt;
+  const int nbt = units > kMDownSmallUnits ? (units - kMDownSmallUnits) / upt : 0;
+  const int bid = blockIdx.x;
+  int tile, rb, npw;
+  if (bid < nbt) {
+    tile = bid;
+    rb = 0;
+    npw = 2 * upt;
+  } else {
+    tile = nbt + (bid - nbt) / upt;
+    rb = (bid - nbt) % upt;
+    npw = 2;
+  }
+  if (tile >= nt) return;
   const int4 tr = w.tiles[tile];
   const int e = __builtin_amdgcn_readfirstlane(tr.x);
   const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
@@ -802,35 +830,51 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
   const size_t eo = shared ? 0 : (size_t)e;
   const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   const int kbn = (K >> 6) / GU;  // batches per pair
-  const int nbw = PW * kbn;       // batches of the wave
-  const int jw = rb * kMDownLdsRows + wave * 32 * PW;  // the wave's first row
-  // the copy sources of both pairs, formed here: the bank's fields are loaded
-  // into registers, and such a load inside the ring loop would wait for every
-  // copy in flight. Pair p's batch: rows jw + 32 p + 8 i + lane / 8 (i < 4, at
-  // the lane's source chunk), scale / bias words of rows jw + 32 p + [0, 32).
-  const int lr = lane >> 3, sc = 16 * ((lane & 7) ^ lr);
-  const uint8_t *wrow[PW][4];
-  const uint16_t *arow[PW][2];
-  {
-    const uint8_t *wb = dbk.m.w + eo * dbk.w_stride + sc;
-    const size_t rbytes = dbk.m.row_bytes;
-#pragma unroll
-    for (int p = 0; p < PW; ++p) {
-      const int rp = jw + 32 * p;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) wrow[p][i] = wb + (size_t)min(rp + 8 * i + lr, a.D - 1) * rbytes;
-      R::aux_ptr(lane, dbk, dbk, eo, {rp, rp + 16}, a.D - 1, arow[p]);
-    }
+  const int nbw = npw * kbn;      // batches of the wave
+  const int jw = rb * kMDownLdsRows + wave * 32 * npw;  // the wave's first row
+  const int dmax = a.D - 1;
+  // the bank's fields, read here: such a load inside the ring loop would wait
+  // for every copy in flight. Pair p's batch kb: rows jw + 32 p + 8 i + lane / 8
+  // (i < 4) at byte 128 kb + the lane's source chunk; scale / bias words as
+  // RingSlot::aux_ptr lays them out (the lane's row arl, arl1 of the pair).
+  const int lr = lane >> 3;
+  const uint8_t *const wb = dbk.m.w + eo * dbk.w_stride + 16 * ((lane & 7) ^ lr);
+  const size_t rbytes = dbk.m.row_bytes;
+  const int ng = dbk.m.ng;
+  const uint16_t *ab;
+  int arl, arl1;
+  if constexpr (BITS == 4) {
+    ab = (lane < 32 ? dbk.m.sc : dbk.m.bi) + eo * dbk.p_stride + 2 * (lane & 1);
+    arl = (lane & 31) >> 1;
+    arl1 = arl + 16;
+  } else {
+    ab = (((lane >> 4) & 1) ? dbk.m.bi : dbk.m.sc) + eo * dbk.p_stride;
+    arl = 16 * (lane >> 5) + (lane & 15);
+    arl1 = arl;
   }
-  static_assert(PW == 2, "pair of a batch index");
-  auto issue = [&](int b) {
-    const bool p1 = b >= kbn;
-    const int kb = p1 ? b - kbn : b;
-    const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(&swt[b % NB][wave][0]));
+  // the next batch to copy (uniform): index, ring slot, pair, k batch. Past the
+  // wave's last batch the cursor stays there and the copy repeats that batch
+  // into its own slot (the same bytes), which keeps the count of copies behind
+  // every batch at 2 NI.
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&swt[0][wave][0]));
+  int ib = 0, is = 0, ip = 0, ik = 0;
+  auto issue_next = [&]() {
+    const uint32_t d = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)is * (WAVES * R::BYTES));
+    const int rp = jw + 32 * ip;
+    const size_t o = (size_t)128 * ik;
     const uint8_t *wr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wr[i] = (p1 ? wrow[1][i] : wrow[0][i]) + 128 * kb;
-    R::issue(d, wr, (p1 ? arow[1][0] : arow[0][0]) + kb * GU, (p1 ? arow[1][1] : arow[0][1]) + kb * GU);
+    for (int i = 0; i < 4; ++i) wr[i] = wb + (size_t)min(rp + 8 * i + lr, dmax) * rbytes + o;
+    R::issue(d, wr, ab + (size_t)min(rp + arl, dmax) * ng + ik * GU,
+             ab + (size_t)min(rp + arl1, dmax) * ng + ik * GU);
+    if (ib < nbw - 1) {
+      ++ib;
+      is = is == NB - 1 ? 0 : is + 1;
+      if (++ik == kbn) {
+        ik = 0;
+        ++ip;
+      }
+    }
   };
   {
     // stage h (hi, lo) of the tile's rows (physical granule P of row m holds
@@ -851,8 +895,8 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
   }
   // the ring's first two batches behind the h copies (a wave with no rows
   // inside D copies clamped rows and stores nothing)
-  issue(0);
-  issue(min(1, nbw - 1));
+  issue_next();
+  issue_next();
   lds_dma_wait_behind<2 * R::NI>();
   __syncthreads();
   UnpackConsts kc;
@@ -874,19 +918,17 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
       xs[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, ones, xs[u], 0, 0, 0);
     }
   }
-#pragma unroll
-  for (int p = 0; p < PW; ++p) {
+  int cs = 0;  // ring slot of the batch multiplied
+  for (int p = 0; p < npw; ++p) {
     f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int kb = 0; kb < KBM; ++kb) {
       if (kb < kbn) {
-        // two batches in flight behind this one; past the wave's last batch
-        // the issue copies that batch again into its own slot (the same
-        // bytes), which keeps the count behind every batch at 2 NI
-        const int b = p * kbn + kb;
-        issue(min(b + 2, nbw - 1));
+        // two batches in flight behind this one
+        issue_next();
         lds_dma_wait_behind<2 * R::NI>();
-        const uint8_t *slot = &swt[b % NB][wave][0];
+        const uint8_t *slot = &swt[cs][wave][0];
+        cs = cs == NB - 1 ? 0 : cs + 1;
         uint32_t sw[2][GU / 2], bw[2][GU / 2];
         R::aux(slot, r16, sw, bw);
 #pragma unroll
@@ -1058,11 +1100,11 @@ static hipError_t moe_down_launch(const MoeArgs &a, const MoeMWs &w, hipStream_t
     const bool lds = a.B > kMGuSmallB && a.down.m.gs == 64 && a.inter % KB == 0 &&
                      (!a.sdown.m.w || (a.sdown.m.gs == 64 && a.sinter % KB == 0));
     if (lds) {
-      const int ipt = (a.D + kMDownLdsRows - 1) / kMDownLdsRows;
+      const int upt = (a.D + kMDownLdsRows - 1) / kMDownLdsRows;
       if (a.down.m.fp16)
-        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, true>), dim3(w.max_tiles * ipt), dim3(512), 0, st, a, w, ipt);
+        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, true>), dim3(w.max_tiles * upt), dim3(512), 0, st, a, w, upt);
       else
-        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, false>), dim3(w.max_tiles * ipt), dim3(512), 0, st, a, w, ipt);
+        hipLaunchKernelGGL((moe_down_lds_kernel<BITS, false>), dim3(w.max_tiles * upt), dim3(512), 0, st, a, w, upt);
       return hipGetLastError();
     }
   }
