@@ -507,6 +507,16 @@ struct RingSlot {
   }
 };
 
+// As with the down blocks below, one 8-wave block fills a CU (the x tile and
+// the ring), so blocks run in rounds and each pays its start (x tile, first
+// batch) and end. When x fits one chunk, the first tiles take whole-tile
+// blocks (all the tile's 128-row groups, one after another in each wave, the
+// x tile staged once and the ring running on from one group into the next)
+// and the last kMGuSmallUnits (tile, 128-row group) units follow as one-group
+// blocks, taken by the CUs whose whole-tile blocks end first.
+
+constexpr int kMGuSmallUnits = 256;  // one round on 256 CUs
+
 template <int BITS, bool FP16>
 __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMWs w, int ipt) {
   constexpr int WAVES = 8, NT = WAVES * 64, RPB = 16 * WAVES;
@@ -519,32 +529,69 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
-  const int tile = blockIdx.x / ipt, rb = blockIdx.x % ipt;
-  if (tile >= *w.n_tiles) return;
+  const int chunk = a.D < kMChunk ? a.D : kMChunk;
+  const int nch = a.D / chunk;
+  // blocks [0, nbt) take whole tiles (ipt row groups); then the tiles from
+  // nbt on one 128-row group per block
+  const int nt = __builtin_amdgcn_readfirstlane(*w.n_tiles);
+  const int units = nt * ipt;
+  const int nbt = nch == 1 && units > kMGuSmallUnits ? (units - kMGuSmallUnits) / ipt : 0;
+  const int bid = blockIdx.x;
+  int tile, rg0, nrg;
+  if (bid < nbt) {
+    tile = bid;
+    rg0 = 0;
+    nrg = ipt;
+  } else {
+    tile = nbt + (bid - nbt) / ipt;
+    rg0 = (bid - nbt) % ipt;
+    nrg = 1;
+  }
+  if (tile >= nt) return;
   const int4 tr = w.tiles[tile];
   const int e = __builtin_amdgcn_readfirstlane(tr.x);
   const int row0 = __builtin_amdgcn_readfirstlane(tr.y);
   const int cnt = __builtin_amdgcn_readfirstlane(tr.z);
   const bool shared = e < 0;
   const int rows = shared ? a.sinter : a.inter;
-  if (rb * RPB >= rows) return;
+  if (rg0 * RPB >= rows) return;
+  nrg = min(nrg, (rows + RPB - 1) / RPB - rg0);
   const DevBank &gbk = shared ? a.sgate : a.gate;
   const DevBank &ubk = shared ? a.sup : a.up;
   const size_t eo = shared ? 0 : (size_t)e;
-  const int jw = rb * RPB + wave * 16;  // the wave's first row
-  // ring group 0 = the gate rows, group 1 = the same rows of up
+  const int jw0 = rg0 * RPB + wave * 16;  // the wave's first row (row group rg0)
+  const int rmax = rows - 1;
+  // the banks' fields, read here: such a load inside the ring loop would wait
+  // for every copy in flight. Ring group 0 = the gate rows, group 1 = the same
+  // rows of up: rows jr + lane / 8 and jr + 8 + lane / 8 at the lane's source
+  // chunk; scale / bias words as RingSlot::aux_ptr lays them out.
   const int lr = lane >> 3, sc = 16 * ((lane & 7) ^ lr);
-  const int jl0 = min(jw + lr, rows - 1), jl1 = min(jw + 8 + lr, rows - 1);
-  const uint8_t *gb = gbk.m.w + eo * gbk.w_stride + sc, *ub = ubk.m.w + eo * ubk.w_stride + sc;
-  const uint8_t *const wrow[4] = {gb + (size_t)jl0 * gbk.m.row_bytes, gb + (size_t)jl1 * gbk.m.row_bytes,
-                                  ub + (size_t)jl0 * ubk.m.row_bytes, ub + (size_t)jl1 * ubk.m.row_bytes};
-  const uint16_t *arow[2];
-  R::aux_ptr(lane, gbk, ubk, eo, {jw, jw}, rows - 1, arow);
+  const uint8_t *const gb = gbk.m.w + eo * gbk.w_stride + sc;
+  const uint8_t *const ub = ubk.m.w + eo * ubk.w_stride + sc;
+  const size_t grb = gbk.m.row_bytes, urb = ubk.m.row_bytes;
+  const uint16_t *ab0, *ab1;
+  int arl, ang0, ang1;
+  if constexpr (BITS == 4) {
+    ab0 = (lane < 32 ? gbk.m.sc : gbk.m.bi) + eo * gbk.p_stride + 2 * (lane & 1);
+    ab1 = (lane < 32 ? ubk.m.sc : ubk.m.bi) + eo * ubk.p_stride + 2 * (lane & 1);
+    arl = (lane & 31) >> 1;
+    ang0 = gbk.m.ng;
+    ang1 = ubk.m.ng;
+  } else {
+    const bool up = lane >= 32;
+    const bool bias = (lane >> 4) & 1;
+    ab0 = up ? (bias ? ubk.m.bi : ubk.m.sc) + eo * ubk.p_stride
+             : (bias ? gbk.m.bi : gbk.m.sc) + eo * gbk.p_stride;
+    ab1 = ab0;
+    arl = lane & 15;
+    ang0 = up ? ubk.m.ng : gbk.m.ng;
+    ang1 = ang0;
+  }
   const int nslots = a.B * a.k;
-  const int chunk = a.D < kMChunk ? a.D : kMChunk;
-  const int nch = a.D / chunk;
   const int bpc = (chunk >> 6) / GU;  // batches per chunk
+  const int nbc = nrg * bpc;          // batches of a chunk over the block's row groups
   const uint16_t *xsrc = BITS == 4 ? w.xop : a.x;  // x in the operand order
+  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
   UnpackConsts kc;
   kc.init();
   const bf16x8_t ones = mfma_ones();
@@ -552,16 +599,34 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   if (tid < kMTok) s_tok[tid] = shared ? row0 - nslots + min(tid, cnt - 1) : w.tok[row0 + min(tid, cnt - 1)];
   __syncthreads();
 
-  // batch b (absolute: bytes [128 b, 128 b + 128) of every row, steps
-  // [GU b, GU b + GU)) into ring slot b % NB
-  auto issue = [&](int b) {
-    const uint32_t d = __builtin_amdgcn_readfirstlane(lds_addr(&swt[b % NB][wave][0]));
-    const size_t o = (size_t)b * 128;
-    const uint8_t *wr[4] = {wrow[0] + o, wrow[1] + o, wrow[2] + o, wrow[3] + o};
-    R::issue(d, wr, arow[0] + (size_t)b * GU, arow[1] + (size_t)b * GU);
+  // the next batch of chunk c to copy (uniform): index in the chunk's row
+  // group major sequence, ring slot, row group, batch in the chunk (bytes
+  // [128 (c bpc + ibl), + 128) of every row, steps GU (c bpc + ibl) on). Past
+  // the chunk's last batch the cursor stays there and the copy repeats that
+  // batch into its own slot (the same bytes, so step() reads them whether or
+  // not the copy has landed), which keeps the count of copies behind every
+  // batch at NI.
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&swt[0][wave][0]));
+  int ib = 0, is = 0, ir = 0, ibl = 0;
+  auto issue_next = [&](int c) {
+    const uint32_t d = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)is * (WAVES * R::BYTES));
+    const int jr = jw0 + ir * RPB;
+    const int kb = c * bpc + ibl;
+    const size_t o = (size_t)128 * kb;
+    const int jl0 = min(jr + lr, rmax), jl1 = min(jr + 8 + lr, rmax), ja = min(jr + arl, rmax);
+    const uint8_t *wr[4] = {gb + (size_t)jl0 * grb + o, gb + (size_t)jl1 * grb + o,
+                            ub + (size_t)jl0 * urb + o, ub + (size_t)jl1 * urb + o};
+    R::issue(d, wr, ab0 + (size_t)ja * ang0 + kb * GU, ab1 + (size_t)ja * ang1 + kb * GU);
+    if (ib < nbc - 1) {
+      ++ib;
+      is ^= 1;
+      if (++ibl == bpc) {
+        ibl = 0;
+        ++ir;
+      }
+    }
   };
-  auto step = [&](int b, int bl) {
-    const uint8_t *slot = &swt[b % NB][wave][0];
+  auto step = [&](const uint8_t *slot, int bl) {
     uint32_t sw[2][GU / 2], bw[2][GU / 2];
     R::aux(slot, r16, sw, bw);
 #pragma unroll
@@ -584,7 +649,6 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   };
 
   for (int c = 0; c < nch; ++c) {
-    const int b0 = c * bpc;
     // the x tile's copies and the chunk's first batch, then one full wait
     if (c > 0) __syncthreads();
     {
@@ -601,39 +665,47 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
       for (int i = 0; i < NV; ++i)
         if (NT * i + 64 * wave < cnt * gpr) dma(NT * i + 64 * wave);
     }
-    issue(b0);
+    ib = 0;
+    is = 0;
+    ir = 0;
+    ibl = 0;
+    issue_next(c);
     lds_dma_wait();
     __syncthreads();
-    // batch bl + 1 in flight while batch bl is multiplied: wait for all but
-    // the NI copies of the batch issued last. At the chunk's last batch the
-    // issue copies that batch again into its own slot (the same bytes, so
-    // step() reads them whether or not the copy has landed), which keeps
-    // the count of copies behind every batch at NI.
-    for (int bl = 0; bl < bpc; ++bl) {
-      issue(b0 + min(bl + 1, bpc - 1));
-      lds_dma_wait_behind<R::NI>();
-      step(b0 + bl, bl);
-    }
-  }
-  lds_dma_wait();  // no copy into LDS outlives the block
-  // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo bf16,
-  // each at its place in the down pass's operand order
-  const int jj = jw + r16;
-  const int hmax = a.inter > a.sinter ? a.inter : a.sinter;
-  if (jj < rows) {
+    // batch b + 1 in flight while batch b is multiplied: wait for all but the
+    // NI copies of the batch issued last
+    int cs = 0;  // ring slot of the batch multiplied
+    for (int rg = 0; rg < nrg; ++rg) {
+      for (int bl = 0; bl < bpc; ++bl) {
+        issue_next(c);
+        lds_dma_wait_behind<R::NI>();
+        step(&swt[cs][wave][0], bl);
+        cs ^= 1;
+      }
+      if (c == nch - 1) {
+        // h = silu(gate) * up (logan-qwen4/src/lib.rs:8807-8809) as hi + lo
+        // bf16, each at its place in the down pass's operand order
+        const int jj = jw0 + rg * RPB + r16;
+        if (jj < rows) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = 4 * g + i;
-      if (m < cnt) {
-        const float h = silu(acc[0][i]) * acc[1][i];
-        const uint32_t hi = f32_to_bf16_rne(h);
-        const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
-        const size_t o = (size_t)(row0 + m) * hmax + S::op_pos(jj);
-        w.h_hi[o] = (uint16_t)hi;
-        w.h_lo[o] = (uint16_t)lo;
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < cnt) {
+              const float h = silu(acc[0][i]) * acc[1][i];
+              const uint32_t hi = f32_to_bf16_rne(h);
+              const uint32_t lo = f32_to_bf16_rne(h - bf16_to_f32(hi));
+              const size_t o = (size_t)(row0 + m) * hmax + S::op_pos(jj);
+              w.h_hi[o] = (uint16_t)hi;
+              w.h_lo[o] = (uint16_t)lo;
+            }
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
   }
+  lds_dma_wait();  // no copy into LDS outlives the block
 }
 
 // ---------------------------------------------------------------------------
