@@ -608,21 +608,33 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   // batch at NI.
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&swt[0][wave][0]));
   int ib = 0, is = 0, ir = 0, ibl = 0;
+  // the copy sources of row group ir at byte 0 of its rows, formed when the
+  // cursor enters the group
+  const uint8_t *cw[4];
+  const uint16_t *ca0, *ca1;
+  auto set_rows = [&]() {
+    const int jr = jw0 + ir * RPB;
+    const int jl0 = min(jr + lr, rmax), jl1 = min(jr + 8 + lr, rmax), ja = min(jr + arl, rmax);
+    cw[0] = gb + (size_t)jl0 * grb;
+    cw[1] = gb + (size_t)jl1 * grb;
+    cw[2] = ub + (size_t)jl0 * urb;
+    cw[3] = ub + (size_t)jl1 * urb;
+    ca0 = ab0 + (size_t)ja * ang0;
+    ca1 = ab1 + (size_t)ja * ang1;
+  };
   auto issue_next = [&](int c) {
     const uint32_t d = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)is * (WAVES * R::BYTES));
-    const int jr = jw0 + ir * RPB;
     const int kb = c * bpc + ibl;
     const size_t o = (size_t)128 * kb;
-    const int jl0 = min(jr + lr, rmax), jl1 = min(jr + 8 + lr, rmax), ja = min(jr + arl, rmax);
-    const uint8_t *wr[4] = {gb + (size_t)jl0 * grb + o, gb + (size_t)jl1 * grb + o,
-                            ub + (size_t)jl0 * urb + o, ub + (size_t)jl1 * urb + o};
-    R::issue(d, wr, ab0 + (size_t)ja * ang0 + kb * GU, ab1 + (size_t)ja * ang1 + kb * GU);
+    const uint8_t *wr[4] = {cw[0] + o, cw[1] + o, cw[2] + o, cw[3] + o};
+    R::issue(d, wr, ca0 + kb * GU, ca1 + kb * GU);
     if (ib < nbc - 1) {
       ++ib;
       is ^= 1;
       if (++ibl == bpc) {
         ibl = 0;
         ++ir;
+        set_rows();
       }
     }
   };
@@ -669,6 +681,7 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
     is = 0;
     ir = 0;
     ibl = 0;
+    set_rows();
     issue_next(c);
     lds_dma_wait();
     __syncthreads();
@@ -930,21 +943,30 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
   // every batch at 2 NI.
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&swt[0][wave][0]));
   int ib = 0, is = 0, ip = 0, ik = 0;
+  // the copy sources of pair ip at byte 0 of its rows, formed when the cursor
+  // enters the pair
+  const uint8_t *cw[4];
+  const uint16_t *ca0, *ca1;
+  auto set_pair = [&]() {
+    const int rp = jw + 32 * ip;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cw[i] = wb + (size_t)min(rp + 8 * i + lr, dmax) * rbytes;
+    ca0 = ab + (size_t)min(rp + arl, dmax) * ng;
+    ca1 = ab + (size_t)min(rp + arl1, dmax) * ng;
+  };
+  set_pair();
   auto issue_next = [&]() {
     const uint32_t d = __builtin_amdgcn_readfirstlane(ring0 + (uint32_t)is * (WAVES * R::BYTES));
-    const int rp = jw + 32 * ip;
     const size_t o = (size_t)128 * ik;
-    const uint8_t *wr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wr[i] = wb + (size_t)min(rp + 8 * i + lr, dmax) * rbytes + o;
-    R::issue(d, wr, ab + (size_t)min(rp + arl, dmax) * ng + ik * GU,
-             ab + (size_t)min(rp + arl1, dmax) * ng + ik * GU);
+    const uint8_t *wr[4] = {cw[0] + o, cw[1] + o, cw[2] + o, cw[3] + o};
+    R::issue(d, wr, ca0 + ik * GU, ca1 + ik * GU);
     if (ib < nbw - 1) {
       ++ib;
       is = is == NB - 1 ? 0 : is + 1;
       if (++ik == kbn) {
         ik = 0;
         ++ip;
+        set_pair();
       }
     }
   };
