@@ -37,6 +37,7 @@ constexpr int kMDownK = 512;       // largest down K (expert intermediate size)
 constexpr int kMMaxSlots = 65536;  // B * k
 constexpr int kMMaxE = 1024;
 constexpr int kMGroupThreads = 1024;
+constexpr int kMGroupKeep = 8;     // routed slots per grouping thread held in registers
 
 struct MoeMWs {
   int *n_tiles;       // [1]
@@ -152,7 +153,18 @@ __global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, M
     s_fill[e] = 0;
   }
   __syncthreads();
-  for (int i = tid; i < nslots; i += kMGroupThreads) atomicAdd(&s_cnt[w.topk_idx[i]], 1);
+  // the first kMGroupKeep slots of each thread stay in registers for the
+  // placement below (one global read of the routes instead of two)
+  int keep[kMGroupKeep];
+#pragma unroll
+  for (int q = 0; q < kMGroupKeep; ++q) {
+    const int i = tid + q * kMGroupThreads;
+    keep[q] = i < nslots ? w.topk_idx[i] : 0;
+  }
+#pragma unroll
+  for (int q = 0; q < kMGroupKeep; ++q)
+    if (tid + q * kMGroupThreads < nslots) atomicAdd(&s_cnt[keep[q]], 1);
+  for (int i = tid + kMGroupKeep * kMGroupThreads; i < nslots; i += kMGroupThreads) atomicAdd(&s_cnt[w.topk_idx[i]], 1);
   __syncthreads();
   {
     // exclusive scan over experts of (slots << 14 | tiles): slots <= 2^16,
@@ -179,7 +191,17 @@ __global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, M
   }
   __syncthreads();
   // placement in arrival order (each row's arithmetic is independent of it)
-  for (int i = tid; i < nslots; i += kMGroupThreads) {
+#pragma unroll
+  for (int q = 0; q < kMGroupKeep; ++q) {
+    const int i = tid + q * kMGroupThreads;
+    if (i < nslots) {
+      const int e = keep[q];
+      const int gp = s_start[e] + atomicAdd(&s_fill[e], 1);
+      w.tok[gp] = i / a.k;
+      w.gpos[i] = gp;
+    }
+  }
+  for (int i = tid + kMGroupKeep * kMGroupThreads; i < nslots; i += kMGroupThreads) {
     const int e = w.topk_idx[i];
     const int gp = s_start[e] + atomicAdd(&s_fill[e], 1);
     w.tok[gp] = i / a.k;
