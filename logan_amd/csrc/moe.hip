@@ -618,27 +618,36 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a, MoeWs w) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     const int t = (int)(i / a.D), d = (int)(i % a.D);
     float acc = 0.f;
-    // eight ranks' rows and weights in flight at a time, added in rank order
-    for (int r0 = 0; r0 < a.k; r0 += 8) {
-      int gp[8];
-      float wt[8], yv[8];
+    // the shared expert's row and gate do not depend on the routes: in flight
+    // with the first round (shared rows follow the routed ones)
+    float ysh = 0.f, gs = 0.f;
+    if (a.sdown.m.w) {
+      ysh = w.y[(size_t)(a.B * a.k + t) * a.D + d];
+      gs = w.gs[t];
+    }
+    // sixteen ranks' rows and weights, then their outputs, in flight at a
+    // time, added in rank order
+    for (int r0 = 0; r0 < a.k; r0 += 16) {
+      int gp[16];
+      float wt[16], yv[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int slot = t * a.k + min(r0 + j, a.k - 1);
-        gp[j] = w.gpos[slot];
-        wt[j] = r0 + j < a.k ? w.topk_w[slot] : 0.f;
+      for (int j = 0; j < 16; ++j) {
+        gp[j] = 0;
+        wt[j] = 0.f;
+        if (r0 + j < a.k) {
+          gp[j] = w.gpos[t * a.k + r0 + j];
+          wt[j] = w.topk_w[t * a.k + r0 + j];
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) yv[j] = w.y[(size_t)gp[j] * a.D + d];
+      for (int j = 0; j < 16; ++j)
+        if (r0 + j < a.k) yv[j] = w.y[(size_t)gp[j] * a.D + d];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < 16; ++j)
         if (r0 + j < a.k) acc = fmaf(yv[j], wt[j], acc);
     }
     float o = acc;
-    if (a.sdown.m.w) {
-      const int row = a.B * a.k + t;  // shared rows follow the routed ones
-      o = fmaf(w.y[(size_t)row * a.D + d], w.gs[t], acc);
-    }
+    if (a.sdown.m.w) o = fmaf(ysh, gs, acc);
     if (a.out_f32)
       reinterpret_cast<float *>(a.out)[i] = o;
     else

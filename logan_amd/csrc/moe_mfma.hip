@@ -1089,28 +1089,48 @@ __global__ __launch_bounds__(512, 1) void moe_down_lds_kernel(MoeArgs a, MoeMWs 
 // ---------------------------------------------------------------------------
 // 5. rank-ordered combine (logan-qwen4/src/lib.rs:8692-8711)
 
+constexpr int kMCombRanks = 16;  // ranks' rows in flight per round (top-k up to 16 in one)
+
 __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) {
   // four consecutive outputs per thread (D % 4 == 0)
   const int D4 = a.D >> 2;
+  // with D a multiple of 256 a wave's 64 outputs share one token, whose route
+  // words are then read once per wave
+  const bool wave_tok = (D4 & 63) == 0;
   const long long n = (long long)a.B * D4;
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
-    const int t = (int)(i / D4), d = 4 * (int)(i % D4);
+    int t = (int)(i / D4);
+    if (wave_tok) t = __builtin_amdgcn_readfirstlane(t);
+    const int d = 4 * (int)(i - (long long)t * D4);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    // eight ranks' rows and weights in flight at a time, added in rank order
-    for (int r0 = 0; r0 < a.k; r0 += 8) {
-      int gp[8];
-      float wt[8];
-      float4 yv[8];
+    // the shared expert's row and gate do not depend on the routes: in flight
+    // with the first round
+    float gs = 0.f;
+    float4 vs = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.sdown.m.w) {
+      gs = w.gs[t];
+      vs = *reinterpret_cast<const float4 *>(w.y + ((size_t)a.B * a.k + t) * a.D + d);
+    }
+    // a round's routed rows and weights, then all its rows' outputs in
+    // flight together, added in rank order (logan-qwen4/src/lib.rs:8692-8711)
+    for (int r0 = 0; r0 < a.k; r0 += kMCombRanks) {
+      int gp[kMCombRanks];
+      float wt[kMCombRanks];
+      float4 yv[kMCombRanks];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int slot = t * a.k + min(r0 + j, a.k - 1);
-        gp[j] = w.gpos[slot];
-        wt[j] = w.topk_w[slot];
+      for (int j = 0; j < kMCombRanks; ++j) {
+        gp[j] = 0;
+        wt[j] = 0.f;
+        if (r0 + j < a.k) {
+          gp[j] = w.gpos[t * a.k + r0 + j];
+          wt[j] = w.topk_w[t * a.k + r0 + j];
+        }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) yv[j] = *reinterpret_cast<const float4 *>(w.y + (size_t)gp[j] * a.D + d);
+      for (int j = 0; j < kMCombRanks; ++j)
+        if (r0 + j < a.k) yv[j] = *reinterpret_cast<const float4 *>(w.y + (size_t)gp[j] * a.D + d);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kMCombRanks; ++j) {
         if (r0 + j < a.k) {
           acc.x = fmaf(yv[j].x, wt[j], acc.x);
           acc.y = fmaf(yv[j].y, wt[j], acc.y);
@@ -1120,12 +1140,10 @@ __global__ __launch_bounds__(256) void moe_mcombine_kernel(MoeArgs a, MoeMWs w) 
       }
     }
     if (a.sdown.m.w) {
-      const float gs = w.gs[t];
-      const float4 v = *reinterpret_cast<const float4 *>(w.y + ((size_t)a.B * a.k + t) * a.D + d);
-      acc.x = fmaf(v.x, gs, acc.x);
-      acc.y = fmaf(v.y, gs, acc.y);
-      acc.z = fmaf(v.z, gs, acc.z);
-      acc.w = fmaf(v.w, gs, acc.w);
+      acc.x = fmaf(vs.x, gs, acc.x);
+      acc.y = fmaf(vs.y, gs, acc.y);
+      acc.z = fmaf(vs.z, gs, acc.z);
+      acc.w = fmaf(vs.w, gs, acc.w);
     }
     const size_t o = (size_t)t * a.D + d;
     if (a.out_f32) {
