@@ -93,11 +93,29 @@ size_t moe_mfma_workspace_bytes(int B, int D, int inter, int sinter, int E, int 
 // ---------------------------------------------------------------------------
 // 1. routing and the shared-expert gate, one wave per token
 
+constexpr int kMRouteXr = 4;  // x granules (8 bf16) per lane held across the routing
+
 template <int KPL, bool F32>
 __global__ __launch_bounds__(256) void moe_mroute_kernel(MoeArgs a, MoeMWs w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= a.B) return;  // whole waves leave together
+  // the token's first 64 kMRouteXr granules of x (and of the shared gate
+  // vector), loaded before the routing so that their latency overlaps it
+  const int n8 = a.D >> 3;
+  const bool op4 = a.gate.m.bits == 4;
+  const bool gdot = a.sgate.m.w && a.se_gate_vec;
+  const uint4 *xs = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D);
+  const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec);
+  uint4 xr[kMRouteXr], gr[kMRouteXr];
+#pragma unroll
+  for (int q = 0; q < kMRouteXr; ++q) {
+    const int c = lane + 64 * q;
+    xr[q] = make_uint4(0u, 0u, 0u, 0u);
+    gr[q] = make_uint4(0u, 0u, 0u, 0u);
+    if (c < n8 && (op4 || gdot)) xr[q] = xs[c];
+    if (c < n8 && gdot) gr[q] = gv[c];
+  }
   int id;
   float wt;
   wave_topk_lanes<KPL, F32>(a.logits, (size_t)t * a.E, a.E, a.k, id, wt);
@@ -108,22 +126,30 @@ __global__ __launch_bounds__(256) void moe_mroute_kernel(MoeArgs a, MoeMWs w) {
     if (a.idx_out) a.idx_out[s] = id;
     if (a.w_out) a.w_out[s] = wt;
   }
-  if (a.gate.m.bits == 4) {
+  if (op4) {
     // x in the operand order of 4-bit codes: pairs (x_p, x_{p+4}) of every 8
-    const uint4 *xs = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D);
     uint4 *xd = reinterpret_cast<uint4 *>(w.xop + (size_t)t * a.D);
-    for (int c = lane; c < (a.D >> 3); c += 64) xd[c] = __builtin_bit_cast(uint4, a_nibble_order(xs[c]));
+#pragma unroll
+    for (int q = 0; q < kMRouteXr; ++q) {
+      const int c = lane + 64 * q;
+      if (c < n8) xd[c] = __builtin_bit_cast(uint4, a_nibble_order(xr[q]));
+    }
+    for (int c = lane + 64 * kMRouteXr; c < n8; c += 64) xd[c] = __builtin_bit_cast(uint4, a_nibble_order(xs[c]));
   }
   if (a.sgate.m.w) {
     // sigmoid(se_g . x_t) (logan-qwen4/src/lib.rs:7602-7604), 8 bf16 per lane per load
     float g = 1.0f;
-    if (a.se_gate_vec) {
+    if (gdot) {
       float acc = 0.f;
-      const int n8 = a.D >> 3;
-      const uint4 *gv = reinterpret_cast<const uint4 *>(a.se_gate_vec);
-      const uint4 *xv = reinterpret_cast<const uint4 *>(a.x + (size_t)t * a.D);
-      for (int c = lane; c < n8; c += 64) {
-        const uint4 gq = gv[c], xq = xv[c];
+#pragma unroll
+      for (int q = 0; q < kMRouteXr; ++q) {
+        acc = dot2(gr[q].x, xr[q].x, acc);
+        acc = dot2(gr[q].y, xr[q].y, acc);
+        acc = dot2(gr[q].z, xr[q].z, acc);
+        acc = dot2(gr[q].w, xr[q].w, acc);
+      }
+      for (int c = lane + 64 * kMRouteXr; c < n8; c += 64) {
+        const uint4 gq = gv[c], xq = xs[c];
         acc = dot2(gq.x, xq.x, acc);
         acc = dot2(gq.y, xq.y, acc);
         acc = dot2(gq.z, xq.z, acc);
