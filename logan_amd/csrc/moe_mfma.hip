@@ -233,15 +233,17 @@ __global__ __launch_bounds__(kMGroupThreads) void moe_mgroup_kernel(MoeArgs a, M
     w.tok[gp] = i / a.k;
     w.gpos[i] = gp;
   }
+  // the shared expert's tiles first, then the routed ones (the launches
+  // give the first tiles whole-tile blocks)
+  const int R = s_routed_tiles;
+  const int S = a.sgate.m.w ? (a.B + kMTok - 1) / kMTok : 0;
   for (int e = tid; e < a.E; e += kMGroupThreads) {
     const int c = s_cnt[e];
     for (int tt = 0; tt * kMTok < c; ++tt)
-      w.tiles[s_tbase[e] + tt] = make_int4(e, s_start[e] + kMTok * tt, min(kMTok, c - kMTok * tt), 0);
+      w.tiles[S + s_tbase[e] + tt] = make_int4(e, s_start[e] + kMTok * tt, min(kMTok, c - kMTok * tt), 0);
   }
-  const int R = s_routed_tiles;
-  const int S = a.sgate.m.w ? (a.B + kMTok - 1) / kMTok : 0;
   for (int tt = tid; tt < S; tt += kMGroupThreads)
-    w.tiles[R + tt] = make_int4(-1, nslots + kMTok * tt, min(kMTok, a.B - kMTok * tt), 0);
+    w.tiles[tt] = make_int4(-1, nslots + kMTok * tt, min(kMTok, a.B - kMTok * tt), 0);
   if (tid == 0) *w.n_tiles = R + S;
 }
 

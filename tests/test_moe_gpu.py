@@ -472,6 +472,39 @@ def test_moe_prefill_chunk_sampled(gpu):
         assert normwise_rel(out32[t], out_d[t]) <= 5e-5
 
 
+@pytest.mark.parametrize("bits,fp16,D,sinter", [(4, True, 2048, 384), (8, False, 1024, 256),
+                                                 (4, False, 768, 512)])
+def test_moe_prefill_whole_tile_blocks(gpu, bits, fp16, D, sinter):
+    """B = 512 over E = 256, top-8: enough tiles that the LDS-staged gate/up
+    and down launches give the first tiles whole-tile blocks and the last
+    units one-group / 512-row blocks. Shared experts narrower than the routed
+    ones (fewer row groups and a shorter down K in their whole-tile blocks),
+    8-bit codes, fp16 sidecars, and D = 768 (down blocks running past D); a
+    sample of tokens against the oracle and every token against the
+    per-token path."""
+    import torch
+    from logan_amd import _lib
+
+    print(f"moe whole-tile blocks bits={bits} fp16={fp16} D={D} sinter={sinter}", flush=True)
+    layer = Layer(torch, 256, 8, D, 512, bits, 64, seed=91 + bits + D, fp16=fp16, sinter=sinter)
+    rng = np.random.default_rng(92 + D)
+    B = 512
+    xb = make_x(rng, B, D)
+    lb = make_logits(rng, B, 256)
+    out32, idx, w = run_layer(torch, layer, xb, lb, torch.float32)
+    out32 = out32.cpu().numpy()
+    _check_tokens(layer, xb, lb, out32, idx, w, range(0, B, 53))
+    _lib.lib().logan_hip_set_moe_mfma_min_batch(1 << 20)
+    try:
+        out_d, idx_d, _ = run_layer(torch, layer, xb, lb, torch.float32)
+    finally:
+        _lib.lib().logan_hip_set_moe_mfma_min_batch(0)
+    np.testing.assert_array_equal(idx, idx_d)
+    out_d = out_d.cpu().numpy()
+    for t in range(B):
+        assert normwise_rel(out32[t], out_d[t]) <= 5e-5
+
+
 @pytest.mark.parametrize("mfma_min_b", [1 << 20], indirect=True)
 def test_moe_large_batch_per_token_passes(gpu, mfma_min_b):
     """With the MFMA path off, B = 100 runs the per-token path in passes of
