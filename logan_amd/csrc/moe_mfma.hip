@@ -573,6 +573,9 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
   using R = RingSlot<BITS>;
   constexpr int GU = R::GU, NB = 2;  // two batches in a wave's ring
   __shared__ __align__(16) uint16_t sx[kMTok * kMChunk];
+  // sums of the tile's x over each 64-code step of the chunk (the fold's bias
+  // term), formed once per chunk for all the block's row groups
+  __shared__ __align__(16) float sxs[kMChunk / 64][kMTok];
   __shared__ __align__(16) uint8_t swt[NB][WAVES][R::BYTES];
   __shared__ int s_tok[kMTok];
   using S = MfmaStep<BITS>;
@@ -696,8 +699,8 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
       bf16x8_t a0, a1, b0, b1;
       S::a_ops(sx + r16 * chunk, ((bl * GU + u) * 64 + 16 * g) >> 3, r16, a0, a1);
       const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
-      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
-      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      const float4 xv = *reinterpret_cast<const float4 *>(&sxs[bl * GU + u][4 * g]);
+      const f32x4_t xs = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         SkRaw<BITS> rw;
@@ -734,6 +737,17 @@ __global__ __launch_bounds__(512, 1) void moe_gateup_lds_kernel(MoeArgs a, MoeMW
     set_rows();
     issue_next(c);
     lds_dma_wait();
+    __syncthreads();
+    // the step sums of x: wave w forms steps w, w + 8, ... (one MFMA pair
+    // against ones each; lanes of one 16-lane row hold the same four tokens)
+    for (int u = wave; u < (chunk >> 6); u += WAVES) {
+      bf16x8_t a0, a1;
+      S::a_ops(sx + r16 * chunk, (u * 64 + 16 * g) >> 3, r16, a0, a1);
+      const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, z, 0, 0, 0);
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, xs, 0, 0, 0);
+      if (r16 == 0) *reinterpret_cast<float4 *>(&sxs[u][4 * g]) = make_float4(xs[0], xs[1], xs[2], xs[3]);
+    }
     __syncthreads();
     // batch b + 1 in flight while batch b is multiplied: wait for all but the
     // NI copies of the batch issued last
