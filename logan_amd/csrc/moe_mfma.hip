@@ -10,13 +10,18 @@
 //   2. moe_mgroup_kernel       one block: group the (token, rank) slots by
 //                              expert and cut each group into tiles of at most
 //                              16 slots; the shared expert gets tiles of 16
-//                              tokens after the routed ones
+//                              tokens ahead of the routed ones
 //   3. moe_gateup_mfma_kernel  per (tile, 64 rows): the tile's x rows staged
 //                              in LDS, gate and up rows of 16 per wave, SwiGLU
 //                              fused; h stored as two bf16 planes (hi, lo with
 //                              h = hi + lo to 2^-17) in grouped row order
+//      moe_gateup_lds_kernel   above 128 tokens (4/8-bit, groups of 64): the
+//                              weights streamed through a per-wave LDS ring,
+//                              whole-tile blocks and then 128-row ones
 //   4. moe_down_mfma_kernel    per (tile, 128 rows): h hi/lo staged in LDS,
 //                              two MFMA passes (hi, lo), y in grouped order
+//      moe_down_lds_kernel     above 128 tokens: the LDS ring again,
+//                              whole-tile blocks and then 512-row ones
 //   5. moe_mcombine_kernel     out[t] = sum_r w_r y[row(t, r)] (rank order)
 //                              + gs_t y[shared row t]
 // Numerics: codes exact, activations exact (x bf16; h to 2^-17), f32
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256) void moe_mroute_kernel(MoeArgs a, MoeMWs w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= a.B) return;  // whole waves leave together
-  // the token's first 64 kMRouteXr granules of x (and of the shared gate
+  // the token's first 64 x kMRouteXr granules of x (and of the shared gate
   // vector), loaded before the routing so that their latency overlaps it
   const int n8 = a.D >> 3;
   const bool op4 = a.gate.m.bits == 4;
